@@ -1,0 +1,157 @@
+/*
+ * mi355x-gemv.h -- the thin C-ABI layer between host C++ and the gfx950 HIP
+ * kernels of the decode GEMV path.
+ *
+ * Everything here takes plain pointers and sizes.  Device pointers are
+ * addresses returned by mi355x_malloc (or any HIP device allocation on the
+ * same device).  No call throws; every int-returning call returns one of the
+ * MI355X_* status codes and, on failure, leaves a message retrievable with
+ * mi355x_last_error() on the calling thread.
+ *
+ * Interfaces replaced (reference file:line):
+ *   mi355x_gemv            XdnaGemvEngine::run / run_quant
+ *                          (include/xdna/xdna_gemv_engine.h:141-170,
+ *                           src/xdna-gemv-engine.cpp:1817-1992)
+ *   mi355x_gemv_bf16       XdnaGemvEngine::run_bf16 / run_quant_bf16
+ *                          (include/xdna/xdna_gemv_engine.h:148-170)
+ *   mi355x_prepack_*       Q4Prepacker::pack / dequantize_packed
+ *                          (include/xdna/q4_prepack.h:25-45) -- successor:
+ *                          repack into the HBM-resident planar layout
+ *   mi355x_ctx_*           the engine object and its XRT device/staging
+ *                          (XdnaGemvEngine ctor, src/xdna-gemv-engine.cpp:1725-1750;
+ *                           DmaStreamer, include/xdna/dma_streamer.h:64-111)
+ *   mi355x_row_bytes       bytes_per_row_for_quant (include/xdna/kquants.h:196-200)
+ *   mi355x_set_iq_grid     ggml's iq3xxs_grid / iq2s_grid tables, which the
+ *                          reference reaches only through ggml-cpu via dlsym
+ *                          (src/xdna-gemv-engine.cpp:1388-1396)
+ */
+#ifndef MI355X_GEMV_H
+#define MI355X_GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355X_API __attribute__((visibility("default")))
+
+/* status codes */
+#define MI355X_OK 0
+#define MI355X_EINVAL (-1)       /* invalid argument: shape, size, type, pointer */
+#define MI355X_EUNSUPPORTED (-2) /* valid ggml input this build does not compute */
+#define MI355X_EHIP (-3)         /* HIP runtime error (message carries hipError) */
+#define MI355X_ENOMEM (-4)       /* device or pinned-host allocation failed */
+
+/* ggml type ids (GGUF on-disk values) of the weight formats */
+#define MI355X_TYPE_F32 0
+#define MI355X_TYPE_Q4_0 2
+#define MI355X_TYPE_Q3_K 11
+#define MI355X_TYPE_Q4_K 12
+#define MI355X_TYPE_Q5_K 13
+#define MI355X_TYPE_Q6_K 14
+#define MI355X_TYPE_IQ3_XXS 18
+#define MI355X_TYPE_IQ3_S 21
+#define MI355X_TYPE_IQ2_S 22
+#define MI355X_TYPE_IQ4_XS 23
+
+typedef struct mi355x_ctx mi355x_ctx; /* one device + one HIP stream */
+
+/* Message of the last failing call on this thread ("" if none). */
+MI355X_API const char *mi355x_last_error(void);
+
+/* ---- devices and contexts ------------------------------------------------ */
+MI355X_API int mi355x_device_count(int *count);
+/* Creates a context on `device` with its own non-blocking HIP stream. */
+MI355X_API int mi355x_ctx_create(int device, mi355x_ctx **out);
+MI355X_API void mi355x_ctx_destroy(mi355x_ctx *ctx);
+/* Waits for all work queued on the context's stream. */
+MI355X_API int mi355x_ctx_sync(mi355x_ctx *ctx);
+/* The context's hipStream_t, as an opaque pointer. */
+MI355X_API void *mi355x_ctx_stream(mi355x_ctx *ctx);
+MI355X_API int mi355x_ctx_device(mi355x_ctx *ctx);
+/* Free and total device memory (hipMemGetInfo) of the context's device. */
+MI355X_API int mi355x_mem_info(mi355x_ctx *ctx, size_t *free_bytes, size_t *total_bytes);
+/* Device name and PCI bus id into caller buffers (NUL-terminated). */
+MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, char *pci,
+                                      size_t pci_len);
+
+/* ---- memory ----------------------------------------------------------------
+ * Copies and fills are ordered on the context's stream; the *_sync forms
+ * return after completion. */
+MI355X_API int mi355x_malloc(mi355x_ctx *ctx, size_t bytes, void **dptr);
+MI355X_API int mi355x_free(mi355x_ctx *ctx, void *dptr);
+MI355X_API int mi355x_memcpy_h2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
+MI355X_API int mi355x_memcpy_d2h(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
+MI355X_API int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Fill with a byte value using a kernel (safe under graph capture). */
+MI355X_API int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes);
+
+/* ---- formats ------------------------------------------------------------- */
+/* Bytes of one ggml row of K values of `type`; -1 if K is not a multiple
+ * of the type's block or the type is unknown. */
+MI355X_API int64_t mi355x_row_bytes(int type, int64_t K);
+/* 1 if this build computes GEMVs of `type` right now (IQ3_XXS and IQ2_S need
+ * their grid installed with mi355x_set_iq_grid first), else 0. */
+MI355X_API int mi355x_type_ready(int type);
+/* Installs the IQ3_XXS (uint32[256]) or IQ2_S (uint64[1024]) grid for every
+ * context created afterwards and every existing one.  `bytes` must equal the
+ * table size.  Table contents are ggml's; this library does not ship them. */
+MI355X_API int mi355x_set_iq_grid(int type, const void *table, size_t bytes);
+
+/* ---- prepack: ggml raw bytes <-> resident layout ----------------------------
+ * The resident layout of a tensor occupies exactly the same bytes as its
+ * ggml encoding (N * row_bytes) and is a row-local byte permutation of it, so
+ * any byte range [offset, offset+size) of the ggml encoding maps to the same
+ * set of rows.  Q4_0 rows become [16-byte nibble groups of every block][fp16
+ * scales of every block]; the other types keep the ggml block order.
+ *
+ * Scatter `size` bytes of ggml encoding (host memory), which start at byte
+ * `offset` of the tensor, into the resident tensor `packed_dev`. */
+MI355X_API int mi355x_prepack_from_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K,
+                                        void *packed_dev, const void *raw_host, size_t offset,
+                                        size_t size);
+/* Same, with the raw bytes already on the device (raw_dev holds `size`
+ * bytes).  raw_dev and packed_dev must not overlap. */
+MI355X_API int mi355x_prepack_from_device(mi355x_ctx *ctx, int type, int64_t N, int64_t K,
+                                          void *packed_dev, const void *raw_dev, size_t offset,
+                                          size_t size);
+/* Gather ggml bytes [offset, offset+size) of a resident tensor into host
+ * memory (the inverse permutation). */
+MI355X_API int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K,
+                                     const void *packed_dev, void *raw_host, size_t offset,
+                                     size_t size);
+
+/* ---- GEMV ----------------------------------------------------------------
+ * y[r] = sum_c w[r][c] * x[c] for r < N, with W the resident (prepacked)
+ * tensor of N rows of K values.  x and y are device pointers; the call only
+ * enqueues work on the context's stream (use mi355x_ctx_sync to wait).
+ * Validation mirrors XdnaGemvEngine::run (src/xdna-gemv-engine.cpp:1823-1839):
+ * K must be a multiple of the block, N*row_bytes must not overflow. */
+MI355X_API int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                           const float *x, float *y);
+/* Same with BF16 activations (raw bits), widened exactly to f32. */
+MI355X_API int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                                const uint16_t *x_bf16, float *y);
+/* M activation rows at once (row m at x + m*x_stride floats, output at
+ * y + m*y_stride floats); the M-row case the reference admits for weights in
+ * its own buffer type (src/ggml-xdna.cpp:110-112, 287-296). */
+MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                                   const float *x, int64_t x_stride, float *y, int64_t y_stride,
+                                   int64_t M);
+
+/* ---- measurement -----------------------------------------------------------
+ * Times `iters` back-to-back launches of mi355x_gemv on the context's stream
+ * with HIP events, rotating through `n_weights` resident copies of W
+ * (weights[i]), after `warmup` untimed launches.  *ms_total receives the
+ * elapsed milliseconds of the timed launches. */
+MI355X_API int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights,
+                                int n_weights, int64_t N, int64_t K, const float *x, float *y,
+                                int warmup, int iters, double *ms_total);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

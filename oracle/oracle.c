@@ -1,0 +1,524 @@
+/*
+ * CPU oracle for the quantized decode GEMV path -- TEST INFRASTRUCTURE ONLY.
+ * See oracle.h for the numerics contract and the reference lines followed.
+ * Build with -ffp-contract=off: the expression order below is the contract.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* scalar conversions                                                        */
+/* ------------------------------------------------------------------------ */
+
+static float bits_to_f32(uint32_t u) {
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+static uint32_t f32_to_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, sizeof u);
+    return u;
+}
+
+/* src/xdna-q4-0-reference.cpp:207-242: sign | exponent rebias | mantissa,
+ * subnormal halves renormalised, inf/nan payload widened. */
+float orc_fp16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0) {
+        if (m == 0) return bits_to_f32(sign);
+        int exp = -14;
+        while (!(m & 0x400u)) {
+            m <<= 1;
+            exp -= 1;
+        }
+        m &= 0x3ffu;
+        return bits_to_f32(sign | ((uint32_t)(exp + 127) << 23) | (m << 13));
+    }
+    if (e == 31) return bits_to_f32(sign | 0x7f800000u | (m << 13));
+    return bits_to_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+float orc_bf16_to_f32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
+
+/* src/xdna-q4-0-reference.cpp:250-259: add 0x7fff + lsb, truncate. */
+uint16_t orc_f32_to_bf16(float v) {
+    uint32_t u = f32_to_bits(v);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ------------------------------------------------------------------------ */
+/* geometry                                                                  */
+/* ------------------------------------------------------------------------ */
+
+int64_t orc_block_values(int type) {
+    switch (type) {
+    case ORC_Q4_0: return 32;
+    case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K:
+    case ORC_IQ4_XS: case ORC_IQ3_S: case ORC_IQ3_XXS: case ORC_IQ2_S:
+        return 256;
+    default: return 0;
+    }
+}
+
+/* include/xdna/kquants.h:182-194 */
+int64_t orc_block_bytes(int type) {
+    switch (type) {
+    case ORC_Q4_0: return 18;
+    case ORC_Q3_K: return 110;
+    case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
+    case ORC_Q6_K: return 210;
+    case ORC_IQ4_XS: return 136;
+    case ORC_IQ3_S: return 110;
+    case ORC_IQ3_XXS: return 98;
+    case ORC_IQ2_S: return 82;
+    default: return 0;
+    }
+}
+
+int64_t orc_row_bytes(int type, int64_t K) {
+    int64_t bv = orc_block_values(type);
+    if (bv == 0 || K < 0 || K % bv != 0) return -1;
+    return (K / bv) * orc_block_bytes(type);
+}
+
+/* src/xdna-q4-0-reference.cpp:261-300 */
+int orc_q4_0_validate_row(uint64_t value_count, uint64_t encoded_bytes) {
+    if (value_count % 32u != 0) return ORC_EINVAL;
+    uint64_t blocks = value_count / 32u;
+    if (blocks > UINT64_MAX / 18u) return ORC_EINVAL;
+    return encoded_bytes == blocks * 18u ? ORC_OK : ORC_EINVAL;
+}
+
+int orc_q4_0_validate_matrix(uint64_t rows, uint64_t values_per_row,
+                             uint64_t encoded_bytes) {
+    if (values_per_row % 32u != 0) return ORC_EINVAL;
+    uint64_t row_bytes = (values_per_row / 32u) * 18u;
+    if (rows != 0 && row_bytes > UINT64_MAX / rows) return ORC_EINVAL;
+    return encoded_bytes == rows * row_bytes ? ORC_OK : ORC_EINVAL;
+}
+
+/* ------------------------------------------------------------------------ */
+/* format tables                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* IQ4_NL codebook (include/xdna/kquants.h:215-217). */
+static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                   1,    13,   25,  38,  53,  69,  89,  113};
+
+/* IQ3_S grid, 512 entries of four odd magnitudes 1..15 (include/xdna/kquants.h:220-285). */
+static const uint32_t k_iq3s_grid[512] = {
+    0x01010101u, 0x01010103u, 0x01010105u, 0x0101010bu, 0x0101010fu, 0x01010301u, 0x01010303u, 0x01010305u,
+    0x01010309u, 0x0101030du, 0x01010501u, 0x01010503u, 0x0101050bu, 0x01010707u, 0x01010901u, 0x01010905u,
+    0x0101090bu, 0x0101090fu, 0x01010b03u, 0x01010b07u, 0x01010d01u, 0x01010d05u, 0x01010f03u, 0x01010f09u,
+    0x01010f0fu, 0x01030101u, 0x01030103u, 0x01030105u, 0x01030109u, 0x01030301u, 0x01030303u, 0x0103030bu,
+    0x01030501u, 0x01030507u, 0x0103050fu, 0x01030703u, 0x0103070bu, 0x01030909u, 0x01030d03u, 0x01030d0bu,
+    0x01030f05u, 0x01050101u, 0x01050103u, 0x0105010bu, 0x0105010fu, 0x01050301u, 0x01050307u, 0x0105030du,
+    0x01050503u, 0x0105050bu, 0x01050701u, 0x01050709u, 0x01050905u, 0x0105090bu, 0x0105090fu, 0x01050b03u,
+    0x01050b07u, 0x01050f01u, 0x01050f07u, 0x01070107u, 0x01070303u, 0x0107030bu, 0x01070501u, 0x01070505u,
+    0x01070703u, 0x01070707u, 0x0107070du, 0x01070909u, 0x01070b01u, 0x01070b05u, 0x01070d0fu, 0x01070f03u,
+    0x01070f0bu, 0x01090101u, 0x01090307u, 0x0109030fu, 0x01090503u, 0x01090509u, 0x01090705u, 0x01090901u,
+    0x01090907u, 0x01090b03u, 0x01090f01u, 0x010b0105u, 0x010b0109u, 0x010b0501u, 0x010b0505u, 0x010b050du,
+    0x010b0707u, 0x010b0903u, 0x010b090bu, 0x010b090fu, 0x010b0d0du, 0x010b0f07u, 0x010d010du, 0x010d0303u,
+    0x010d0307u, 0x010d0703u, 0x010d0b05u, 0x010d0f03u, 0x010f0101u, 0x010f0105u, 0x010f0109u, 0x010f0501u,
+    0x010f0505u, 0x010f050du, 0x010f0707u, 0x010f0b01u, 0x010f0b09u, 0x03010101u, 0x03010103u, 0x03010105u,
+    0x03010109u, 0x03010301u, 0x03010303u, 0x03010307u, 0x0301030bu, 0x0301030fu, 0x03010501u, 0x03010505u,
+    0x03010703u, 0x03010709u, 0x0301070du, 0x03010b09u, 0x03010b0du, 0x03010d03u, 0x03010f05u, 0x03030101u,
+    0x03030103u, 0x03030107u, 0x0303010du, 0x03030301u, 0x03030309u, 0x03030503u, 0x03030701u, 0x03030707u,
+    0x03030903u, 0x03030b01u, 0x03030b05u, 0x03030f01u, 0x03030f0du, 0x03050101u, 0x03050305u, 0x0305030bu,
+    0x0305030fu, 0x03050501u, 0x03050509u, 0x03050705u, 0x03050901u, 0x03050907u, 0x03050b0bu, 0x03050d01u,
+    0x03050f05u, 0x03070103u, 0x03070109u, 0x0307010fu, 0x03070301u, 0x03070307u, 0x03070503u, 0x0307050fu,
+    0x03070701u, 0x03070709u, 0x03070903u, 0x03070d05u, 0x03070f01u, 0x03090107u, 0x0309010bu, 0x03090305u,
+    0x03090309u, 0x03090703u, 0x03090707u, 0x03090905u, 0x0309090du, 0x03090b01u, 0x03090b09u, 0x030b0103u,
+    0x030b0301u, 0x030b0307u, 0x030b0503u, 0x030b0701u, 0x030b0705u, 0x030b0b03u, 0x030d0501u, 0x030d0509u,
+    0x030d050fu, 0x030d0909u, 0x030d090du, 0x030f0103u, 0x030f0107u, 0x030f0301u, 0x030f0305u, 0x030f0503u,
+    0x030f070bu, 0x030f0903u, 0x030f0d05u, 0x030f0f01u, 0x05010101u, 0x05010103u, 0x05010107u, 0x0501010bu,
+    0x0501010fu, 0x05010301u, 0x05010305u, 0x05010309u, 0x0501030du, 0x05010503u, 0x05010507u, 0x0501050fu,
+    0x05010701u, 0x05010705u, 0x05010903u, 0x05010907u, 0x0501090bu, 0x05010b01u, 0x05010b05u, 0x05010d0fu,
+    0x05010f01u, 0x05010f07u, 0x05010f0bu, 0x05030101u, 0x05030105u, 0x05030301u, 0x05030307u, 0x0503030fu,
+    0x05030505u, 0x0503050bu, 0x05030703u, 0x05030709u, 0x05030905u, 0x05030b03u, 0x05050103u, 0x05050109u,
+    0x0505010fu, 0x05050503u, 0x05050507u, 0x05050701u, 0x0505070fu, 0x05050903u, 0x05050b07u, 0x05050b0fu,
+    0x05050f03u, 0x05050f09u, 0x05070101u, 0x05070105u, 0x0507010bu, 0x05070303u, 0x05070505u, 0x05070509u,
+    0x05070703u, 0x05070707u, 0x05070905u, 0x05070b01u, 0x05070d0du, 0x05090103u, 0x0509010fu, 0x05090501u,
+    0x05090507u, 0x05090705u, 0x0509070bu, 0x05090903u, 0x05090f05u, 0x05090f0bu, 0x050b0109u, 0x050b0303u,
+    0x050b0505u, 0x050b070fu, 0x050b0901u, 0x050b0b07u, 0x050b0f01u, 0x050d0101u, 0x050d0105u, 0x050d010fu,
+    0x050d0503u, 0x050d0b0bu, 0x050d0d03u, 0x050f010bu, 0x050f0303u, 0x050f050du, 0x050f0701u, 0x050f0907u,
+    0x050f0b01u, 0x07010105u, 0x07010303u, 0x07010307u, 0x0701030bu, 0x0701030fu, 0x07010505u, 0x07010703u,
+    0x07010707u, 0x0701070bu, 0x07010905u, 0x07010909u, 0x0701090fu, 0x07010b03u, 0x07010d07u, 0x07010f03u,
+    0x07030103u, 0x07030107u, 0x0703010bu, 0x07030309u, 0x07030503u, 0x07030507u, 0x07030901u, 0x07030d01u,
+    0x07030f05u, 0x07030f0du, 0x07050101u, 0x07050305u, 0x07050501u, 0x07050705u, 0x07050709u, 0x07050b01u,
+    0x07070103u, 0x07070301u, 0x07070309u, 0x07070503u, 0x07070507u, 0x0707050fu, 0x07070701u, 0x07070903u,
+    0x07070907u, 0x0707090fu, 0x07070b0bu, 0x07070f07u, 0x07090107u, 0x07090303u, 0x0709030du, 0x07090505u,
+    0x07090703u, 0x07090b05u, 0x07090d01u, 0x07090d09u, 0x070b0103u, 0x070b0301u, 0x070b0305u, 0x070b050bu,
+    0x070b0705u, 0x070b0909u, 0x070b0b0du, 0x070b0f07u, 0x070d030du, 0x070d0903u, 0x070f0103u, 0x070f0107u,
+    0x070f0501u, 0x070f0505u, 0x070f070bu, 0x09010101u, 0x09010109u, 0x09010305u, 0x09010501u, 0x09010509u,
+    0x0901050fu, 0x09010705u, 0x09010903u, 0x09010b01u, 0x09010f01u, 0x09030105u, 0x0903010fu, 0x09030303u,
+    0x09030307u, 0x09030505u, 0x09030701u, 0x0903070bu, 0x09030907u, 0x09030b03u, 0x09030b0bu, 0x09050103u,
+    0x09050107u, 0x09050301u, 0x0905030bu, 0x09050503u, 0x09050707u, 0x09050901u, 0x09050b0fu, 0x09050d05u,
+    0x09050f01u, 0x09070109u, 0x09070303u, 0x09070307u, 0x09070501u, 0x09070505u, 0x09070703u, 0x0907070bu,
+    0x09090101u, 0x09090105u, 0x09090509u, 0x0909070fu, 0x09090901u, 0x09090f03u, 0x090b010bu, 0x090b010fu,
+    0x090b0503u, 0x090b0d05u, 0x090d0307u, 0x090d0709u, 0x090d0d01u, 0x090f0301u, 0x090f030bu, 0x090f0701u,
+    0x090f0907u, 0x090f0b03u, 0x0b010105u, 0x0b010301u, 0x0b010309u, 0x0b010505u, 0x0b010901u, 0x0b010909u,
+    0x0b01090fu, 0x0b010b05u, 0x0b010d0du, 0x0b010f09u, 0x0b030103u, 0x0b030107u, 0x0b03010bu, 0x0b030305u,
+    0x0b030503u, 0x0b030705u, 0x0b030f05u, 0x0b050101u, 0x0b050303u, 0x0b050507u, 0x0b050701u, 0x0b05070du,
+    0x0b050b07u, 0x0b070105u, 0x0b07010fu, 0x0b070301u, 0x0b07050fu, 0x0b070909u, 0x0b070b03u, 0x0b070d0bu,
+    0x0b070f07u, 0x0b090103u, 0x0b090109u, 0x0b090501u, 0x0b090705u, 0x0b09090du, 0x0b0b0305u, 0x0b0b050du,
+    0x0b0b0b03u, 0x0b0b0b07u, 0x0b0d0905u, 0x0b0f0105u, 0x0b0f0109u, 0x0b0f0505u, 0x0d010303u, 0x0d010307u,
+    0x0d01030bu, 0x0d010703u, 0x0d010707u, 0x0d010d01u, 0x0d030101u, 0x0d030501u, 0x0d03050fu, 0x0d030d09u,
+    0x0d050305u, 0x0d050709u, 0x0d050905u, 0x0d050b0bu, 0x0d050d05u, 0x0d050f01u, 0x0d070101u, 0x0d070309u,
+    0x0d070503u, 0x0d070901u, 0x0d09050bu, 0x0d090907u, 0x0d090d05u, 0x0d0b0101u, 0x0d0b0107u, 0x0d0b0709u,
+    0x0d0b0d01u, 0x0d0d010bu, 0x0d0d0901u, 0x0d0f0303u, 0x0d0f0307u, 0x0f010101u, 0x0f010109u, 0x0f01010fu,
+    0x0f010501u, 0x0f010505u, 0x0f01070du, 0x0f010901u, 0x0f010b09u, 0x0f010d05u, 0x0f030105u, 0x0f030303u,
+    0x0f030509u, 0x0f030907u, 0x0f03090bu, 0x0f050103u, 0x0f050109u, 0x0f050301u, 0x0f05030du, 0x0f050503u,
+    0x0f050701u, 0x0f050b03u, 0x0f070105u, 0x0f070705u, 0x0f07070bu, 0x0f070b07u, 0x0f090103u, 0x0f09010bu,
+    0x0f090307u, 0x0f090501u, 0x0f090b01u, 0x0f0b0505u, 0x0f0b0905u, 0x0f0d0105u, 0x0f0d0703u, 0x0f0f0101u,
+};
+
+uint8_t orc_ksigns_iq2xs(int i) {
+    int parity = __builtin_popcount((unsigned)i) & 1;
+    return (uint8_t)(i | (parity << 7));
+}
+
+/* ------------------------------------------------------------------------ */
+/* per-type row dequantizers                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Q4_0: 18-byte block, fp16 d then 16 bytes; value j = (qs[j] & 15) - 8,
+ * value j + 16 = (qs[j] >> 4) - 8; w = (float)q * d
+ * (include/xdna/q4_0_reference.h:15-33, src/xdna-q4-0-reference.cpp:302-328). */
+static void dq_q4_0(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 32; ++b) {
+        const uint8_t *blk = row + 18 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2;
+        for (int j = 0; j < 16; ++j) {
+            y[32 * b + j] = (float)((int)(qs[j] & 15) - 8) * d;
+            y[32 * b + 16 + j] = (float)((int)(qs[j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* 6-bit scale/min pair j of a Q4_K/Q5_K block (include/xdna/kquants.h:204-212). */
+static void scale_min_k4(int j, const uint8_t *q, int *sc, int *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Q4_K: d, dmin (fp16), 12 scale bytes, 128 quant bytes.  Each 64-value
+ * chunk uses two sub-blocks: low nibbles with (sc0,m0), high nibbles with
+ * (sc1,m1): w = (d*sc)*q - dmin*m (include/xdna/kquants.h:290-315). */
+static void dq_q4_k(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 144 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        float dmin = orc_fp16_to_f32(rd16(blk + 2));
+        const uint8_t *sc = blk + 4;
+        const uint8_t *q = blk + 16;
+        for (int c = 0; c < 4; ++c) {
+            int s0, m0, s1, m1;
+            scale_min_k4(2 * c, sc, &s0, &m0);
+            scale_min_k4(2 * c + 1, sc, &s1, &m1);
+            float d0 = d * (float)s0, n0 = dmin * (float)m0;
+            float d1 = d * (float)s1, n1 = dmin * (float)m1;
+            for (int l = 0; l < 32; ++l) *y++ = d0 * (float)(q[l] & 15) - n0;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] >> 4) - n1;
+            q += 32;
+        }
+    }
+}
+
+/* Q5_K: as Q4_K plus a fifth bit from qh[32]; chunk c takes bit 2c for the
+ * low-nibble half and bit 2c+1 for the high half (include/xdna/kquants.h:317-348). */
+static void dq_q5_k(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 176 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        float dmin = orc_fp16_to_f32(rd16(blk + 2));
+        const uint8_t *sc = blk + 4;
+        const uint8_t *qh = blk + 16;
+        const uint8_t *ql = blk + 48;
+        for (int c = 0; c < 4; ++c) {
+            int s0, m0, s1, m1;
+            scale_min_k4(2 * c, sc, &s0, &m0);
+            scale_min_k4(2 * c + 1, sc, &s1, &m1);
+            float d0 = d * (float)s0, n0 = dmin * (float)m0;
+            float d1 = d * (float)s1, n1 = dmin * (float)m1;
+            unsigned lo_bit = 1u << (2 * c), hi_bit = 2u << (2 * c);
+            for (int l = 0; l < 32; ++l)
+                *y++ = d0 * (float)((ql[l] & 15) + ((qh[l] & lo_bit) ? 16 : 0)) - n0;
+            for (int l = 0; l < 32; ++l)
+                *y++ = d1 * (float)((ql[l] >> 4) + ((qh[l] & hi_bit) ? 16 : 0)) - n1;
+            ql += 32;
+        }
+    }
+}
+
+/* Q3_K: hmask[32], qs[64], 12 packed bytes of sixteen 6-bit scales, fp16 d
+ * at byte 108.  Scale s (0..15): low 4 bits from byte s%8 (nibble s/8), high
+ * 2 bits from byte 8 + s%4 (bit pair s/4).  Value = 2-bit q minus 4 when the
+ * hmask bit is clear; w = (d*(s-32)) * v (include/xdna/kquants.h:350-389). */
+static void q3_k_scales(const uint8_t *p, int out[16]) {
+    for (int s = 0; s < 16; ++s) {
+        int lo = (p[s % 8] >> (4 * (s / 8))) & 15;
+        int hi = (p[8 + s % 4] >> (2 * (s / 4))) & 3;
+        out[s] = lo | (hi << 4);
+    }
+}
+
+static void dq_q3_k(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 110 * b;
+        const uint8_t *hm = blk;
+        const uint8_t *q = blk + 32;
+        int sc[16];
+        q3_k_scales(blk + 96, sc);
+        float dall = orc_fp16_to_f32(rd16(blk + 108));
+        int is = 0;
+        unsigned mbit = 1;
+        for (int half = 0; half < 2; ++half) {
+            for (int shift = 0; shift < 8; shift += 2) {
+                for (int g = 0; g < 2; ++g) {
+                    float dl = dall * ((float)sc[is++] - 32.0f);
+                    for (int l = 0; l < 16; ++l) {
+                        int idx = 16 * g + l;
+                        float v = (float)((q[idx] >> shift) & 3) -
+                                  ((hm[idx] & mbit) ? 0.0f : 4.0f);
+                        *y++ = dl * v;
+                    }
+                }
+                mbit <<= 1;
+            }
+            q += 32;
+        }
+    }
+}
+
+/* Q6_K: ql[128], qh[64], int8 scales[16], fp16 d at byte 208.  Per 128-value
+ * half: four 32-value groups (ql low, ql+32 low, ql high, ql+32 high) with
+ * qh bit pairs 0,2,4,6; q = 6-bit - 32; w = (d*sc)*q
+ * (include/xdna/kquants.h:391-419). */
+static void dq_q6_k(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 210 * b;
+        const uint8_t *ql = blk;
+        const uint8_t *qh = blk + 128;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        float d = orc_fp16_to_f32(rd16(blk + 208));
+        for (int half = 0; half < 2; ++half) {
+            for (int l = 0; l < 32; ++l) {
+                int is = l / 16;
+                int q1 = (int)(int8_t)((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                int q2 = (int)(int8_t)((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                int q3 = (int)(int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                int q4 = (int)(int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l] = d * (float)sc[is] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
+/* IQ4_XS: fp16 d, scales_h (u16), scales_l[4], qs[128].  Sub-block ib of 32:
+ * 6-bit ls = nibble ib of scales_l | 2 bits ib of scales_h; dl = d*(ls-32);
+ * first 16 values from low nibbles, next 16 from high nibbles through the
+ * IQ4_NL codebook (include/xdna/kquants.h:421-441). */
+static void dq_iq4_xs(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 136 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        unsigned sh = rd16(blk + 2);
+        const uint8_t *sl = blk + 4;
+        const uint8_t *qs = blk + 8;
+        for (int ib = 0; ib < 8; ++ib) {
+            int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+            float dl = d * (float)(ls - 32);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = dl * (float)k_iq4nl[qs[j] & 15];
+                y[j + 16] = dl * (float)k_iq4nl[qs[j] >> 4];
+            }
+            y += 32;
+            qs += 16;
+        }
+    }
+}
+
+/* IQ3_S: fp16 d, qs[64], qh[8], signs[32], scales[4].  Eight groups of 32;
+ * group g uses scale nibble g of scales (db = d*(1+2*nib)), qh[g] supplies
+ * the 9th index bit of its eight grid lookups (bit k for lookup k), signs
+ * bytes 4g..4g+3 one bit per value (include/xdna/kquants.h:443-490). */
+static void dq_iq3_s(const uint8_t *row, int64_t K, float *y) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 110 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2;
+        const uint8_t *qh = blk + 66;
+        const uint8_t *signs = blk + 74;
+        const uint8_t *scales = blk + 106;
+        for (int g = 0; g < 8; ++g) {
+            int nib = (scales[g / 2] >> (4 * (g % 2))) & 15;
+            float db = d * (1.0f + 2.0f * (float)nib);
+            for (int k = 0; k < 8; ++k) {
+                unsigned idx = qs[8 * g + k] | (((unsigned)qh[g] >> k & 1u) << 8);
+                uint32_t gv = k_iq3s_grid[idx];
+                uint8_t sb = signs[4 * g + k / 2];
+                for (int j = 0; j < 4; ++j) {
+                    float mag = (float)((gv >> (8 * j)) & 0xffu);
+                    int bit = 4 * (k & 1) + j;
+                    *y++ = db * mag * (((sb >> bit) & 1) ? -1.0f : 1.0f);
+                }
+            }
+        }
+    }
+}
+
+/* IQ3_XXS (ggml, external): fp16 d, qs[64] grid indices, then eight u32
+ * words (one per 32-value group): bits 0..27 four 7-bit sign indices, bits
+ * 28..31 the scale; db = (d*(0.5+ls))*0.5.  Parity unpinned. */
+static void dq_iq3_xxs(const uint8_t *row, int64_t K, float *y, const uint32_t *grid) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 98 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2;
+        const uint8_t *ss = blk + 66;
+        for (int g = 0; g < 8; ++g) {
+            uint32_t aux = (uint32_t)ss[4 * g] | ((uint32_t)ss[4 * g + 1] << 8) |
+                           ((uint32_t)ss[4 * g + 2] << 16) | ((uint32_t)ss[4 * g + 3] << 24);
+            float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+            for (int l = 0; l < 4; ++l) {
+                uint8_t sg = orc_ksigns_iq2xs((aux >> (7 * l)) & 127);
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t gv = grid[qs[8 * g + 2 * l + h]];
+                    for (int j = 0; j < 4; ++j) {
+                        float mag = (float)((gv >> (8 * j)) & 0xffu);
+                        *y++ = db * mag * (((sg >> (4 * h + j)) & 1) ? -1.0f : 1.0f);
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* IQ2_S (ggml, external): fp16 d, qs[32] low index bytes, signs[32], qh[8]
+ * (two index bits per lookup), scales[8] (two nibbles per 32-value group:
+ * low for the first 16 values, high for the next 16); db = (d*(0.5+s))*0.25.
+ * Parity unpinned. */
+static void dq_iq2_s(const uint8_t *row, int64_t K, float *y, const uint64_t *grid) {
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const uint8_t *blk = row + 82 * b;
+        float d = orc_fp16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2;
+        const uint8_t *signs = blk + 34;
+        const uint8_t *qh = blk + 66;
+        const uint8_t *scales = blk + 74;
+        for (int g = 0; g < 8; ++g) {
+            float db0 = d * (0.5f + (float)(scales[g] & 15)) * 0.25f;
+            float db1 = d * (0.5f + (float)(scales[g] >> 4)) * 0.25f;
+            for (int l = 0; l < 4; ++l) {
+                float dl = l < 2 ? db0 : db1;
+                unsigned idx = qs[4 * g + l] | ((((unsigned)qh[g]) >> (2 * l) & 3u) << 8);
+                uint64_t gv = grid[idx];
+                uint8_t sg = signs[4 * g + l];
+                for (int j = 0; j < 8; ++j) {
+                    float mag = (float)((gv >> (8 * j)) & 0xffu);
+                    *y++ = dl * mag * (((sg >> j) & 1) ? -1.0f : 1.0f);
+                }
+            }
+        }
+    }
+}
+
+int orc_dequant_row(int type, const uint8_t *row, int64_t K, float *out, const void *grid) {
+    if (orc_row_bytes(type, K) < 0 || (K > 0 && (!row || !out))) return ORC_EINVAL;
+    switch (type) {
+    case ORC_Q4_0: dq_q4_0(row, K, out); return ORC_OK;
+    case ORC_Q4_K: dq_q4_k(row, K, out); return ORC_OK;
+    case ORC_Q5_K: dq_q5_k(row, K, out); return ORC_OK;
+    case ORC_Q3_K: dq_q3_k(row, K, out); return ORC_OK;
+    case ORC_Q6_K: dq_q6_k(row, K, out); return ORC_OK;
+    case ORC_IQ4_XS: dq_iq4_xs(row, K, out); return ORC_OK;
+    case ORC_IQ3_S: dq_iq3_s(row, K, out); return ORC_OK;
+    case ORC_IQ3_XXS:
+        if (!grid) return ORC_ENOGRID;
+        dq_iq3_xxs(row, K, out, (const uint32_t *)grid);
+        return ORC_OK;
+    case ORC_IQ2_S:
+        if (!grid) return ORC_ENOGRID;
+        dq_iq2_s(row, K, out, (const uint64_t *)grid);
+        return ORC_OK;
+    default: return ORC_EINVAL;
+    }
+}
+
+/* y[r] = sequential fp32 sum of fl(w*x): the order of
+ * src/xdna-q4-0-reference.cpp:169-203 and include/xdna/kquants.h:495-577. */
+int orc_gemv_f32(int type, const uint8_t *W, int64_t N, int64_t K,
+                 const float *x, float *y, const void *grid) {
+    int64_t rb = orc_row_bytes(type, K);
+    if (rb < 0 || N < 0) return ORC_EINVAL;
+    if ((type == ORC_IQ3_XXS || type == ORC_IQ2_S) && !grid) return ORC_ENOGRID;
+    if (N == 0) return ORC_OK;
+    if (!W || !y || (K > 0 && !x)) return ORC_EINVAL;
+    float *w = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    if (!w) return ORC_EINVAL;
+    for (int64_t r = 0; r < N; ++r) {
+        orc_dequant_row(type, W + r * rb, K, w, grid);
+        float s = 0.0f;
+        for (int64_t c = 0; c < K; ++c) {
+            float p = w[c] * x[c];
+            s = s + p;
+        }
+        y[r] = s;
+    }
+    free(w);
+    return ORC_OK;
+}
+
+int orc_gemv_bf16(int type, const uint8_t *W, int64_t N, int64_t K,
+                  const uint16_t *x_bf16, float *y, const void *grid) {
+    if (K < 0) return ORC_EINVAL;
+    float *x = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    if (!x) return ORC_EINVAL;
+    for (int64_t c = 0; c < K; ++c) x[c] = orc_bf16_to_f32(x_bf16[c]);
+    int rc = orc_gemv_f32(type, W, N, K, x, y, grid);
+    free(x);
+    return rc;
+}
+
+int orc_row_norms(int type, const uint8_t *W, int64_t N, int64_t K, double *norms,
+                  const void *grid) {
+    int64_t rb = orc_row_bytes(type, K);
+    if (rb < 0 || N < 0) return ORC_EINVAL;
+    if ((type == ORC_IQ3_XXS || type == ORC_IQ2_S) && !grid) return ORC_ENOGRID;
+    if (N == 0) return ORC_OK;
+    float *w = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    if (!w) return ORC_EINVAL;
+    for (int64_t r = 0; r < N; ++r) {
+        orc_dequant_row(type, W + r * rb, K, w, grid);
+        double s = 0.0;
+        for (int64_t c = 0; c < K; ++c) s += (double)w[c] * (double)w[c];
+        norms[r] = sqrt(s);
+    }
+    free(w);
+    return ORC_OK;
+}

@@ -1,0 +1,162 @@
+"""Q4_0 GEMV on the GPU vs the CPU oracle (through the C-ABI).
+
+Mirrors the reference's Q4_0 checks: known answers of
+tests/test-q4-0-reference.cpp:157-210 and tests/test-backend.cpp:58-98,
+the accuracy/zero/sweep cases of tests/test-gemv-accuracy.cpp:103-409, and
+the BASELINE shapes at full size.
+"""
+import numpy as np
+import pytest
+
+import mi355x
+import synth
+from tolerance import check_gemv
+
+pytestmark = pytest.mark.gpu
+
+Q4_0 = mi355x.Q4_0
+
+
+def run_gpu(ctx, raw, N, K, x, chunk=None):
+    w = ctx.resident(Q4_0, raw, N, K, chunk=chunk)
+    try:
+        return ctx.gemv(w, x)
+    finally:
+        w.free()
+
+
+def parity(ctx, oracle, raw, N, K, x, what):
+    y = run_gpu(ctx, raw, N, K, x)
+    ref = oracle.gemv(Q4_0, raw, N, K, x)
+    norms = oracle.row_norms(Q4_0, raw, N, K)
+    return check_gemv(y, ref, norms, x, what)
+
+
+def test_known_answer_backend_128(ctx):
+    # tests/test-backend.cpp:58-98: 128x256, qs 0x99 (+1,+1), d = 1.0, x = 0.5 -> 128.0
+    N, K = 128, 256
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:] = 0x99
+    raw = np.tile(blk, N * K // 32)
+    y = run_gpu(ctx, raw, N, K, np.full(K, 0.5, dtype=np.float32))
+    assert np.array_equal(y, np.full(N, 128.0, dtype=np.float32))
+
+
+def test_known_answer_two_rows(ctx):
+    # tests/test-q4-0-reference.cpp:128-143,193-210: rows give 528 and -264 for x = 1..32
+    raw = np.zeros(36, dtype=np.uint8)
+    raw[0:2] = [0x00, 0x3C]
+    raw[2:18] = 0x99
+    raw[18:20] = [0x00, 0x38]
+    raw[20:36] = 0x77
+    x = np.arange(1, 33, dtype=np.float32)
+    y = run_gpu(ctx, raw, 2, 32, x)
+    assert y.tolist() == [528.0, -264.0]
+
+
+def test_known_answer_edge_block(ctx):
+    # tests/test-q4-0-reference.cpp:49-54,186-191: low nibbles 0..15, high 15..0 -> dot = -264
+    edge = np.array([0x00, 0x3c, 0xf0, 0xe1, 0xd2, 0xc3, 0xb4, 0xa5, 0x96,
+                     0x87, 0x78, 0x69, 0x5a, 0x4b, 0x3c, 0x2d, 0x1e, 0x0f], dtype=np.uint8)
+    x = np.arange(1, 33, dtype=np.float32)
+    assert run_gpu(ctx, edge, 1, 32, x).tolist() == [-264.0]
+
+
+def test_every_nibble_value(ctx, oracle):
+    # all 16 codes in every position, scales spanning fp16 normal/subnormal range
+    N, K = 64, 512
+    rng = np.random.default_rng(3)
+    raw = synth.random_q4_0(N, K, seed=5).reshape(N, K // 32, 18)
+    scales = np.array([0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0xBC00, 0x8001, 0x2E66], dtype=np.uint16)
+    raw[..., 0:2] = scales[rng.integers(0, len(scales), size=(N, K // 32))].view(np.uint8).reshape(N, K // 32, 2)
+    raw = raw.reshape(-1)
+    x = synth.activations(K, seed=6) * np.float32(1e-3)
+    parity(ctx, oracle, raw, N, K, x, "edge scales")
+
+
+def test_uniform_weights(ctx, oracle):
+    # tests/test-gemv-accuracy.cpp:128-153: qs 0x99, d = 0.5, x = 0.25 -> 32.0 for all rows
+    N, K = 256, 256
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[0:2] = [0x00, 0x38]
+    blk[2:] = 0x99
+    raw = np.tile(blk, N * K // 32)
+    y = run_gpu(ctx, raw, N, K, np.full(K, 0.25, dtype=np.float32))
+    assert np.array_equal(y, np.full(N, 32.0, dtype=np.float32))
+
+
+@pytest.mark.parametrize("N,K", [(16, 64), (128, 256), (256, 512), (512, 1024), (1024, 2048)])
+def test_zero_activation_is_exact_zero(ctx, N, K):
+    # tests/test-gemv-accuracy.cpp:184-217
+    raw = synth.random_q4_0(N, K, seed=505)
+    y = run_gpu(ctx, raw, N, K, np.zeros(K, dtype=np.float32))
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("N,K", [(512, 512), (256, 256), (1024, 1024), (4096, 4096), (1, 32), (1, 4096),
+                                 (33, 64), (127, 128), (255, 64), (384, 128), (513, 64), (1536, 128),
+                                 (11008, 4096), (100, 96), (64, 5120), (40, 14336), (24, 17408)])
+def test_random_codes(ctx, oracle, N, K):
+    # tests/test-gemv-accuracy.cpp:315-396 shapes, plus odd block counts and K beyond one LDS chunk
+    raw = synth.random_q4_0(N, K, seed=810 + N + K)
+    x = np.random.default_rng(811).uniform(-1, 1, K).astype(np.float32)
+    parity(ctx, oracle, raw, N, K, x, f"random {N}x{K}")
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (8192, 8192), (17408, 5120), (151936, 2048)])
+def test_baseline_shapes(ctx, oracle, N, K):
+    # f32 N(0,0.02) weights quantized to Q4_0, x ~ N(0,1)
+    raw = synth.quantize_q4_0(synth.normal_weights(N, K, seed=1000 + K))
+    x = synth.activations(K, seed=2000 + K)
+    stats = parity(ctx, oracle, raw, N, K, x, f"baseline {N}x{K}")
+    print(f"Q4_0 {N}x{K}: {stats}")
+
+
+def test_bf16_activations(ctx, oracle):
+    # tests/test-gemv-accuracy.cpp:156-178 (run_bf16 vs gemv_bf16)
+    N, K = 512, 256
+    raw = synth.random_q4_0(N, K, seed=303)
+    xf = np.random.default_rng(404).uniform(-1, 1, K).astype(np.float32)
+    xb = np.array([oracle.f32_to_bf16(float(v)) for v in xf], dtype=np.uint16)
+    y = run_gpu(ctx, raw, N, K, xb)
+    ref = oracle.gemv(Q4_0, raw, N, K, xb)
+    xw = np.array([oracle.bf16_to_f32(int(b)) for b in xb], dtype=np.float32)
+    check_gemv(y, ref, oracle.row_norms(Q4_0, raw, N, K), xw, "bf16")
+
+
+def test_prepack_round_trip_and_chunks(ctx):
+    N, K = 96, 2048
+    raw = synth.random_q4_0(N, K, seed=11).reshape(-1)
+    for chunk in (None, 7, 1000, 18 * 64 + 5):
+        w = ctx.resident(Q4_0, raw, N, K, chunk=chunk)
+        try:
+            assert np.array_equal(w.raw_bytes(), raw), f"chunk={chunk}"
+            assert np.array_equal(w.raw_bytes(1001, 333), raw[1001:1334])
+        finally:
+            w.free()
+
+
+def test_chunked_upload_gives_same_gemv(ctx, oracle):
+    N, K = 200, 4096
+    raw = synth.random_q4_0(N, K, seed=12)
+    x = synth.activations(K, seed=13)
+    a = run_gpu(ctx, raw, N, K, x)
+    b = run_gpu(ctx, raw, N, K, x, chunk=12345)
+    assert np.array_equal(a, b)
+
+
+def test_rejects_bad_shapes(ctx):
+    buf = ctx.alloc(4096)
+    try:
+        rc = ctx.gemv_ptr(Q4_0, buf.ptr, 10, 33, buf.ptr, buf.ptr)
+        assert rc == mi355x.EINVAL and "multiple of 32" in mi355x.last_error()
+        rc = ctx.gemv_ptr(Q4_0, 0, 10, 64, buf.ptr, buf.ptr)
+        assert rc == mi355x.EINVAL and "null pointer" in mi355x.last_error()
+        rc = ctx.gemv_ptr(Q4_0, buf.ptr, -1, 64, buf.ptr, buf.ptr)
+        assert rc == mi355x.EINVAL
+        rc = ctx.gemv_ptr(Q4_0, buf.ptr, 1 << 62, 1 << 20, buf.ptr, buf.ptr)
+        assert rc == mi355x.EINVAL and "overflow" in mi355x.last_error()
+        assert ctx.gemv_ptr(Q4_0, buf.ptr, 0, 64, buf.ptr, buf.ptr) == mi355x.OK
+    finally:
+        buf.free()

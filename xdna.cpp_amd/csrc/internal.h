@@ -1,0 +1,68 @@
+// Host-side internals of the HIP layer (not part of the public C-ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "mi355x-gemv.h"
+
+struct mi355x_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int num_cus = 0;
+    size_t max_lds_per_block = 0;
+    // device staging for raw weight bytes on their way into a resident tensor
+    void *staging = nullptr;
+    size_t staging_bytes = 0;
+    // per-context copies of the IQ grids (device), valid when non-null
+    void *iq3xxs_grid = nullptr;
+    void *iq2s_grid = nullptr;
+    uint64_t grids_version = 0;
+    std::mutex mu;  // serialises calls that share the staging buffer
+};
+
+namespace mi355x {
+
+// Thread-local error message plumbing.
+int set_error(int code, const std::string &msg);
+int hip_error(hipError_t e, const char *what);
+void clear_error();
+
+#define MI355X_HIP(call)                                \
+    do {                                                \
+        hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return ::mi355x::hip_error(e_, #call); \
+    } while (0)
+
+struct GemvArgs {
+    int type;
+    const uint8_t *W;
+    int64_t N;
+    int64_t K;
+    const void *x;  // float or bf16 bits
+    bool x_bf16;
+    float *y;
+};
+
+// Kernel launchers, one per weight family; return MI355X_* codes.
+int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
+int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a);
+
+// Prepack kernels: byte-range scatter/gather between ggml and resident order.
+int launch_prepack_scatter(mi355x_ctx *ctx, int type, int64_t N, int64_t K, uint8_t *packed,
+                           const uint8_t *raw, size_t offset, size_t size);
+int launch_prepack_gather(mi355x_ctx *ctx, int type, int64_t N, int64_t K, uint8_t *raw,
+                          const uint8_t *packed, size_t offset, size_t size);
+int launch_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes);
+
+// Resident workgroups per CU of `kernel` at this block size and LDS (cached).
+int occupancy(const void *kernel, int block_threads, size_t lds_bytes);
+
+// Refresh the context's device copies of the IQ grids from the global table.
+int sync_iq_grids(mi355x_ctx *ctx);
+
+}  // namespace mi355x

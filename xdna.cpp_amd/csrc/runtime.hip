@@ -1,0 +1,516 @@
+// C-ABI of the HIP layer: contexts, memory, prepack entry points, GEMV
+// dispatch with the reference's validation rules, and a timing helper.
+#include "internal.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <tuple>
+#include <vector>
+
+namespace mi355x {
+
+namespace {
+thread_local std::string g_last_error;
+
+// Process-wide IQ grid tables (host copies) installed by mi355x_set_iq_grid.
+std::mutex g_grid_mu;
+std::vector<uint8_t> g_iq3xxs_grid;  // 256 * 4 bytes
+std::vector<uint8_t> g_iq2s_grid;    // 1024 * 8 bytes
+std::atomic<uint64_t> g_grid_version{0};
+constexpr size_t kIq3xxsGridBytes = 256 * 4;
+constexpr size_t kIq2sGridBytes = 1024 * 8;
+
+constexpr size_t kStagingMax = size_t(64) << 20;
+
+int64_t block_values(int type) {
+    switch (type) {
+    case MI355X_TYPE_Q4_0: return 32;
+    case MI355X_TYPE_Q3_K: case MI355X_TYPE_Q4_K: case MI355X_TYPE_Q5_K: case MI355X_TYPE_Q6_K:
+    case MI355X_TYPE_IQ4_XS: case MI355X_TYPE_IQ3_S: case MI355X_TYPE_IQ3_XXS: case MI355X_TYPE_IQ2_S:
+        return 256;
+    default: return 0;
+    }
+}
+
+int64_t block_bytes(int type) {
+    switch (type) {
+    case MI355X_TYPE_Q4_0: return 18;
+    case MI355X_TYPE_Q3_K: return 110;
+    case MI355X_TYPE_Q4_K: return 144;
+    case MI355X_TYPE_Q5_K: return 176;
+    case MI355X_TYPE_Q6_K: return 210;
+    case MI355X_TYPE_IQ4_XS: return 136;
+    case MI355X_TYPE_IQ3_S: return 110;
+    case MI355X_TYPE_IQ3_XXS: return 98;
+    case MI355X_TYPE_IQ2_S: return 82;
+    default: return 0;
+    }
+}
+
+const char *type_name(int type) {
+    switch (type) {
+    case MI355X_TYPE_Q4_0: return "Q4_0";
+    case MI355X_TYPE_Q3_K: return "Q3_K";
+    case MI355X_TYPE_Q4_K: return "Q4_K";
+    case MI355X_TYPE_Q5_K: return "Q5_K";
+    case MI355X_TYPE_Q6_K: return "Q6_K";
+    case MI355X_TYPE_IQ4_XS: return "IQ4_XS";
+    case MI355X_TYPE_IQ3_S: return "IQ3_S";
+    case MI355X_TYPE_IQ3_XXS: return "IQ3_XXS";
+    case MI355X_TYPE_IQ2_S: return "IQ2_S";
+    default: return "unknown";
+    }
+}
+
+// Validates a (type, N, K) weight tensor; returns its total bytes in *total.
+int check_tensor(int type, int64_t N, int64_t K, uint64_t *total, const char *who) {
+    const int64_t bv = block_values(type);
+    if (bv == 0) return set_error(MI355X_EINVAL, std::string(who) + ": unsupported weight type id " + std::to_string(type));
+    if (N < 0 || K < 0)
+        return set_error(MI355X_EINVAL, std::string(who) + ": negative dimension N=" + std::to_string(N) +
+                                            " K=" + std::to_string(K));
+    if (K % bv != 0)
+        return set_error(MI355X_EINVAL, std::string(who) + ": K must be a multiple of " + std::to_string(bv) +
+                                            " for " + type_name(type) + " (got " + std::to_string(K) + ")");
+    const uint64_t rb = static_cast<uint64_t>(K / bv) * static_cast<uint64_t>(block_bytes(type));
+    if (N != 0 && rb > UINT64_MAX / static_cast<uint64_t>(N))
+        return set_error(MI355X_EINVAL, std::string(who) + ": integer overflow computing weight bytes (N=" +
+                                            std::to_string(N) + ", bytes_per_row=" + std::to_string(rb) + ")");
+    *total = rb * static_cast<uint64_t>(N);
+    return MI355X_OK;
+}
+
+int ensure_staging(mi355x_ctx *ctx, size_t want) {
+    want = std::min(want, kStagingMax);
+    if (ctx->staging_bytes >= want) return MI355X_OK;
+    if (ctx->staging) {
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        MI355X_HIP(hipFree(ctx->staging));
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+    }
+    hipError_t e = hipMalloc(&ctx->staging, want);
+    if (e != hipSuccess) {
+        ctx->staging = nullptr;
+        return set_error(MI355X_ENOMEM, std::string("staging allocation failed: ") + hipGetErrorString(e));
+    }
+    ctx->staging_bytes = want;
+    return MI355X_OK;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *x, bool xbf16,
+                float *y, const char *who) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
+    uint64_t total = 0;
+    int rc = check_tensor(type, N, K, &total, who);
+    if (rc) return rc;
+    if (N == 0) return MI355X_OK;
+    if (!W || !x || !y) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
+    if (!mi355x_type_ready(type))
+        return set_error(MI355X_EUNSUPPORTED, std::string(who) + ": " + type_name(type) +
+                                                  " needs its grid table (mi355x_set_iq_grid)");
+    DeviceGuard dg(ctx->device);
+    if (type == MI355X_TYPE_IQ3_XXS || type == MI355X_TYPE_IQ2_S) {
+        rc = sync_iq_grids(ctx);
+        if (rc) return rc;
+    }
+    GemvArgs a{type, static_cast<const uint8_t *>(W), N, K, x, xbf16, y};
+    if (type == MI355X_TYPE_Q4_0) return launch_gemv_q4_0(ctx, a);
+    return launch_gemv_kquant(ctx, a);
+}
+
+}  // namespace
+
+int set_error(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_error(hipError_t e, const char *what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+    return e == hipErrorOutOfMemory ? MI355X_ENOMEM : MI355X_EHIP;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int occupancy(const void *kernel, int block_threads, size_t lds_bytes) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, size_t>, int> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto key = std::make_tuple(kernel, block_threads, lds_bytes);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block_threads, lds_bytes) != hipSuccess ||
+        occ < 1)
+        occ = 1;
+    cache.emplace(key, occ);
+    return occ;
+}
+
+int sync_iq_grids(mi355x_ctx *ctx) {
+    const uint64_t v = g_grid_version.load();
+    if (ctx->grids_version == v) return MI355X_OK;
+    std::lock_guard<std::mutex> lk(g_grid_mu);
+    auto upload = [&](std::vector<uint8_t> &host, void **dev) -> int {
+        if (host.empty()) return MI355X_OK;
+        if (!*dev) MI355X_HIP(hipMalloc(dev, host.size()));
+        MI355X_HIP(hipMemcpyAsync(*dev, host.data(), host.size(), hipMemcpyHostToDevice, ctx->stream));
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        return MI355X_OK;
+    };
+    int rc = upload(g_iq3xxs_grid, &ctx->iq3xxs_grid);
+    if (!rc) rc = upload(g_iq2s_grid, &ctx->iq2s_grid);
+    if (!rc) ctx->grids_version = g_grid_version.load();
+    return rc;
+}
+
+}  // namespace mi355x
+
+using namespace mi355x;
+
+extern "C" {
+
+const char *mi355x_last_error(void) { return g_last_error.c_str(); }
+
+int mi355x_device_count(int *count) {
+    clear_error();
+    if (!count) return set_error(MI355X_EINVAL, "mi355x_device_count: null pointer");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) n = 0;
+    else if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+    *count = n;
+    return MI355X_OK;
+}
+
+int mi355x_ctx_create(int device, mi355x_ctx **out) {
+    clear_error();
+    if (!out) return set_error(MI355X_EINVAL, "mi355x_ctx_create: null output pointer");
+    *out = nullptr;
+    int n = 0;
+    int rc = mi355x_device_count(&n);
+    if (rc) return rc;
+    if (device < 0 || device >= n)
+        return set_error(MI355X_EINVAL, "mi355x_ctx_create: device " + std::to_string(device) + " of " +
+                                            std::to_string(n) + " HIP devices");
+    DeviceGuard dg(device);
+    auto *ctx = new (std::nothrow) mi355x_ctx();
+    if (!ctx) return set_error(MI355X_ENOMEM, "mi355x_ctx_create: out of host memory");
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_error(e, "hipGetDeviceProperties");
+    }
+    ctx->num_cus = prop.multiProcessorCount;
+    ctx->max_lds_per_block = prop.sharedMemPerBlock;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_error(e, "hipStreamCreateWithFlags");
+    }
+    *out = ctx;
+    return MI355X_OK;
+}
+
+void mi355x_ctx_destroy(mi355x_ctx *ctx) {
+    if (!ctx) return;
+    DeviceGuard dg(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->iq3xxs_grid) (void)hipFree(ctx->iq3xxs_grid);
+    if (ctx->iq2s_grid) (void)hipFree(ctx->iq2s_grid);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int mi355x_ctx_sync(mi355x_ctx *ctx) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_sync: null context");
+    MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    return MI355X_OK;
+}
+
+void *mi355x_ctx_stream(mi355x_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+
+int mi355x_ctx_device(mi355x_ctx *ctx) { return ctx ? ctx->device : -1; }
+
+int mi355x_mem_info(mi355x_ctx *ctx, size_t *free_bytes, size_t *total_bytes) {
+    clear_error();
+    if (!ctx || !free_bytes || !total_bytes) return set_error(MI355X_EINVAL, "mi355x_mem_info: null pointer");
+    DeviceGuard dg(ctx->device);
+    MI355X_HIP(hipMemGetInfo(free_bytes, total_bytes));
+    return MI355X_OK;
+}
+
+int mi355x_device_describe(int device, char *name, size_t name_len, char *pci, size_t pci_len) {
+    clear_error();
+    hipDeviceProp_t prop;
+    MI355X_HIP(hipGetDeviceProperties(&prop, device));
+    if (name && name_len) {
+        std::snprintf(name, name_len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    }
+    if (pci && pci_len) {
+        std::snprintf(pci, pci_len, "%04x:%02x:%02x.0", prop.pciDomainID, prop.pciBusID, prop.pciDeviceID);
+    }
+    return MI355X_OK;
+}
+
+int mi355x_malloc(mi355x_ctx *ctx, size_t bytes, void **dptr) {
+    clear_error();
+    if (!ctx || !dptr) return set_error(MI355X_EINVAL, "mi355x_malloc: null pointer");
+    DeviceGuard dg(ctx->device);
+    *dptr = nullptr;
+    hipError_t e = hipMalloc(dptr, bytes == 0 ? 256 : bytes);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        return set_error(MI355X_ENOMEM, "hipMalloc(" + std::to_string(bytes) + "): " + hipGetErrorString(e));
+    }
+    return MI355X_OK;
+}
+
+int mi355x_free(mi355x_ctx *ctx, void *dptr) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_free: null context");
+    if (!dptr) return MI355X_OK;
+    DeviceGuard dg(ctx->device);
+    MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    MI355X_HIP(hipFree(dptr));
+    return MI355X_OK;
+}
+
+static int copy_sync(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind,
+                     const char *who) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
+    if (bytes == 0) return MI355X_OK;
+    if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
+    DeviceGuard dg(ctx->device);
+    MI355X_HIP(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    return MI355X_OK;
+}
+
+int mi355x_memcpy_h2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyHostToDevice, "mi355x_memcpy_h2d");
+}
+int mi355x_memcpy_d2h(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyDeviceToHost, "mi355x_memcpy_d2h");
+}
+int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, "mi355x_memcpy_d2d");
+}
+
+int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_fill: null context");
+    if (bytes && !dst) return set_error(MI355X_EINVAL, "mi355x_fill: null pointer");
+    DeviceGuard dg(ctx->device);
+    return launch_fill(ctx, dst, value, bytes);
+}
+
+int64_t mi355x_row_bytes(int type, int64_t K) {
+    const int64_t bv = block_values(type);
+    if (bv == 0 || K < 0 || K % bv != 0) return -1;
+    return (K / bv) * block_bytes(type);
+}
+
+int mi355x_type_ready(int type) {
+    switch (type) {
+    case MI355X_TYPE_Q4_0: case MI355X_TYPE_Q3_K: case MI355X_TYPE_Q4_K: case MI355X_TYPE_Q5_K:
+    case MI355X_TYPE_Q6_K: case MI355X_TYPE_IQ4_XS: case MI355X_TYPE_IQ3_S:
+        return 1;
+    case MI355X_TYPE_IQ3_XXS: {
+        std::lock_guard<std::mutex> lk(g_grid_mu);
+        return g_iq3xxs_grid.empty() ? 0 : 1;
+    }
+    case MI355X_TYPE_IQ2_S: {
+        std::lock_guard<std::mutex> lk(g_grid_mu);
+        return g_iq2s_grid.empty() ? 0 : 1;
+    }
+    default: return 0;
+    }
+}
+
+int mi355x_set_iq_grid(int type, const void *table, size_t bytes) {
+    clear_error();
+    if (!table) return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: null table");
+    std::lock_guard<std::mutex> lk(g_grid_mu);
+    const uint8_t *p = static_cast<const uint8_t *>(table);
+    if (type == MI355X_TYPE_IQ3_XXS) {
+        if (bytes != kIq3xxsGridBytes)
+            return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: IQ3_XXS grid is 1024 bytes");
+        g_iq3xxs_grid.assign(p, p + bytes);
+    } else if (type == MI355X_TYPE_IQ2_S) {
+        if (bytes != kIq2sGridBytes)
+            return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: IQ2_S grid is 8192 bytes");
+        g_iq2s_grid.assign(p, p + bytes);
+    } else {
+        return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: only IQ3_XXS and IQ2_S take a grid");
+    }
+    g_grid_version.fetch_add(1);
+    return MI355X_OK;
+}
+
+static int check_range(int type, int64_t N, int64_t K, size_t offset, size_t size, const char *who) {
+    uint64_t total = 0;
+    int rc = check_tensor(type, N, K, &total, who);
+    if (rc) return rc;
+    if (offset > total || size > total - offset)
+        return set_error(MI355X_EINVAL, std::string(who) + ": byte range [" + std::to_string(offset) + ", +" +
+                                            std::to_string(size) + ") exceeds tensor of " + std::to_string(total) +
+                                            " bytes");
+    return MI355X_OK;
+}
+
+int mi355x_prepack_from_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, void *packed_dev,
+                             const void *raw_host, size_t offset, size_t size) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_prepack_from_host: null context");
+    int rc = check_range(type, N, K, offset, size, "mi355x_prepack_from_host");
+    if (rc || size == 0) return rc;
+    if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_prepack_from_host: null pointer");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DeviceGuard dg(ctx->device);
+    if (type != MI355X_TYPE_Q4_0) {  // resident order == ggml order
+        MI355X_HIP(hipMemcpyAsync(static_cast<uint8_t *>(packed_dev) + offset, raw_host, size,
+                                  hipMemcpyHostToDevice, ctx->stream));
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        return MI355X_OK;
+    }
+    rc = ensure_staging(ctx, size);
+    if (rc) return rc;
+    const uint8_t *src = static_cast<const uint8_t *>(raw_host);
+    for (size_t done = 0; done < size;) {
+        const size_t n = std::min(size - done, ctx->staging_bytes);
+        MI355X_HIP(hipMemcpyAsync(ctx->staging, src + done, n, hipMemcpyHostToDevice, ctx->stream));
+        rc = launch_prepack_scatter(ctx, type, N, K, static_cast<uint8_t *>(packed_dev),
+                                    static_cast<const uint8_t *>(ctx->staging), offset + done, n);
+        if (rc) return rc;
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        done += n;
+    }
+    return MI355X_OK;
+}
+
+int mi355x_prepack_from_device(mi355x_ctx *ctx, int type, int64_t N, int64_t K, void *packed_dev,
+                               const void *raw_dev, size_t offset, size_t size) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_prepack_from_device: null context");
+    int rc = check_range(type, N, K, offset, size, "mi355x_prepack_from_device");
+    if (rc || size == 0) return rc;
+    if (!packed_dev || !raw_dev) return set_error(MI355X_EINVAL, "mi355x_prepack_from_device: null pointer");
+    DeviceGuard dg(ctx->device);
+    rc = launch_prepack_scatter(ctx, type, N, K, static_cast<uint8_t *>(packed_dev),
+                                static_cast<const uint8_t *>(raw_dev), offset, size);
+    if (rc) return rc;
+    MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    return MI355X_OK;
+}
+
+int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, const void *packed_dev,
+                          void *raw_host, size_t offset, size_t size) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_unpack_to_host: null context");
+    int rc = check_range(type, N, K, offset, size, "mi355x_unpack_to_host");
+    if (rc || size == 0) return rc;
+    if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_unpack_to_host: null pointer");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DeviceGuard dg(ctx->device);
+    if (type != MI355X_TYPE_Q4_0) {
+        MI355X_HIP(hipMemcpyAsync(raw_host, static_cast<const uint8_t *>(packed_dev) + offset, size,
+                                  hipMemcpyDeviceToHost, ctx->stream));
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        return MI355X_OK;
+    }
+    rc = ensure_staging(ctx, size);
+    if (rc) return rc;
+    uint8_t *dst = static_cast<uint8_t *>(raw_host);
+    for (size_t done = 0; done < size;) {
+        const size_t n = std::min(size - done, ctx->staging_bytes);
+        rc = launch_prepack_gather(ctx, type, N, K, static_cast<uint8_t *>(ctx->staging),
+                                   static_cast<const uint8_t *>(packed_dev), offset + done, n);
+        if (rc) return rc;
+        MI355X_HIP(hipMemcpyAsync(dst + done, ctx->staging, n, hipMemcpyDeviceToHost, ctx->stream));
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        done += n;
+    }
+    return MI355X_OK;
+}
+
+int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x, float *y) {
+    return gemv_common(ctx, type, W, N, K, x, false, y, "mi355x_gemv");
+}
+
+int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const uint16_t *x_bf16,
+                     float *y) {
+    return gemv_common(ctx, type, W, N, K, x_bf16, true, y, "mi355x_gemv_bf16");
+}
+
+int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x,
+                        int64_t x_stride, float *y, int64_t y_stride, int64_t M) {
+    clear_error();
+    if (M < 0) return set_error(MI355X_EINVAL, "mi355x_gemv_batched: negative M");
+    if (M > 1 && (x_stride < K || y_stride < N))
+        return set_error(MI355X_EINVAL, "mi355x_gemv_batched: strides smaller than a row");
+    for (int64_t m = 0; m < M; ++m) {
+        int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, "mi355x_gemv_batched");
+        if (rc) return rc;
+    }
+    return MI355X_OK;
+}
+
+int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int n_weights, int64_t N, int64_t K,
+                     const float *x, float *y, int warmup, int iters, double *ms_total) {
+    clear_error();
+    if (!ctx || !weights || n_weights < 1 || iters < 1 || warmup < 0 || !ms_total)
+        return set_error(MI355X_EINVAL, "mi355x_time_gemv: bad arguments");
+    DeviceGuard dg(ctx->device);
+    for (int i = 0; i < warmup; ++i) {
+        int rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, y);
+        if (rc) return rc;
+    }
+    hipEvent_t e0, e1;
+    MI355X_HIP(hipEventCreate(&e0));
+    hipError_t e = hipEventCreate(&e1);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return hip_error(e, "hipEventCreate");
+    }
+    int rc = MI355X_OK;
+    if (hipEventRecord(e0, ctx->stream) != hipSuccess) rc = set_error(MI355X_EHIP, "hipEventRecord");
+    for (int i = 0; i < iters && rc == MI355X_OK; ++i) rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, y);
+    if (rc == MI355X_OK && hipEventRecord(e1, ctx->stream) != hipSuccess) rc = set_error(MI355X_EHIP, "hipEventRecord");
+    if (rc == MI355X_OK) {
+        e = hipEventSynchronize(e1);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e != hipSuccess) rc = hip_error(e, "hipEventElapsedTime");
+        else *ms_total = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
+}  // extern "C"
