@@ -1,0 +1,191 @@
+"""Decode-GEMV benchmark on one MI355X.
+
+One step = one Q4_0 GEMV at N x K = 8192 x 8192 (the
+north-star shape) over one f32 activation row, with the weights already
+resident in HBM.  Launches rotate through enough resident weight copies
+(>= 1 GiB) that the 256 MB Infinity Cache cannot serve them, so the figure is
+HBM bandwidth.  Timing: HIP events around `--steps` back-to-back launches on
+the library's own stream (mi355x_time_gemv), after `--warmup` launches.
+
+Prints one JSON line (see README of the driver contract):
+  value      = algorithmic GB/s of the whole job (one GPU)
+  roofline   = the GEMV kernel against the 8 TB/s HBM3E peak
+  cpu_baseline = the reference's own AVX2/OpenMP Q4GemvEngine
+                 (oracle/_ref, 4 threads) on a bounded sample of the same
+                 workload, timed on this host
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "xdna.cpp_amd"))
+
+import mi355x  # noqa: E402
+import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_0 GEMV HBM GB/s (% of roofline) at 8192x8192; decode tok/s, 3B shape"
+ROTATE_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_0_gemv_8192x8192_traffic.json")
+
+
+def algorithmic_bytes(t: int, N: int, K: int) -> int:
+    return N * mi355x.row_bytes(t, K) + 4 * K + 4 * N
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes):
+    """Returns (ms_per_launch, copies, y) for `steps` launches over resident copies."""
+    wbytes = N * mi355x.row_bytes(t, K)
+    copies = max(1, -(-rotate_bytes // wbytes)) if rotate_bytes else 1
+    first = ctx.resident(t, raw, N, K)
+    bufs = [first.buf]
+    for _ in range(copies - 1):
+        b = ctx.alloc(wbytes)
+        mi355x.check(ctx.lib.mi355x_memcpy_d2d(ctx.h, b.ptr, first.ptr, wbytes))
+        bufs.append(b)
+    xb = ctx.to_device(x)
+    yb = ctx.alloc(4 * N)
+    try:
+        ms = ctx.time_gemv(t, [b.ptr for b in bufs], N, K, xb.ptr, yb.ptr, warmup, steps)
+        y = yb.download(np.float32, N)
+    finally:
+        for b in bufs:
+            b.free()
+        xb.free()
+        yb.free()
+    return ms / steps, copies, y
+
+
+def cpu_baseline(raw, N, K, x, budget_s: float):
+    """Time the reference's Q4GemvEngine (oracle/_ref) -- or the C oracle when
+    the reference build is absent -- on the same bytes for ~budget_s seconds."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    raw = np.ascontiguousarray(raw.reshape(-1))
+    y = np.empty(N, dtype=np.float32)
+    if orc.RefLib.available():
+        eng = orc.RefCpuEngine(orc.RefLib())
+        run = lambda: eng.run(raw, N, K, x, y)  # noqa: E731
+        kind, cores, what = "reference", orc.RefCpuEngine.THREADS, "xdna::Q4GemvEngine::run (AVX2+OpenMP)"
+    else:
+        o = orc.Oracle()
+        run = lambda: o.gemv(2, raw, N, K, x)  # noqa: E731
+        kind, cores, what = "port", 1, "scalar C oracle (port of gemv_f32)"
+    run()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
+    sec = dt / n
+    return {"value": round(algorithmic_bytes(mi355x.Q4_0, N, K) / sec / 1e9, 3), "unit": "GB/s",
+            "cores": cores, "kind": kind,
+            "sample": f"{n} GEMVs of Q4_0 {N}x{K} (same bytes and x) in {dt:.1f} s, {what}, "
+                      f"{sec * 1e3:.3f} ms/GEMV; host has {os.cpu_count()} logical CPUs"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--N", type=int, default=8192)
+    ap.add_argument("--K", type=int, default=8192)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding plan is described in DESIGN.md", file=sys.stderr)
+        return 2
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: run without torch.distributed; one GPU only", file=sys.stderr)
+        return 2
+
+    N, K, t = args.N, args.K, mi355x.Q4_0
+    log(f"bench: generating Q4_0 {N}x{K} (N(0,0.02) -> Q4_0) and x ~ N(0,1)")
+    raw = synth.quantize_q4_0(synth.normal_weights(N, K, seed=42))
+    x = synth.activations(K, seed=43)
+    alg = algorithmic_bytes(t, N, K)
+
+    with mi355x.Context(0) as ctx:
+        name, pci = ctx.describe()
+        log(f"bench: device {name} at {pci}; timing {args.steps} launches after {args.warmup} warmup")
+        ms, copies, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES)
+        log(f"bench: {ms * 1e3:.2f} us/launch over {copies} resident copies")
+        ms_hot, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, 0)
+        log(f"bench: cache-hot (one copy) {ms_hot * 1e3:.2f} us/launch")
+        sweep = {}
+        if args.sweep:
+            for (n2, k2) in ((4096, 4096), (17408, 5120), (151936, 2048)):
+                raw2 = synth.quantize_q4_0(synth.normal_weights(n2, k2, seed=42))
+                x2 = synth.activations(k2, seed=43)
+                ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES)
+                gbs2 = algorithmic_bytes(t, n2, k2) / (ms2 * 1e-3) / 1e9
+                sweep[f"{n2}x{k2}"] = {"us": round(ms2 * 1e3, 3), "GB/s": round(gbs2, 1),
+                                       "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2}
+                log(f"bench: Q4_0 {n2}x{k2}: {ms2 * 1e3:.2f} us, {gbs2:.1f} GB/s")
+
+    # the timed output must still be the right answer (checked, not measured)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle
+    ref = Oracle().gemv(2, raw, N, K, x)
+    cos = float(np.dot(y.astype(np.float64), ref) / (np.linalg.norm(y) * np.linalg.norm(ref)))
+
+    gbs = alg / (ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: f32 N(0,0.02) weights (seed 42) quantized to Q4_0, x ~ N(0,1) (seed 43)",
+        "config": {"workload": f"Q4_0 GEMV {N}x{K} (N rows x K), 1 f32 activation row, "
+                               f"weights rotated over {copies} resident copies "
+                               f"({copies * (alg - 4 * K - 4 * N) / 2**30:.2f} GiB) so HBM, not cache, serves them",
+                   "N": N, "K": K, "weight_type": "Q4_0", "rotate_copies": copies,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cache_hot": {"us_per_launch": round(ms_hot * 1e3, 3),
+                      "GB/s": round(alg / (ms_hot * 1e-3) / 1e9, 2),
+                      "note": "single resident copy, served partly from MALL/L2; not the HBM figure"},
+        "parity": {"cosine_vs_oracle": cos},
+    }
+    if sweep:
+        out["sweep"] = sweep
+    if not args.no_cpu:
+        log(f"bench: CPU baseline for ~{args.cpu_seconds:.0f} s")
+        out["cpu_baseline"] = cpu_baseline(raw, N, K, x, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -77,6 +77,25 @@ MI355X_API int mi355x_mem_info(mi355x_ctx *ctx, size_t *free_bytes, size_t *tota
 MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, char *pci,
                                       size_t pci_len);
 
+/* Per-context options.
+ *   MI355X_OPT_VARIANT: which kernel family computes Q4_0 GEMVs --
+ *     MI355X_VARIANT_AUTO (default: digit planes where they apply),
+ *     MI355X_VARIANT_EXACT_F32 (nibbles -> f32, fp32 FMA; activations used
+ *       exactly as given), MI355X_VARIANT_DIGITS (activations as 20-bit
+ *       fixed point per 32-value block, integer dot8 products).
+ *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step.
+ *   MI355X_OPT_WAVES_PER_GROUP: 0 (auto), 8 or 16 wavefronts per workgroup
+ *     (digit-plane Q4_0 kernel).
+ *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups. */
+#define MI355X_OPT_VARIANT 1
+#define MI355X_OPT_ROWS_PER_WAVE 2
+#define MI355X_OPT_WAVES_PER_GROUP 3
+#define MI355X_OPT_GRID 4
+#define MI355X_VARIANT_AUTO 0
+#define MI355X_VARIANT_EXACT_F32 1
+#define MI355X_VARIANT_DIGITS 2
+MI355X_API int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value);
+
 /* ---- memory ----------------------------------------------------------------
  * Copies and fills are ordered on the context's stream; the *_sync forms
  * return after completion. */

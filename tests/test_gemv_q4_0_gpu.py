@@ -17,6 +17,15 @@ pytestmark = pytest.mark.gpu
 Q4_0 = mi355x.Q4_0
 
 
+@pytest.fixture(params=["digits", "exact_f32"], autouse=True)
+def variant(request, ctx):
+    """Every test runs on both Q4_0 kernel families."""
+    v = mi355x.VARIANT_AUTO if request.param == "digits" else mi355x.VARIANT_EXACT_F32
+    ctx.set_option(mi355x.OPT_VARIANT, v)
+    yield request.param
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+
+
 def run_gpu(ctx, raw, N, K, x, chunk=None):
     w = ctx.resident(Q4_0, raw, N, K, chunk=chunk)
     try:
@@ -144,6 +153,36 @@ def test_chunked_upload_gives_same_gemv(ctx, oracle):
     a = run_gpu(ctx, raw, N, K, x)
     b = run_gpu(ctx, raw, N, K, x, chunk=12345)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("waves,rows", [(8, 1), (8, 2), (8, 4), (16, 1), (16, 2), (16, 4)])
+@pytest.mark.parametrize("N,K", [(1000, 2048), (777, 8192), (300, 14336)])
+def test_tuning_options_keep_results(ctx, oracle, variant, waves, rows, N, K):
+    # every launch shape the tuning options can select computes the same GEMV
+    raw = synth.random_q4_0(N, K, seed=N * 7 + K)
+    x = synth.activations(K, seed=99)
+    ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, waves)
+    ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, rows)
+    try:
+        parity(ctx, oracle, raw, N, K, x, f"{variant} waves={waves} rows={rows} {N}x{K}")
+        ctx.set_option(mi355x.OPT_GRID, 7)
+        parity(ctx, oracle, raw, N, K, x, f"{variant} grid=7 {N}x{K}")
+    finally:
+        ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, 0)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+        ctx.set_option(mi355x.OPT_GRID, 0)
+
+
+def test_activation_extremes(ctx, oracle):
+    # large dynamic range inside a block, exact zeros, and a block that is all zero
+    N, K = 128, 1024
+    raw = synth.random_q4_0(N, K, seed=21)
+    x = synth.activations(K, seed=22)
+    x[0:32] = 0.0
+    x[32:64] *= np.float32(1e-6)
+    x[64] = np.float32(3e4)
+    x[100:132] = np.float32(-7.5)
+    parity(ctx, oracle, raw, N, K, x, "activation extremes")
 
 
 def test_rejects_bad_shapes(ctx):

@@ -55,6 +55,11 @@ __device__ __forceinline__ void nibbles_to_float(uint32_t bytes, float out[4]) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Word 3 of a raw (untyped, stride 0) buffer descriptor on gfx9-family GPUs.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of buffer loads: non-temporal (read-once data).
+constexpr int kNonTemporal = 2;
+
 // 16-byte load of streamed (read-once) weight bytes; 16-byte aligned.
 __device__ __forceinline__ u32x4 load_stream16(const uint8_t *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));

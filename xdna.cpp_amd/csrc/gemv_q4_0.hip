@@ -4,6 +4,7 @@
 //
 // Resident row layout (made by the prepack stage, same bytes as ggml):
 //   [qs of block 0 .. qs of block B-1 : 16*B bytes][fp16 d of every block : 2*B]
+//   (code bytes XOR 0x88, d plane lane-major: see q4_0_layout.h)
 // Work split:
 //   * a workgroup of WAVES wavefronts stages the f32 activation row in LDS,
 //     transposed so that lane b reads float4 k of block b at xs[k*KC + b]
@@ -19,6 +20,7 @@
 // once per workgroup when the whole row fits in one LDS chunk.
 #include "device_common.h"
 #include "internal.h"
+#include "q4_0_layout.h"
 
 #include <algorithm>
 #include <mutex>
@@ -60,12 +62,13 @@ __device__ __forceinline__ void stage_x_chunk(const void *__restrict__ xv, int c
     }
 }
 
-// (1/512) * sum_j q_j x_j over one block, x from registers.
+// (1/512) * sum_j q_j x_j over one block, x from registers.  The resident
+// code bytes hold q XOR 8 per nibble; the XOR is undone here.
 __device__ __forceinline__ float q4_block_dot(u32x4 q, const float4 xv[8]) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t w = q[k];
+        const uint32_t w = q[k] ^ 0x88888888u;
         float lo[4], hi[4];
         nibbles_to_float(w & 0x0F0F0F0Fu, lo);
         nibbles_to_float((w >> 4) & 0x0F0F0F0Fu, hi);
@@ -117,38 +120,33 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_q4_0_kernel(
             for (int s0 = 0; s0 < cn; s0 += 64 * NBL) {
                 u32x4 q[R][NBL];
                 float d[R][NBL];
+                // unconditional loads from clamped addresses keep every
+                // request in flight; blocks past the chunk get scale 0
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const int row = row0 + r;
-                    const uint8_t *rp = W + static_cast<int64_t>(min(row, N - 1)) * row_bytes;
+                    const uint8_t *rp = W + static_cast<int64_t>(min(row0 + r, N - 1)) * row_bytes;
 #pragma unroll
                     for (int j = 0; j < NBL; ++j) {
                         const int b = s0 + lane + 64 * j;
-                        if (b < cn && row < N) {
-                            const int64_t blk = c0 + b;
-                            const uint8_t *qp = rp + 16 * blk;
-                            q[r][j] = A16 ? load_stream16(qp) : load_16_a2(qp);
-                            const uint16_t dh = *reinterpret_cast<const uint16_t *>(rp + scale_off + 2 * blk);
-                            d[r][j] = half_bits_to_float(dh) * kNibbleFp8Scale;
-                        } else {
-                            q[r][j] = u32x4{0u, 0u, 0u, 0u};
-                            d[r][j] = 0.0f;
-                        }
+                        const int64_t blk = c0 + min(b, cn - 1);
+                        const uint8_t *qp = rp + 16 * blk;
+                        q[r][j] = A16 ? load_stream16(qp) : load_16_a2(qp);
+                        const uint16_t dh = *reinterpret_cast<const uint16_t *>(
+                            rp + scale_off + 2 * static_cast<int64_t>(q4_0_d_slot(blk, B)));
+                        d[r][j] = b < cn ? half_bits_to_float(dh) * kNibbleFp8Scale : 0.0f;
                     }
                 }
 #pragma unroll
                 for (int j = 0; j < NBL; ++j) {
-                    const int b = s0 + lane + 64 * j;
-                    if (b < cn) {
-                        float4 xv[8];
+                    const int bc = min(s0 + lane + 64 * j, cn - 1);
+                    float4 xv[8];
 #pragma unroll
-                        for (int k = 0; k < 8; ++k) xv[k] = xs[k * KC + b];
-                        const float sb = bias[b];
+                    for (int k = 0; k < 8; ++k) xv[k] = xs[k * KC + bc];
+                    const float sb = bias[bc];
 #pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const float t = q4_block_dot(q[r][j], xv) - sb;
-                            acc[r] = fmaf(d[r][j], t, acc[r]);
-                        }
+                    for (int r = 0; r < R; ++r) {
+                        const float t = q4_block_dot(q[r][j], xv) - sb;
+                        acc[r] = fmaf(d[r][j], t, acc[r]);
                     }
                 }
             }
@@ -197,6 +195,10 @@ int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a) {
         return set_error(MI355X_EUNSUPPORTED, "Q4_0 GEMV: N or K beyond 32-bit kernel indexing");
     if (reinterpret_cast<uintptr_t>(a.W) % 2 != 0)
         return set_error(MI355X_EINVAL, "Q4_0 GEMV: weight pointer must be 2-byte aligned");
+    if (ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && q4_0_dp_supports(ctx, a))
+        return launch_gemv_q4_0_dp(ctx, a);
+    if (ctx->kernel_variant == MI355X_VARIANT_DIGITS)
+        return set_error(MI355X_EUNSUPPORTED, "Q4_0 GEMV: digit-plane kernel does not take this shape/activation type");
     const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
     const bool x_al16 = !a.x_bf16 && (reinterpret_cast<uintptr_t>(a.x) % 16 == 0);
 
@@ -206,7 +208,8 @@ int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a) {
     kc_cap = std::max<int64_t>(64, (kc_cap / 64) * 64);
     const int KC = static_cast<int>(std::min<int64_t>(B, kc_cap));
     const int nbl = B <= 64 ? 1 : (B <= 128 ? 2 : 4);
-    const int R = nbl == 4 ? 2 : 4;
+    int R = nbl == 4 ? 2 : 4;
+    if (ctx->rows_override) R = ctx->rows_override;
     const size_t lds = per_block * static_cast<size_t>(KC);
 
     q4_kernel_t k = pick(nbl, R, a16, a.x_bf16);

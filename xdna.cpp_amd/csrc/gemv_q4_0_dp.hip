@@ -1,0 +1,399 @@
+// Q4_0 decode GEMV, "digit-plane" form, for gfx950.
+//
+// Same resident row layout as gemv_q4_0.hip ([qs planes][fp16 d plane]).
+// The activation row is re-expressed once per workgroup, per 32-value block
+// b, as a fixed-point integer vector: Z_j = rint(x_j / u_b) with u_b the
+// power of two that puts max_j |x_j| / u_b in (244667, 489335], so
+// |Z_j| <= 489335 < 2^19 and the scaling itself is exact.  Each Z_j is split into
+// five signed base-16 digits z_p in [-8, 7] (balanced: Z + 0x88888 has
+// nibbles z_p + 8), stored as five 32-nibble "digit planes" in the nibble
+// order of the Q4_0 bytes.  The block dot product is then exact integer
+// arithmetic on the dot8 unit (v_dot8c_i32_i4, 8 signed 4-bit products per
+// instruction):
+//   A_p = sum_j (q_j - 8) * z_p(j)           (4 dot8 per plane)
+//   T   = sum_p 16^p A_p = sum_j (q_j - 8) Z_j,  |T| < 1.5e8
+//   y_r += d_rb * u_b * float(T)
+// Compared with converting nibbles to f32 (2 VALU ops per weight) this costs
+// about 1.1 VALU ops per weight.  The only approximation beyond f32 rounding
+// is the activation quantization: |x_j - Z_j u_b| <= u_b/2 <= 2^-18.9 max|x_b|.
+//
+// Work split: workgroups of 16 wavefronts; each wavefront owns R rows per
+// step and walks its row groups grid-stride, prefetching the next group's
+// weight bytes before it computes the current one; the first group's loads
+// are issued before the activation row is staged, so HBM traffic starts at
+// once.  Lane l owns blocks l, l+64, ... of a row (contiguous 1 KiB per
+// 16-byte load instruction); row partials are folded with DPP.
+#include "device_common.h"
+#include "internal.h"
+#include "q4_0_layout.h"
+
+#include <algorithm>
+
+namespace mi355x {
+namespace {
+
+constexpr int kPlanes = 5;
+constexpr float kZmax = 489335.0f;  // 0x77777: largest balanced 5-digit value
+constexpr uint32_t kBalance = 0x88888u;
+// 1.5 * 2^23 + 0x88888: adding it to a value of magnitude < 2^21 rounds the
+// value to an integer and leaves integer + 0x88888 in the low mantissa bits
+constexpr float kMagic = 13142152.0f;
+
+// Digit planes of the activation row: planes[p * B + b] holds, as four
+// dwords k = 0..3, the digit p of values 4k+e (nibble 2e) and 16+4k+e
+// (nibble 2e+1), e = 0..3 -- the nibble positions of Q4_0 byte 4k+e.
+//
+// Staging is split in two so that the activation loads can be issued before
+// the weight loads: the vector-memory counter retires loads in order, so
+// data loaded *after* the weights could only be used once every weight
+// byte had arrived.  Thread t handles value group i = t + it*blockDim.x
+// (block b = i/4, dword k = i%4), XI groups per thread.
+template <int XI>
+struct XTile {
+    float v[XI][8];
+
+    __device__ __forceinline__ void load(const float *__restrict__ x, int B, bool x_al16) {
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int i = min(static_cast<int>(threadIdx.x + it * blockDim.x), 4 * B - 1);
+            const float *xb = x + 32 * static_cast<int64_t>(i >> 2) + 4 * (i & 3);
+            if (x_al16) {
+                const float4 lo = *reinterpret_cast<const float4 *>(xb);
+                const float4 hi = *reinterpret_cast<const float4 *>(xb + 16);
+                v[it][0] = lo.x; v[it][1] = hi.x; v[it][2] = lo.y; v[it][3] = hi.y;
+                v[it][4] = lo.z; v[it][5] = hi.z; v[it][6] = lo.w; v[it][7] = hi.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[it][2 * e] = xb[e];
+                    v[it][2 * e + 1] = xb[16 + e];
+                }
+            }
+        }
+    }
+
+    // The math runs for every thread (groups past the row repeat the last
+    // group); only the LDS stores are predicated.  A branch around the math
+    // would let the compiler sink the activation loads behind the weights.
+    __device__ __forceinline__ void store(int B, uint32_t *planes, float *ub) const {
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int i = threadIdx.x + it * blockDim.x;
+            const int ic = min(i, 4 * B - 1);
+            stage_group(v[it], ic >> 2, ic & 3, B, i < 4 * B, planes, ub);
+        }
+    }
+
+    // one group of 8 values -> five plane dwords (+ the block scale)
+    __device__ __forceinline__ static void stage_group(const float *v, int b, int k, int B, bool write,
+                                                       uint32_t *planes, float *ub) {
+        float m = 0.0f;
+        float poison = 0.0f;  // NaN iff some value of the block is inf or NaN
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m = fmaxf(m, fabsf(v[e]));
+            poison += v[e] * 0.0f;
+        }
+        // the four threads of block b are one DPP quad (i = 4b + k)
+        m = fmaxf(m, dpp_mov<0xB1>(m));
+        m = fmaxf(m, dpp_mov<0x4E>(m));
+        poison += dpp_mov<0xB1>(poison);
+        poison += dpp_mov<0x4E>(poison);
+        // power-of-two block scale 2^e0 with max|x|/2^e0 in (kZmax/2, kZmax]:
+        // scaling is exact, so activations with <= 19 significant bits are
+        // represented exactly
+        int ex;
+        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
+        int e0 = ex - 19;
+        if (ldexpf(m, -e0) > kZmax) e0 += 1;
+        const bool live = m > 0.0f && poison == 0.0f;
+        // One FMA per value gives rint(v * 2^-e0) + 0x88888 in the low 20 bits
+        // of a float in [2^23, 2^24) (ulp 1, round-to-nearest-even); XOR 0x88888
+        // turns its five nibbles into the balanced signed digits.  |v| <= m
+        // and m * 2^-e0 <= kZmax keep the value inside the 20-bit field.
+        const float s = live ? ldexpf(1.0f, -e0) : 0.0f;
+        uint32_t L[4], H[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            L[e] = __builtin_bit_cast(uint32_t, fmaf(v[2 * e], s, kMagic)) ^ kBalance;
+            H[e] = __builtin_bit_cast(uint32_t, fmaf(v[2 * e + 1], s, kMagic)) ^ kBalance;
+        }
+        // Nibble transpose: byte e of plane p = digit p of L[e] (low nibble)
+        // and of H[e] (high nibble).  M[e] holds planes 0/2/4 in bytes 0/1/2,
+        // N[e] planes 1/3 in bytes 0/1; byte permutes gather them.
+        uint32_t M[4], Nn[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            M[e] = (L[e] & 0x0F0F0F0Fu) | ((H[e] << 4) & 0xF0F0F0F0u);
+            Nn[e] = ((L[e] >> 4) & 0x0F0F0F0Fu) | (H[e] & 0xF0F0F0F0u);
+        }
+        const uint32_t m01 = __builtin_amdgcn_perm(M[1], M[0], 0x05010400u);
+        const uint32_t m23 = __builtin_amdgcn_perm(M[3], M[2], 0x05010400u);
+        const uint32_t c01 = __builtin_amdgcn_perm(M[1], M[0], 0x0C0C0602u);
+        const uint32_t c23 = __builtin_amdgcn_perm(M[3], M[2], 0x0C0C0602u);
+        const uint32_t n01 = __builtin_amdgcn_perm(Nn[1], Nn[0], 0x05010400u);
+        const uint32_t n23 = __builtin_amdgcn_perm(Nn[3], Nn[2], 0x05010400u);
+        uint32_t w[kPlanes];
+        w[0] = __builtin_amdgcn_perm(m23, m01, 0x05040100u);
+        w[2] = __builtin_amdgcn_perm(m23, m01, 0x07060302u);
+        w[4] = __builtin_amdgcn_perm(c23, c01, 0x05040100u);
+        w[1] = __builtin_amdgcn_perm(n23, n01, 0x05040100u);
+        w[3] = __builtin_amdgcn_perm(n23, n01, 0x07060302u);
+        // non-finite activations poison the block the way f32 arithmetic would
+        const float scale = live ? ldexpf(1.0f, e0) : poison;
+        if (write) {
+#pragma unroll
+            for (int p = 0; p < kPlanes; ++p) planes[(p * B + b) * 4 + k] = w[p];
+            if (k == 0) ub[b] = scale;
+        }
+    }
+};
+
+// sum_j (q_j - 8) * Z_j for one block.  The resident bytes already hold the
+// signed nibbles q - 8 (prepack XORs every nibble with 8).  Horner over the
+// planes runs inside the dot8 accumulator: T <- dot8 chain seeded with 16*T.
+__device__ __forceinline__ int block_dot_digits(u32x4 qs, const uint4 P[kPlanes]) {
+    int T = 0;
+#pragma unroll
+    for (int p = kPlanes - 1; p >= 0; --p) {
+        int a = __builtin_amdgcn_sdot8(static_cast<int>(qs[0]), static_cast<int>(P[p].x), T * 16, false);
+        a = __builtin_amdgcn_sdot8(static_cast<int>(qs[1]), static_cast<int>(P[p].y), a, false);
+        a = __builtin_amdgcn_sdot8(static_cast<int>(qs[2]), static_cast<int>(P[p].z), a, false);
+        T = __builtin_amdgcn_sdot8(static_cast<int>(qs[3]), static_cast<int>(P[p].w), a, false);
+    }
+    return T;
+}
+
+// Weight bytes of R rows x NBL blocks per lane, read through a buffer
+// descriptor based at the wave's first row: every load is unconditional with
+// a 32-bit offset, reads past the tensor end return 0 (buffer range check),
+// and blocks past the row end are neutralised by a zero scale, so
+// the compiler keeps all requests in flight.
+//
+// Scales: the F = NBL - TAIL full 64-block columns have lane-major scale
+// slots (q4_0_layout.h), so for F in {1, 2, 4, 8} one 2F-byte load fetches a
+// lane's scales; other F use one 2-byte load per column.  The tail column
+// (TAIL: B % 64 != 0) keeps natural slots; lanes past the row end get 0.
+template <int NBL, int R, bool A16, bool TAIL>
+struct RowGroup {
+    static constexpr int F = NBL - (TAIL ? 1 : 0);
+    static constexpr bool WIDE = F == 1 || F == 2 || F == 4 || F == 8;
+    static constexpr int DW = WIDE ? (F + 1) / 2 : (F > 0 ? F : 1);
+    u32x4 q[R][NBL];
+    uint32_t dw[R][DW];  // fp16 bits of the full-column scales
+    uint32_t dt[R];      // fp16 bits of the tail-column scale
+
+    // fp16 bits of the scale of block column j of row r
+    __device__ __forceinline__ uint32_t d_bits(int r, int j, uint32_t tail_mask) const {
+        if (TAIL && j == F) return dt[r] & tail_mask;
+        if constexpr (WIDE) return (dw[r][j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+        return dw[r][j] & 0xFFFFu;
+    }
+
+    // Lane-dependent parts of the offsets stay in VGPRs (16*lane, 2*F*lane);
+    // row and block-column parts go in the scalar soffset operand.
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ W, int row0, int N, int B,
+                                         int64_t row_bytes, int lane) {
+        const uint8_t *base = W + static_cast<int64_t>(row0) * row_bytes;
+        // a group past the last row gets an empty descriptor: every access is
+        // out of range and returns 0 without touching memory
+        const int64_t left = static_cast<int64_t>(N - row0) * row_bytes;
+        const uint32_t records =
+            left <= 0 ? 0u : static_cast<uint32_t>(left < 0xFFFFFFFFll ? left : 0xFFFFFFFFll);
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
+        const int scale_off = 16 * B;
+        const int qv = 16 * lane;
+        const int dv = 2 * F * lane;
+        const int tv = 2 * lane;
+        // scales first (one or few loads), then code bytes in the order
+        // accumulate() consumes them (block column major)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int roff = r * static_cast<int>(row_bytes);
+            if constexpr (F == 1) {
+                dw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, dv, roff + scale_off, 0);
+            } else if constexpr (F == 2) {
+                dw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, dv, roff + scale_off, 0);
+            } else if constexpr (F == 4) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, dv, roff + scale_off, 0);
+                dw[r][0] = v[0];
+                dw[r][1] = v[1];
+            } else if constexpr (F == 8) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, dv, roff + scale_off, 0);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) dw[r][h] = v[h];
+            } else {
+#pragma unroll
+                for (int j = 0; j < F; ++j)
+                    dw[r][j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, dv, roff + scale_off + 2 * j, 0);
+            }
+            if constexpr (TAIL)
+                dt[r] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, tv, roff + scale_off + 128 * F, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < NBL; ++j) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int roff = r * static_cast<int>(row_bytes);
+                if constexpr (A16) {
+                    q[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, qv, roff + 1024 * j, kNonTemporal);
+                } else {
+                    u32x4 v;
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rsrc, qv + 4 * h, roff + 1024 * j, kNonTemporal);
+                        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rsrc, qv + 4 * h + 2, roff + 1024 * j, kNonTemporal);
+                        v[h] = lo | (hi << 16);
+                    }
+                    q[r][j] = v;
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void accumulate(float acc[R], const uint4 *planes, const float *ub, int B,
+                                               const int bc[NBL], uint32_t tail_mask) const {
+#pragma unroll
+        for (int j = 0; j < NBL; ++j) {
+            // one block column at a time: keeps the scheduler from hoisting
+            // every column's digit planes into registers at once
+            if (j > 0) __builtin_amdgcn_sched_barrier(0);
+            uint4 P[kPlanes];
+#pragma unroll
+            for (int p = 0; p < kPlanes; ++p) P[p] = planes[p * B + bc[j]];
+            const float u = ub[bc[j]];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int T = block_dot_digits(q[r][j], P);
+                const float dr = half_bits_to_float(static_cast<uint16_t>(d_bits(r, j, tail_mask)));
+                acc[r] = fmaf(dr * u, static_cast<float>(T), acc[r]);
+            }
+        }
+    }
+};
+
+// One kernel covers rows whose blocks fit NBL per lane (B <= 64*NBL);
+// TAIL <=> B % 64 != 0.  WAVES wavefronts per workgroup: 16 caps a wave at
+// 128 VGPRs, 8 at 256.
+template <int NBL, int R, int WAVES, bool A16, bool TAIL>
+__global__ __launch_bounds__(64 * WAVES) void gemv_q4_0_dp_kernel(
+    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int B,
+    int64_t row_bytes, int x_al16) {
+    extern __shared__ uint4 lds_dp[];
+    uint4 *planes = lds_dp;
+    float *ub = reinterpret_cast<float *>(lds_dp + kPlanes * B);
+    const int lane = threadIdx.x & 63;
+    // wave index made explicitly uniform so row bases and buffer descriptors
+    // live in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    constexpr int ROWS = WAVES * R;
+    const int n_groups = (N + ROWS - 1) / ROWS;
+
+    int bc[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
+    const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
+
+    // Order of the prologue: activation loads, then the first group's weight
+    // loads (HBM traffic starts with the kernel), then the staging math,
+    // which waits only for the activation loads.  Later groups rely on the
+    // other wavefronts of the SIMD to cover their latency.
+    constexpr int XI = (4 * NBL + WAVES - 1) / WAVES;
+    XTile<XI> xt;
+    xt.load(x, B, x_al16 != 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+    int g = blockIdx.x;
+    RowGroup<NBL, R, A16, TAIL> grp;
+    // unconditional (a missing group reads nothing): a branch here would make
+    // the wait before the staging math cover the weight loads as well
+    grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+    xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
+    __syncthreads();
+
+    while (g < n_groups) {
+        const int row0 = g * ROWS + wave * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        grp.accumulate(acc, planes, ub, B, bc, tail_mask);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == 0 && row0 + r < N) y[row0 + r] = s;
+        }
+        g += gridDim.x;
+        grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+    }
+}
+
+typedef void (*dp_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int);
+
+template <int NBL, int R, int WAVES>
+dp_kernel_t pick_dp_at(bool a16, bool tail) {
+    if (a16) return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, true, true> : gemv_q4_0_dp_kernel<NBL, R, WAVES, true, false>;
+    return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, false, true> : gemv_q4_0_dp_kernel<NBL, R, WAVES, false, false>;
+}
+
+template <int NBL, int WAVES>
+dp_kernel_t pick_dp_r(int r, bool a16, bool tail) {
+    switch (r) {
+    case 1: return pick_dp_at<NBL, 1, WAVES>(a16, tail);
+    case 2: return pick_dp_at<NBL, 2, WAVES>(a16, tail);
+    default: return pick_dp_at<NBL, 4, WAVES>(a16, tail);
+    }
+}
+
+template <int WAVES>
+dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail) {
+    switch (nbl) {
+    case 1: return pick_dp_r<1, WAVES>(r, a16, tail);
+    case 2: return pick_dp_r<2, WAVES>(r, a16, tail);
+    case 3: return pick_dp_r<3, WAVES>(r, a16, tail);
+    case 4: return pick_dp_r<4, WAVES>(r, a16, tail);
+    case 5: return pick_dp_r<5, WAVES>(r, a16, tail);
+    case 6: return pick_dp_r<6, WAVES>(r, a16, tail);
+    case 7: return pick_dp_r<7, WAVES>(r, a16, tail);
+    default: return pick_dp_r<8, WAVES>(r, a16, tail);
+    }
+}
+
+}  // namespace
+
+// Largest blocks-per-row the digit-plane kernel takes (8 blocks per lane).
+constexpr int64_t kDpMaxBlocks = 64 * 8;
+
+bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a) {
+    const int64_t B = a.K / 32;
+    const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float));
+    return !a.x_bf16 && B > 0 && B <= kDpMaxBlocks && lds <= ctx->max_lds_per_block && a.N <= INT32_MAX &&
+           static_cast<int64_t>(a.N) * 18 * B < (int64_t(1) << 40);
+}
+
+int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
+    const int64_t B = a.K / 32;
+    const int64_t row_bytes = 18 * B;
+    const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
+    const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
+    const int nbl = static_cast<int>((B + 63) / 64);
+    // defaults: about 8 KiB of weight loads per wave step, no register spills
+    int waves = nbl <= 2 ? 16 : 8;
+    int R = nbl <= 1 ? 4 : (nbl <= 2 ? 4 : (nbl <= 4 ? 4 : 2));
+    if (ctx->waves_override == 8 || ctx->waves_override == 16) waves = ctx->waves_override;
+    if (ctx->rows_override == 1 || ctx->rows_override == 2 || ctx->rows_override == 4) R = ctx->rows_override;
+    const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float));
+    const bool tail = B % 64 != 0;
+    dp_kernel_t k = waves == 16 ? pick_dp_n<16>(nbl, R, a16, tail) : pick_dp_n<8>(nbl, R, a16, tail);
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * waves, lds);
+    const int64_t rows_per_group = static_cast<int64_t>(waves) * R;
+    const int64_t n_groups = (a.N + rows_per_group - 1) / rows_per_group;
+    int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * occ);
+    if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds, ctx->stream, a.W,
+                       static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),
+                       row_bytes, x_al16 ? 1 : 0);
+    MI355X_HIP(hipGetLastError());
+    return MI355X_OK;
+}
+
+}  // namespace mi355x

@@ -22,6 +22,11 @@ struct mi355x_ctx {
     void *iq3xxs_grid = nullptr;
     void *iq2s_grid = nullptr;
     uint64_t grids_version = 0;
+    // tuning / numerics options (mi355x_ctx_set_option)
+    int kernel_variant = MI355X_VARIANT_AUTO;
+    int rows_override = 0;
+    int waves_override = 0;
+    int64_t grid_override = 0;
     std::mutex mu;  // serialises calls that share the staging buffer
 };
 
@@ -50,6 +55,8 @@ struct GemvArgs {
 
 // Kernel launchers, one per weight family; return MI355X_* codes.
 int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
+bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
+int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a);
 
 // Prepack kernels: byte-range scatter/gather between ggml and resident order.

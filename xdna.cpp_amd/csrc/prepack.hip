@@ -5,40 +5,53 @@
 // planes are per row and keep the exact fp16 scale bits, so the resident
 // tensor is a row-local byte permutation of the ggml bytes:
 //   ggml row  : B blocks of [d lo, d hi, qs[0..15]]          (18*B bytes)
-//   resident  : [qs of block 0..B-1 (16*B)][d of block 0..B-1 (2*B)]
+//   resident  : [qs of block 0..B-1 (16*B)][d plane (2*B)]
+// every qs byte is stored XOR 0x88, i.e. as the two signed 4-bit codes
+// q - 8 that the integer kernels consume directly, and the d plane is
+// lane-major over full 64-block columns (q4_0_layout.h).
 // A byte of the ggml encoding at tensor offset o maps to exactly one resident
 // byte, so set_tensor/get_tensor with any (offset, size) can be served
 // without touching other bytes.  Other weight types keep the ggml order.
 #include "device_common.h"
 #include "internal.h"
+#include "q4_0_layout.h"
 
 #include <algorithm>
 
 namespace mi355x {
 namespace {
 
-// resident offset of ggml byte `o` in a Q4_0 tensor with `B` blocks per row
-__device__ __forceinline__ uint64_t q4_0_to_resident(uint64_t o, uint64_t row_bytes, uint64_t B) {
+// Resident offset of ggml byte `o` in a Q4_0 tensor with `B` blocks per row;
+// *xor_mask receives the byte transform (0x88 for code bytes, 0 for scales).
+__device__ __forceinline__ uint64_t q4_0_to_resident(uint64_t o, uint64_t row_bytes, uint64_t B,
+                                                     uint8_t *xor_mask) {
     const uint64_t row = o / row_bytes;
     const uint64_t p = o - row * row_bytes;
     const uint64_t blk = p / 18;
     const uint64_t e = p - blk * 18;
-    const uint64_t in_row = e < 2 ? 16 * B + 2 * blk + e : 16 * blk + (e - 2);
+    *xor_mask = e < 2 ? 0 : 0x88;
+    const uint64_t in_row = e < 2 ? 16 * B + 2 * q4_0_d_slot(blk, B) + e : 16 * blk + (e - 2);
     return row * row_bytes + in_row;
 }
 
 __global__ void q4_0_scatter_kernel(uint8_t *__restrict__ packed, const uint8_t *__restrict__ raw,
                                     uint64_t offset, uint64_t size, uint64_t row_bytes, uint64_t B) {
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < size; i += stride)
-        packed[q4_0_to_resident(offset + i, row_bytes, B)] = raw[i];
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < size; i += stride) {
+        uint8_t m;
+        const uint64_t dst = q4_0_to_resident(offset + i, row_bytes, B, &m);
+        packed[dst] = raw[i] ^ m;
+    }
 }
 
 __global__ void q4_0_gather_kernel(uint8_t *__restrict__ raw, const uint8_t *__restrict__ packed,
                                    uint64_t offset, uint64_t size, uint64_t row_bytes, uint64_t B) {
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < size; i += stride)
-        raw[i] = packed[q4_0_to_resident(offset + i, row_bytes, B)];
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < size; i += stride) {
+        uint8_t m;
+        const uint64_t src = q4_0_to_resident(offset + i, row_bytes, B, &m);
+        raw[i] = packed[src] ^ m;
+    }
 }
 
 __global__ void fill_kernel(uint8_t *__restrict__ dst, uint8_t value, uint64_t bytes) {

@@ -251,6 +251,34 @@ int mi355x_ctx_sync(mi355x_ctx *ctx) {
     return MI355X_OK;
 }
 
+int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: null context");
+    switch (option) {
+    case MI355X_OPT_VARIANT:
+        if (value != MI355X_VARIANT_AUTO && value != MI355X_VARIANT_EXACT_F32 && value != MI355X_VARIANT_DIGITS)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: unknown kernel variant");
+        ctx->kernel_variant = static_cast<int>(value);
+        return MI355X_OK;
+    case MI355X_OPT_ROWS_PER_WAVE:
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: rows per wave must be 0, 1, 2 or 4");
+        ctx->rows_override = static_cast<int>(value);
+        return MI355X_OK;
+    case MI355X_OPT_WAVES_PER_GROUP:
+        if (value != 0 && value != 8 && value != 16)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: waves per workgroup must be 0, 8 or 16");
+        ctx->waves_override = static_cast<int>(value);
+        return MI355X_OK;
+    case MI355X_OPT_GRID:
+        if (value < 0) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: negative grid");
+        ctx->grid_override = value;
+        return MI355X_OK;
+    default:
+        return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: unknown option " + std::to_string(option));
+    }
+}
+
 void *mi355x_ctx_stream(mi355x_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
 
 int mi355x_ctx_device(mi355x_ctx *ctx) { return ctx ? ctx->device : -1; }

@@ -26,6 +26,10 @@ BLOCK_BYTES = {Q4_0: 18, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98
                IQ2_S: 82, IQ4_XS: 136}
 
 
+OPT_VARIANT, OPT_ROWS_PER_WAVE, OPT_WAVES_PER_GROUP, OPT_GRID = 1, 2, 3, 4
+VARIANT_AUTO, VARIANT_EXACT_F32, VARIANT_DIGITS = 0, 1, 2
+
+
 class Mi355xError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"[{code}] {msg}")
@@ -40,6 +44,7 @@ _SIGNATURES = {
     "mi355x_ctx_create": (_c.c_int, [_c.c_int, _c.POINTER(_vp)]),
     "mi355x_ctx_destroy": (None, [_vp]),
     "mi355x_ctx_sync": (_c.c_int, [_vp]),
+    "mi355x_ctx_set_option": (_c.c_int, [_vp, _c.c_int, _c.c_int64]),
     "mi355x_ctx_stream": (_vp, [_vp]),
     "mi355x_ctx_device": (_c.c_int, [_vp]),
     "mi355x_mem_info": (_c.c_int, [_vp, _c.POINTER(_c.c_size_t), _c.POINTER(_c.c_size_t)]),
@@ -196,6 +201,9 @@ class Context:
 
     def __exit__(self, *exc):
         self.close()
+
+    def set_option(self, option: int, value: int) -> None:
+        check(self.lib.mi355x_ctx_set_option(self.h, option, value))
 
     def sync(self) -> None:
         check(self.lib.mi355x_ctx_sync(self.h))
