@@ -108,6 +108,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one device-to-device copy of 256 MiB (a plain copy kernel of known size, "
+                         "the reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -125,6 +128,14 @@ def main() -> int:
     alg = algorithmic_bytes(t, N, K)
 
     with mi355x.Context(0) as ctx:
+        if args.copy_calibration:
+            nbytes = 256 << 20
+            src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+            mi355x.check(ctx.lib.mi355x_fill(ctx.h, src.ptr, 1, nbytes))
+            mi355x.check(ctx.lib.mi355x_memcpy_d2d(ctx.h, dst.ptr, src.ptr, nbytes))
+            src.free()
+            dst.free()
+            log(f"bench: copy calibration: one {nbytes} B device-to-device copy done")
         name, pci = ctx.describe()
         log(f"bench: device {name} at {pci}; timing {args.steps} launches after {args.warmup} warmup")
         ms, copies, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES)

@@ -86,11 +86,14 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step.
  *   MI355X_OPT_WAVES_PER_GROUP: 0 (auto), 8 or 16 wavefronts per workgroup
  *     (digit-plane Q4_0 kernel).
- *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups. */
+ *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups.
+ *   MI355X_OPT_PREFETCH: 0 (auto), 1 (each wavefront requests its next row
+ *     group before reducing the current one), 2 (off). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3
 #define MI355X_OPT_GRID 4
+#define MI355X_OPT_PREFETCH 5
 #define MI355X_VARIANT_AUTO 0
 #define MI355X_VARIANT_EXACT_F32 1
 #define MI355X_VARIANT_DIGITS 2

@@ -155,21 +155,24 @@ def test_chunked_upload_gives_same_gemv(ctx, oracle):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("prefetch", [1, 2])
 @pytest.mark.parametrize("waves,rows", [(8, 1), (8, 2), (8, 4), (16, 1), (16, 2), (16, 4)])
-@pytest.mark.parametrize("N,K", [(1000, 2048), (777, 8192), (300, 14336)])
-def test_tuning_options_keep_results(ctx, oracle, variant, waves, rows, N, K):
+@pytest.mark.parametrize("N,K", [(1000, 2048), (777, 8192), (300, 14336), (130, 5120), (64, 16384)])
+def test_tuning_options_keep_results(ctx, oracle, variant, waves, rows, prefetch, N, K):
     # every launch shape the tuning options can select computes the same GEMV
     raw = synth.random_q4_0(N, K, seed=N * 7 + K)
     x = synth.activations(K, seed=99)
     ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, waves)
     ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, rows)
+    ctx.set_option(mi355x.OPT_PREFETCH, prefetch)
     try:
-        parity(ctx, oracle, raw, N, K, x, f"{variant} waves={waves} rows={rows} {N}x{K}")
+        parity(ctx, oracle, raw, N, K, x, f"{variant} waves={waves} rows={rows} pf={prefetch} {N}x{K}")
         ctx.set_option(mi355x.OPT_GRID, 7)
         parity(ctx, oracle, raw, N, K, x, f"{variant} grid=7 {N}x{K}")
     finally:
         ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, 0)
         ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+        ctx.set_option(mi355x.OPT_PREFETCH, 0)
         ctx.set_option(mi355x.OPT_GRID, 0)
 
 

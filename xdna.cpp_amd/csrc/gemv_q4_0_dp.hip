@@ -17,12 +17,12 @@
 // about 1.1 VALU ops per weight.  The only approximation beyond f32 rounding
 // is the activation quantization: |x_j - Z_j u_b| <= u_b/2 <= 2^-18.9 max|x_b|.
 //
-// Work split: workgroups of 16 wavefronts; each wavefront owns R rows per
-// step and walks its row groups grid-stride, prefetching the next group's
-// weight bytes before it computes the current one; the first group's loads
-// are issued before the activation row is staged, so HBM traffic starts at
-// once.  Lane l owns blocks l, l+64, ... of a row (contiguous 1 KiB per
-// 16-byte load instruction); row partials are folded with DPP.
+// Work split: workgroups of 8 or 16 wavefronts; each wavefront owns R rows
+// per step and walks its row groups grid-stride.  The first group's weight
+// loads are issued right after the activation loads and before the digit
+// planes are built, so HBM traffic starts with the kernel.  Lane l owns
+// blocks l, l+64, ... of a row (contiguous 1 KiB per 16-byte load
+// instruction); row partials are folded with DPP.
 #include "device_common.h"
 #include "internal.h"
 #include "q4_0_layout.h"
@@ -276,7 +276,7 @@ struct RowGroup {
 // One kernel covers rows whose blocks fit NBL per lane (B <= 64*NBL);
 // TAIL <=> B % 64 != 0.  WAVES wavefronts per workgroup: 16 caps a wave at
 // 128 VGPRs, 8 at 256.
-template <int NBL, int R, int WAVES, bool A16, bool TAIL>
+template <int NBL, int R, int WAVES, bool A16, bool TAIL, bool PF>
 __global__ __launch_bounds__(64 * WAVES) void gemv_q4_0_dp_kernel(
     const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int B,
     int64_t row_bytes, int x_al16) {
@@ -313,6 +313,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q4_0_dp_kernel(
 
     while (g < n_groups) {
         const int row0 = g * ROWS + wave * R;
+        const int gn = g + gridDim.x;
+        // PF: the next group's bytes are requested before this group is
+        // reduced (two register sets in flight per wave)
+        RowGroup<NBL, R, A16, TAIL> nxt;
+        if constexpr (PF) nxt.load(W, gn * ROWS + wave * R, N, B, row_bytes, lane);
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -322,39 +327,47 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q4_0_dp_kernel(
             const float s = wave_sum(acc[r]);
             if (lane == 0 && row0 + r < N) y[row0 + r] = s;
         }
-        g += gridDim.x;
-        grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+        g = gn;
+        if constexpr (PF) grp = nxt;
+        else grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
     }
 }
 
 typedef void (*dp_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int);
 
+// A16 = false (rows not 16-byte aligned: K % 256 != 0) only in its plain form.
 template <int NBL, int R, int WAVES>
-dp_kernel_t pick_dp_at(bool a16, bool tail) {
-    if (a16) return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, true, true> : gemv_q4_0_dp_kernel<NBL, R, WAVES, true, false>;
-    return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, false, true> : gemv_q4_0_dp_kernel<NBL, R, WAVES, false, false>;
+dp_kernel_t pick_dp_at(bool a16, bool tail, bool pf) {
+    if (!a16)
+        return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, false, true, false>
+                    : gemv_q4_0_dp_kernel<NBL, R, WAVES, false, false, false>;
+    if (pf)
+        return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, true, true, true>
+                    : gemv_q4_0_dp_kernel<NBL, R, WAVES, true, false, true>;
+    return tail ? gemv_q4_0_dp_kernel<NBL, R, WAVES, true, true, false>
+                : gemv_q4_0_dp_kernel<NBL, R, WAVES, true, false, false>;
 }
 
 template <int NBL, int WAVES>
-dp_kernel_t pick_dp_r(int r, bool a16, bool tail) {
+dp_kernel_t pick_dp_r(int r, bool a16, bool tail, bool pf) {
     switch (r) {
-    case 1: return pick_dp_at<NBL, 1, WAVES>(a16, tail);
-    case 2: return pick_dp_at<NBL, 2, WAVES>(a16, tail);
-    default: return pick_dp_at<NBL, 4, WAVES>(a16, tail);
+    case 1: return pick_dp_at<NBL, 1, WAVES>(a16, tail, pf);
+    case 2: return pick_dp_at<NBL, 2, WAVES>(a16, tail, pf);
+    default: return pick_dp_at<NBL, 4, WAVES>(a16, tail, pf);
     }
 }
 
 template <int WAVES>
-dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail) {
+dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail, bool pf) {
     switch (nbl) {
-    case 1: return pick_dp_r<1, WAVES>(r, a16, tail);
-    case 2: return pick_dp_r<2, WAVES>(r, a16, tail);
-    case 3: return pick_dp_r<3, WAVES>(r, a16, tail);
-    case 4: return pick_dp_r<4, WAVES>(r, a16, tail);
-    case 5: return pick_dp_r<5, WAVES>(r, a16, tail);
-    case 6: return pick_dp_r<6, WAVES>(r, a16, tail);
-    case 7: return pick_dp_r<7, WAVES>(r, a16, tail);
-    default: return pick_dp_r<8, WAVES>(r, a16, tail);
+    case 1: return pick_dp_r<1, WAVES>(r, a16, tail, pf);
+    case 2: return pick_dp_r<2, WAVES>(r, a16, tail, pf);
+    case 3: return pick_dp_r<3, WAVES>(r, a16, tail, pf);
+    case 4: return pick_dp_r<4, WAVES>(r, a16, tail, pf);
+    case 5: return pick_dp_r<5, WAVES>(r, a16, tail, pf);
+    case 6: return pick_dp_r<6, WAVES>(r, a16, tail, pf);
+    case 7: return pick_dp_r<7, WAVES>(r, a16, tail, pf);
+    default: return pick_dp_r<8, WAVES>(r, a16, tail, pf);
     }
 }
 
@@ -376,18 +389,21 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
     const int nbl = static_cast<int>((B + 63) / 64);
-    // defaults: about 8 KiB of weight loads per wave step, no register spills
-    int waves = nbl <= 2 ? 16 : 8;
-    int R = nbl <= 1 ? 4 : (nbl <= 2 ? 4 : (nbl <= 4 ? 4 : 2));
+    // defaults from sweeps on MI355X (8192x8192, 17408x5120, 151936x2048,
+    // 4096x4096, 2048x11008): 8-wave groups; long rows one row per wave with
+    // two workgroups per CU, short rows several rows per wave
+    int waves = 8;
+    int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
     if (ctx->waves_override == 8 || ctx->waves_override == 16) waves = ctx->waves_override;
     if (ctx->rows_override == 1 || ctx->rows_override == 2 || ctx->rows_override == 4) R = ctx->rows_override;
     const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float));
     const bool tail = B % 64 != 0;
-    dp_kernel_t k = waves == 16 ? pick_dp_n<16>(nbl, R, a16, tail) : pick_dp_n<8>(nbl, R, a16, tail);
+    const bool pf = ctx->prefetch_override == 1;
+    dp_kernel_t k = waves == 16 ? pick_dp_n<16>(nbl, R, a16, tail, pf) : pick_dp_n<8>(nbl, R, a16, tail, pf);
     const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * waves, lds);
     const int64_t rows_per_group = static_cast<int64_t>(waves) * R;
     const int64_t n_groups = (a.N + rows_per_group - 1) / rows_per_group;
-    int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * occ);
+    int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
     if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds, ctx->stream, a.W,
                        static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),

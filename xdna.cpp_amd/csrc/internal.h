@@ -26,6 +26,7 @@ struct mi355x_ctx {
     int kernel_variant = MI355X_VARIANT_AUTO;
     int rows_override = 0;
     int waves_override = 0;
+    int prefetch_override = 0;
     int64_t grid_override = 0;
     std::mutex mu;  // serialises calls that share the staging buffer
 };

@@ -270,6 +270,11 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
             return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: waves per workgroup must be 0, 8 or 16");
         ctx->waves_override = static_cast<int>(value);
         return MI355X_OK;
+    case MI355X_OPT_PREFETCH:
+        if (value != 0 && value != 1 && value != 2)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: prefetch must be 0 (auto), 1 (on) or 2 (off)");
+        ctx->prefetch_override = static_cast<int>(value);
+        return MI355X_OK;
     case MI355X_OPT_GRID:
         if (value < 0) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: negative grid");
         ctx->grid_override = value;
