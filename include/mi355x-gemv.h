@@ -104,6 +104,9 @@ MI355X_API int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value)
  * return after completion. */
 MI355X_API int mi355x_malloc(mi355x_ctx *ctx, size_t bytes, void **dptr);
 MI355X_API int mi355x_free(mi355x_ctx *ctx, void *dptr);
+/* Page-locked host memory (hipHostMalloc) for staging transfers. */
+MI355X_API int mi355x_host_malloc(size_t bytes, void **hptr);
+MI355X_API int mi355x_host_free(void *hptr);
 MI355X_API int mi355x_memcpy_h2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2h(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);

@@ -1,0 +1,913 @@
+// ggml backend plugin for MI355X: registry, device, device/host buffer types,
+// backend and graph_compute for single-row quantized MUL_MAT.  Host C++ only;
+// all device work goes through the C-ABI of mi355x-gemv.h.
+//
+// Reference counterparts (random-unknown-username/xdna.cpp):
+//   supports_op_impl       src/ggml-xdna.cpp:95-147
+//   process_mul_mat_node   src/ggml-xdna.cpp:150-308
+//   buffer / buffer type   src/ggml-xdna.cpp:316-489 (host memory there; HBM here)
+//   device / registry      src/ggml-xdna.cpp:495-671
+//   backend, entry points  src/ggml-xdna.cpp:677-844
+#include "ggml_abi.h"
+
+#include "ggml-mi355x.h"
+#include "mi355x-gemv.h"
+
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr uint32_t kBackendMagic = 0x4D333535;  // "M355"
+constexpr size_t kAlignment = 256;
+
+// ---------------------------------------------------------------------------
+// op id of GGML_OP_MUL_MAT in the host's ggml
+// ---------------------------------------------------------------------------
+std::atomic<int> g_op_mul_mat{-1};
+
+int op_mul_mat() {
+    int v = g_op_mul_mat.load(std::memory_order_relaxed);
+    if (v >= 0) return v;
+    if (const char *env = std::getenv("MI355X_GGML_OP_MUL_MAT")) {
+        v = std::atoi(env);
+        if (v >= 0) {
+            g_op_mul_mat.store(v);
+            return v;
+        }
+    }
+    // ggml exports `const char *ggml_op_name(enum ggml_op)`; MUL_MAT sits well
+    // inside its table in every ggml release, so the scan stops there.
+    typedef const char *(*op_name_fn)(int);
+    auto fn = reinterpret_cast<op_name_fn>(dlsym(RTLD_DEFAULT, "ggml_op_name"));
+    if (fn) {
+        for (int i = 0; i < 128; ++i) {
+            const char *n = fn(i);
+            if (n && std::strcmp(n, "MUL_MAT") == 0) {
+                g_op_mul_mat.store(i);
+                return i;
+            }
+        }
+    }
+    return -1;
+}
+
+bool trace_supports() {
+    static const bool t = std::getenv("MI355X_TRACE_SUPPORTS") != nullptr;
+    return t;
+}
+bool trace_nodes() {
+    static const bool t = std::getenv("MI355X_TRACE_NODES") != nullptr;
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// weight formats
+// ---------------------------------------------------------------------------
+// Block size of a claimable weight type (0 = not claimable), bytes per block.
+// Same table as the reference's type switch (src/ggml-xdna.cpp:185-254).
+int block_values(int type) {
+    switch (type) {
+    case GGML_TYPE_Q4_0: return 32;
+    case GGML_TYPE_Q4_K: case GGML_TYPE_Q5_K: case GGML_TYPE_Q3_K: case GGML_TYPE_Q6_K:
+    case GGML_TYPE_IQ4_XS: case GGML_TYPE_IQ3_S: case GGML_TYPE_IQ3_XXS: case GGML_TYPE_IQ2_S:
+        return 256;
+    default: return 0;
+    }
+}
+
+const char *type_name(int type) {
+    switch (type) {
+    case GGML_TYPE_Q4_0: return "Q4_0";
+    case GGML_TYPE_Q4_K: return "Q4_K";
+    case GGML_TYPE_Q5_K: return "Q5_K";
+    case GGML_TYPE_Q3_K: return "Q3_K";
+    case GGML_TYPE_Q6_K: return "Q6_K";
+    case GGML_TYPE_IQ4_XS: return "IQ4_XS";
+    case GGML_TYPE_IQ3_S: return "IQ3_S";
+    case GGML_TYPE_IQ3_XXS: return "IQ3_XXS";
+    case GGML_TYPE_IQ2_S: return "IQ2_S";
+    default: return "?";
+    }
+}
+
+// (block values, bytes per block) of any type ggml may place in our buffer,
+// for byte-size computations; 0/0 for types this plugin does not know.
+void type_geometry(int type, int64_t *blk, int64_t *bytes) {
+    *blk = 1;
+    *bytes = 0;
+    switch (type) {
+    case GGML_TYPE_F32: *bytes = 4; return;
+    case GGML_TYPE_F16: case 30 /* BF16 */: *bytes = 2; return;
+    case 24 /* I8 */: *bytes = 1; return;
+    case 25 /* I16 */: *bytes = 2; return;
+    case 26 /* I32 */: *bytes = 4; return;
+    case 27 /* I64 */: case 28 /* F64 */: *bytes = 8; return;
+    case 3 /* Q4_1 */: *blk = 32; *bytes = 20; return;
+    case 6 /* Q5_0 */: *blk = 32; *bytes = 22; return;
+    case 7 /* Q5_1 */: *blk = 32; *bytes = 24; return;
+    case 8 /* Q8_0 */: *blk = 32; *bytes = 34; return;
+    default: break;
+    }
+    const int bv = block_values(type);
+    if (bv) {
+        *blk = bv;
+        *bytes = mi355x_row_bytes(type, bv);
+    }
+}
+
+// ggml_nbytes of a tensor (row 0 in full, then strides of the other dims).
+size_t tensor_nbytes(const ggml_tensor *t) {
+    int64_t blk, bytes;
+    type_geometry(t->type, &blk, &bytes);
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (t->ne[i] <= 0) return 0;
+    typedef size_t (*nbytes_fn)(const ggml_tensor *);
+    static auto *p_nbytes = reinterpret_cast<nbytes_fn>(dlsym(RTLD_DEFAULT, "ggml_nbytes"));
+    if (bytes == 0) return p_nbytes ? p_nbytes(t) : 0;
+    size_t n = static_cast<size_t>(t->ne[0] / blk) * static_cast<size_t>(bytes);
+    for (int i = 1; i < GGML_MAX_DIMS; ++i) n += static_cast<size_t>(t->ne[i] - 1) * t->nb[i];
+    return n;
+}
+
+// ---------------------------------------------------------------------------
+// claim rule (src/ggml-xdna.cpp:95-147) on any tensor-like struct
+// ---------------------------------------------------------------------------
+template <typename T>
+bool claim_mul_mat(const T *op, int mul_mat_id, bool weights_resident) {
+    if (!op || mul_mat_id < 0 || static_cast<int>(op->op) != mul_mat_id) return false;
+    const auto *src0 = op->src[0];
+    const auto *src1 = op->src[1];
+    if (!src0 || !src1) return false;
+    if (src1->type != GGML_TYPE_F32) return false;
+    if (src1->nb[0] != 0 && src1->nb[0] != sizeof(float)) return false;
+    const int64_t K = src0->ne[0];
+    const int64_t N = src0->ne[1];
+    const int64_t M = src1->ne[1];
+    // size cutoff: N >= 32 and N % 4 == 0; M == 1 unless the weights live in
+    // this plugin's buffer (src/ggml-xdna.cpp:110-112)
+    if (N < 32 || N % 4 != 0) return false;
+    if (!weights_resident && M != 1) return false;
+    const int bv = block_values(src0->type);
+    if (bv == 0 || K % bv != 0) return false;
+    if (!mi355x_type_ready(src0->type)) return false;
+    const int64_t rb = mi355x_row_bytes(src0->type, K);
+    return src0->nb[1] == 0 || static_cast<int64_t>(src0->nb[1]) == rb;
+}
+
+// ---------------------------------------------------------------------------
+// devices
+// ---------------------------------------------------------------------------
+struct DevCtx {
+    int device = 0;
+    std::string name, description, pci;
+    ggml_backend_device dev{};
+    ggml_backend_buffer_type buft{};
+    ggml_backend_buffer_type host_buft{};
+    std::mutex mu;
+    mi355x_ctx *xfer = nullptr;  // context for buffer transfers
+
+    mi355x_ctx *transfer_ctx() {
+        std::lock_guard<std::mutex> lk(mu);
+        if (!xfer && mi355x_ctx_create(device, &xfer) != MI355X_OK) xfer = nullptr;
+        return xfer;
+    }
+};
+
+ggml_backend_reg g_reg{};
+std::vector<DevCtx *> g_devs;
+std::once_flag g_reg_once;
+
+void init_registry();
+
+DevCtx *dev_ctx(ggml_backend_dev_t dev) { return dev ? static_cast<DevCtx *>(dev->context) : nullptr; }
+DevCtx *buft_dev(ggml_backend_buffer_type_t buft) {
+    return buft && buft->device ? static_cast<DevCtx *>(buft->device->context) : nullptr;
+}
+
+// ---------------------------------------------------------------------------
+// device buffer (HBM)
+// ---------------------------------------------------------------------------
+struct BufCtx {
+    DevCtx *dc = nullptr;
+    void *base = nullptr;  // device pointer (or pinned host pointer)
+    size_t size = 0;
+    bool host = false;
+    bool own_struct = false;  // ggml_backend_buffer allocated here (no ggml-base)
+};
+
+void log_error(const char *what) {
+    std::fprintf(stderr, "[mi355x error] %s: %s\n", what, mi355x_last_error());
+}
+
+// The base tensor whose rows define the resident layout of `t`'s bytes.
+const ggml_tensor *layout_base(const ggml_tensor *t) { return t->view_src ? t->view_src : t; }
+
+// Number of K-value rows of a contiguous weight tensor.
+int64_t weight_rows(const ggml_tensor *t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+
+// Tensors whose resident byte order differs from ggml's (Q4_0 weights).
+bool prepacked(const ggml_tensor *t) {
+    const ggml_tensor *b = layout_base(t);
+    return b->type == GGML_TYPE_Q4_0 && t->type == GGML_TYPE_Q4_0 && b->ne[0] % 32 == 0;
+}
+
+void buf_free(ggml_backend_buffer_t buffer) {
+    if (!buffer || !buffer->context) return;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    if (bc->host) {
+        mi355x_host_free(bc->base);
+    } else if (mi355x_ctx *x = bc->dc->transfer_ctx()) {
+        mi355x_free(x, bc->base);
+    }
+    const bool own = bc->own_struct;
+    delete bc;
+    buffer->context = nullptr;
+    if (own) delete buffer;
+}
+
+void *buf_get_base(ggml_backend_buffer_t buffer) {
+    return buffer && buffer->context ? static_cast<BufCtx *>(buffer->context)->base : nullptr;
+}
+
+enum ggml_status buf_init_tensor(ggml_backend_buffer_t, ggml_tensor *) { return GGML_STATUS_SUCCESS; }
+
+// Host -> tensor bytes [offset, offset+size) in ggml encoding, on the stream
+// of `x` (synchronous).  Q4_0 weights are scattered into the resident layout.
+void upload(mi355x_ctx *x, ggml_tensor *tensor, const void *data, size_t offset, size_t size) {
+    uint8_t *dst = static_cast<uint8_t *>(tensor->data) + offset;
+    if (prepacked(tensor)) {
+        const ggml_tensor *b = layout_base(tensor);
+        const size_t o = static_cast<size_t>(dst - static_cast<const uint8_t *>(b->data));
+        if (mi355x_prepack_from_host(x, GGML_TYPE_Q4_0, weight_rows(b), b->ne[0], b->data, data, o, size))
+            log_error("set_tensor: prepack");
+        return;
+    }
+    if (mi355x_memcpy_h2d(x, dst, data, size)) log_error("set_tensor");
+}
+
+// Tensor bytes [offset, offset+size) in ggml encoding -> host (synchronous).
+void download(mi355x_ctx *x, const ggml_tensor *tensor, void *data, size_t offset, size_t size) {
+    const uint8_t *src = static_cast<const uint8_t *>(tensor->data) + offset;
+    if (prepacked(tensor)) {
+        const ggml_tensor *b = layout_base(tensor);
+        const size_t o = static_cast<size_t>(src - static_cast<const uint8_t *>(b->data));
+        if (mi355x_unpack_to_host(x, GGML_TYPE_Q4_0, weight_rows(b), b->ne[0], b->data, data, o, size))
+            log_error("get_tensor: unpack");
+        return;
+    }
+    if (mi355x_memcpy_d2h(x, data, src, size)) log_error("get_tensor");
+}
+
+void buf_set_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, const void *data, size_t offset,
+                    size_t size) {
+    if (!buffer || !tensor || !tensor->data || !data || size == 0) return;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    if (bc->host) {
+        std::memcpy(static_cast<uint8_t *>(tensor->data) + offset, data, size);
+        return;
+    }
+    mi355x_ctx *x = bc->dc->transfer_ctx();
+    if (!x) return log_error("set_tensor: no device context");
+    upload(x, tensor, data, offset, size);
+}
+
+void buf_get_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *tensor, void *data, size_t offset,
+                    size_t size) {
+    if (!buffer || !tensor || !tensor->data || !data || size == 0) return;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    if (bc->host) {
+        std::memcpy(data, static_cast<const uint8_t *>(tensor->data) + offset, size);
+        return;
+    }
+    mi355x_ctx *x = bc->dc->transfer_ctx();
+    if (!x) return log_error("get_tensor: no device context");
+    download(x, tensor, data, offset, size);
+}
+
+void buf_memset_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, uint8_t value, size_t offset,
+                       size_t size) {
+    if (!buffer || !tensor || !tensor->data || size == 0) return;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    uint8_t *dst = static_cast<uint8_t *>(tensor->data) + offset;
+    if (bc->host) {
+        std::memset(dst, value, size);
+        return;
+    }
+    if (prepacked(tensor)) {
+        // fill the ggml bytes with `value` through the prepack permutation
+        const size_t chunk = std::min<size_t>(size, size_t(16) << 20);
+        std::vector<uint8_t> fill(chunk, value);
+        for (size_t done = 0; done < size; done += chunk)
+            buf_set_tensor(buffer, tensor, fill.data(), offset + done, std::min(chunk, size - done));
+        return;
+    }
+    mi355x_ctx *x = bc->dc->transfer_ctx();
+    if (!x || mi355x_fill(x, dst, value, size) || mi355x_ctx_sync(x)) log_error("memset_tensor");
+}
+
+bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *src, ggml_tensor *dst) {
+    // device-to-device copies between tensors of this plugin on one device;
+    // both sides share the resident layout when their rows match
+    if (!buffer || !src || !dst || !src->buffer || !src->data || !dst->data) return false;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    if (bc->host || src->buffer->iface.get_base != buffer->iface.get_base) return false;
+    auto *sbc = static_cast<BufCtx *>(src->buffer->context);
+    if (!sbc || sbc->host || sbc->dc != bc->dc) return false;
+    if (prepacked(src) != prepacked(dst)) return false;
+    if (prepacked(src) && (src->view_src || dst->view_src || src->ne[0] != dst->ne[0])) return false;
+    const size_t n = tensor_nbytes(src);
+    if (n != tensor_nbytes(dst)) return false;
+    mi355x_ctx *x = bc->dc->transfer_ctx();
+    return x && mi355x_memcpy_d2d(x, dst->data, src->data, n) == MI355X_OK;
+}
+
+void buf_clear(ggml_backend_buffer_t buffer, uint8_t value) {
+    if (!buffer || !buffer->context) return;
+    auto *bc = static_cast<BufCtx *>(buffer->context);
+    if (bc->host) {
+        std::memset(bc->base, value, bc->size);
+        return;
+    }
+    mi355x_ctx *x = bc->dc->transfer_ctx();
+    if (!x || mi355x_fill(x, bc->base, value, bc->size) || mi355x_ctx_sync(x)) log_error("clear");
+}
+
+const ggml_backend_buffer_i kBufferIface = {
+    /* .free_buffer   = */ buf_free,
+    /* .get_base      = */ buf_get_base,
+    /* .init_tensor   = */ buf_init_tensor,
+    /* .memset_tensor = */ buf_memset_tensor,
+    /* .set_tensor    = */ buf_set_tensor,
+    /* .get_tensor    = */ buf_get_tensor,
+    /* .set_tensor_2d = */ nullptr,
+    /* .get_tensor_2d = */ nullptr,
+    /* .cpy_tensor    = */ buf_cpy_tensor,
+    /* .clear         = */ buf_clear,
+    /* .reset         = */ nullptr,
+    /* .set_tensor_n  = */ nullptr,
+    /* .get_tensor_n  = */ nullptr,
+    /* .cpy_tensor_n  = */ nullptr,
+};
+
+// Buffers are made by ggml-base's ggml_backend_buffer_init when the host
+// exports it (ggml then owns and deletes the struct); otherwise here.
+ggml_backend_buffer_t make_buffer(ggml_backend_buffer_type_t buft, BufCtx *bc, size_t size) {
+    typedef ggml_backend_buffer_t (*init_fn)(ggml_backend_buffer_type_t, ggml_backend_buffer_i, void *, size_t);
+    static auto *p_init = reinterpret_cast<init_fn>(dlsym(RTLD_DEFAULT, "ggml_backend_buffer_init"));
+    if (p_init) return p_init(buft, kBufferIface, bc, size);
+    auto *buf = new (std::nothrow) ggml_backend_buffer{kBufferIface, buft, bc, size, GGML_BACKEND_BUFFER_USAGE_ANY};
+    if (buf) bc->own_struct = true;
+    return buf;
+}
+
+const char *buft_get_name(ggml_backend_buffer_type_t buft) {
+    DevCtx *dc = buft_dev(buft);
+    return buft == (dc ? &dc->host_buft : nullptr) ? "MI355X_Host" : "MI355X";
+}
+
+ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t size) {
+    DevCtx *dc = buft_dev(buft);
+    if (!dc) return nullptr;
+    const bool host = buft == &dc->host_buft;
+    void *p = nullptr;
+    if (host) {
+        if (mi355x_host_malloc(size, &p) != MI355X_OK) return log_error("alloc_buffer (host)"), nullptr;
+    } else {
+        mi355x_ctx *x = dc->transfer_ctx();
+        if (!x || mi355x_malloc(x, size, &p) != MI355X_OK) return log_error("alloc_buffer"), nullptr;
+    }
+    auto *bc = new (std::nothrow) BufCtx{dc, p, size, host, false};
+    ggml_backend_buffer_t buf = bc ? make_buffer(buft, bc, size) : nullptr;
+    if (!buf) {
+        if (host) mi355x_host_free(p);
+        else mi355x_free(dc->transfer_ctx(), p);
+        delete bc;
+    }
+    return buf;
+}
+
+size_t buft_get_alignment(ggml_backend_buffer_type_t) { return kAlignment; }
+size_t buft_get_max_size(ggml_backend_buffer_type_t) { return SIZE_MAX; }
+size_t buft_get_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor *t) { return t ? tensor_nbytes(t) : 0; }
+bool buft_is_host(ggml_backend_buffer_type_t buft) {
+    DevCtx *dc = buft_dev(buft);
+    return dc && buft == &dc->host_buft;
+}
+
+const ggml_backend_buffer_type_i kBufferTypeIface = {
+    /* .get_name         = */ buft_get_name,
+    /* .alloc_buffer     = */ buft_alloc_buffer,
+    /* .alloc_buffer_n   = */ nullptr,
+    /* .get_alignment    = */ buft_get_alignment,
+    /* .get_max_size     = */ buft_get_max_size,
+    /* .get_alloc_size   = */ buft_get_alloc_size,
+    /* .get_alloc_size_n = */ nullptr,
+    /* .is_host          = */ buft_is_host,
+};
+
+bool in_our_device_buffer(const ggml_tensor *t) {
+    if (!t || !t->buffer || !t->buffer->buft) return false;
+    DevCtx *dc = buft_dev(t->buffer->buft);
+    if (!dc || t->buffer->buft != &dc->buft) return false;
+    return std::find(g_devs.begin(), g_devs.end(), dc) != g_devs.end();
+}
+
+// ---------------------------------------------------------------------------
+// backend
+// ---------------------------------------------------------------------------
+struct BackendCtx {
+    uint32_t magic = kBackendMagic;
+    DevCtx *dc = nullptr;
+    mi355x_ctx *ctx = nullptr;
+    std::mutex mu;
+    // device scratch for the compatibility path (host-pointer graphs)
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+
+    ~BackendCtx() {
+        if (ctx) {
+            if (scratch) mi355x_free(ctx, scratch);
+            mi355x_ctx_destroy(ctx);
+        }
+        magic = 0;
+    }
+
+    void *ensure_scratch(size_t bytes) {
+        if (scratch_bytes >= bytes) return scratch;
+        if (scratch) mi355x_free(ctx, scratch);
+        scratch = nullptr;
+        scratch_bytes = 0;
+        if (mi355x_malloc(ctx, bytes, &scratch) != MI355X_OK) return nullptr;
+        scratch_bytes = bytes;
+        return scratch;
+    }
+};
+
+ggml_guid_t backend_guid() {
+    static ggml_guid guid = {0x4d, 0x49, 0x33, 0x35, 0x35, 0x58, 0x2d, 0x67,
+                             0x65, 0x6d, 0x76, 0x2d, 0x71, 0x75, 0x61, 0x6e};
+    return &guid;
+}
+
+BackendCtx *backend_ctx(ggml_backend_t backend) {
+    if (!backend || !backend->guid) return nullptr;
+    if (std::memcmp(backend->guid, backend_guid(), sizeof(ggml_guid)) != 0) return nullptr;
+    auto *bc = static_cast<BackendCtx *>(backend->context);
+    return bc && bc->magic == kBackendMagic ? bc : nullptr;
+}
+
+const char *backend_get_name(ggml_backend_t backend) {
+    BackendCtx *bc = backend_ctx(backend);
+    return bc ? bc->dc->name.c_str() : "MI355X";
+}
+
+void backend_free(ggml_backend_t backend) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc) return;
+    delete bc;
+    delete backend;
+}
+
+// Copies for tensors in this backend's device memory run on the backend's own
+// stream, so they are ordered after the kernels already queued there (an
+// activation upload cannot overtake the GEMV still reading the previous one).
+// They complete before returning.
+bool on_backend_device(BackendCtx *bc, const ggml_tensor *t) {
+    return in_our_device_buffer(t) && buft_dev(t->buffer->buft) == bc->dc;
+}
+
+void backend_set_tensor_async(ggml_backend_t backend, ggml_tensor *tensor, const void *data, size_t offset,
+                              size_t size) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc || !tensor || !tensor->buffer || !tensor->data || !data || size == 0) return;
+    if (!on_backend_device(bc, tensor)) return buf_set_tensor(tensor->buffer, tensor, data, offset, size);
+    std::lock_guard<std::mutex> lk(bc->mu);
+    upload(bc->ctx, tensor, data, offset, size);
+}
+
+void backend_get_tensor_async(ggml_backend_t backend, const ggml_tensor *tensor, void *data, size_t offset,
+                              size_t size) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc || !tensor || !tensor->buffer || !tensor->data || !data || size == 0) return;
+    if (!on_backend_device(bc, tensor)) {
+        if (mi355x_ctx_sync(bc->ctx)) log_error("get_tensor_async: sync");
+        return buf_get_tensor(tensor->buffer, tensor, data, offset, size);
+    }
+    std::lock_guard<std::mutex> lk(bc->mu);
+    download(bc->ctx, tensor, data, offset, size);
+}
+
+void backend_synchronize(ggml_backend_t backend) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (bc && mi355x_ctx_sync(bc->ctx)) log_error("synchronize");
+}
+
+// One MUL_MAT node: validation and batch/row iteration of the reference's
+// process_mul_mat_node (src/ggml-xdna.cpp:150-308).  `host` selects the
+// compatibility path, whose data pointers are host memory.
+template <typename T>
+bool process_mul_mat(BackendCtx *bc, T *node, bool host) {
+    auto *src0 = node->src[0];
+    auto *src1 = node->src[1];
+    if (!src0 || !src1) {
+        std::fprintf(stderr, "[mi355x error] node '%s' missing src0/src1\n", node->name);
+        return false;
+    }
+    if (src1->type != GGML_TYPE_F32) {
+        std::fprintf(stderr, "[mi355x error] node '%s' src1 type %d != F32\n", node->name, src1->type);
+        return false;
+    }
+    if (!node->data || !src0->data || !src1->data) {
+        std::fprintf(stderr, "[mi355x error] node '%s' null data ptrs: node->data=%p src0->data=%p src1->data=%p\n",
+                     node->name, node->data, src0->data, src1->data);
+        return false;
+    }
+    const int64_t K = src0->ne[0];
+    const int64_t N = src0->ne[1];
+    const int64_t M = src1->ne[1];
+    if (M == 0 || N == 0) return true;
+    if (M < 0 || N < 0 || K < 0) {
+        std::fprintf(stderr, "[mi355x error] node '%s' negative dim: M=%ld N=%ld K=%ld\n", node->name, (long)M,
+                     (long)N, (long)K);
+        return false;
+    }
+    const int type = src0->type;
+    const int bv = block_values(type);
+    if (bv == 0) {
+        std::fprintf(stderr, "[mi355x error] node '%s' unsupported src0 type=%d\n", node->name, type);
+        return false;
+    }
+    if (K % bv != 0) {
+        std::fprintf(stderr, "[mi355x error] node '%s' %s K=%ld not div by %d\n", node->name, type_name(type),
+                     (long)K, bv);
+        return false;
+    }
+    const size_t row_bytes = static_cast<size_t>(mi355x_row_bytes(type, K));
+    if (src0->nb[1] != 0 && src0->nb[1] != row_bytes) {
+        std::fprintf(stderr, "[mi355x error] node '%s' src0 nb1 mismatch: %zu != %zu\n", node->name,
+                     (size_t)src0->nb[1], row_bytes);
+        return false;
+    }
+    if (src1->nb[0] != 0 && src1->nb[0] != sizeof(float)) {
+        std::fprintf(stderr, "[mi355x error] node '%s' src1 rows are not contiguous\n", node->name);
+        return false;
+    }
+    const size_t total_weight_bytes = static_cast<size_t>(N) * row_bytes;
+    const int64_t ne2 = node->ne[2] > 0 ? node->ne[2] : 1;
+    const int64_t ne3 = node->ne[3] > 0 ? node->ne[3] : 1;
+    const size_t dst_stride1 = node->nb[1] > 0 ? node->nb[1] : static_cast<size_t>(N) * sizeof(float);
+    const size_t dst_stride2 = node->nb[2] > 0 ? node->nb[2] : dst_stride1 * M;
+    const size_t dst_stride3 = node->nb[3] > 0 ? node->nb[3] : dst_stride2 * ne2;
+    const size_t src1_stride1 = src1->nb[1] > 0 ? src1->nb[1] : static_cast<size_t>(K) * sizeof(float);
+    const size_t src1_stride2 = src1->ne[2] > 1 ? (src1->nb[2] > 0 ? src1->nb[2] : src1_stride1 * M) : 0;
+    const size_t src1_stride3 = src1->ne[3] > 1 ? (src1->nb[3] > 0 ? src1->nb[3] : src1_stride2 * ne2) : 0;
+    const size_t src0_stride2 = src0->ne[2] > 1 ? (src0->nb[2] > 0 ? src0->nb[2] : total_weight_bytes) : 0;
+    const size_t src0_stride3 = src0->ne[3] > 1 ? (src0->nb[3] > 0 ? src0->nb[3] : src0_stride2 * ne2) : 0;
+
+    const auto *w_base = static_cast<const uint8_t *>(src0->data);
+    const auto *a_base = static_cast<const uint8_t *>(src1->data);
+    auto *o_base = static_cast<uint8_t *>(node->data);
+
+    if (!host) {
+        for (int64_t i3 = 0; i3 < ne3; ++i3) {
+            for (int64_t i2 = 0; i2 < ne2; ++i2) {
+                const uint8_t *w = w_base + i3 * src0_stride3 + i2 * src0_stride2;
+                const uint8_t *a = a_base + i3 * src1_stride3 + i2 * src1_stride2;
+                uint8_t *o = o_base + i3 * dst_stride3 + i2 * dst_stride2;
+                for (int64_t m = 0; m < M; ++m) {
+                    if (mi355x_gemv(bc->ctx, type, w, N, K, reinterpret_cast<const float *>(a + m * src1_stride1),
+                                    reinterpret_cast<float *>(o + m * dst_stride1)) != MI355X_OK) {
+                        std::fprintf(stderr, "[mi355x error] node '%s' GEMV dispatch: %s\n", node->name,
+                                     mi355x_last_error());
+                        return false;
+                    }
+                }
+            }
+        }
+        return true;
+    }
+
+    // compatibility path: weights, activation rows and outputs are host memory;
+    // each weight matrix is uploaded (prepacked) into device scratch per call
+    const size_t w_al = (total_weight_bytes + 255) & ~size_t(255);
+    const size_t x_bytes = static_cast<size_t>(K) * sizeof(float);
+    const size_t y_bytes = static_cast<size_t>(N) * sizeof(float);
+    uint8_t *scratch = static_cast<uint8_t *>(bc->ensure_scratch(w_al + x_bytes + 256 + y_bytes));
+    if (!scratch) {
+        std::fprintf(stderr, "[mi355x error] node '%s' scratch allocation: %s\n", node->name, mi355x_last_error());
+        return false;
+    }
+    uint8_t *dw = scratch;
+    float *dx = reinterpret_cast<float *>(scratch + w_al);
+    float *dy = reinterpret_cast<float *>(scratch + w_al + ((x_bytes + 255) & ~size_t(255)));
+    for (int64_t i3 = 0; i3 < ne3; ++i3) {
+        for (int64_t i2 = 0; i2 < ne2; ++i2) {
+            const uint8_t *w = w_base + i3 * src0_stride3 + i2 * src0_stride2;
+            if (mi355x_prepack_from_host(bc->ctx, type, N, K, dw, w, 0, total_weight_bytes) != MI355X_OK) {
+                std::fprintf(stderr, "[mi355x error] node '%s' weight upload: %s\n", node->name, mi355x_last_error());
+                return false;
+            }
+            const uint8_t *a = a_base + i3 * src1_stride3 + i2 * src1_stride2;
+            uint8_t *o = o_base + i3 * dst_stride3 + i2 * dst_stride2;
+            for (int64_t m = 0; m < M; ++m) {
+                if (mi355x_memcpy_h2d(bc->ctx, dx, a + m * src1_stride1, x_bytes) != MI355X_OK ||
+                    mi355x_gemv(bc->ctx, type, dw, N, K, dx, dy) != MI355X_OK ||
+                    mi355x_memcpy_d2h(bc->ctx, o + m * dst_stride1, dy, y_bytes) != MI355X_OK) {
+                    std::fprintf(stderr, "[mi355x error] node '%s' GEMV: %s\n", node->name, mi355x_last_error());
+                    return false;
+                }
+            }
+        }
+    }
+    return true;
+}
+
+enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
+    if (!backend || !cgraph) return GGML_STATUS_FAILED;
+    if (cgraph->n_nodes > 0 && !cgraph->nodes) return GGML_STATUS_FAILED;
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc) return GGML_STATUS_FAILED;
+    std::lock_guard<std::mutex> lk(bc->mu);
+    const int mm = op_mul_mat();
+    const bool trace = trace_nodes();
+    double total_ms = 0.0;
+    int count = 0;
+    for (int i = 0; i < cgraph->n_nodes; ++i) {
+        ggml_tensor *node = cgraph->nodes[i];
+        if (!node || mm < 0 || node->op != mm) continue;  // other nodes carry no work here
+        auto t0 = std::chrono::steady_clock::now();
+        if (!process_mul_mat(bc, node, false)) return GGML_STATUS_FAILED;
+        if (trace) {
+            if (mi355x_ctx_sync(bc->ctx)) return GGML_STATUS_FAILED;
+            const double ms =
+                std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+            total_ms += ms;
+            ++count;
+            std::fprintf(stderr, "[mi355x trace] node %3d: %-30s | type=%2d | N=%6ld K=%5ld | %6.3f ms\n", i,
+                         node->name[0] ? node->name : "unnamed", node->src[0]->type, (long)node->src[0]->ne[1],
+                         (long)node->src[0]->ne[0], ms);
+        }
+    }
+    if (trace && count > 0) std::fprintf(stderr, "[mi355x trace] TOTAL: %d nodes, %6.3f ms\n", count, total_ms);
+    return GGML_STATUS_SUCCESS;
+}
+
+const ggml_backend_i kBackendIface = {
+    /* .get_name            = */ backend_get_name,
+    /* .free                = */ backend_free,
+    /* .set_tensor_async    = */ backend_set_tensor_async,
+    /* .get_tensor_async    = */ backend_get_tensor_async,
+    /* .set_tensor_2d_async = */ nullptr,
+    /* .get_tensor_2d_async = */ nullptr,
+    /* .cpy_tensor_async    = */ nullptr,
+    /* .synchronize         = */ backend_synchronize,
+    /* .graph_plan_create   = */ nullptr,
+    /* .graph_plan_free     = */ nullptr,
+    /* .graph_plan_update   = */ nullptr,
+    /* .graph_plan_compute  = */ nullptr,
+    /* .graph_compute       = */ backend_graph_compute,
+    /* .event_record        = */ nullptr,
+    /* .event_wait          = */ nullptr,
+    /* .graph_optimize      = */ nullptr,
+};
+
+ggml_backend_t make_backend(size_t dev_num) {
+    init_registry();
+    if (dev_num >= g_devs.size()) return nullptr;
+    auto *bc = new (std::nothrow) BackendCtx();
+    if (!bc) return nullptr;
+    bc->dc = g_devs[dev_num];
+    if (mi355x_ctx_create(bc->dc->device, &bc->ctx) != MI355X_OK) {
+        log_error("backend init");
+        delete bc;
+        return nullptr;
+    }
+    auto *backend = new (std::nothrow) ggml_backend{backend_guid(), kBackendIface, &bc->dc->dev, bc};
+    if (!backend) delete bc;
+    return backend;
+}
+
+// ---------------------------------------------------------------------------
+// device interface
+// ---------------------------------------------------------------------------
+const char *dev_get_name(ggml_backend_dev_t dev) { return dev_ctx(dev)->name.c_str(); }
+const char *dev_get_description(ggml_backend_dev_t dev) { return dev_ctx(dev)->description.c_str(); }
+
+void dev_get_memory(ggml_backend_dev_t dev, size_t *free, size_t *total) {
+    size_t f = 0, t = 0;
+    if (mi355x_ctx *x = dev_ctx(dev)->transfer_ctx()) mi355x_mem_info(x, &f, &t);
+    if (free) *free = f;
+    if (total) *total = t;
+}
+
+enum ggml_backend_dev_type dev_get_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
+
+void dev_get_props(ggml_backend_dev_t dev, ggml_backend_dev_props *props) {
+    if (!props) return;
+    DevCtx *dc = dev_ctx(dev);
+    props->name = dc->name.c_str();
+    props->description = dc->description.c_str();
+    props->type = GGML_BACKEND_DEVICE_TYPE_GPU;
+    dev_get_memory(dev, &props->memory_free, &props->memory_total);
+    props->device_id = dc->pci.c_str();
+    props->caps.async = true;
+    props->caps.host_buffer = true;
+    props->caps.buffer_from_host_ptr = false;
+    props->caps.events = false;
+    props->caps.mmap_support = false;
+}
+
+ggml_backend_t dev_init_backend(ggml_backend_dev_t dev, const char *) {
+    DevCtx *dc = dev_ctx(dev);
+    for (size_t i = 0; i < g_devs.size(); ++i)
+        if (g_devs[i] == dc) return make_backend(i);
+    return nullptr;
+}
+
+ggml_backend_buffer_type_t dev_get_buffer_type(ggml_backend_dev_t dev) { return &dev_ctx(dev)->buft; }
+ggml_backend_buffer_type_t dev_get_host_buffer_type(ggml_backend_dev_t dev) { return &dev_ctx(dev)->host_buft; }
+
+bool dev_supports_op(ggml_backend_dev_t dev, const ggml_tensor *op) {
+    (void)dev;
+    const int mm = op_mul_mat();
+    // The loader probes with weights in a zero-size buffer or in this
+    // plugin's buffer type (src/ggml-xdna.cpp:81-89); both lift M == 1.
+    const ggml_tensor *src0 = op && op->src[0] ? op->src[0] : nullptr;
+    const bool resident = src0 && src0->buffer && (src0->buffer->size == 0 || in_our_device_buffer(src0));
+    const bool res = claim_mul_mat(op, mm, resident);
+    if (trace_supports() && op && op->op == mm) {
+        const ggml_tensor *s1 = op->src[1];
+        std::fprintf(stderr, "[supports_op] %-25s | type=%2d | N=%6ld K=%5ld M=%3ld buf_sz=%zu | -> %s\n", op->name,
+                     src0 ? src0->type : -1, src0 ? (long)src0->ne[1] : 0L, src0 ? (long)src0->ne[0] : 0L,
+                     s1 ? (long)s1->ne[1] : 0L, (src0 && src0->buffer) ? src0->buffer->size : size_t(0),
+                     res ? "YES" : "NO");
+    }
+    return res;
+}
+
+bool dev_supports_buft(ggml_backend_dev_t dev, ggml_backend_buffer_type_t buft) {
+    return buft && buft == &dev_ctx(dev)->buft;
+}
+
+// Weights outside this plugin's buffer would cross PCIe for every token, so
+// no op is pulled onto the device from host buffers.
+bool dev_offload_op(ggml_backend_dev_t, const ggml_tensor *) { return false; }
+
+const ggml_backend_device_i kDeviceIface = {
+    /* .get_name             = */ dev_get_name,
+    /* .get_description      = */ dev_get_description,
+    /* .get_memory           = */ dev_get_memory,
+    /* .get_type             = */ dev_get_type,
+    /* .get_props            = */ dev_get_props,
+    /* .init_backend         = */ dev_init_backend,
+    /* .get_buffer_type      = */ dev_get_buffer_type,
+    /* .get_host_buffer_type = */ dev_get_host_buffer_type,
+    /* .buffer_from_host_ptr = */ nullptr,
+    /* .supports_op          = */ dev_supports_op,
+    /* .supports_buft        = */ dev_supports_buft,
+    /* .offload_op           = */ dev_offload_op,
+    /* .event_new            = */ nullptr,
+    /* .event_free           = */ nullptr,
+    /* .event_synchronize    = */ nullptr,
+};
+
+// ---------------------------------------------------------------------------
+// registry
+// ---------------------------------------------------------------------------
+const char *reg_get_name(ggml_backend_reg_t) { return "MI355X"; }
+size_t reg_get_device_count(ggml_backend_reg_t) {
+    init_registry();
+    return g_devs.size();
+}
+ggml_backend_dev_t reg_get_device(ggml_backend_reg_t, size_t index) {
+    init_registry();
+    return index < g_devs.size() ? &g_devs[index]->dev : nullptr;
+}
+
+void *reg_get_proc_address(ggml_backend_reg_t, const char *name) {
+    if (!name) return nullptr;
+    if (!std::strcmp(name, "ggml_backend_mi355x_init")) return reinterpret_cast<void *>(ggml_backend_mi355x_init);
+    if (!std::strcmp(name, "ggml_backend_is_mi355x")) return reinterpret_cast<void *>(ggml_backend_is_mi355x);
+    if (!std::strcmp(name, "ggml_backend_mi355x_free")) return reinterpret_cast<void *>(ggml_backend_mi355x_free);
+    if (!std::strcmp(name, "ggml_backend_mi355x_load_iq_grids_from_ggml"))
+        return reinterpret_cast<void *>(ggml_backend_mi355x_load_iq_grids_from_ggml);
+    return nullptr;
+}
+
+const ggml_backend_reg_i kRegIface = {
+    /* .get_name         = */ reg_get_name,
+    /* .get_device_count = */ reg_get_device_count,
+    /* .get_device       = */ reg_get_device,
+    /* .get_proc_address = */ reg_get_proc_address,
+};
+
+void init_registry() {
+    std::call_once(g_reg_once, [] {
+        g_reg.api_version = GGML_MI355X_BACKEND_API_VERSION;
+        g_reg.iface = kRegIface;
+        g_reg.context = nullptr;
+        int n = 0;
+        if (mi355x_device_count(&n) != MI355X_OK) n = 0;
+        for (int d = 0; d < n; ++d) {
+            auto *dc = new DevCtx();
+            dc->device = d;
+            dc->name = "MI355X" + std::to_string(d);
+            char desc[256] = {0}, pci[64] = {0};
+            if (mi355x_device_describe(d, desc, sizeof desc, pci, sizeof pci) == MI355X_OK) {
+                dc->description = desc;
+                dc->pci = pci;
+            } else {
+                dc->description = "AMD Instinct MI355X";
+            }
+            dc->dev = ggml_backend_device{kDeviceIface, &g_reg, dc};
+            dc->buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
+            dc->host_buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
+            g_devs.push_back(dc);
+        }
+    });
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// IQ grids from the host's ggml (defined in ggml_mi355x_iq.cpp)
+// ---------------------------------------------------------------------------
+int mi355x_iq_grids_from_ggml_impl();
+
+extern "C" {
+
+ggml_backend_reg *ggml_backend_init(void) {
+    init_registry();
+    ggml_backend_mi355x_load_iq_grids_from_ggml();
+    return &g_reg;
+}
+
+int ggml_backend_score(void) {
+    int n = 0;
+    return mi355x_device_count(&n) == MI355X_OK && n > 0 ? 100 : 0;
+}
+
+ggml_backend_reg *ggml_backend_mi355x_reg(void) {
+    init_registry();
+    return &g_reg;
+}
+
+ggml_backend *ggml_backend_mi355x_init(size_t dev_num) { return make_backend(dev_num); }
+
+bool ggml_backend_is_mi355x(ggml_backend *backend) { return backend_ctx(backend) != nullptr; }
+
+void ggml_backend_mi355x_free(ggml_backend *backend) { backend_free(backend); }
+
+ggml_backend_buffer_type *ggml_backend_mi355x_buffer_type(size_t dev_num) {
+    init_registry();
+    return dev_num < g_devs.size() ? &g_devs[dev_num]->buft : nullptr;
+}
+
+ggml_backend_buffer_type *ggml_backend_mi355x_host_buffer_type(void) {
+    init_registry();
+    return g_devs.empty() ? nullptr : &g_devs[0]->host_buft;
+}
+
+int ggml_backend_mi355x_graph_compute(ggml_backend *backend, ggml_cgraph *cgraph) {
+    return backend_graph_compute(backend, cgraph);
+}
+
+bool ggml_backend_mi355x_supports_op(ggml_backend *backend, const ggml_tensor_mi355x *op) {
+    (void)backend;
+    return claim_mul_mat(op, GGML_MI355X_OP_MUL_MAT, false);
+}
+
+bool ggml_backend_mi355x_compute_graph(ggml_backend *backend, ggml_tensor_mi355x **nodes, size_t n_nodes) {
+    if (!backend || !nodes || n_nodes == 0) return false;
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc) return false;
+    std::lock_guard<std::mutex> lk(bc->mu);
+    for (size_t i = 0; i < n_nodes; ++i) {
+        ggml_tensor_mi355x *node = nodes[i];
+        if (!node || node->op != GGML_MI355X_OP_MUL_MAT) continue;
+        if (!process_mul_mat(bc, node, true)) return false;
+    }
+    return true;
+}
+
+bool ggml_backend_mi355x_set_op_mul_mat(int op) {
+    if (op < 0) return false;
+    g_op_mul_mat.store(op);
+    return true;
+}
+
+int ggml_backend_mi355x_load_iq_grids_from_ggml(void) { return mi355x_iq_grids_from_ggml_impl(); }
+
+}  // extern "C"

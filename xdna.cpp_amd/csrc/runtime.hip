@@ -332,6 +332,25 @@ int mi355x_free(mi355x_ctx *ctx, void *dptr) {
     return MI355X_OK;
 }
 
+int mi355x_host_malloc(size_t bytes, void **hptr) {
+    clear_error();
+    if (!hptr) return set_error(MI355X_EINVAL, "mi355x_host_malloc: null pointer");
+    *hptr = nullptr;
+    hipError_t e = hipHostMalloc(hptr, bytes == 0 ? 64 : bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        *hptr = nullptr;
+        return set_error(MI355X_ENOMEM, "hipHostMalloc(" + std::to_string(bytes) + "): " + hipGetErrorString(e));
+    }
+    return MI355X_OK;
+}
+
+int mi355x_host_free(void *hptr) {
+    clear_error();
+    if (!hptr) return MI355X_OK;
+    MI355X_HIP(hipHostFree(hptr));
+    return MI355X_OK;
+}
+
 static int copy_sync(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind,
                      const char *who) {
     clear_error();

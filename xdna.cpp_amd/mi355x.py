@@ -51,6 +51,8 @@ _SIGNATURES = {
     "mi355x_device_describe": (_c.c_int, [_c.c_int, _c.c_char_p, _c.c_size_t, _c.c_char_p, _c.c_size_t]),
     "mi355x_malloc": (_c.c_int, [_vp, _c.c_size_t, _c.POINTER(_vp)]),
     "mi355x_free": (_c.c_int, [_vp, _vp]),
+    "mi355x_host_malloc": (_c.c_int, [_c.c_size_t, _c.POINTER(_vp)]),
+    "mi355x_host_free": (_c.c_int, [_vp]),
     "mi355x_memcpy_h2d": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
     "mi355x_memcpy_d2h": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
     "mi355x_memcpy_d2d": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
