@@ -1,0 +1,487 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Four independent sources:
+  1. golden vectors written by the reference's own compiled code
+     (tests/golden/ref_vectors.npz, made by tests/golden/make_golden.py);
+  2. the compiled reference itself (oracle/_ref), on fresh random inputs,
+     when it is built in this checkout;
+  3. the known answers the reference's tests hold
+     (tests/test-q4-0-reference.cpp:49-54,128-143,157-210,
+      tests/test-backend.cpp:58-98, tests/test-gemv-accuracy.cpp:128-153,184-217,
+      tests/test-kquants-gemv.cpp:258-270);
+  4. closed forms: exhaustive fp16/bf16 conversion against numpy, and each
+     K/IQ format's decode against an independent *encoder* written from ggml's
+     quantizer packing (the inverse direction), so a wrong shift, index or
+     nibble order in the oracle's decoder fails.
+IQ3_XXS / IQ2_S have no reference code, vectors or tests: only the structural
+invariants at the end apply to them (parity unpinned).
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+from oracle import (IQ2_S, IQ3_S, IQ3_XXS, IQ4_XS, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, TYPE_NAMES, RefLib)
+import synth
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_vectors.npz")
+REF_TYPES = (Q4_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS, IQ3_S)
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+def half(v):
+    return np.array([v], dtype=np.float16).view(np.uint8)
+
+
+# ---- 1. golden vectors from the reference build -----------------------------
+
+@pytest.mark.parametrize("t", REF_TYPES, ids=[TYPE_NAMES[t] for t in REF_TYPES])
+def test_golden_vectors_bit_exact(oracle, golden, t):
+    name = TYPE_NAMES[t]
+    i = 0
+    while f"{name}_{i}_W" in golden:
+        k = f"{name}_{i}"
+        N, K = (int(v) for v in golden[k + "_shape"])
+        W, x = golden[k + "_W"], golden[k + "_x"]
+        y = oracle.gemv(t, W, N, K, x)
+        assert np.array_equal(bits(y), bits(golden[k + "_y"])), k
+        d0 = oracle.dequant_row(t, W.reshape(N, -1)[0], K)
+        assert np.array_equal(bits(d0), bits(golden[k + "_deq0"])), k
+        if t == Q4_0:
+            yb = oracle.gemv(t, W, N, K, golden[k + "_xbf16"])
+            assert np.array_equal(bits(yb), bits(golden[k + "_ybf16"])), k
+        i += 1
+    assert i >= 1
+
+
+def test_golden_validation_rules(oracle, golden):
+    # src/xdna-q4-0-reference.cpp:261-300: same accept/reject decisions
+    for (v, b), rc in zip(golden["validate_row_cases"], golden["validate_row_rc"]):
+        assert (oracle.lib.orc_q4_0_validate_row(int(v), int(b)) == 0) == (rc == 0), (v, b)
+    for (r, v, b), rc in zip(golden["validate_matrix_cases"], golden["validate_matrix_rc"]):
+        assert (oracle.lib.orc_q4_0_validate_matrix(int(r), int(v), int(b)) == 0) == (rc == 0), (r, v, b)
+
+
+def test_golden_bf16_rounding(oracle, golden):
+    got = np.array([oracle.f32_to_bf16(float(v)) for v in golden["bf16_in"]], dtype=np.uint16)
+    assert np.array_equal(got, golden["bf16_out"])
+
+
+def test_golden_iq3s_grid_hash(oracle, golden):
+    grid = extract_iq3s_grid(oracle)
+    h = hashlib.sha256(grid.astype("<u4").tobytes()).digest()
+    assert h == golden["iq3s_grid_sha256"].tobytes()
+
+
+# ---- 2. the compiled reference on fresh inputs ------------------------------
+
+@pytest.mark.parametrize("t", REF_TYPES, ids=[TYPE_NAMES[t] for t in REF_TYPES])
+def test_oracle_matches_reference_build(oracle, reflib, t):
+    rng = np.random.default_rng(t)
+    for trial in range(6):
+        bv = 32 if t == Q4_0 else 256
+        N = int(rng.integers(1, 9))
+        K = bv * int(rng.integers(1, 7))
+        if t == Q4_0:
+            W = synth.random_q4_0(N, K, seed=trial)
+        else:
+            d = int(rng.choice([0x2E66, 0x3C00, 0x1400, 0xB800]))
+            W = synth.random_blocks(t, N, K, seed=trial, d_bits=d, dmin_bits=int(rng.choice([0x2A00, 0x0000, 0xB000])))
+        x = (rng.standard_normal(K) * rng.choice([1e-3, 1.0, 100.0])).astype(np.float32)
+        assert np.array_equal(bits(oracle.gemv(t, W, N, K, x)), bits(reflib.gemv(t, W, N, K, x))), (trial, N, K)
+        for r in range(N):
+            row = W.reshape(N, -1)[r]
+            assert np.array_equal(bits(oracle.dequant_row(t, row, K)), bits(reflib.dequant_row(t, row, K)))
+
+
+def test_oracle_matches_reference_build_bf16(oracle, reflib):
+    W = synth.random_q4_0(16, 512, seed=3)
+    xb = np.random.default_rng(5).integers(0, 1 << 16, 512).astype(np.uint16)
+    xb[(xb & 0x7F80) == 0x7F80] = 0x3F80  # no inf/NaN activations
+    assert np.array_equal(bits(oracle.gemv(Q4_0, W, 16, 512, xb)), bits(reflib.gemv(Q4_0, W, 16, 512, xb)))
+
+
+def test_iq3s_grid_matches_reference_build(oracle, reflib):
+    assert np.array_equal(extract_iq3s_grid(oracle), reflib.iq3s_grid())
+
+
+# ---- 3. the reference tests' known answers ----------------------------------
+
+EDGE = np.array([0x00, 0x3c, 0xf0, 0xe1, 0xd2, 0xc3, 0xb4, 0xa5, 0x96,
+                 0x87, 0x78, 0x69, 0x5a, 0x4b, 0x3c, 0x2d, 0x1e, 0x0f], dtype=np.uint8)
+
+
+def test_q4_0_edge_block_order_and_dot(oracle):
+    # tests/test-q4-0-reference.cpp:49-54,157-191
+    d = oracle.dequant_row(Q4_0, EDGE, 32)
+    assert d[:16].tolist() == [j - 8.0 for j in range(16)]
+    assert d[16:].tolist() == [7.0 - j for j in range(16)]
+    x = np.arange(1, 33, dtype=np.float32)
+    assert oracle.gemv(Q4_0, EDGE, 1, 32, x).tolist() == [-264.0]
+    xb = np.array([oracle.f32_to_bf16(float(v)) for v in x], dtype=np.uint16)
+    assert oracle.gemv(Q4_0, EDGE, 1, 32, xb).tolist() == [-264.0]
+
+
+def test_q4_0_two_row_gemv(oracle):
+    # tests/test-q4-0-reference.cpp:128-143,193-210: 528 and -264
+    W = np.zeros(36, dtype=np.uint8)
+    W[0:2], W[2:18] = [0x00, 0x3c], 0x99
+    W[18:20], W[20:36] = [0x00, 0x38], 0x77
+    x = np.arange(1, 33, dtype=np.float32)
+    assert oracle.gemv(Q4_0, W, 2, 32, x).tolist() == [528.0, -264.0]
+    xb = np.array([oracle.f32_to_bf16(float(v)) for v in x], dtype=np.uint16)
+    assert oracle.gemv(Q4_0, W, 2, 32, xb).tolist() == [528.0, -264.0]
+
+
+def test_q4_0_uniform_weights(oracle):
+    # tests/test-backend.cpp:58-98 (d=1, +1 codes, x=0.5, K=256 -> 128) and
+    # tests/test-gemv-accuracy.cpp:128-153 (d=0.5, x=0.25, K=256 -> 32)
+    for d, xv, want in ((0x3C00, 0.5, 128.0), (0x3800, 0.25, 32.0)):
+        blk = np.array([d & 0xFF, d >> 8] + [0x99] * 16, dtype=np.uint8)
+        W = np.tile(blk, 128 * 8)
+        y = oracle.gemv(Q4_0, W, 128, 256, np.full(256, xv, np.float32))
+        assert np.all(y == want)
+
+
+@pytest.mark.parametrize("t", REF_TYPES, ids=[TYPE_NAMES[t] for t in REF_TYPES])
+def test_zero_activations_give_exact_zero(oracle, t):
+    # tests/test-gemv-accuracy.cpp:184-217, tests/test-kquants-gemv.cpp:258-270
+    K = 512
+    W = synth.random_q4_0(64, K, 505) if t == Q4_0 else synth.random_blocks(t, 64, K, 505)
+    y = oracle.gemv(t, W, 64, K, np.zeros(K, np.float32))
+    assert np.all(y == 0.0)
+
+
+def test_fp16_known_values(oracle):
+    # tests/test-q4-0-reference.cpp:163-172
+    assert oracle.fp16_to_f32(0x3c00) == 1.0
+    assert oracle.fp16_to_f32(0xc000) == -2.0
+    assert oracle.fp16_to_f32(0x0001) == 2.0 ** -24
+    assert oracle.fp16_to_f32(0x7bff) == 65504.0
+    assert oracle.bf16_to_f32(0x3f80) == 1.0
+    assert oracle.bf16_to_f32(0xc000) == -2.0
+
+
+def test_q4_0_validation_messages_cases(oracle):
+    # tests/test-q4-0-reference.cpp:212-222 and the row/matrix spans
+    assert oracle.lib.orc_q4_0_validate_row(31, 18) != 0
+    assert oracle.lib.orc_q4_0_validate_row(32, 17) != 0
+    assert oracle.lib.orc_q4_0_validate_row(32, 19) != 0
+    assert oracle.lib.orc_q4_0_validate_row(32, 18) == 0
+    assert oracle.lib.orc_q4_0_validate_row(0, 0) == 0
+    assert oracle.lib.orc_q4_0_validate_matrix(2, 32, 36) == 0
+    assert oracle.row_bytes(Q4_0, 32) == 18 and oracle.row_bytes(Q4_0, 0) == 0
+
+
+# ---- 4. closed forms ----------------------------------------------------------
+
+def test_fp16_exhaustive(oracle):
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.fp16_to_f32(int(v)) for v in h], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+
+
+def test_bf16_widen_exhaustive_and_round_to_nearest_even(oracle):
+    b = np.arange(1 << 16, dtype=np.uint32)
+    want = (b << 16).view(np.float32)
+    got = np.array([oracle.bf16_to_f32(int(v)) for v in b], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan])) and np.isnan(got[nan]).all()
+    # f32 -> bf16 is round-to-nearest-even on the dropped 16 bits
+    for u, r in ((0x3F808000, 0x3F80), (0x3F818000, 0x3F82), (0x3F808001, 0x3F81), (0x3F807FFF, 0x3F80),
+                 (0xBF808000, 0xBF80)):
+        assert oracle.f32_to_bf16(float(np.uint32(u).view(np.float32))) == r
+
+
+def test_block_geometry(oracle):
+    # include/xdna/kquants.h:182-200 and the ggml structs
+    want = {Q4_0: (32, 18), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
+            IQ3_XXS: (256, 98), IQ3_S: (256, 110), IQ2_S: (256, 82), IQ4_XS: (256, 136)}
+    for t, (bv, bb) in want.items():
+        assert oracle.block_values(t) == bv and oracle.block_bytes(t) == bb
+        assert oracle.row_bytes(t, 3 * bv) == 3 * bb
+        assert oracle.row_bytes(t, bv + 1) < 0
+
+
+# Independent encoders, from ggml's quantizer packing (ggml-quants.c,
+# quantize_row_*_ref): logical codes/scales in, block bytes out.
+
+def pack_k4_scales(ls, lm):
+    """Q4_K / Q5_K: eight 6-bit (scale, min) pairs into 12 bytes."""
+    s = np.zeros(12, dtype=np.uint8)
+    for j in range(8):
+        if j < 4:
+            s[j] = ls[j]
+            s[j + 4] = lm[j]
+        else:
+            s[j + 4] = (ls[j] & 0xF) | ((lm[j] & 0xF) << 4)
+            s[j - 4] |= (ls[j] >> 4) << 6
+            s[j] |= (lm[j] >> 4) << 6
+    return s
+
+
+def enc_q4_k(d, dmin, ls, lm, L):
+    blk = np.zeros(144, dtype=np.uint8)
+    blk[0:2], blk[2:4] = half(d), half(dmin)
+    blk[4:16] = pack_k4_scales(ls, lm)
+    q = blk[16:]
+    for j in range(0, 256, 64):
+        for l in range(32):
+            q[j // 2 + l] = L[j + l] | (L[j + l + 32] << 4)
+    return blk
+
+
+def enc_q5_k(d, dmin, ls, lm, L):
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2], blk[2:4] = half(d), half(dmin)
+    blk[4:16] = pack_k4_scales(ls, lm)
+    qh, ql = blk[16:48], blk[48:]
+    m1, m2 = 1, 2
+    for n in range(0, 256, 64):
+        for j in range(32):
+            l1, l2 = int(L[n + j]), int(L[n + j + 32])
+            if l1 > 15:
+                l1 -= 16
+                qh[j] |= m1
+            if l2 > 15:
+                l2 -= 16
+                qh[j] |= m2
+            ql[n // 2 + j] = l1 | (l2 << 4)
+        m1 <<= 2
+        m2 <<= 2
+    return blk
+
+
+def enc_q3_k(d, Ls, L):
+    """Ls: sixteen 6-bit scales (value + 32); L: 256 codes in 0..7 (value + 4)."""
+    blk = np.zeros(110, dtype=np.uint8)
+    hm, q, sc = blk[0:32], blk[32:96], blk[96:108]
+    for j in range(16):
+        lv = int(Ls[j])
+        if j < 8:
+            sc[j] = lv & 0xF
+        else:
+            sc[j - 8] |= (lv & 0xF) << 4
+        sc[j % 4 + 8] |= (lv >> 4) << (2 * (j // 4))
+    L = np.array(L, dtype=np.int64)
+    m, bit = 0, 1
+    for j in range(256):
+        if L[j] > 3:
+            hm[m] |= bit
+            L[j] -= 4
+        m += 1
+        if m == 32:
+            m, bit = 0, bit << 1
+    for j in range(0, 256, 128):
+        for l in range(32):
+            q[j // 4 + l] = L[j + l] | (L[j + l + 32] << 2) | (L[j + l + 64] << 4) | (L[j + l + 96] << 6)
+    blk[108:110] = half(d)
+    return blk
+
+
+def enc_q6_k(d, sc, L):
+    """sc: sixteen int8 scales; L: 256 codes in 0..63 (value + 32)."""
+    blk = np.zeros(210, dtype=np.uint8)
+    ql, qh = blk[0:128], blk[128:192]
+    for j in range(0, 256, 128):
+        for l in range(32):
+            a, b, c, e = (int(L[j + l + 32 * i]) for i in range(4))
+            ql[j // 2 + l] = (a & 0xF) | ((c & 0xF) << 4)
+            ql[j // 2 + l + 32] = (b & 0xF) | ((e & 0xF) << 4)
+            qh[j // 4 + l] = (a >> 4) | ((b >> 4) << 2) | ((c >> 4) << 4) | ((e >> 4) << 6)
+    blk[192:208] = np.array(sc, dtype=np.int8).view(np.uint8)
+    blk[208:210] = half(d)
+    return blk
+
+
+def enc_iq4_xs(d, ls, L):
+    """ls: eight 6-bit scales (value + 32); L: 256 codebook indices 0..15."""
+    blk = np.zeros(136, dtype=np.uint8)
+    blk[0:2] = half(d)
+    sh = 0
+    for ib in range(8):
+        sh |= (int(ls[ib]) >> 4) << (2 * ib)
+        blk[4 + ib // 2] |= (int(ls[ib]) & 0xF) << (4 * (ib % 2))
+        for j in range(16):
+            blk[8 + 16 * ib + j] = L[32 * ib + j] | (L[32 * ib + j + 16] << 4)
+    blk[2:4] = np.array([sh], dtype=np.uint16).view(np.uint8)
+    return blk
+
+
+KVALUES_IQ4NL = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def f32(v):
+    return np.float32(v)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_q4_k_and_q5_k_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(seed)
+    ls, lm = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    d, dmin = f32(0.03125), f32(0.0078125)  # exact in fp16
+    for t, top in ((Q4_K, 16), (Q5_K, 32)):
+        L = rng.integers(0, top, 256)
+        blk = (enc_q4_k if t == Q4_K else enc_q5_k)(d, dmin, ls, lm, L)
+        got = oracle.dequant_row(t, blk, 256)
+        sub = np.arange(256) // 32
+        want = (d * ls[sub].astype(np.float32)) * L.astype(np.float32) - dmin * lm[sub].astype(np.float32)
+        assert np.array_equal(bits(got), bits(want.astype(np.float32))), TYPE_NAMES[t]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_q3_k_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(seed)
+    Ls, L = rng.integers(0, 64, 16), rng.integers(0, 8, 256)
+    d = f32(0.25)
+    got = oracle.dequant_row(Q3_K, enc_q3_k(d, Ls, L), 256)
+    want = (d * (Ls[np.arange(256) // 16] - 32).astype(np.float32)) * (L - 4).astype(np.float32)
+    assert np.array_equal(bits(got), bits(want.astype(np.float32)))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_q6_k_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(seed)
+    sc, L = rng.integers(-128, 128, 16), rng.integers(0, 64, 256)
+    d = f32(0.0625)
+    got = oracle.dequant_row(Q6_K, enc_q6_k(d, sc, L), 256)
+    want = (d * sc[np.arange(256) // 16].astype(np.float32)) * (L - 32).astype(np.float32)
+    assert np.array_equal(bits(got), bits(want.astype(np.float32)))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_iq4_xs_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(seed)
+    ls, L = rng.integers(0, 64, 8), rng.integers(0, 16, 256)
+    d = f32(0.5)
+    got = oracle.dequant_row(IQ4_XS, enc_iq4_xs(d, ls, L), 256)
+    kv = np.array(KVALUES_IQ4NL, dtype=np.float32)
+    want = (d * (ls[np.arange(256) // 32] - 32).astype(np.float32)) * kv[L]
+    assert np.array_equal(bits(got), bits(want.astype(np.float32)))
+
+
+def extract_iq3s_grid(oracle):
+    """Read the oracle's iq3s_grid back through its decoder: d = 1, scale
+    nibble 0 (db = 1), no sign bits; lookup k of group g of block b holds
+    index 64b + 8g + k (bit 8 from qh)."""
+    grid = np.zeros(512, dtype=np.uint32)
+    for b in range(8):
+        blk = np.zeros(110, dtype=np.uint8)
+        blk[0:2] = half(1.0)
+        for g in range(8):
+            for k in range(8):
+                idx = 64 * b + 8 * g + k
+                blk[2 + 8 * g + k] = idx & 0xFF
+                blk[66 + g] |= ((idx >> 8) & 1) << k
+        v = oracle.dequant_row(IQ3_S, blk, 256).astype(np.int64)
+        assert np.all((v >= 0) & (v < 256))
+        grid[64 * b:64 * (b + 1)] = (v.reshape(64, 4) << np.array([0, 8, 16, 24])).sum(axis=1)
+    return grid
+
+
+def test_iq3_s_signs_and_scales(oracle):
+    # sign bit (4*(k&1)+j) of byte 4g + k/2 negates value j of lookup k;
+    # scale nibble s gives db = d * (1 + 2s)
+    rng = np.random.default_rng(1)
+    blk = synth.random_blocks(IQ3_S, 1, 256, 9, d_bits=0x3C00)[0]
+    base = blk.copy()
+    base[74:106] = 0
+    base[106:110] = 0
+    mag = oracle.dequant_row(IQ3_S, base, 256)
+    assert np.all(mag >= 0)
+    signed = base.copy()
+    signed[74:106] = rng.integers(0, 256, 32, dtype=np.uint8)
+    s = np.unpackbits(signed[74:106], bitorder="little").astype(bool)
+    assert np.array_equal(oracle.dequant_row(IQ3_S, signed, 256), np.where(s, -mag, mag))
+    scaled = base.copy()
+    scaled[106:110] = [0x21, 0x43, 0x65, 0x87]  # groups 0..7 -> nibbles 1..8
+    nib = np.repeat(np.arange(1, 9), 32).astype(np.float32)
+    assert np.array_equal(oracle.dequant_row(IQ3_S, scaled, 256), mag * (np.float32(1) + np.float32(2) * nib))
+
+
+def test_ksigns_table_structure(oracle):
+    k = oracle.ksigns()
+    assert np.array_equal(k & 0x7F, np.arange(128))
+    assert all(bin(int(v)).count("1") % 2 == 0 for v in k)
+
+
+# ---- IQ3_XXS / IQ2_S: parity unpinned; structural invariants only -------------
+
+def synthetic_grid(t, seed=0):
+    rng = np.random.default_rng(seed)
+    n, w = (256, 4) if t == IQ3_XXS else (1024, 8)
+    g = rng.integers(0, 64, (n, w)).astype(np.uint8)
+    return g.view(np.uint32 if w == 4 else np.uint64).reshape(n)
+
+
+def test_iq_grid_types_require_a_grid(oracle):
+    row = np.zeros(98, dtype=np.uint8)
+    with pytest.raises(ValueError):
+        oracle.dequant_row(IQ3_XXS, row, 256)
+    with pytest.raises(ValueError):
+        oracle.dequant_row(IQ2_S, np.zeros(82, dtype=np.uint8), 256)
+
+
+def test_iq3_xxs_probe_reads_back_the_grid(oracle):
+    grid = synthetic_grid(IQ3_XXS)
+    for b in range(4):
+        blk = np.zeros(98, dtype=np.uint8)
+        blk[0:2] = half(1.0)
+        blk[2:66] = np.arange(64 * b, 64 * (b + 1)) & 0xFF
+        v = oracle.dequant_row(IQ3_XXS, blk, 256, grid=grid) * 4  # db = 0.25
+        want = grid[64 * b:64 * (b + 1)].view(np.uint8).astype(np.float32)
+        assert np.array_equal(v, want)
+
+
+def test_iq2_s_probe_reads_back_the_grid(oracle):
+    grid = synthetic_grid(IQ2_S)
+    for b in range(32):
+        blk = np.zeros(82, dtype=np.uint8)
+        blk[0:2] = half(1.0)
+        for g in range(8):
+            for l in range(4):
+                idx = 32 * b + 4 * g + l
+                blk[2 + 4 * g + l] = idx & 0xFF
+                blk[66 + g] |= ((idx >> 8) & 3) << (2 * l)
+        v = oracle.dequant_row(IQ2_S, blk, 256, grid=grid) * 8  # db = 0.125
+        want = grid[32 * b:32 * (b + 1)].view(np.uint8).astype(np.float32)
+        assert np.array_equal(v, want)
+
+
+# ---- the Q4_0 quantizer used to build the BASELINE configs ------------------
+
+def test_quantize_q4_0_invariants(oracle):
+    w = synth.normal_weights(64, 512, seed=1)
+    raw = synth.quantize_q4_0(w)
+    deq = np.stack([oracle.dequant_row(Q4_0, raw[r], 512) for r in range(64)])
+    blk = w.reshape(64, 16, 32)
+    dq = deq.reshape(64, 16, 32)
+    d = raw.reshape(64, 16, 18)[..., :2].copy().view(np.float16)[..., 0].astype(np.float32)
+    # every value is within half a step of its input (plus the fp16 rounding
+    # of d, at most 8 * 2^-11 * |d|), except where the code clamps at 15
+    # (+7 d: the side opposite the absmax reaches only 7/8 of it), where the
+    # error stays within one step
+    err = np.abs(blk - dq)
+    ad = np.broadcast_to(np.abs(d)[..., None], err.shape)
+    clamped = dq == 7 * d[..., None]
+    slack = np.float32(8 * 2.0 ** -11)
+    assert np.all(err[~clamped] <= ad[~clamped] * (np.float32(0.5) + slack))
+    assert np.all(err[clamped] <= ad[clamped] * (np.float32(1.0) + slack))
+    assert clamped.any()
+    # the signed absmax element maps to code 0 (value -8 d)
+    idx = np.argmax(np.abs(blk), axis=2)
+    at = np.take_along_axis(dq, idx[..., None], axis=2)[..., 0]
+    assert np.array_equal(at, -8 * d)
