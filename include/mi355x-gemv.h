@@ -130,7 +130,10 @@ MI355X_API int mi355x_set_iq_grid(int type, const void *table, size_t bytes);
  * ggml encoding (N * row_bytes) and is a row-local byte permutation of it, so
  * any byte range [offset, offset+size) of the ggml encoding maps to the same
  * set of rows.  Q4_0 rows become [16-byte nibble groups of every block][fp16
- * scales of every block]; the other types keep the ggml block order.
+ * scales of every block]; K-quant and IQ rows become one plane per block
+ * field (codes, high bits, signs, scales, fp16 d).  The plane order of a
+ * K/IQ row depends on the row's address mod 4, so resident tensors of those
+ * types must start on a 4-byte boundary (mi355x_malloc gives 256).
  *
  * Scatter `size` bytes of ggml encoding (host memory), which start at byte
  * `offset` of the tensor, into the resident tensor `packed_dev`. */

@@ -1,0 +1,156 @@
+"""K-quant and IQ GEMVs on the GPU vs the CPU oracle (through the C-ABI).
+
+Mirrors tests/test-kquants-gemv.cpp of the reference: accuracy against the
+scalar refs on random blocks (218-270), zero-activation invariance (258-270),
+BF16 activations (272-330); plus the BASELINE K-quant shapes at full size,
+odd superblock counts (rows whose planes flip), K beyond one LDS chunk, and
+the prepack round trip.  IQ3_XXS / IQ2_S run with a synthetic grid installed
+through mi355x_set_iq_grid (their ggml grids are not available here), so
+their parity is against the oracle's restatement only.
+"""
+import numpy as np
+import pytest
+
+import mi355x
+import synth
+from tolerance import check_gemv
+
+pytestmark = pytest.mark.gpu
+
+REF_TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_XS": 23, "IQ3_S": 21}
+GRID_TYPES = {"IQ3_XXS": 18, "IQ2_S": 22}
+ALL = {**REF_TYPES, **GRID_TYPES}
+
+
+def synthetic_grid(t, seed=0):
+    # magnitudes in the range of ggml's grids (odd values up to 62)
+    rng = np.random.default_rng(seed)
+    n, w = (256, 4) if t == 18 else (1024, 8)
+    g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
+    return g.view(np.uint32 if w == 4 else np.uint64).reshape(n)
+
+
+GRIDS = {t: synthetic_grid(t, seed=t) for t in GRID_TYPES.values()}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def install_grids():
+    for t, g in GRIDS.items():
+        mi355x.set_iq_grid(t, g)
+    yield
+
+
+def blocks(t, N, K, seed):
+    # spread d (and dmin) over several binades, per block
+    raw = synth.random_blocks(t, N, K, seed).reshape(N, K // 256, -1)
+    rng = np.random.default_rng(seed + 7)
+    for i, off in enumerate(synth.HALF_FIELDS[t]):
+        h = rng.choice(np.array([0x2E66, 0x3266, 0x2A00, 0x1C00, 0x3800, 0xAE66], dtype=np.uint16),
+                       size=raw.shape[:2])
+        raw[..., off] = (h & 0xFF).astype(np.uint8)
+        raw[..., off + 1] = (h >> 8).astype(np.uint8)
+    return raw.reshape(N, -1)
+
+
+def run(ctx, t, raw, N, K, x):
+    w = ctx.resident(t, raw, N, K)
+    try:
+        return ctx.gemv(w, x)
+    finally:
+        w.free()
+
+
+def parity(ctx, oracle, t, N, K, seed, x=None, what=""):
+    raw = blocks(t, N, K, seed)
+    if x is None:
+        x = np.random.default_rng(seed + 1).uniform(-0.5, 0.5, K).astype(np.float32)
+    y = run(ctx, t, raw, N, K, x)
+    grid = GRIDS.get(t)
+    xr = x if x.dtype != np.uint16 else x
+    ref = oracle.gemv(t, raw, N, K, xr, grid=grid)
+    norms = oracle.row_norms(t, raw, N, K, grid=grid)
+    xf = x if x.dtype != np.uint16 else (x.astype(np.uint32) << 16).view(np.float32)
+    return check_gemv(y, ref, norms, xf, what or f"type {t} {N}x{K}")
+
+
+@pytest.mark.parametrize("name", list(ALL))
+@pytest.mark.parametrize("N,K", [(1, 256), (64, 256), (37, 768), (128, 4096), (96, 5120), (64, 11008)])
+def test_parity_random_blocks(ctx, oracle, name, N, K):
+    parity(ctx, oracle, ALL[name], N, K, seed=N + K)
+
+
+@pytest.mark.parametrize("name", list(ALL))
+def test_parity_two_lds_chunks(ctx, oracle, name):
+    # K = 61 superblocks > one 60-superblock activation chunk
+    parity(ctx, oracle, ALL[name], 40, 61 * 256, seed=5)
+
+
+@pytest.mark.parametrize("name", ["Q3_K", "Q4_K", "Q5_K", "Q6_K"])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_parity_baseline_kquant_shapes(ctx, oracle, name, N, K):
+    # BASELINE config 3 at full size
+    parity(ctx, oracle, REF_TYPES[name], N, K, seed=3)
+
+
+@pytest.mark.parametrize("name", ["IQ2_S", "IQ3_S", "IQ3_XXS", "IQ4_XS"])
+def test_parity_baseline_iq_shape(ctx, oracle, name):
+    # BASELINE config 4 at full size (8192 x 8192)
+    parity(ctx, oracle, ALL[name], 8192, 8192, seed=4)
+
+
+@pytest.mark.parametrize("name", list(ALL))
+def test_zero_activations_give_exact_zero(ctx, name):
+    t = ALL[name]
+    raw = blocks(t, 64, 1024, 9)
+    y = run(ctx, t, raw, 64, 1024, np.zeros(1024, np.float32))
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("name", list(ALL))
+def test_bf16_activations(ctx, oracle, name):
+    # tests/test-kquants-gemv.cpp:272-330: x = (i % 32) / 32 in BF16
+    K = 512
+    xf = ((np.arange(K) % 32) * 0.03125).astype(np.float32)
+    xb = (xf.view(np.uint32) >> 16).astype(np.uint16)
+    parity(ctx, oracle, ALL[name], 128, K, seed=8, x=xb)
+
+
+@pytest.mark.parametrize("name", list(ALL))
+def test_activation_scales(ctx, oracle, name):
+    t = ALL[name]
+    for i, scale in enumerate((1e-20, 1e-3, 1.0, 1e4, 1e15)):
+        x = (np.random.default_rng(i).standard_normal(2048) * scale).astype(np.float32)
+        parity(ctx, oracle, t, 48, 2048, seed=20 + i, x=x, what=f"{name} scale {scale}")
+
+
+@pytest.mark.parametrize("name", list(ALL))
+def test_prepack_round_trip(ctx, name):
+    t = ALL[name]
+    for N, K in ((5, 768), (8, 2048), (3, 256)):
+        raw = blocks(t, N, K, N * K).reshape(-1)
+        w = ctx.resident(t, raw, N, K, chunk=97)
+        try:
+            assert np.array_equal(w.raw_bytes(), raw)
+            rng = np.random.default_rng(1)
+            for _ in range(10):
+                off = int(rng.integers(0, raw.size))
+                n = int(rng.integers(1, raw.size - off + 1))
+                assert np.array_equal(w.raw_bytes(off, n), raw[off:off + n])
+        finally:
+            w.free()
+
+
+def test_rows_per_wave_option_keeps_results(ctx, oracle):
+    t = REF_TYPES["Q4_K"]
+    for r in (1, 2):
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, r)
+        try:
+            parity(ctx, oracle, t, 300, 2048, seed=r)
+        finally:
+            ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+
+
+def test_grid_types_refuse_without_grid_or_bad_table(ctx):
+    bad = np.zeros(7, dtype=np.uint8)
+    with pytest.raises(mi355x.Mi355xError):
+        mi355x.set_iq_grid(18, bad)

@@ -217,10 +217,12 @@ const ggml_tensor *layout_base(const ggml_tensor *t) { return t->view_src ? t->v
 // Number of K-value rows of a contiguous weight tensor.
 int64_t weight_rows(const ggml_tensor *t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
 
-// Tensors whose resident byte order differs from ggml's (Q4_0 weights).
+// Tensors whose resident byte order differs from ggml's: every weight type
+// the kernels read (Q4_0 code/scale planes, K/IQ field planes).
 bool prepacked(const ggml_tensor *t) {
     const ggml_tensor *b = layout_base(t);
-    return b->type == GGML_TYPE_Q4_0 && t->type == GGML_TYPE_Q4_0 && b->ne[0] % 32 == 0;
+    const int bv = block_values(b->type);
+    return bv != 0 && t->type == b->type && b->ne[0] % bv == 0;
 }
 
 void buf_free(ggml_backend_buffer_t buffer) {
@@ -250,7 +252,7 @@ void upload(mi355x_ctx *x, ggml_tensor *tensor, const void *data, size_t offset,
     if (prepacked(tensor)) {
         const ggml_tensor *b = layout_base(tensor);
         const size_t o = static_cast<size_t>(dst - static_cast<const uint8_t *>(b->data));
-        if (mi355x_prepack_from_host(x, GGML_TYPE_Q4_0, weight_rows(b), b->ne[0], b->data, data, o, size))
+        if (mi355x_prepack_from_host(x, b->type, weight_rows(b), b->ne[0], b->data, data, o, size))
             log_error("set_tensor: prepack");
         return;
     }
@@ -263,7 +265,7 @@ void download(mi355x_ctx *x, const ggml_tensor *tensor, void *data, size_t offse
     if (prepacked(tensor)) {
         const ggml_tensor *b = layout_base(tensor);
         const size_t o = static_cast<size_t>(src - static_cast<const uint8_t *>(b->data));
-        if (mi355x_unpack_to_host(x, GGML_TYPE_Q4_0, weight_rows(b), b->ne[0], b->data, data, o, size))
+        if (mi355x_unpack_to_host(x, b->type, weight_rows(b), b->ne[0], b->data, data, o, size))
             log_error("get_tensor: unpack");
         return;
     }

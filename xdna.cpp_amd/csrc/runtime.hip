@@ -124,6 +124,8 @@ int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
     if (rc) return rc;
     if (N == 0) return MI355X_OK;
     if (!W || !x || !y) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
+    if (type != MI355X_TYPE_Q4_0 && (reinterpret_cast<uintptr_t>(W) & 1) != 0)
+        return set_error(MI355X_EINVAL, std::string(who) + ": W must be a row of a resident tensor (2-byte aligned)");
     if (!mi355x_type_ready(type))
         return set_error(MI355X_EUNSUPPORTED, std::string(who) + ": " + type_name(type) +
                                                   " needs its grid table (mi355x_set_iq_grid)");
@@ -424,6 +426,14 @@ int mi355x_set_iq_grid(int type, const void *table, size_t bytes) {
     return MI355X_OK;
 }
 
+// K/IQ resident rows pick their plane order from the row address mod 4
+// (kq_layout.h), so a resident tensor must start on a 4-byte boundary.
+static int check_resident_base(int type, const void *base, const char *who) {
+    if (type != MI355X_TYPE_Q4_0 && (reinterpret_cast<uintptr_t>(base) & 3) != 0)
+        return set_error(MI355X_EINVAL, std::string(who) + ": resident tensor must start on a 4-byte boundary");
+    return MI355X_OK;
+}
+
 static int check_range(int type, int64_t N, int64_t K, size_t offset, size_t size, const char *who) {
     uint64_t total = 0;
     int rc = check_tensor(type, N, K, &total, who);
@@ -442,14 +452,10 @@ int mi355x_prepack_from_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, vo
     int rc = check_range(type, N, K, offset, size, "mi355x_prepack_from_host");
     if (rc || size == 0) return rc;
     if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_prepack_from_host: null pointer");
+    rc = check_resident_base(type, packed_dev, "mi355x_prepack_from_host");
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
-    if (type != MI355X_TYPE_Q4_0) {  // resident order == ggml order
-        MI355X_HIP(hipMemcpyAsync(static_cast<uint8_t *>(packed_dev) + offset, raw_host, size,
-                                  hipMemcpyHostToDevice, ctx->stream));
-        MI355X_HIP(hipStreamSynchronize(ctx->stream));
-        return MI355X_OK;
-    }
     rc = ensure_staging(ctx, size);
     if (rc) return rc;
     const uint8_t *src = static_cast<const uint8_t *>(raw_host);
@@ -472,6 +478,8 @@ int mi355x_prepack_from_device(mi355x_ctx *ctx, int type, int64_t N, int64_t K, 
     int rc = check_range(type, N, K, offset, size, "mi355x_prepack_from_device");
     if (rc || size == 0) return rc;
     if (!packed_dev || !raw_dev) return set_error(MI355X_EINVAL, "mi355x_prepack_from_device: null pointer");
+    rc = check_resident_base(type, packed_dev, "mi355x_prepack_from_device");
+    if (rc) return rc;
     DeviceGuard dg(ctx->device);
     rc = launch_prepack_scatter(ctx, type, N, K, static_cast<uint8_t *>(packed_dev),
                                 static_cast<const uint8_t *>(raw_dev), offset, size);
@@ -487,14 +495,10 @@ int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, const
     int rc = check_range(type, N, K, offset, size, "mi355x_unpack_to_host");
     if (rc || size == 0) return rc;
     if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_unpack_to_host: null pointer");
+    rc = check_resident_base(type, packed_dev, "mi355x_unpack_to_host");
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
-    if (type != MI355X_TYPE_Q4_0) {
-        MI355X_HIP(hipMemcpyAsync(raw_host, static_cast<const uint8_t *>(packed_dev) + offset, size,
-                                  hipMemcpyDeviceToHost, ctx->stream));
-        MI355X_HIP(hipStreamSynchronize(ctx->stream));
-        return MI355X_OK;
-    }
     rc = ensure_staging(ctx, size);
     if (rc) return rc;
     uint8_t *dst = static_cast<uint8_t *>(raw_host);
