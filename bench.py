@@ -98,6 +98,33 @@ def cpu_baseline(raw, N, K, x, budget_s: float):
                       f"{sec * 1e3:.3f} ms/GEMV; host has {os.cpu_count()} logical CPUs"}
 
 
+KQ_TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+IQ_TYPES = {"IQ2_S": 22, "IQ3_S": 21, "IQ3_XXS": 18, "IQ4_XS": 23}
+
+
+def kquant_sweep(ctx, steps, warmup):
+    """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
+    (rotated) weights.  Inputs are random valid blocks (any encoding is a
+    valid input for a dequant-dot kernel); IQ3_XXS / IQ2_S run with a
+    synthetic grid, as ggml's grids are not part of this build."""
+    rng = np.random.default_rng(0)
+    for t, (n, w) in ((18, (256, 4)), (22, (1024, 8))):
+        g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
+        mi355x.set_iq_grid(t, g.view(np.uint32 if w == 4 else np.uint64).reshape(n))
+    res = {}
+    shapes = [(name, t, N, K) for name, t in KQ_TYPES.items() for (N, K) in ((14336, 4096), (4096, 14336))]
+    shapes += [(name, t, 8192, 8192) for name, t in IQ_TYPES.items()]
+    for name, t, N, K in shapes:
+        raw = synth.random_blocks(t, N, K, seed=7)
+        x = synth.activations(K, seed=43)
+        ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES)
+        gbs = algorithmic_bytes(t, N, K) / (ms * 1e-3) / 1e9
+        res[f"{name} {N}x{K}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        log(f"bench: {name} {N}x{K}: {ms * 1e3:.2f} us, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +135,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
+    ap.add_argument("--kquants", action="store_true",
+                    help="also time the K-quant (14336x4096, 4096x14336) and IQ (8192x8192) BASELINE configs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one device-to-device copy of 256 MiB (a plain copy kernel of known size, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -153,6 +182,10 @@ def main() -> int:
                                        "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2}
                 log(f"bench: Q4_0 {n2}x{k2}: {ms2 * 1e3:.2f} us, {gbs2:.1f} GB/s")
 
+        kq = {}
+        if args.kquants:
+            kq = kquant_sweep(ctx, args.steps, args.warmup)
+
     # the timed output must still be the right answer (checked, not measured)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle
@@ -191,6 +224,8 @@ def main() -> int:
     }
     if sweep:
         out["sweep"] = sweep
+    if kq:
+        out["kquants"] = kq
     if not args.no_cpu:
         log(f"bench: CPU baseline for ~{args.cpu_seconds:.0f} s")
         out["cpu_baseline"] = cpu_baseline(raw, N, K, x, args.cpu_seconds)

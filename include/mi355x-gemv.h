@@ -78,11 +78,13 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
                                       size_t pci_len);
 
 /* Per-context options.
- *   MI355X_OPT_VARIANT: which kernel family computes Q4_0 GEMVs --
- *     MI355X_VARIANT_AUTO (default: digit planes where they apply),
- *     MI355X_VARIANT_EXACT_F32 (nibbles -> f32, fp32 FMA; activations used
- *       exactly as given), MI355X_VARIANT_DIGITS (activations as 20-bit
- *       fixed point per 32-value block, integer dot8 products).
+ *   MI355X_OPT_VARIANT: which kernel family computes GEMVs --
+ *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply,
+ *       for the K/IQ types f32 activations),
+ *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
+ *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
+ *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
+ *       for the K/IQ types with int8 dot4 products).
  *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step.
  *   MI355X_OPT_WAVES_PER_GROUP: 0 (auto), 8 or 16 wavefronts per workgroup
  *     (digit-plane Q4_0 kernel).

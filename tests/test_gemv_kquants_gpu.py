@@ -40,6 +40,17 @@ def install_grids():
     yield
 
 
+@pytest.fixture(params=["digits", "exact_f32"], autouse=True)
+def variant(request, ctx):
+    """Every test runs on both kernel families: activations as 22-bit digit
+    planes with integer dot products, and f32 activations as given (the
+    default for these types)."""
+    v = mi355x.VARIANT_DIGITS if request.param == "digits" else mi355x.VARIANT_EXACT_F32
+    ctx.set_option(mi355x.OPT_VARIANT, v)
+    yield request.param
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+
+
 def blocks(t, N, K, seed):
     # spread d (and dmin) over several binades, per block
     raw = synth.random_blocks(t, N, K, seed).reshape(N, K // 256, -1)

@@ -8,17 +8,24 @@
 // f32 rounding, and the sum order differs from the sequential reference only
 // by re-association.
 //
-// Work split: a 512-thread workgroup stages the activations of one K chunk in
-// LDS once, together with their sums over every 8 values, and (IQ types) the
-// codebook.  Each wavefront then owns R rows at a time; its 64 lanes cover
-// 8 superblocks per step, 8 lanes per superblock, one 32-value slice per
-// lane.  A lane reads its slice's codes and its block's scales from the
-// field planes with buffer loads (out-of-range reads return 0), decodes codes
-// to f32 with byte converts, and forms
+// Work split.  A 512-thread workgroup stages the activations of one K chunk
+// in LDS once, with their sums over every 8 values, and (IQ types) the
+// codebook.  Each wavefront owns R rows at a time; its 64 lanes cover 8
+// superblocks per step, 8 lanes per superblock, one 32-value slice per lane,
+// NIT steps per row (NIT = ceil(superblocks / 8), a template parameter).
+// A lane reads its slices' codes and scales from the field planes with
+// buffer loads (out-of-range reads return 0) and forms
 //     sum_i scale_g * (code_i - offset_g) * x_i
 //       = sum_g scale_g * (sum_i code_i * x_i - offset_g * sum_i x_i)
-// so the per-value work is one convert and one FMA; the offsets (Q6_K 32,
-// Q3_K 4, IQ4_XS codebook bias 128, Q4_K/Q5_K mins) use the staged sums.
+// so the per-value work is one byte convert and one FMA; the offsets (Q6_K
+// 32, Q3_K 4, IQ4_XS codebook bias 128, Q4_K/Q5_K mins) use the staged sums.
+//
+// Latency.  Every load a row group needs (R rows x NIT steps) is issued at
+// once, before any of it is used, so each wavefront keeps R * row_bytes in
+// flight.  In the prologue the activation loads are issued first, then the
+// first group's weight loads, and only then are the activations written to
+// LDS: loads retire in order, so the LDS writes wait for the activations
+// alone while the weight stream is already under way.
 #include "device_common.h"
 #include "internal.h"
 #include "iq3s_grid.h"
@@ -26,26 +33,35 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 namespace mi355x {
 namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kSlices = 8;                 // lanes per superblock
+constexpr int kSlices = 8;  // lanes per superblock
 constexpr int kBlocksPerStep = 64 / kSlices;
+// LDS strides (floats) of one staged superblock and of its 32 sums.  Lane
+// l works on superblock l % 8 and slice l / 8, so the 8 lanes served by one
+// LDS cycle read 8 different superblocks at the same offset; the 4-float
+// pad puts those 8 reads on 8 different bank groups for every slice shape.
+constexpr int kXStride = 256 + 4;
+constexpr int kSumStride = 32 + 1;
 // Superblocks of x staged per pass: 60 (15360 values) keeps the LDS of a
 // workgroup under 80 KB with the largest codebook, so two fit on a CU.
 constexpr int kChunkBlocks = 60;
+// Staging items (8 values each) per thread: 60 * 32 / 512 rounded up.
+constexpr int kStageItems = (kChunkBlocks * 32 + kThreads - 1) / kThreads;
 
 struct KqArgs {
     const uint8_t *W;
     int64_t N;
     int64_t row_bytes;
-    int B;       // superblocks per row
-    int b0;      // first superblock of this chunk
-    int nb;      // superblocks in this chunk
-    const void *x;
+    int B;   // superblocks per row
+    int b0;  // first superblock of this chunk
+    int nb;  // superblocks in this chunk
+    const float *x;
     float *y;
     int accumulate;
     const uint32_t *grid;  // device codebook (IQ3_XXS, IQ2_S), else null
@@ -89,8 +105,7 @@ __device__ __forceinline__ uint32_t ld8(const Row &r, uint32_t off) {
 
 __device__ __forceinline__ float half_f(uint32_t bits) { return half_bits_to_float(static_cast<uint16_t>(bits)); }
 
-// The activation slice of lane slice s of one superblock: 32 values in
-// xv[0..31] and the sums of its runs in xs[].
+// The activations of one lane slice: 32 values and the sums of its runs.
 struct XSlice {
     float v[32];
     float s[4];
@@ -135,50 +150,60 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t w0, uint32_t w1, ui
     m = static_cast<float>(j < 4 ? m_lo : m_hi);
 }
 
+__device__ __forceinline__ float k4_finish(int s, const u32x4 &hd, float slo, float shi, const XSlice &x) {
+    const int c = s >> 1;
+    float sc0, m0, sc1, m1;
+    scale_min_k4(2 * c, hd[1], hd[2], hd[3], sc0, m0);
+    scale_min_k4(2 * c + 1, hd[1], hd[2], hd[3], sc1, m1);
+    const float d = half_f(hd[0] & 0xFFFF), dmin = half_f(hd[0] >> 16);
+    return (d * sc0) * slo - (dmin * m0) * x.s[0] + (d * sc1) * shi - (dmin * m1) * x.s[1];
+}
+
 template <>
 struct Kq<MI355X_TYPE_Q4_K> {
     static constexpr int kGrid = 0;
+    struct Regs {
+        u32x4 q, hd;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k4(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *) {
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int c = s >> 1, h = s & 1;
-        const u32x4 q = ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h);
-        const u32x4 hd = ld128(r, r.P[1] + 16 * b);
-        float sc0, m0, sc1, m1;
-        scale_min_k4(2 * c, hd[1], hd[2], hd[3], sc0, m0);
-        scale_min_k4(2 * c + 1, hd[1], hd[2], hd[3], sc1, m1);
-        const float d = half_f(hd[0] & 0xFFFF), dmin = half_f(hd[0] >> 16);
+        return {ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h), ld128(r, r.P[1] + 16 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            slo = dot4(q[i] & 0x0F0F0F0Fu, &x.v[4 * i], slo);
-            shi = dot4((q[i] >> 4) & 0x0F0F0F0Fu, &x.v[16 + 4 * i], shi);
+            slo = dot4(g.q[i] & 0x0F0F0F0Fu, &x.v[4 * i], slo);
+            shi = dot4((g.q[i] >> 4) & 0x0F0F0F0Fu, &x.v[16 + 4 * i], shi);
         }
-        return (d * sc0) * slo - (dmin * m0) * x.s[0] + (d * sc1) * shi - (dmin * m1) * x.s[1];
+        return k4_finish(s, g.hd, slo, shi, x);
     }
 };
 
 template <>
 struct Kq<MI355X_TYPE_Q5_K> {
     static constexpr int kGrid = 0;
+    struct Regs {
+        u32x4 q, qh, hd;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k4(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *) {
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int c = s >> 1, h = s & 1;
-        const u32x4 q = ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h);
-        const u32x4 qh = ld128(r, r.P[1] + 32 * b + 16 * h);
-        const u32x4 hd = ld128(r, r.P[2] + 16 * b);
-        float sc0, m0, sc1, m1;
-        scale_min_k4(2 * c, hd[1], hd[2], hd[3], sc0, m0);
-        scale_min_k4(2 * c + 1, hd[1], hd[2], hd[3], sc1, m1);
-        const float d = half_f(hd[0] & 0xFFFF), dmin = half_f(hd[0] >> 16);
+        return {ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h), ld128(r, r.P[1] + 32 * b + 16 * h),
+                ld128(r, r.P[2] + 16 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
+        const int c = s >> 1;
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c)) & 0x01010101u) << 4);
-            const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            const uint32_t lo = (g.q[i] & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c)) & 0x01010101u) << 4);
+            const uint32_t hi = ((g.q[i] >> 4) & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
             slo = dot4(lo, &x.v[4 * i], slo);
             shi = dot4(hi, &x.v[16 + 4 * i], shi);
         }
-        return (d * sc0) * slo - (dmin * m0) * x.s[0] + (d * sc1) * shi - (dmin * m1) * x.s[1];
+        return k4_finish(s, g.hd, slo, shi, x);
     }
 };
 
@@ -209,18 +234,23 @@ __device__ __forceinline__ void x_slice_k6(int s, const float *xb, const float *
 template <>
 struct Kq<MI355X_TYPE_Q6_K> {
     static constexpr int kGrid = 0;
+    struct Regs {
+        u32x2 qa, qb, qh, sw;
+        uint32_t d;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *) {
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int hh = s >> 2, k = s & 3;
-        const u32x2 qa = ld64(r, r.P[0] + 128 * b + 64 * hh + 8 * k);
-        const u32x2 qb = ld64(r, r.P[0] + 128 * b + 64 * hh + 32 + 8 * k);
-        const u32x2 qh = ld64(r, r.P[1] + 64 * b + 32 * hh + 8 * k);
-        const u32x2 sw = ld64(r, r.P[2] + 16 * b + 8 * hh);
-        const float d = half_f(ld16(r, r.P[3] + 2 * b));
+        return {ld64(r, r.P[0] + 128 * b + 64 * hh + 8 * k), ld64(r, r.P[0] + 128 * b + 64 * hh + 32 + 8 * k),
+                ld64(r, r.P[1] + 64 * b + 32 * hh + 8 * k), ld64(r, r.P[2] + 16 * b + 8 * hh),
+                ld16(r, r.P[3] + 2 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
+        const int k = s & 3;
         float sg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-            const uint32_t A = qa[w], Bq = qb[w], H = qh[w];
+            const uint32_t A = g.qa[w], Bq = g.qb[w], H = g.qh[w];
             sg[0] = dot4((A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u), &x.v[0 + 4 * w], sg[0]);
             sg[1] = dot4((Bq & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u), &x.v[8 + 4 * w], sg[1]);
             sg[2] = dot4(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), &x.v[16 + 4 * w], sg[2]);
@@ -230,12 +260,12 @@ struct Kq<MI355X_TYPE_Q6_K> {
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t word = j < 2 ? sw[0] : sw[1];
+            const uint32_t word = j < 2 ? g.sw[0] : g.sw[1];
             const int idx = 2 * (j & 1) + kk;
             const float sc = static_cast<float>(static_cast<int32_t>(word << (24 - 8 * idx)) >> 24);
             acc = fmaf(sc, sg[j] - 32.0f * x.s[j], acc);
         }
-        return d * acc;
+        return half_f(g.d) * acc;
     }
 };
 
@@ -245,20 +275,25 @@ struct Kq<MI355X_TYPE_Q6_K> {
 template <>
 struct Kq<MI355X_TYPE_Q3_K> {
     static constexpr int kGrid = 0;
+    struct Regs {
+        u32x2 q, hm, sw01;
+        uint32_t sw2, d;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *) {
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int hh = s >> 2, k = s & 3;
-        const u32x2 q = ld64(r, r.P[0] + 64 * b + 32 * hh + 8 * k);
-        const u32x2 hm = ld64(r, r.P[1] + 32 * b + 8 * k);
-        const u32x2 sw01 = ld64(r, r.P[2] + 12 * b);
-        const uint32_t sw2 = ld32(r, r.P[2] + 12 * b + 8);
-        const float d = half_f(ld16(r, r.P[3] + 2 * b));
+        return {ld64(r, r.P[0] + 64 * b + 32 * hh + 8 * k), ld64(r, r.P[1] + 32 * b + 8 * k),
+                ld64(r, r.P[2] + 12 * b), ld32(r, r.P[2] + 12 * b + 8), ld16(r, r.P[3] + 2 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
+        const int hh = s >> 2, k = s & 3;
         float sg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t code = ((q[w] >> (2 * j)) & 0x03030303u) | (((hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
+                const uint32_t code =
+                    ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
                 sg[j] = dot4(code, &x.v[8 * j + 4 * w], sg[j]);
             }
         }
@@ -270,13 +305,13 @@ struct Kq<MI355X_TYPE_Q3_K> {
             // (nibble sidx / 8 = hh), high 2 bits from byte 8 + sidx % 4
             // (bit pair sidx / 4 = 2hh + j/2)
             const int lo_byte = 2 * j + kk;
-            const uint32_t lo_w = lo_byte < 4 ? sw01[0] : sw01[1];
+            const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
             const uint32_t lo = (byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u;
-            const uint32_t hi = (byte_u(sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
+            const uint32_t hi = (byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
             const float sc = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
             acc = fmaf(sc, sg[j] - 4.0f * x.s[j], acc);
         }
-        return d * acc;
+        return half_f(g.d) * acc;
     }
 };
 
@@ -304,6 +339,10 @@ struct Kq<MI355X_TYPE_IQ4_XS> {
     static constexpr int kGrid = 0;
     // kvalues_iq4nl + 128: {1, 24, 45, 63, 79, 93, 106, 118, 129, 141, 153, 166, 181, 197, 217, 241}
     static constexpr uint32_t kT0 = 0x3F2D1801u, kT1 = 0x766A5D4Fu, kT2 = 0xA6998D81u, kT3 = 0xF1D9C5B5u;
+    struct Regs {
+        u32x4 q;
+        u32x2 hd;
+    };
     __device__ static uint32_t lookup(uint32_t n) {
         const uint32_t sel = n & 0x07070707u;
         const uint32_t lo = __builtin_amdgcn_perm(kT1, kT0, sel);
@@ -313,17 +352,18 @@ struct Kq<MI355X_TYPE_IQ4_XS> {
         return (hi & mask) | (lo & ~mask);
     }
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *) {
-        const u32x4 q = ld128(r, r.P[0] + 128 * b + 16 * s);
-        const u32x2 hd = ld64(r, r.P[1] + 8 * b);
-        const float d = half_f(hd[0] & 0xFFFF);
-        const uint32_t sh = hd[0] >> 16;
-        const uint32_t ls = ((hd[1] >> (4 * s)) & 15u) | (((sh >> (2 * s)) & 3u) << 4);
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
+        return {ld128(r, r.P[0] + 128 * b + 16 * s), ld64(r, r.P[1] + 8 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
+        const float d = half_f(g.hd[0] & 0xFFFF);
+        const uint32_t sh = g.hd[0] >> 16;
+        const uint32_t ls = ((g.hd[1] >> (4 * s)) & 15u) | (((sh >> (2 * s)) & 3u) << 4);
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            acc = dot4(lookup(q[i] & 0x0F0F0F0Fu), &x.v[4 * i], acc);
-            acc = dot4(lookup((q[i] >> 4) & 0x0F0F0F0Fu), &x.v[16 + 4 * i], acc);
+            acc = dot4(lookup(g.q[i] & 0x0F0F0F0Fu), &x.v[4 * i], acc);
+            acc = dot4(lookup((g.q[i] >> 4) & 0x0F0F0F0Fu), &x.v[16 + 4 * i], acc);
         }
         return (d * static_cast<float>(static_cast<int>(ls) - 32)) * (acc - 128.0f * x.s[0]);
     }
@@ -341,21 +381,24 @@ __device__ __forceinline__ float signed_x(float x, uint32_t signs, int bit) {
 template <>
 struct Kq<MI355X_TYPE_IQ3_S> {
     static constexpr int kGrid = kIq3sGridSize;  // u32 words
+    struct Regs {
+        u32x2 qs;
+        uint32_t sg, qh, scb, d;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *grid) {
-        const u32x2 qs = ld64(r, r.P[0] + 64 * b + 8 * s);
-        const uint32_t sg = ld32(r, r.P[1] + 32 * b + 4 * s);
-        const uint32_t qh = ld8(r, r.P[2] + 8 * b + s);
-        const uint32_t scb = ld8(r, r.P[3] + 4 * b + (s >> 1));
-        const float d = half_f(ld16(r, r.P[4] + 2 * b));
-        const float db = d * (1.0f + 2.0f * static_cast<float>((scb >> (4 * (s & 1))) & 15u));
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
+        return {ld64(r, r.P[0] + 64 * b + 8 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld8(r, r.P[2] + 8 * b + s),
+                ld8(r, r.P[3] + 4 * b + (s >> 1)), ld16(r, r.P[4] + 2 * b)};
+    }
+    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *grid) {
+        const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t idx = byte_u(qs[k >> 2], k & 3) | (((qh >> k) & 1u) << 8);
+            const uint32_t idx = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
             const uint32_t gv = grid[idx];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = fmaf(byte_f(gv, j), signed_x(x.v[4 * k + j], sg, 4 * k + j), acc);
+            for (int j = 0; j < 4; ++j) acc = fmaf(byte_f(gv, j), signed_x(x.v[4 * k + j], g.sg, 4 * k + j), acc);
         }
         return db * acc;
     }
@@ -369,19 +412,23 @@ __device__ __forceinline__ uint32_t ksigns(uint32_t i7) { return i7 | ((__builti
 template <>
 struct Kq<MI355X_TYPE_IQ3_XXS> {
     static constexpr int kGrid = 256;
+    struct Regs {
+        u32x2 qs;
+        uint32_t aux, d;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *grid) {
-        const u32x2 qs = ld64(r, r.P[0] + 64 * b + 8 * s);
-        const uint32_t aux = ld32(r, r.P[1] + 32 * b + 4 * s);
-        const float d = half_f(ld16(r, r.P[2] + 2 * b));
-        const float db = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
+        return {ld64(r, r.P[0] + 64 * b + 8 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld16(r, r.P[2] + 2 * b)};
+    }
+    __device__ static float compute(const Regs &g, int, const XSlice &x, const uint32_t *grid) {
+        const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
         float acc = 0.f;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t sg = ksigns((aux >> (7 * l)) & 127u);
+            const uint32_t sg = ksigns((g.aux >> (7 * l)) & 127u);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint32_t gv = grid[byte_u(qs[l >> 1], 2 * (l & 1) + h)];
+                const uint32_t gv = grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + h)];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc = fmaf(byte_f(gv, j), signed_x(x.v[8 * l + 4 * h + j], sg, 4 * h + j), acc);
@@ -396,124 +443,573 @@ struct Kq<MI355X_TYPE_IQ3_XXS> {
 template <>
 struct Kq<MI355X_TYPE_IQ2_S> {
     static constexpr int kGrid = 2048;  // 1024 x u64 as u32 pairs
+    struct Regs {
+        uint32_t qs, sg, qh, scb, d;
+    };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
-    __device__ static float dot(const Row &r, uint32_t b, int s, const XSlice &x, const uint32_t *grid) {
-        const uint32_t qs = ld32(r, r.P[0] + 32 * b + 4 * s);
-        const uint32_t sg = ld32(r, r.P[1] + 32 * b + 4 * s);
-        const uint32_t qh = ld8(r, r.P[2] + 8 * b + s);
-        const uint32_t scb = ld8(r, r.P[3] + 8 * b + s);
-        const float d = half_f(ld16(r, r.P[4] + 2 * b));
+    __device__ static Regs load(const Row &r, uint32_t b, int s) {
+        return {ld32(r, r.P[0] + 32 * b + 4 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld8(r, r.P[2] + 8 * b + s),
+                ld8(r, r.P[3] + 8 * b + s), ld16(r, r.P[4] + 2 * b)};
+    }
+    __device__ static float compute(const Regs &g, int, const XSlice &x, const uint32_t *grid) {
         float part[2] = {0.f, 0.f};
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t idx = byte_u(qs, l) | (((qh >> (2 * l)) & 3u) << 8);
+            const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
             const uint32_t g0 = grid[2 * idx], g1 = grid[2 * idx + 1];
-            const uint32_t sb8 = byte_u(sg, l);
+            const uint32_t sb8 = byte_u(g.sg, l);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 part[l >> 1] = fmaf(byte_f(j < 4 ? g0 : g1, j & 3), signed_x(x.v[8 * l + j], sb8, j), part[l >> 1]);
         }
-        const float db0 = d * (0.5f + static_cast<float>(scb & 15u)) * 0.25f;
-        const float db1 = d * (0.5f + static_cast<float>(scb >> 4)) * 0.25f;
+        const float d = half_f(g.d);
+        const float db0 = d * (0.5f + static_cast<float>(g.scb & 15u)) * 0.25f;
+        const float db1 = d * (0.5f + static_cast<float>(g.scb >> 4)) * 0.25f;
         return db0 * part[0] + db1 * part[1];
     }
 };
 
-// ---- kernel ------------------------------------------------------------------
-template <int TYPE, int R, bool XBF16>
-__global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
-    extern __shared__ float4 lds_kq[];
-    float *xs = reinterpret_cast<float *>(lds_kq);       // nb * 256 values
-    float *sums = xs + a.nb * 256;                        // nb * 32 sums of 8
-    uint32_t *grid = reinterpret_cast<uint32_t *>(sums + a.nb * 32);
+// ---- digit path ---------------------------------------------------------------
+// Activations as fixed point: each 32-value block b of x has a power-of-two
+// scale with x = Z * 2^e(b), |Z| < 2^22 (the block's largest |x| maps into
+// [2^21, 2^22)), and Z = z0 + 2^8 z1 + 2^16 z2 in balanced signed bytes.  A
+// staged superblock in LDS (kDgStride bytes) holds three digit planes of 256
+// bytes in value order, e(b) of its 8 blocks, and sum(Z) over every 8 values.
+// Weight codes (small unsigned integers, or signed bytes for the signed
+// codebooks) meet the digits in v_dot4_i32_i8: sum_i code_i * Z_i over a run
+// is s0 + 2^8 s1 + 2^16 s2 with s_p = sum_i code_i * z_p,i, exact in int32.
+// Rounding x to Z changes each product by at most 2^-22 of its block's
+// largest |x|, well inside the GEMV tolerance of 1e-4 * |w_r| * |x|.
+constexpr int kDgPlane = 256;                       // bytes per digit plane
+constexpr int kDgExp = 3 * kDgPlane;                // 8 x int32 exponents
+constexpr int kDgZsum = kDgExp + 32;                // 32 x f32 sums of Z per 8 values
+constexpr int kDgStride = 260 * 4;                  // bytes per superblock (4-word pad mod 32 banks)
+static_assert(kDgZsum + 128 <= kDgStride, "digit superblock layout");
 
-    // stage x[b0*256 .. (b0+nb)*256) and its 8-value sums
-    const int n8 = a.nb * 32;
-    for (int i = threadIdx.x; i < n8; i += kThreads) {
-        float v[8];
-        const int64_t base = static_cast<int64_t>(a.b0) * 256 + 8 * i;
-        if constexpr (XBF16) {
-            const uint16_t *xb = static_cast<const uint16_t *>(a.x) + base;
+struct XDig {
+    uint32_t z[3][8];  // digit planes: 8 dwords (32 values) per plane
+    int e[4];          // exponents of the 32-blocks the slice's runs lie in
+    float zs[4];       // sum of Z over each run
+};
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// s0 + 2^8 s1 + 2^16 s2 in f32
+__device__ __forceinline__ float combine(const int (&s)[3]) {
+    return fmaf(static_cast<float>(s[2]), 65536.0f, fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0])));
+}
+
+// Accumulates code dword `c` (4 values) against dword `i` of the 3 planes.
+__device__ __forceinline__ void dot3(uint32_t c, const XDig &x, int i, int (&s)[3]) {
+    s[0] = sdot4(c, x.z[0][i], s[0]);
+    s[1] = sdot4(c, x.z[1][i], s[1]);
+    s[2] = sdot4(c, x.z[2][i], s[2]);
+}
+
+// Byte mask 0xFF where bit j (j < 4) of `bits` is set.
+__device__ __forceinline__ uint32_t sign_mask4(uint32_t bits) {
+    const uint32_t m1 = ((bits & 15u) * 0x00204081u) & 0x01010101u;  // bit j -> byte j
+    return (m1 << 8) - m1;
+}
+
+// Magnitude bytes g (each <= 127) negated where `mask` is 0xFF; carry-free:
+// (0x80 - g) ^ 0x80 is -g as a signed byte.
+__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t mask) {
+    const uint32_t neg = (0x80808080u - g) ^ 0x80808080u;
+    return (neg & mask) | (g & ~mask);
+}
+
+__device__ __forceinline__ void dg_load_run16(const uint8_t *xb, int off, XDig &x, int slot) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] = bf16_bits_to_float(xb[t]);
-        } else {
-            const float *xf = static_cast<const float *>(a.x) + base;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] = xf[t];
-        }
-        float4 *dst = reinterpret_cast<float4 *>(xs + 8 * i);
-        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
-        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
-        sums[i] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    for (int p = 0; p < 3; ++p) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(xb + kDgPlane * p + off);
+        x.z[p][slot + 0] = v.x;
+        x.z[p][slot + 1] = v.y;
+        x.z[p][slot + 2] = v.z;
+        x.z[p][slot + 3] = v.w;
     }
-    if constexpr (Kq<TYPE>::kGrid > 0) {
+}
+
+__device__ __forceinline__ void dg_load_run8(const uint8_t *xb, int off, XDig &x, int slot) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(xb + kDgPlane * p + off);
+        x.z[p][slot + 0] = v.x;
+        x.z[p][slot + 1] = v.y;
+    }
+}
+
+__device__ __forceinline__ int dg_exp(const uint8_t *xb, int blk32) {
+    return reinterpret_cast<const int *>(xb + kDgExp)[blk32];
+}
+__device__ __forceinline__ float dg_zsum(const uint8_t *xb, int run8) {
+    return reinterpret_cast<const float *>(xb + kDgZsum)[run8];
+}
+
+// Q4_K / Q5_K slice: runs [64c+16h, +16) and [64c+32+16h, +16).
+__device__ __forceinline__ void dg_slice_k4(int s, const uint8_t *xb, XDig &x) {
+    const int c = s >> 1, h = s & 1;
+    const int a = 64 * c + 16 * h, b = a + 32;
+    dg_load_run16(xb, a, x, 0);
+    dg_load_run16(xb, b, x, 4);
+    x.e[0] = dg_exp(xb, 2 * c);
+    x.e[1] = dg_exp(xb, 2 * c + 1);
+    x.zs[0] = dg_zsum(xb, a >> 3) + dg_zsum(xb, (a >> 3) + 1);
+    x.zs[1] = dg_zsum(xb, b >> 3) + dg_zsum(xb, (b >> 3) + 1);
+}
+
+// Q3_K / Q6_K slice: runs [128hh + 32j + 8k, +8), j = 0..3.
+__device__ __forceinline__ void dg_slice_k6(int s, const uint8_t *xb, XDig &x) {
+    const int hh = s >> 2, k = s & 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int off = 128 * hh + 32 * j + 8 * k;
+        dg_load_run8(xb, off, x, 2 * j);
+        x.e[j] = dg_exp(xb, 4 * hh + j);
+        x.zs[j] = dg_zsum(xb, off >> 3);
+    }
+}
+
+// 32-value slice [32s, +32).
+__device__ __forceinline__ void dg_slice_32(int s, const uint8_t *xb, XDig &x) {
+    dg_load_run16(xb, 32 * s, x, 0);
+    dg_load_run16(xb, 32 * s + 16, x, 4);
+    x.e[0] = dg_exp(xb, s);
+}
+
+template <int TYPE>
+struct KqDg;
+
+template <>
+struct KqDg<MI355X_TYPE_Q4_K> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k4(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_Q4_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
+        int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dot3(g.q[i] & 0x0F0F0F0Fu, x, i, sa);
+            dot3((g.q[i] >> 4) & 0x0F0F0F0Fu, x, 4 + i, sb);
+        }
+        const int c = s >> 1;
+        float sc0, m0, sc1, m1;
+        scale_min_k4(2 * c, g.hd[1], g.hd[2], g.hd[3], sc0, m0);
+        scale_min_k4(2 * c + 1, g.hd[1], g.hd[2], g.hd[3], sc1, m1);
+        const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
+        return ldexpf((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
+               ldexpf((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_Q5_K> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k4(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_Q5_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
+        const int c = s >> 1;
+        int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dot3((g.q[i] & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c)) & 0x01010101u) << 4), x, i, sa);
+            dot3(((g.q[i] >> 4) & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c + 1)) & 0x01010101u) << 4), x, 4 + i, sb);
+        }
+        float sc0, m0, sc1, m1;
+        scale_min_k4(2 * c, g.hd[1], g.hd[2], g.hd[3], sc0, m0);
+        scale_min_k4(2 * c + 1, g.hd[1], g.hd[2], g.hd[3], sc1, m1);
+        const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
+        return ldexpf((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
+               ldexpf((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_Q6_K> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k6(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_Q6_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
+        int sg[4][3] = {};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t A = g.qa[w], Bq = g.qb[w], H = g.qh[w];
+            dot3((A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u), x, 0 + w, sg[0]);
+            dot3((Bq & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u), x, 2 + w, sg[1]);
+            dot3(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), x, 4 + w, sg[2]);
+            dot3(((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u), x, 6 + w, sg[3]);
+        }
+        const int kk = (s & 3) >> 1;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t word = j < 2 ? g.sw[0] : g.sw[1];
+            const int idx = 2 * (j & 1) + kk;
+            const float sc = static_cast<float>(static_cast<int32_t>(word << (24 - 8 * idx)) >> 24);
+            acc = fmaf(sc, ldexpf(combine(sg[j]) - 32.0f * x.zs[j], x.e[j]), acc);
+        }
+        return half_f(g.d) * acc;
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_Q3_K> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k6(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
+        const int hh = s >> 2, k = s & 3;
+        int sg[4][3] = {};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t code =
+                    ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
+                dot3(code, x, 2 * j + w, sg[j]);
+            }
+        }
+        const int kk = k >> 1;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int lo_byte = 2 * j + kk;
+            const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
+            const uint32_t lo = (byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u;
+            const uint32_t hi = (byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
+            const float sc = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
+            acc = fmaf(sc, ldexpf(combine(sg[j]) - 4.0f * x.zs[j], x.e[j]), acc);
+        }
+        return half_f(g.d) * acc;
+    }
+};
+
+// IQ4_XS: the codebook as signed bytes, looked up four indices at a time.
+template <>
+struct KqDg<MI355X_TYPE_IQ4_XS> {
+    // kvalues_iq4nl: {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}
+    static constexpr uint32_t kT0 = 0xBFAD9881u, kT1 = 0xF6EADDCFu, kT2 = 0x26190D01u, kT3 = 0x71594535u;
+    __device__ static uint32_t lookup(uint32_t n) {
+        const uint32_t sel = n & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(kT1, kT0, sel);
+        const uint32_t hi = __builtin_amdgcn_perm(kT3, kT2, sel);
+        const uint32_t m1 = (n >> 3) & 0x01010101u;
+        const uint32_t mask = (m1 << 8) - m1;
+        return (hi & mask) | (lo & ~mask);
+    }
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_IQ4_XS>::Regs &g, int s, const XDig &x, const uint32_t *) {
+        int sm[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dot3(lookup(g.q[i] & 0x0F0F0F0Fu), x, i, sm);
+            dot3(lookup((g.q[i] >> 4) & 0x0F0F0F0Fu), x, 4 + i, sm);
+        }
+        const float d = half_f(g.hd[0] & 0xFFFF);
+        const uint32_t sh = g.hd[0] >> 16;
+        const uint32_t ls = ((g.hd[1] >> (4 * s)) & 15u) | (((sh >> (2 * s)) & 3u) << 4);
+        return (d * static_cast<float>(static_cast<int>(ls) - 32)) * ldexpf(combine(sm), x.e[0]);
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_IQ3_S> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_IQ3_S>::Regs &g, int s, const XDig &x,
+                                    const uint32_t *grid) {
+        int sm[3] = {0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t idx = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
+            dot3(apply_signs(grid[idx], sign_mask4(g.sg >> (4 * k))), x, k, sm);
+        }
+        const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
+        return db * ldexpf(combine(sm), x.e[0]);
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_IQ3_XXS> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_IQ3_XXS>::Regs &g, int, const XDig &x,
+                                    const uint32_t *grid) {
+        int sm[3] = {0, 0, 0};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t sg = ksigns((g.aux >> (7 * l)) & 127u);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t gv = grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + h)];
+                dot3(apply_signs(gv, sign_mask4(sg >> (4 * h))), x, 2 * l + h, sm);
+            }
+        }
+        const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
+        return db * ldexpf(combine(sm), x.e[0]);
+    }
+};
+
+template <>
+struct KqDg<MI355X_TYPE_IQ2_S> {
+    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
+    __device__ static float compute(const Kq<MI355X_TYPE_IQ2_S>::Regs &g, int, const XDig &x,
+                                    const uint32_t *grid) {
+        int s0[3] = {0, 0, 0}, s1[3] = {0, 0, 0};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
+            const uint32_t sb8 = byte_u(g.sg, l);
+            const uint32_t g0 = apply_signs(grid[2 * idx], sign_mask4(sb8));
+            const uint32_t g1 = apply_signs(grid[2 * idx + 1], sign_mask4(sb8 >> 4));
+            if (l < 2) {
+                dot3(g0, x, 2 * l, s0);
+                dot3(g1, x, 2 * l + 1, s0);
+            } else {
+                dot3(g0, x, 2 * l, s1);
+                dot3(g1, x, 2 * l + 1, s1);
+            }
+        }
+        const float d = half_f(g.d);
+        const float db0 = d * (0.5f + static_cast<float>(g.scb & 15u)) * 0.25f;
+        const float db1 = d * (0.5f + static_cast<float>(g.scb >> 4)) * 0.25f;
+        return ldexpf(db0 * combine(s0) + db1 * combine(s1), x.e[0]);
+    }
+};
+
+// Digits of one 32-value block (values v[0..31]) into a staged superblock.
+__device__ __forceinline__ void stage_digits(const float (&v)[32], uint8_t *xb, int j) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
+    const int se = min(275 - E, 254);  // biased exponent of s = 2^-e: m * s in [2^21, 2^22)
+    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
+    uint32_t pl[3][8];
+    float zs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t b0 = 0, b1 = 0, b2 = 0;
+        int zsum = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            // round to nearest integer: |v * s| < 2^22, so 1.5 * 2^23 + v * s
+            // lies in [2^23, 2^24) where f32 spacing is 1
+            const int Z = __builtin_bit_cast(int, fmaf(v[4 * w + t], sc, 12582912.0f)) - 0x4B400000;
+            const int z0 = (Z << 24) >> 24;
+            const int Z1 = (Z - z0) >> 8;
+            const int z1 = (Z1 << 24) >> 24;
+            const int z2 = (Z1 - z1) >> 8;
+            b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
+            b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
+            b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
+            zsum += Z;
+        }
+        pl[0][w] = b0;
+        pl[1][w] = b1;
+        pl[2][w] = b2;
+        zs[w >> 1] += static_cast<float>(zsum);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        uint4 *dst = reinterpret_cast<uint4 *>(xb + kDgPlane * p + 32 * j);
+        dst[0] = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
+        dst[1] = make_uint4(pl[p][4], pl[p][5], pl[p][6], pl[p][7]);
+    }
+    reinterpret_cast<int *>(xb + kDgExp)[j] = 127 - se;
+    *reinterpret_cast<float4 *>(xb + kDgZsum + 16 * j) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+}
+
+// ---- kernel ------------------------------------------------------------------
+template <int TYPE, int R>
+__device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows)[R]) {
+    constexpr KqLayout L = kq_layout(TYPE);
+    const uint32_t records = static_cast<uint32_t>(a.row_bytes);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = g * R + r < a.N ? g * R + r : a.N - 1;
+        const uint8_t *base = a.W + row * a.row_bytes;
+        rows[r].rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
+        const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
+#pragma unroll
+        for (int i = 0; i < 5; ++i)
+            rows[r].P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+    }
+}
+
+// Loads of row group g: regs[r][t] for step t (superblock it = 8t + lane/8,
+// clamped into the chunk; lanes past the chunk's end are masked at use).
+template <int TYPE, int R, int NIT>
+__device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, int bl,
+                                           typename Kq<TYPE>::Regs (&regs)[R][NIT]) {
+    Row rows[R];
+    make_rows<TYPE, R>(a, g, rows);
+#pragma unroll
+    for (int t = 0; t < NIT; ++t) {
+        const int bloc = kBlocksPerStep * t + bl;
+        const int bc = bloc < a.nb ? bloc : a.nb - 1;
+        const uint32_t babs = static_cast<uint32_t>(a.b0 + bc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) regs[r][t] = Kq<TYPE>::load(rows[r], babs, s);
+    }
+}
+
+static_assert(kChunkBlocks * 8 <= kThreads, "one 32-value block per thread when staging digits");
+
+template <int TYPE, int R, int NIT, bool DG>
+__global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
+    using K = Kq<TYPE>;
+    extern __shared__ float4 lds_kq[];
+    // f32 path: nb * kXStride values, then nb * kSumStride sums of 8;
+    // digit path: nb * kDgStride bytes; then the codebook
+    uint8_t *lds = reinterpret_cast<uint8_t *>(lds_kq);
+    float *xs = reinterpret_cast<float *>(lds_kq);
+    float *sums = xs + a.nb * kXStride;
+    uint32_t *grid = DG ? reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride)
+                        : reinterpret_cast<uint32_t *>(sums + a.nb * kSumStride);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int s = lane / kBlocksPerStep;
+    const int bl = lane % kBlocksPerStep;
+    const int64_t n_groups = (a.N + R - 1) / R;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+    int64_t g = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+
+    // 1. activation loads for staging (clamped index): the f32 path takes
+    // kStageItems runs of 8 values per thread, the digit path one 32-value
+    // block per thread
+    const int n8 = a.nb * 32;
+    const int n32 = a.nb * 8;
+    constexpr int kXv = DG ? 4 : kStageItems;
+    float4 xv[kXv][2];
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+        const float *src;
+        if constexpr (DG) {
+            const int t = threadIdx.x < n32 ? static_cast<int>(threadIdx.x) : n32 - 1;
+            src = a.x + static_cast<int64_t>(a.b0) * 256 + 32 * t + 8 * j;
+        } else {
+            const int i = threadIdx.x + kThreads * j;
+            const int ic = i < n8 ? i : n8 - 1;
+            src = a.x + static_cast<int64_t>(a.b0) * 256 + 8 * ic;
+        }
+        xv[j][0] = reinterpret_cast<const float4 *>(src)[0];
+        xv[j][1] = reinterpret_cast<const float4 *>(src)[1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. weight loads of the first row group (clamped; results unused past N)
+    typename K::Regs regs[R][NIT];
+    load_group<TYPE, R, NIT>(a, g < n_groups ? g : n_groups - 1, s, bl, regs);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. activations into LDS (f32 with 8-value sums, or digit planes); codebook
+    if constexpr (DG) {
+        if (static_cast<int>(threadIdx.x) < n32) {
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * j + 0] = xv[j][0].x;
+                v[8 * j + 1] = xv[j][0].y;
+                v[8 * j + 2] = xv[j][0].z;
+                v[8 * j + 3] = xv[j][0].w;
+                v[8 * j + 4] = xv[j][1].x;
+                v[8 * j + 5] = xv[j][1].y;
+                v[8 * j + 6] = xv[j][1].z;
+                v[8 * j + 7] = xv[j][1].w;
+            }
+            stage_digits(v, lds + kDgStride * (threadIdx.x >> 3), threadIdx.x & 7);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kStageItems; ++j) {
+            const int i = threadIdx.x + kThreads * j;
+            if (i < n8) {
+                float4 *dst = reinterpret_cast<float4 *>(xs + kXStride * (i >> 5) + 8 * (i & 31));
+                dst[0] = xv[j][0];
+                dst[1] = xv[j][1];
+                const float4 p = xv[j][0], q = xv[j][1];
+                sums[kSumStride * (i >> 5) + (i & 31)] = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
+            }
+        }
+    }
+    if constexpr (K::kGrid > 0) {
         const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
-        for (int i = threadIdx.x; i < Kq<TYPE>::kGrid; i += kThreads) grid[i] = src[i];
+        for (int i = threadIdx.x; i < K::kGrid; i += kThreads) grid[i] = src[i];
     }
     __syncthreads();
 
-    constexpr KqLayout L = kq_layout(TYPE);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int s = lane & (kSlices - 1);
-    const int bl = lane / kSlices;
-    const int64_t n_groups = (a.N + R - 1) / R;
-    const uint32_t records = static_cast<uint32_t>(a.row_bytes);
-
-    for (int64_t g = static_cast<int64_t>(blockIdx.x) * kWaves + wave; g < n_groups;
-         g += static_cast<int64_t>(gridDim.x) * kWaves) {
-        Row rows[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t row = g * R + r < a.N ? g * R + r : a.N - 1;
-            const uint8_t *base = a.W + row * a.row_bytes;
-            rows[r].rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
-            const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
-#pragma unroll
-            for (int i = 0; i < 5; ++i)
-                rows[r].P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
-        }
+    // 4. row groups
+    for (; g < n_groups; g += stride) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.f;
-        for (int it = 0; it < a.nb; it += kBlocksPerStep) {
-            const int bloc = it + bl;
+#pragma unroll
+        for (int t = 0; t < NIT; ++t) {
+            const int bloc = kBlocksPerStep * t + bl;
             const bool valid = bloc < a.nb;
             const int bc = valid ? bloc : a.nb - 1;
-            XSlice x;
-            Kq<TYPE>::x_slice(s, xs + 256 * bc, sums + 32 * bc, x);
-            const uint32_t babs = static_cast<uint32_t>(a.b0 + bc);
+            if constexpr (DG) {
+                XDig x;
+                KqDg<TYPE>::x_slice(s, lds + kDgStride * bc, x);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float p = Kq<TYPE>::dot(rows[r], babs, s, x, grid);
-                acc[r] += valid ? p : 0.f;
+                for (int r = 0; r < R; ++r) {
+                    const float p = KqDg<TYPE>::compute(regs[r][t], s, x, grid);
+                    acc[r] += valid ? p : 0.f;
+                }
+            } else {
+                XSlice x;
+                K::x_slice(s, xs + kXStride * bc, sums + kSumStride * bc, x);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float p = K::compute(regs[r][t], s, x, grid);
+                    acc[r] += valid ? p : 0.f;
+                }
             }
+            // one step's activations live at a time (no hoisting of the
+            // next step's LDS reads into this one)
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float t = wave_sum(acc[r]);
+            const float tot = wave_sum(acc[r]);
             const int64_t row = g * R + r;
-            if (lane == 0 && row < a.N) a.y[row] = a.accumulate ? a.y[row] + t : t;
+            if (lane == 0 && row < a.N) a.y[row] = a.accumulate ? a.y[row] + tot : tot;
         }
+        const int64_t gn = g + stride;
+        if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
+    }
+}
+
+typedef void (*kq_kernel_fn)(KqArgs);
+
+// R = 2 rows per wavefront only for short rows (NIT <= 2), where both rows'
+// loads and decode stay within ~128 VGPRs.
+constexpr int kMaxNitR2 = 2;
+
+template <int TYPE, bool DG>
+kq_kernel_fn pick_dg(int R, int nit) {
+    if (R == 2 && nit <= kMaxNitR2) return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG> : gemv_kq_kernel<TYPE, 2, 2, DG>;
+    switch (nit) {
+    case 1: return gemv_kq_kernel<TYPE, 1, 1, DG>;
+    case 2: return gemv_kq_kernel<TYPE, 1, 2, DG>;
+    case 3: return gemv_kq_kernel<TYPE, 1, 3, DG>;
+    case 4: return gemv_kq_kernel<TYPE, 1, 4, DG>;
+    case 5: return gemv_kq_kernel<TYPE, 1, 5, DG>;
+    case 6: return gemv_kq_kernel<TYPE, 1, 6, DG>;
+    case 7: return gemv_kq_kernel<TYPE, 1, 7, DG>;
+    default: return gemv_kq_kernel<TYPE, 1, 8, DG>;
     }
 }
 
 template <int TYPE>
-const void *pick(int R, bool bf16) {
-    if (R == 2) return bf16 ? (const void *)gemv_kq_kernel<TYPE, 2, true> : (const void *)gemv_kq_kernel<TYPE, 2, false>;
-    return bf16 ? (const void *)gemv_kq_kernel<TYPE, 1, true> : (const void *)gemv_kq_kernel<TYPE, 1, false>;
+kq_kernel_fn pick(int R, int nit, bool dg) {
+    return dg ? pick_dg<TYPE, true>(R, nit) : pick_dg<TYPE, false>(R, nit);
 }
 
-const void *pick_kernel(int type, int R, bool bf16) {
+kq_kernel_fn pick_kernel(int type, int R, int nit, bool dg) {
     switch (type) {
-    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, bf16);
-    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, bf16);
-    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, bf16);
-    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, bf16);
-    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, bf16);
-    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, bf16);
-    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, bf16);
-    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, bf16);
+    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, nit, dg);
+    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, nit, dg);
+    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, nit, dg);
+    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, nit, dg);
+    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, nit, dg);
+    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, nit, dg);
+    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, nit, dg);
+    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, nit, dg);
     default: return nullptr;
     }
 }
@@ -525,6 +1021,13 @@ int grid_words(int type) {
     case MI355X_TYPE_IQ2_S: return 2048;
     default: return 0;
     }
+}
+
+// BF16 activations widened to f32 (exact) ahead of the GEMV.
+__global__ void bf16_to_f32_kernel(const uint16_t *__restrict__ in, float *__restrict__ out, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = bf16_bits_to_float(in[i]);
 }
 
 }  // namespace
@@ -543,25 +1046,61 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
     if (a.type == MI355X_TYPE_IQ2_S) grid = static_cast<const uint32_t *>(ctx->iq2s_grid);
     if (grid_words(a.type) > 0 && a.type != MI355X_TYPE_IQ3_S && !grid)
         return set_error(MI355X_EUNSUPPORTED, "grid table not installed for this IQ type");
-    int R = a.N >= 8192 ? 2 : 1;
-    if (ctx->rows_override == 1 || ctx->rows_override == 2) R = ctx->rows_override;
-    const void *k = pick_kernel(a.type, R, a.x_bf16);
-    const int64_t n_groups = (a.N + R - 1) / R;
+
+    // activations as 16-byte aligned f32 (bf16 and unaligned inputs go
+    // through the context's activation buffer; the context lock keeps the
+    // buffer in place from the conversion to the last launch that reads it)
+    const float *x = static_cast<const float *>(a.x);
+    std::unique_lock<std::mutex> lk(ctx->mu, std::defer_lock);
+    if (a.x_bf16 || (reinterpret_cast<uintptr_t>(a.x) & 15) != 0) {
+        lk.lock();
+        const size_t need = static_cast<size_t>(a.K) * sizeof(float);
+        if (ctx->xconv_bytes < need) {
+            MI355X_HIP(hipStreamSynchronize(ctx->stream));
+            if (ctx->xconv) MI355X_HIP(hipFree(ctx->xconv));
+            ctx->xconv = nullptr;
+            ctx->xconv_bytes = 0;
+            MI355X_HIP(hipMalloc(&ctx->xconv, need));
+            ctx->xconv_bytes = need;
+        }
+        float *dst = static_cast<float *>(ctx->xconv);
+        if (a.x_bf16) {
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((a.K + 255) / 256, 1024));
+            hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
+                               static_cast<const uint16_t *>(a.x), dst, a.K);
+            MI355X_HIP(hipGetLastError());
+        } else {
+            MI355X_HIP(hipMemcpyAsync(dst, a.x, need, hipMemcpyDeviceToDevice, ctx->stream));
+        }
+        x = dst;
+    }
+
+    // f32 activations unless the caller asks for the digit path: with the
+    // activations re-staged by every workgroup, the digit path's cheaper
+    // dot products do not yet pay for its costlier staging
+    const bool dg = ctx->kernel_variant == MI355X_VARIANT_DIGITS;
+
     // equal chunks of at most kChunkBlocks superblocks
     const int64_t n_chunks = (B + kChunkBlocks - 1) / kChunkBlocks;
     const int64_t per_chunk = (B + n_chunks - 1) / n_chunks;
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
-        const size_t lds = static_cast<size_t>(nb) * (256 + 32) * sizeof(float) + grid_words(a.type) * 4u;
+        const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
+        int R = a.N >= 8192 && nit <= kMaxNitR2 ? 2 : 1;
+        if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= kMaxNitR2)) R = ctx->rows_override;
+        const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
+        const int64_t n_groups = (a.N + R - 1) / R;
+        const size_t per_block = dg ? kDgStride : (kXStride + kSumStride) * sizeof(float);
+        const size_t lds = static_cast<size_t>(nb) * per_block + grid_words(a.type) * 4u;
         if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
-        const int occ = occupancy(k, kThreads, lds);
+        const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
         int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
         if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);
-        KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, a.x, a.y, b0 > 0 ? 1 : 0,
+        KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, x, a.y, b0 > 0 ? 1 : 0,
                     grid};
-        void *params[] = {&args};
-        MI355X_HIP(hipLaunchKernel(k, dim3(static_cast<unsigned>(std::max<int64_t>(wgs, 1))), dim3(kThreads), params,
-                                   lds, ctx->stream));
+        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(wgs, 1))), dim3(kThreads), lds,
+                           ctx->stream, args);
+        MI355X_HIP(hipGetLastError());
     }
     return MI355X_OK;
 }

@@ -18,6 +18,10 @@ struct mi355x_ctx {
     // device staging for raw weight bytes on their way into a resident tensor
     void *staging = nullptr;
     size_t staging_bytes = 0;
+    // f32 activations for the K/IQ kernels when the caller's are BF16 or not
+    // 16-byte aligned (grown on demand, freed with the context)
+    void *xconv = nullptr;
+    size_t xconv_bytes = 0;
     // per-context copies of the IQ grids (device), valid when non-null
     void *iq3xxs_grid = nullptr;
     void *iq2s_grid = nullptr;

@@ -240,6 +240,7 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     DeviceGuard dg(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->xconv) (void)hipFree(ctx->xconv);
     if (ctx->iq3xxs_grid) (void)hipFree(ctx->iq3xxs_grid);
     if (ctx->iq2s_grid) (void)hipFree(ctx->iq2s_grid);
     (void)hipStreamDestroy(ctx->stream);
