@@ -33,6 +33,9 @@ import synth  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 METRIC = "Q4_0 GEMV HBM GB/s (% of roofline) at 8192x8192; decode tok/s, 3B shape"
 ROTATE_BYTES = 1 << 30
+# The reference's published Q4_0 8192x8192 GEMV throughput (README.md:98;
+# weight bytes / time on its host CPU).
+REFERENCE_GBS = 40.41
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_0_gemv_8192x8192_traffic.json")
 
 
@@ -207,7 +210,9 @@ def main() -> int:
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": round(gbs / REFERENCE_GBS, 2),
+        "baseline_note": f"value / {REFERENCE_GBS} GB/s, the reference's published Q4_0 8192x8192 GEMV rate "
+                         "(README.md:98, host CPU, weight bytes only)",
         "dtype": "f32",
         "data": "synthetic: f32 N(0,0.02) weights (seed 42) quantized to Q4_0, x ~ N(0,1) (seed 43)",
         "config": {"workload": f"Q4_0 GEMV {N}x{K} (N rows x K), 1 f32 activation row, "
