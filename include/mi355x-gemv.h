@@ -90,15 +90,23 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     (digit-plane Q4_0 kernel).
  *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups.
  *   MI355X_OPT_PREFETCH: 0 (auto), 1 (each wavefront requests its next row
- *     group before reducing the current one), 2 (off). */
+ *     group before reducing the current one), 2 (off).
+ *   MI355X_OPT_FORM: work split of the digit-plane Q4_0 kernel --
+ *     MI355X_FORM_AUTO (default), MI355X_FORM_ROWS (a wavefront owns whole
+ *     rows), MI355X_FORM_KSPLIT (a wavefront owns one 64-block column of 2 or
+ *     4 rows; needs rows of a multiple of 8 blocks). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3
 #define MI355X_OPT_GRID 4
 #define MI355X_OPT_PREFETCH 5
+#define MI355X_OPT_FORM 6
 #define MI355X_VARIANT_AUTO 0
 #define MI355X_VARIANT_EXACT_F32 1
 #define MI355X_VARIANT_DIGITS 2
+#define MI355X_FORM_AUTO 0
+#define MI355X_FORM_ROWS 1
+#define MI355X_FORM_KSPLIT 2
 MI355X_API int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value);
 
 /* ---- memory ----------------------------------------------------------------

@@ -202,3 +202,23 @@ def test_rejects_bad_shapes(ctx):
         assert ctx.gemv_ptr(Q4_0, buf.ptr, 0, 64, buf.ptr, buf.ptr) == mi355x.OK
     finally:
         buf.free()
+
+
+@pytest.mark.parametrize("rows", [2, 4])
+@pytest.mark.parametrize("N,K", [(8192, 8192), (4096, 4096), (17408, 5120), (1000, 2048), (37, 8192), (64, 256),
+                                 (300, 16384)])
+def test_ksplit_form(ctx, oracle, variant, rows, N, K):
+    """The K-split work split (one 64-block column of R rows per wavefront)
+    against the oracle, including partial last columns (K = 5120) and row
+    counts that leave workgroups partly empty."""
+    if variant != "digits":
+        pytest.skip("the K-split form is a digit-plane kernel")
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_KSPLIT)
+    ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, rows)
+    try:
+        raw = synth.random_q4_0(N, K, seed=N + K)
+        x = synth.activations(K, seed=K)
+        parity(ctx, oracle, raw, N, K, x, f"ksplit R{rows} {N}x{K}")
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)

@@ -333,6 +333,121 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q4_0_dp_kernel(
     }
 }
 
+// ---- K-split form -------------------------------------------------------------
+// For long matrices the digit-plane reads, not the weight stream, limit the
+// per-wave form above: every row re-reads the planes of all its blocks from
+// LDS.  Here a wavefront owns one 64-block column (lane = block) of R rows,
+// so one plane read serves R rows, and only R code vectors are live, which
+// keeps 32 wavefronts per CU resident.  A workgroup holds G row groups x
+// NBL columns (G * NBL <= 16 wavefronts); the NBL column partials of a row
+// meet in LDS and are added in column order.  Every load of a workgroup's
+// rows is issued in the prologue, before the activation staging.
+template <int R>
+struct ColumnGroup {
+    u32x4 q[R];
+    uint32_t d[R];  // fp16 bits of this lane's block scale, per row
+
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ W, int row0, int N, int B, int64_t row_bytes,
+                                         int b, int slot) {
+        const uint8_t *base = W + static_cast<int64_t>(row0) * row_bytes;
+        const int64_t left = static_cast<int64_t>(N - row0) * row_bytes;
+        const uint32_t records =
+            left <= 0 ? 0u : static_cast<uint32_t>(left < 0xFFFFFFFFll ? left : 0xFFFFFFFFll);
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
+        const int scale_off = 16 * B;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            d[r] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, 2 * slot, r * static_cast<int>(row_bytes) + scale_off, 0);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * b, r * static_cast<int>(row_bytes), kNonTemporal);
+    }
+};
+
+template <int R, int G, int NBL>
+__global__ __launch_bounds__(64 * G * NBL) void gemv_q4_0_ks_kernel(const uint8_t *__restrict__ W,
+                                                                    const float *__restrict__ x,
+                                                                    float *__restrict__ y, int N, int B,
+                                                                    int64_t row_bytes, int x_al16) {
+    constexpr int WAVES = G * NBL;
+    constexpr int ROWS = G * R;  // rows per workgroup step
+    extern __shared__ uint4 lds_dp[];
+    uint4 *planes = lds_dp;
+    float *ub = reinterpret_cast<float *>(lds_dp + kPlanes * B);
+    float *red = ub + B;  // [G][R][NBL] column partials
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int gi = wave / NBL;  // row group of this wavefront
+    const int c = wave % NBL;   // block column of this wavefront
+    const int n_groups = (N + ROWS - 1) / ROWS;
+
+    // lane's block; past the row end a lane reads the last block and its
+    // scale is masked to 0
+    const int braw = 64 * c + lane;
+    const bool live = braw < B;
+    const int b = live ? braw : B - 1;
+    const int F = B >> 6;  // full 64-block columns (lane-major scale slots)
+    const int slot = b < 64 * F ? (b & 63) * F + (b >> 6) : b;
+    const uint32_t dmask = live ? 0xFFFFu : 0u;
+
+    constexpr int XI = (4 * NBL + WAVES - 1) / WAVES;
+    XTile<XI> xt;
+    xt.load(x, B, x_al16 != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    int g = blockIdx.x;
+    ColumnGroup<R> grp;
+    grp.load(W, g * ROWS + gi * R, N, B, row_bytes, b, slot);
+    xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
+    __syncthreads();
+
+    uint4 P[kPlanes];
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) P[p] = planes[p * B + b];
+    const float u = ub[b];
+
+    while (g < n_groups) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int T = block_dot_digits(grp.q[r], P);
+            const float dr = half_bits_to_float(static_cast<uint16_t>(grp.d[r] & dmask));
+            const float s = wave_sum(dr * u * static_cast<float>(T));
+            if (lane == 0) red[(gi * R + r) * NBL + c] = s;
+        }
+        const int gn = g + gridDim.x;
+        if (gn < n_groups) grp.load(W, gn * ROWS + gi * R, N, B, row_bytes, b, slot);
+        __syncthreads();
+        if (threadIdx.x < ROWS) {
+            const int row = g * ROWS + threadIdx.x;
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NBL; ++j) s += red[threadIdx.x * NBL + j];
+            if (row < N) y[row] = s;
+        }
+        __syncthreads();
+        g = gn;
+    }
+}
+
+typedef void (*ks_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int);
+
+template <int R>
+ks_kernel_t pick_ks_r(int nbl) {
+    switch (nbl) {
+    case 1: return gemv_q4_0_ks_kernel<R, 16, 1>;
+    case 2: return gemv_q4_0_ks_kernel<R, 8, 2>;
+    case 3: return gemv_q4_0_ks_kernel<R, 5, 3>;
+    case 4: return gemv_q4_0_ks_kernel<R, 4, 4>;
+    case 5: return gemv_q4_0_ks_kernel<R, 3, 5>;
+    case 6: return gemv_q4_0_ks_kernel<R, 2, 6>;
+    case 7: return gemv_q4_0_ks_kernel<R, 2, 7>;
+    default: return gemv_q4_0_ks_kernel<R, 2, 8>;
+    }
+}
+
+// row groups (of R rows) per workgroup for a given column count
+constexpr int ks_groups(int nbl) { return nbl <= 1 ? 16 : (nbl == 3 ? 5 : (nbl >= 6 ? 2 : 16 / nbl)); }
+
 typedef void (*dp_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int);
 
 // A16 = false (rows not 16-byte aligned: K % 256 != 0) only in its plain form.
@@ -389,6 +504,29 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
     const int nbl = static_cast<int>((B + 63) / 64);
+    // K-split form: 16-byte aligned rows.  By default (sweeps on MI355X) for
+    // tall matrices with 1 or 3 block columns (151936x2048: 26.9 vs 27.8 us,
+    // 17408x5120: 9.8 vs 10.1 us), with 2 rows per wavefront; the row form
+    // stays ahead at 2 and 4 columns (4096x4096, 8192x8192).
+    const bool ks = a16 && (ctx->form_override == MI355X_FORM_KSPLIT ||
+                            (ctx->form_override == MI355X_FORM_AUTO && (nbl == 1 || nbl == 3) && a.N >= 16384));
+    if (ks) {
+        const int R = ctx->rows_override == 4 ? 4 : 2;
+        const ks_kernel_t k = R == 2 ? pick_ks_r<2>(nbl) : pick_ks_r<4>(nbl);
+        const int G = ks_groups(nbl);
+        const int waves = G * nbl;
+        const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float)) +
+                           static_cast<size_t>(G) * R * nbl * sizeof(float);
+        const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * waves, lds);
+        const int64_t n_groups = (a.N + static_cast<int64_t>(G) * R - 1) / (static_cast<int64_t>(G) * R);
+        int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * occ);
+        if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
+        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds, ctx->stream, a.W,
+                           static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),
+                           row_bytes, x_al16 ? 1 : 0);
+        MI355X_HIP(hipGetLastError());
+        return MI355X_OK;
+    }
     // defaults from sweeps on MI355X (8192x8192, 17408x5120, 151936x2048,
     // 4096x4096, 2048x11008): 8-wave groups; long rows one row per wave with
     // two workgroups per CU, short rows several rows per wave

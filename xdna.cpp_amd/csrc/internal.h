@@ -32,6 +32,7 @@ struct mi355x_ctx {
     int waves_override = 0;
     int prefetch_override = 0;
     int64_t grid_override = 0;
+    int form_override = MI355X_FORM_AUTO;
     std::mutex mu;  // serialises calls that share the staging buffer
 };
 

@@ -278,6 +278,11 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
             return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: prefetch must be 0 (auto), 1 (on) or 2 (off)");
         ctx->prefetch_override = static_cast<int>(value);
         return MI355X_OK;
+    case MI355X_OPT_FORM:
+        if (value != MI355X_FORM_AUTO && value != MI355X_FORM_ROWS && value != MI355X_FORM_KSPLIT)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: form must be 0 (auto), 1 (rows) or 2 (K-split)");
+        ctx->form_override = static_cast<int>(value);
+        return MI355X_OK;
     case MI355X_OPT_GRID:
         if (value < 0) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: negative grid");
         ctx->grid_override = value;
