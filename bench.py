@@ -128,6 +128,87 @@ def kquant_sweep(ctx, steps, warmup):
     return res
 
 
+def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
+    """greedy decode of the Qwen2.5-3B-shaped Q4_0 model,
+    every matrix-vector product on the GPU (weights resident in HBM), the
+    rest of the step on the host.  tok/s = generation-phase passes / their
+    wall time.  With `cpu`, the same decode with the reference's CPU GEMV
+    engine is the baseline and the token-identity check."""
+    import decode
+
+    cfg = decode.QWEN25_3B
+    threads = min(16, os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    model = decode.Model(threads=threads, **cfg)
+    gemv_bytes = sum(algorithmic_bytes(mi355x.Q4_0, *model.matrix(i)[1:]) for i in range(model.n_matrices()))
+    log(f"bench: decode: built the 3B-shape model ({model.weight_bytes() / 2**30:.2f} GiB Q4_0) "
+        f"in {time.perf_counter() - t0:.1f} s with {threads} threads")
+    prompt = decode.prompt_tokens(n_prompt, cfg["vocab"], seed=512)
+    try:
+        t0 = time.perf_counter()
+        model.attach_gpu(0)
+        log(f"bench: decode: weights prepacked into HBM in {time.perf_counter() - t0:.1f} s")
+        model.generate(prompt[:8], 4)  # warm-up: first launches of each kernel form
+        gpu_toks, t = model.generate(prompt, n_gen)
+        passes = t["gen_passes"]
+        tok_s = passes / t["gen_s"]
+        launches = model.last_launches() / passes
+        # the same decode with one launch per weight matrix, as a ggml graph
+        # with one MUL_MAT node per weight dispatches them
+        model.set_fuse(False)
+        node_toks, tn = model.generate(prompt, n_gen)
+        model.set_fuse(True)
+        node_launches = model.last_launches() / passes
+        log(f"bench: decode: per-matrix launches {passes / tn['gen_s']:.1f} tok/s")
+        log(f"bench: decode: GPU {tok_s:.1f} tok/s ({t['gen_s'] / passes * 1e3:.3f} ms/token, "
+            f"GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops {t['gen_host_s'] / passes * 1e3:.3f} ms); "
+            f"prompt {n_prompt / t['prompt_s']:.1f} tok/s token by token")
+        res = {
+            "tok_s": round(tok_s, 2), "unit": "tok/s",
+            "workload": f"Qwen2.5-3B shape (36 layers, hidden 2048, 16q/2kv x 128, FFN 11008, vocab 151936, "
+                        f"tied), Q4_0 of N(0,0.02), {n_prompt}-token uniform-random prompt then {n_gen} "
+                        f"greedy tokens; tok/s over the {passes} generation-phase forward passes",
+            "ms_per_token": round(t["gen_s"] / passes * 1e3, 4),
+            "gemv_ms_per_token": round(t["gen_gemv_s"] / passes * 1e3, 4),
+            "host_ms_per_token": round(t["gen_host_s"] / passes * 1e3, 4),
+            "gemv_bytes_per_token": gemv_bytes,
+            "gemv_GB_s": round(gemv_bytes / (t["gen_gemv_s"] / passes) / 1e9, 1),
+            "prompt_tok_s": round(n_prompt / t["prompt_s"], 2),
+            "gemv_launches_per_token": launches,
+            "per_node": {"tok_s": round(passes / tn["gen_s"], 2), "gemv_launches_per_token": node_launches,
+                         "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
+                         "tokens_match_fused": bool(np.array_equal(node_toks, gpu_toks)),
+                         "note": "one GEMV launch per weight matrix (q, k, v, gate, up separately)"},
+            "split": "the 253 weight GEMVs per token on the GPU (q|k|v and gate|up, adjacent in HBM, as one "
+                     "launch each); norms, RoPE, attention, SwiGLU, argmax on the host",
+        }
+        if cpu:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle as orc
+
+            kind = "reference" if orc.RefLib.available() else "oracle"
+            f, cores = orc.decode_gemv(kind)
+            log(f"bench: decode: CPU run ({kind} GEMV) for the baseline and the token-identity check")
+            cpu_toks, tc = model.generate(prompt, n_gen, f)
+            same = np.array_equal(cpu_toks, gpu_toks)
+            diff = np.nonzero(cpu_toks != gpu_toks)[0]
+            res["token_identical"] = bool(same)
+            res["first_mismatch"] = None if same else int(diff[0])
+            res["cpu_baseline"] = {
+                "tok_s": round(passes / tc["gen_s"], 3), "unit": "tok/s", "cores": cores, "kind": kind,
+                "sample": f"the same {n_prompt}+{n_gen}-token decode with every GEMV on "
+                          + ("the reference's AVX2+OpenMP Q4GemvEngine (src/cpu-q4-gemv-engine.cpp)"
+                             if kind == "reference" else "the scalar C oracle")
+                          + f" and the same host ops ({threads} OpenMP threads for attention); "
+                            "not ggml-cpu, which is not in this build",
+                "ms_per_token": round(tc["gen_s"] / passes * 1e3, 3),
+            }
+            log(f"bench: decode: CPU {passes / tc['gen_s']:.2f} tok/s; token-identical: {same}")
+    finally:
+        model.close()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +224,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one device-to-device copy of 256 MiB (a plain copy kernel of known size, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--decode", type=int, default=1, help="1: also run the 3B-shape decode (config 5); 0: skip")
+    ap.add_argument("--decode-prompt", type=int, default=512)
+    ap.add_argument("--decode-tokens", type=int, default=128)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -234,6 +318,8 @@ def main() -> int:
     if not args.no_cpu:
         log(f"bench: CPU baseline for ~{args.cpu_seconds:.0f} s")
         out["cpu_baseline"] = cpu_baseline(raw, N, K, x, args.cpu_seconds)
+    if args.decode:
+        out["decode"] = decode_leg(args.decode_prompt, args.decode_tokens, not args.no_cpu)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -222,3 +222,35 @@ class RefCpuEngine:
         if self.h:
             self.ref.lib.ref_cpu_engine_free(self.h)
             self.h = None
+
+
+def decode_gemv(kind: str = "reference"):
+    """CPU GEMV for the decode harness's callback backend (qwen2_decode.h):
+    returns f(id, w, N, K, x, y) over raw addresses of ggml Q4_0 bytes, the
+    f32 activation and the f32 output, and the number of threads it uses.
+
+    kind "reference": the reference's AVX2+OpenMP Q4GemvEngine
+    (src/cpu-q4-gemv-engine.cpp), from oracle/_ref;
+    kind "oracle": the scalar C restatement (liboracle.so)."""
+    if kind == "reference":
+        ref = RefLib()
+        eng = RefCpuEngine(ref)
+        run = ref.lib.ref_cpu_engine_run
+
+        def f(i, w, N, K, x, y):
+            rc = run(eng.h, ctypes.cast(w, _u8p), N * (K // 32) * 18, N, K, ctypes.cast(x, _f32p),
+                     ctypes.cast(y, _f32p))
+            if rc != 0:
+                raise ValueError(ref.error())
+        f.engine = eng  # keeps the engine alive with the callable
+        return f, RefCpuEngine.THREADS
+    if kind == "oracle":
+        o = Oracle()
+        gemv = o.lib.orc_gemv_f32
+
+        def f(i, w, N, K, x, y):
+            rc = gemv(Q4_0, ctypes.cast(w, _u8p), N, K, ctypes.cast(x, _f32p), ctypes.cast(y, _f32p), None)
+            if rc != 0:
+                raise ValueError(f"orc_gemv_f32 rc={rc}")
+        return f, 1
+    raise ValueError(kind)

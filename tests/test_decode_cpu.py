@@ -1,0 +1,93 @@
+"""The end-to-end decode harness on the CPU (callback backend): its weight
+quantizer against the Q4_0 recipe pinned elsewhere, its forward pass against
+an independent float64 numpy Qwen2 decoder, and its error paths."""
+import numpy as np
+import pytest
+
+import decode
+import oracle as orc
+import synth
+from qwen2_numpy import Qwen2Numpy, dequantized
+
+TINY = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+            rope_theta=1e6, norm_eps=1e-6, seed=7)
+# a second shape: one KV head for four query heads, other theta/eps
+TINY_MQA = dict(n_layers=3, hidden=128, n_heads=4, n_kv_heads=1, head_dim=32, ffn=320, vocab=500,
+                rope_theta=1e4, norm_eps=1e-5, seed=11)
+
+
+def test_quantizer_matches_q4_0_recipe():
+    w = synth.normal_weights(64, 1024, seed=3)
+    w[5, :32] = 0.0          # all-zero block: d = 0
+    w[6, 40] = 1.0           # positive absmax: d < 0
+    w[7, 64:96] *= 1e-3      # tiny block: d is a subnormal half
+    assert np.array_equal(decode.quantize_q4_0(w).reshape(-1), synth.quantize_q4_0(w).reshape(-1))
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY_MQA], ids=["gqa2", "mqa"])
+def test_forward_matches_numpy_qwen2(oracle, cfg):
+    with decode.Model(threads=4, **cfg) as m:
+        ref = Qwen2Numpy(m, oracle)
+        p = decode.prompt_tokens(10, cfg["vocab"], 3)
+        f, _ = orc.decode_gemv("oracle")
+        toks, t = m.generate(p, 6, f)
+        rt, rl = ref.generate(p, 6)
+        assert np.array_equal(toks, rt)
+        lg = m.last_logits()
+        assert np.abs(lg - rl).max() <= 1e-5 * np.abs(rl).max()
+        assert t["gen_passes"] == 5 and t["gen_s"] > 0
+
+
+def test_model_shapes_and_vectors():
+    with decode.Model(threads=2, **TINY) as m:
+        assert m.n_matrices() == 7 * 2 + 1
+        H, Q, KV, F = 256, 4 * 64, 2 * 64, 512
+        want = [(Q, H), (KV, H), (KV, H), (H, Q), (F, H), (F, H), (H, F)] * 2 + [(1000, H)]
+        assert [m.matrix(i)[1:] for i in range(m.n_matrices())] == want
+        assert np.all(m.vector(0) == 1.0) and np.all(m.vector(5 * 2) == 1.0)
+        b = m.vector(2)
+        assert b.shape == (Q,) and 0.01 < b.std() < 0.04
+        with pytest.raises(IndexError):
+            m.vector(5 * 2 + 1)
+
+
+def test_weights_are_normal_0_02(oracle):
+    with decode.Model(threads=4, **TINY) as m:
+        w = dequantized(m, oracle, 4).reshape(-1)  # gate, 512 x 256
+        assert abs(w.mean()) < 5e-4 and 0.0195 < w.std() < 0.0205
+        # fourth moment of a normal: 3 sigma^4 (a uniform or clipped generator fails this)
+        assert 2.8 < np.mean(w ** 4) / w.var() ** 2 < 3.2
+
+
+def test_reference_engine_callback_agrees(reflib, oracle):
+    with decode.Model(threads=4, **TINY) as m:
+        p = decode.prompt_tokens(12, 1000, 9)
+        out = {}
+        for kind in ("oracle", "reference"):
+            f, _ = orc.decode_gemv(kind)
+            out[kind] = (m.generate(p, 8, f)[0], m.last_logits())
+        assert np.array_equal(out["oracle"][0], out["reference"][0])
+        a, b = (v[1].astype(np.float64) for v in out.values())
+        assert np.dot(a, b) / np.linalg.norm(a) / np.linalg.norm(b) >= 0.999999
+
+
+def test_seeded_weights_are_reproducible():
+    with decode.Model(threads=3, **TINY) as a, decode.Model(threads=1, **TINY) as b:
+        for i in (0, 6, 14):
+            pa, N, K = a.matrix(i)
+            pb, _, _ = b.matrix(i)
+            n = N * (K // 32) * 18
+            assert bytes((decode.C.c_uint8 * n).from_address(pa)) == bytes((decode.C.c_uint8 * n).from_address(pb))
+
+
+def test_errors():
+    with pytest.raises(RuntimeError, match="invalid configuration"):
+        decode.Model(**dict(TINY, hidden=250))
+    with decode.Model(threads=1, **TINY) as m:
+        with pytest.raises(RuntimeError, match="qd_attach_gpu first"):
+            m.generate(np.array([1, 2], dtype=np.int32), 2)
+
+        def bad(*a):
+            raise ValueError("boom")
+        with pytest.raises(RuntimeError, match="GEMV failed"):
+            m.generate(np.array([1, 2], dtype=np.int32), 2, bad)

@@ -1,0 +1,96 @@
+/*
+ * qwen2_decode.h -- batch-1 greedy decoder of a Qwen2-shaped model with Q4_0
+ * weights, for end-to-end measurement of the decode GEMV path.
+ *
+ * Everything except the matrix-vector products runs on the host in C++
+ * (RMSNorm, RoPE, grouped-query attention over a f32 KV cache, SwiGLU,
+ * residuals, embedding lookup, argmax).  Every weight matrix -- per layer
+ * q, k, v, o, gate, up, down, plus the tied output projection -- is a Q4_0
+ * GEMV done by a backend: either the MI355X library (weights prepacked once
+ * into HBM) or a caller-supplied function (a CPU reference).
+ *
+ * Weights are random: seeded N(0, 0.02) f32 values quantized with ggml's Q4_0
+ * rule; norms are 1, q/k/v biases N(0, 0.02).
+ */
+#ifndef QWEN2_DECODE_H
+#define QWEN2_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QD_API __attribute__((visibility("default")))
+
+typedef struct qd_config {
+    int n_layers;       /* 36 for the 3B shape */
+    int hidden;         /* 2048 */
+    int n_heads;        /* 16 */
+    int n_kv_heads;     /* 2 */
+    int head_dim;       /* 128 (a multiple of 8) */
+    int ffn;            /* 11008 */
+    int vocab;          /* 151936 */
+    float rope_theta;   /* 1e6 */
+    float norm_eps;     /* 1e-6 */
+    uint64_t seed;
+} qd_config;
+
+typedef struct qd_model qd_model;
+
+/* Matrix ids: 7 per layer (q, k, v, o, gate, up, down) in that order, then
+ * the output projection (tied to the token embedding) at 7 * n_layers. */
+#define QD_Q 0
+#define QD_K 1
+#define QD_V 2
+#define QD_O 3
+#define QD_GATE 4
+#define QD_UP 5
+#define QD_DOWN 6
+
+/* A backend GEMV: y[0..N) = W_id (N x K, ggml Q4_0 bytes) * x[0..K). */
+typedef int (*qd_gemv_fn)(void *user, int id, const uint8_t *w, int64_t N, int64_t K, const float *x,
+                          float *y);
+
+QD_API qd_model *qd_model_create(const qd_config *cfg, int threads);
+QD_API void qd_model_free(qd_model *m);
+QD_API int qd_n_matrices(const qd_model *m);
+/* ggml Q4_0 bytes of matrix `id` and its shape. */
+QD_API const uint8_t *qd_matrix(const qd_model *m, int id, int64_t *N, int64_t *K);
+/* Vector `id`: 5 per layer (attn norm, ffn norm, q bias, k bias, v bias),
+ * then the output norm at 5 * n_layers. */
+QD_API const float *qd_vector(const qd_model *m, int id, int *n);
+QD_API const char *qd_last_error(void);
+/* Logits (n = vocab floats) behind the last token of the last qd_generate. */
+QD_API int qd_last_logits(const qd_model *m, float *out, int n);
+/* The weight quantizer (ggml's Q4_0 rule), exposed for tests. */
+QD_API void qd_quantize_q4_0(const float *x, int64_t N, int64_t K, uint8_t *out);
+
+/* Moves every matrix into HBM (prepacked) on `device`; later runs with
+ * backend 0 use it. */
+QD_API int qd_attach_gpu(qd_model *m, int device);
+
+/* GEMV groups (q|k|v, gate|up) whose matrices lie back to back in HBM run
+ * as one launch when `on` (the default); off = one launch per matrix, as a
+ * ggml graph with one MUL_MAT node per weight dispatches them. */
+QD_API void qd_set_fuse(qd_model *m, int on);
+/* GPU GEMV launches in the generation phase of the last qd_generate. */
+QD_API int64_t qd_last_launches(const qd_model *m);
+
+/* Greedy decode: processes `n_prompt` tokens one at a time, then generates
+ * `n_gen` tokens into out_tokens.  backend 0 = MI355X, 1 = `cpu_gemv`.
+ * The generation phase is the n_gen - 1 forward passes after the prompt
+ * (the first generated token comes from the last prompt position).
+ * timings (optional, 4 doubles): prompt seconds, generation-phase seconds,
+ * seconds inside GEMV calls in the generation phase (backend 0: activation
+ * upload, GEMV launches and output download), host-op seconds in the
+ * generation phase. */
+QD_API int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const int32_t *prompt,
+                       int n_prompt, int n_gen, int32_t *out_tokens, double *timings);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
