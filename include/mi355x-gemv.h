@@ -85,7 +85,8 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
  *       for the K/IQ types with int8 dot4 products).
- *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step.
+ *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step
+ *     (rows and K-split forms); 4, 8 or 16 rows per step (stream form).
  *   MI355X_OPT_WAVES_PER_GROUP: 0 (auto), 8 or 16 wavefronts per workgroup
  *     (digit-plane Q4_0 kernel).
  *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups.
@@ -94,7 +95,9 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *   MI355X_OPT_FORM: work split of the digit-plane Q4_0 kernel --
  *     MI355X_FORM_AUTO (default), MI355X_FORM_ROWS (a wavefront owns whole
  *     rows), MI355X_FORM_KSPLIT (a wavefront owns one 64-block column of 2 or
- *     4 rows; needs rows of a multiple of 8 blocks). */
+ *     4 rows; needs rows of a multiple of 8 blocks), MI355X_FORM_STREAM (one
+ *     workgroup per CU; a lane owns one block of every row of its team and
+ *     keeps that block's activation digits in registers; K <= 16384). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3
@@ -107,6 +110,7 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 #define MI355X_FORM_AUTO 0
 #define MI355X_FORM_ROWS 1
 #define MI355X_FORM_KSPLIT 2
+#define MI355X_FORM_STREAM 3
 MI355X_API int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value);
 
 /* ---- memory ----------------------------------------------------------------

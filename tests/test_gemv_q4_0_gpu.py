@@ -222,3 +222,71 @@ def test_ksplit_form(ctx, oracle, variant, rows, N, K):
     finally:
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
         ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+
+
+@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("rows", [0, 4, 8, 16])
+@pytest.mark.parametrize("N,K", [(1, 32), (2, 32), (33, 64), (127, 128), (100, 96), (513, 64), (1000, 2048),
+                                 (37, 8192), (4096, 4096), (8192, 8192), (2048, 11008), (17408, 5120),
+                                 (300, 16384), (24, 4096)])
+def test_stream_form(ctx, oracle, variant, waves, rows, N, K):
+    """The stream work split (one workgroup per CU; a lane owns one block of
+    every row of its team, digit planes in registers, batched butterfly
+    reduction) against the oracle: single blocks, partial 64-block columns,
+    row counts that leave teams and steps partly empty, every rows-per-step
+    and wavefront setting."""
+    if variant != "digits":
+        pytest.skip("the stream form is a digit-plane kernel")
+    if rows == 16 and waves == 16:
+        pytest.skip("16 rows per step run with 8 wavefronts (register budget)")
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_STREAM)
+    ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, rows)
+    ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, waves)
+    try:
+        raw = synth.random_q4_0(N, K, seed=N + K)
+        x = synth.activations(K, seed=K)
+        parity(ctx, oracle, raw, N, K, x, f"stream R{rows} W{waves} {N}x{K}")
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+        ctx.set_option(mi355x.OPT_WAVES_PER_GROUP, 0)
+
+
+def test_stream_form_edges(ctx, oracle):
+    """Known answer, non-finite activations poisoning every row (as f32
+    arithmetic does), and a misaligned activation row (the stream form needs
+    16-byte alignment and hands such calls to the row form)."""
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_STREAM)
+    try:
+        N, K = 128, 256
+        blk = np.zeros(18, dtype=np.uint8)
+        blk[0:2] = [0x00, 0x3C]
+        blk[2:] = 0x99
+        y = run_gpu(ctx, np.tile(blk, N * K // 32), N, K, np.full(K, 0.5, dtype=np.float32))
+        assert np.array_equal(y, np.full(N, 128.0, dtype=np.float32))
+
+        N, K = 64, 512
+        raw = synth.random_q4_0(N, K, seed=3)
+        x = synth.activations(K, seed=4)
+        x[40] = np.inf
+        x[300] = np.nan
+        assert np.all(np.isnan(run_gpu(ctx, raw, N, K, x)))
+
+        N, K = 300, 2048
+        raw = synth.random_q4_0(N, K, seed=5)
+        x = synth.activations(K, seed=6)
+        w = ctx.resident(Q4_0, raw, N, K)
+        xb = ctx.alloc(4 * K + 16)
+        yb = ctx.alloc(4 * N)
+        try:
+            xb.upload(x, offset=4)
+            mi355x.check(ctx.gemv_ptr(Q4_0, w.ptr, N, K, xb.ptr + 4, yb.ptr))
+            ctx.sync()
+            y = yb.download(np.float32, N)
+        finally:
+            w.free()
+            xb.free()
+            yb.free()
+        check_gemv(y, oracle.gemv(Q4_0, raw, N, K, x), oracle.row_norms(Q4_0, raw, N, K), x, "stream misaligned x")
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)

@@ -195,6 +195,9 @@ int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a) {
         return set_error(MI355X_EUNSUPPORTED, "Q4_0 GEMV: N or K beyond 32-bit kernel indexing");
     if (reinterpret_cast<uintptr_t>(a.W) % 2 != 0)
         return set_error(MI355X_EINVAL, "Q4_0 GEMV: weight pointer must be 2-byte aligned");
+    if (ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && ctx->form_override == MI355X_FORM_STREAM &&
+        q4_0_st_supports(ctx, a))
+        return launch_gemv_q4_0_st(ctx, a);
     if (ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && q4_0_dp_supports(ctx, a))
         return launch_gemv_q4_0_dp(ctx, a);
     if (ctx->kernel_variant == MI355X_VARIANT_DIGITS)

@@ -63,6 +63,8 @@ struct GemvArgs {
 int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
+bool q4_0_st_supports(const mi355x_ctx *ctx, const GemvArgs &a);
+int launch_gemv_q4_0_st(mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a);
 
 // Prepack kernels: byte-range scatter/gather between ggml and resident order.

@@ -264,8 +264,8 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
         ctx->kernel_variant = static_cast<int>(value);
         return MI355X_OK;
     case MI355X_OPT_ROWS_PER_WAVE:
-        if (value != 0 && value != 1 && value != 2 && value != 4)
-            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: rows per wave must be 0, 1, 2 or 4");
+        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8 && value != 16)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: rows per wave must be 0, 1, 2, 4, 8 or 16");
         ctx->rows_override = static_cast<int>(value);
         return MI355X_OK;
     case MI355X_OPT_WAVES_PER_GROUP:
@@ -279,8 +279,10 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
         ctx->prefetch_override = static_cast<int>(value);
         return MI355X_OK;
     case MI355X_OPT_FORM:
-        if (value != MI355X_FORM_AUTO && value != MI355X_FORM_ROWS && value != MI355X_FORM_KSPLIT)
-            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: form must be 0 (auto), 1 (rows) or 2 (K-split)");
+        if (value != MI355X_FORM_AUTO && value != MI355X_FORM_ROWS && value != MI355X_FORM_KSPLIT &&
+            value != MI355X_FORM_STREAM)
+            return set_error(MI355X_EINVAL,
+                             "mi355x_ctx_set_option: form must be 0 (auto), 1 (rows), 2 (K-split) or 3 (stream)");
         ctx->form_override = static_cast<int>(value);
         return MI355X_OK;
     case MI355X_OPT_GRID:
