@@ -153,13 +153,19 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         passes = t["gen_passes"]
         tok_s = passes / t["gen_s"]
         launches = model.last_launches() / passes
-        # the same decode with one launch per weight matrix, as a ggml graph
-        # with one MUL_MAT node per weight dispatches them
+        # the same decode with activations and outputs copied through HBM
+        # (staged I/O) ...
+        model.set_io(model.IO_STAGED)
+        staged_toks, ts = model.generate(prompt, n_gen)
+        # ... and, in addition, one launch per weight matrix: the traffic of a
+        # ggml graph with one MUL_MAT node per weight on a device-memory backend
         model.set_fuse(False)
         node_toks, tn = model.generate(prompt, n_gen)
         model.set_fuse(True)
+        model.set_io(model.IO_MAPPED)
         node_launches = model.last_launches() / passes
-        log(f"bench: decode: per-matrix launches {passes / tn['gen_s']:.1f} tok/s")
+        log(f"bench: decode: staged I/O {passes / ts['gen_s']:.1f} tok/s; per-matrix launches with staged I/O "
+            f"{passes / tn['gen_s']:.1f} tok/s")
         log(f"bench: decode: GPU {tok_s:.1f} tok/s ({t['gen_s'] / passes * 1e3:.3f} ms/token, "
             f"GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops {t['gen_host_s'] / passes * 1e3:.3f} ms); "
             f"prompt {n_prompt / t['prompt_s']:.1f} tok/s token by token")
@@ -175,12 +181,19 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
             "gemv_GB_s": round(gemv_bytes / (t["gen_gemv_s"] / passes) / 1e9, 1),
             "prompt_tok_s": round(n_prompt / t["prompt_s"], 2),
             "gemv_launches_per_token": launches,
+            "staged_io": {"tok_s": round(passes / ts["gen_s"], 2),
+                          "gemv_ms_per_token": round(ts["gen_gemv_s"] / passes * 1e3, 4),
+                          "tokens_match": bool(np.array_equal(staged_toks, gpu_toks)),
+                          "note": "activation copied host->HBM and outputs HBM->host around every GEMV group"},
             "per_node": {"tok_s": round(passes / tn["gen_s"], 2), "gemv_launches_per_token": node_launches,
                          "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
                          "tokens_match_fused": bool(np.array_equal(node_toks, gpu_toks)),
-                         "note": "one GEMV launch per weight matrix (q, k, v, gate, up separately)"},
+                         "note": "one GEMV launch per weight matrix (q, k, v, gate, up separately) with staged I/O: "
+                                 "the pattern of a ggml graph with one MUL_MAT node per weight on this backend"},
             "split": "the 253 weight GEMVs per token on the GPU (q|k|v and gate|up, adjacent in HBM, as one "
-                     "launch each); norms, RoPE, attention, SwiGLU, argmax on the host",
+                     "launch each); norms, RoPE, attention, SwiGLU, argmax on the host; the kernels read the "
+                     "activation from and write outputs to pinned host memory (the 151936-float vocabulary "
+                     "output goes through HBM and one copy)",
         }
         if cpu:
             sys.path.insert(0, os.path.join(ROOT, "oracle"))

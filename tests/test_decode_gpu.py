@@ -77,3 +77,23 @@ def test_fused_launches_match_per_matrix_launches():
         assert m.last_launches() == 5 * (7 * TINY["n_layers"] + 1)
         assert np.array_equal(fused, single)
         assert np.abs(lf - ls).max() <= 1e-5 * np.abs(ls).max()
+
+
+def test_mapped_io_matches_staged_io():
+    """Kernels reading the activation from / writing outputs to pinned host
+    memory (mapped I/O, the default) against copies through HBM (staged
+    I/O): the same kernels on the same numbers, so tokens and logits are
+    bit-identical; the vocabulary projection (above the mapped-output limit)
+    takes the copy path in both."""
+    cfg = dict(TINY, vocab=70000)
+    with decode.Model(threads=4, **cfg) as m:
+        m.attach_gpu(0)
+        p = decode.prompt_tokens(7, cfg["vocab"], 5)
+        mapped, _ = m.generate(p, 5)
+        lm = m.last_logits()
+        m.set_io(m.IO_STAGED)
+        staged, _ = m.generate(p, 5)
+        assert np.array_equal(mapped, staged)
+        assert np.array_equal(lm, m.last_logits())
+        with pytest.raises(RuntimeError, match="unknown mode"):
+            m.set_io(7)

@@ -52,6 +52,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_last_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_quantize_q4_0.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
     lib.qd_set_fuse.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_set_io.restype = C.c_int
+    lib.qd_set_io.argtypes = [C.c_void_p, C.c_int]
     lib.qd_last_launches.restype = C.c_int64
     lib.qd_last_launches.argtypes = [C.c_void_p]
     lib.qd_attach_gpu.restype = C.c_int
@@ -124,6 +126,14 @@ class Model:
 
     def set_fuse(self, on: bool) -> None:
         self.lib.qd_set_fuse(self.h, 1 if on else 0)
+
+    IO_STAGED, IO_MAPPED = 0, 1
+
+    def set_io(self, mode: int) -> None:
+        """IO_STAGED: activations/outputs copied through HBM around each GEMV
+        group; IO_MAPPED (default): kernels read/write pinned host memory."""
+        if self.lib.qd_set_io(self.h, mode) != 0:
+            raise RuntimeError(self.lib.qd_last_error().decode())
 
     def last_launches(self) -> int:
         return self.lib.qd_last_launches(self.h)

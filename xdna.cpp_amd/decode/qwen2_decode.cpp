@@ -178,6 +178,11 @@ struct qd_model {
     float *dx = nullptr, *dy = nullptr;  // activation in, outputs out
     size_t dy_floats = 0;
     float *hx = nullptr, *hy = nullptr;  // pinned staging
+    // device addresses of hx / hy (pinned host memory the kernels can read
+    // and write directly over PCIe)
+    const float *hx_dev = nullptr;
+    float *hy_dev = nullptr;
+    int io_mode = QD_IO_MAPPED;
 
     ~qd_model() {
         if (ctx) {
@@ -428,6 +433,13 @@ void qd_set_fuse(qd_model *m, int on) {
     if (m) m->fuse = on != 0;
 }
 
+int qd_set_io(qd_model *m, int mode) {
+    if (!m) return fail("qd_set_io: null model");
+    if (mode != QD_IO_STAGED && mode != QD_IO_MAPPED) return fail("qd_set_io: unknown mode");
+    m->io_mode = mode;
+    return 0;
+}
+
 int64_t qd_last_launches(const qd_model *m) { return m ? m->last_launches : 0; }
 
 int qd_last_logits(const qd_model *m, float *out, int n) {
@@ -478,6 +490,11 @@ int qd_attach_gpu(qd_model *m, int device) {
     m->hx = static_cast<float *>(p);
     if (mi355x_host_malloc(m->dy_floats * 4, &p) != MI355X_OK) return fail(mi355x_last_error());
     m->hy = static_cast<float *>(p);
+    void *dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, m->hx, 0) != hipSuccess) return fail("qd_attach_gpu: hipHostGetDevicePointer");
+    m->hx_dev = static_cast<const float *>(dp);
+    if (hipHostGetDevicePointer(&dp, m->hy, 0) != hipSuccess) return fail("qd_attach_gpu: hipHostGetDevicePointer");
+    m->hy_dev = static_cast<float *>(dp);
     return 0;
 }
 
@@ -505,14 +522,25 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     int rc = 0;
 
     // GEMVs that share one activation: y_i = W_ids[i] x; outputs land in
-    // outs[i].  The GPU path uploads x once and downloads all outputs once.
+    // outs[i].  Staged I/O uploads x once and downloads all outputs once;
+    // mapped I/O lets the kernels read x from, and write y to, pinned host
+    // memory (outputs above kMappedOutMax floats still go through HBM and
+    // one copy: a 600 KB vocabulary row is faster as one DMA).
+    constexpr int64_t kMappedOutMax = 65536;
     auto gemvs = [&](const float *x, int64_t K, std::initializer_list<int> ids, std::initializer_list<float *> outs) {
         const double t0 = now();
         if (backend == 0) {
-            // pinned staging, all on the context's stream: one wait per group
+            // all on the context's stream: one wait per group
             const hipStream_t st = static_cast<hipStream_t>(mi355x_ctx_stream(m->ctx));
+            int64_t n_out = 0;
+            for (int id : ids) n_out += m->mats[id].N;
+            const bool map_x = m->io_mode == QD_IO_MAPPED;
+            const bool map_y = map_x && n_out <= kMappedOutMax;
+            const float *xin = map_x ? m->hx_dev : m->dx;
+            float *yout = map_y ? m->hy_dev : m->dy;
             std::memcpy(m->hx, x, static_cast<size_t>(K) * 4);
-            if (hipMemcpyAsync(m->dx, m->hx, static_cast<size_t>(K) * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+            if (!map_x &&
+                hipMemcpyAsync(m->dx, m->hx, static_cast<size_t>(K) * 4, hipMemcpyHostToDevice, st) != hipSuccess)
                 return -1;
             // consecutive matrices adjacent in HBM with the same K run as one
             int64_t off = 0, run_n = 0;
@@ -524,20 +552,21 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
                     run_n += mat.N;
                     continue;
                 }
-                if (run && mi355x_gemv(m->ctx, MI355X_TYPE_Q4_0, run->dev, run_n, run->K, m->dx, m->dy + off) != MI355X_OK)
+                if (run && mi355x_gemv(m->ctx, MI355X_TYPE_Q4_0, run->dev, run_n, run->K, xin, yout + off) != MI355X_OK)
                     return -1;
                 if (run) ++launches;
                 off += run_n;
                 run = &mat;
                 run_n = mat.N;
             }
-            if (mi355x_gemv(m->ctx, MI355X_TYPE_Q4_0, run->dev, run_n, run->K, m->dx, m->dy + off) != MI355X_OK)
+            if (mi355x_gemv(m->ctx, MI355X_TYPE_Q4_0, run->dev, run_n, run->K, xin, yout + off) != MI355X_OK)
                 return -1;
             off += run_n;
             ++launches;
-            if (hipMemcpyAsync(m->hy, m->dy, static_cast<size_t>(off) * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
-                hipStreamSynchronize(st) != hipSuccess)
+            if (!map_y &&
+                hipMemcpyAsync(m->hy, m->dy, static_cast<size_t>(off) * 4, hipMemcpyDeviceToHost, st) != hipSuccess)
                 return -1;
+            if (hipStreamSynchronize(st) != hipSuccess) return -1;
             off = 0;
             auto oi = outs.begin();
             for (int id : ids) {

@@ -75,6 +75,16 @@ QD_API int qd_attach_gpu(qd_model *m, int device);
  * as one launch when `on` (the default); off = one launch per matrix, as a
  * ggml graph with one MUL_MAT node per weight dispatches them. */
 QD_API void qd_set_fuse(qd_model *m, int on);
+/* How activations and outputs cross PCIe on the GPU path:
+ * QD_IO_STAGED: x is copied into HBM and y back from HBM around the launches
+ * (the traffic pattern of a ggml backend whose buffers are device memory);
+ * QD_IO_MAPPED (default): the kernels read x from and write y to pinned
+ * host memory directly, saving two copy commands per GEMV group (outputs
+ * longer than 65536 floats, i.e. the vocabulary projection, still use one
+ * device-to-host copy). */
+#define QD_IO_STAGED 0
+#define QD_IO_MAPPED 1
+QD_API int qd_set_io(qd_model *m, int mode);
 /* GPU GEMV launches in the generation phase of the last qd_generate. */
 QD_API int64_t qd_last_launches(const qd_model *m);
 
