@@ -217,6 +217,24 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                 "ms_per_token": round(tc["gen_s"] / passes * 1e3, 3),
             }
             log(f"bench: decode: CPU {passes / tc['gen_s']:.2f} tok/s; token-identical: {same}")
+            # ggml-cpu does not multiply by f32 activations: it quantizes them
+            # to Q8_0 first.  The same decode with that arithmetic (restated
+            # in the oracle; ggml itself is not part of this build) shows
+            # whether the GPU's f32-activation tokens survive it.
+            fq, qcores = orc.decode_gemv("ggml_q8")
+            q8_toks, tq = model.generate(prompt, n_gen, fq)
+            q8_same = np.array_equal(q8_toks, gpu_toks)
+            q8_diff = np.nonzero(q8_toks != gpu_toks)[0]
+            res["ggml_q8_numerics"] = {
+                "token_identical": bool(q8_same),
+                "first_mismatch": None if q8_same else int(q8_diff[0]),
+                "matching_tokens": int(np.sum(q8_toks == gpu_toks)),
+                "tok_s": round(passes / tq["gen_s"], 3), "cores": qcores,
+                "note": "every GEMV with ggml-cpu's Q8_0-activation arithmetic (quantize_row_q8_0 + "
+                        "vec_dot_q4_0_q8_0, restated from ggml's generic C path; ggml is not in this build)",
+            }
+            log(f"bench: decode: ggml Q8_0 numerics: token-identical {q8_same}"
+                + ("" if q8_same else f", first mismatch at {int(q8_diff[0])}"))
     finally:
         model.close()
     return res

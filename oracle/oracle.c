@@ -9,6 +9,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
 /* ------------------------------------------------------------------------ */
 /* scalar conversions                                                        */
 /* ------------------------------------------------------------------------ */
@@ -520,5 +524,97 @@ int orc_row_norms(int type, const uint8_t *W, int64_t N, int64_t K, double *norm
         norms[r] = sqrt(s);
     }
     free(w);
+    return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml-cpu's Q4_0 x Q8_0 numerics (EXTERNAL, parity unpinned)               */
+/* ------------------------------------------------------------------------ */
+/* ggml's CPU backend does not multiply Q4_0 weights by f32 activations: it
+ * first quantizes the activation row to Q8_0 (quantize_row_q8_0) and then
+ * takes integer block dot products (ggml_vec_dot_q4_0_q8_0).  Restated here
+ * from ggml's published generic C path (llama.cpp 0ec4027a2, the pinned
+ * build of README.md:64; not vendored in the reference, so not comparable
+ * against ggml itself in this container):
+ *   block of 32: amax = max|x|, d = amax / 127, id = d ? 1/d : 0,
+ *                q_j = roundf(x_j * id), d stored as fp16 (round to even);
+ *   row:         sumf += (sum_j (q4_j - 8) * q8_j) * d_w * d_x, blocks in
+ *                order, low nibbles against q8[0..15], high against [16..31].
+ * The reference's own engines never take this path (src/cpu-q4-gemv-engine.cpp
+ * and src/xdna-gemv-engine.cpp multiply by f32 activations).  Used only to
+ * measure whether f32-activation decode and ggml-cpu-numerics decode pick
+ * the same tokens. */
+
+uint16_t orc_f32_to_fp16(float f) {
+    uint32_t x = f32_to_bits(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    x &= 0x7fffffffu;
+    if (x >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (x > 0x7f800000u ? 0x200u : 0u));
+    if (x >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: rounds to inf */
+    if (x < 0x38800000u) {                                     /* result subnormal (or 0) */
+        if (x < 0x33000000u) return (uint16_t)sign;           /* < 2^-25: rounds to 0 */
+        uint32_t e = x >> 23, m = (x & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e; /* value = m * 2^(e-150) = (m >> shift) * 2^-24 */
+        uint32_t q = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = ((x >> 23) - 112u) << 10 | ((x >> 13) & 0x3ffu);
+    uint32_t rem = x & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+int orc_quantize_row_q8_0(const float *x, int64_t K, uint8_t *out) {
+    if (K < 0 || K % 32 != 0 || (K > 0 && (!x || !out))) return ORC_EINVAL;
+    for (int64_t b = 0; b < K / 32; ++b) {
+        const float *xb = x + 32 * b;
+        uint8_t *ob = out + 34 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            float a = fabsf(xb[j]);
+            amax = a > amax ? a : amax;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t h = orc_f32_to_fp16(d);
+        ob[0] = (uint8_t)(h & 0xff);
+        ob[1] = (uint8_t)(h >> 8);
+        for (int j = 0; j < 32; ++j) ob[2 + j] = (uint8_t)(int8_t)roundf(xb[j] * id);
+    }
+    return ORC_OK;
+}
+
+int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, float *y) {
+    const int64_t rb = orc_row_bytes(ORC_Q4_0, K);
+    if (rb < 0 || N < 0) return ORC_EINVAL;
+    if (N == 0) return ORC_OK;
+    if (!W || !y || (K > 0 && !x)) return ORC_EINVAL;
+    const int64_t nb = K / 32;
+    uint8_t *xq = (uint8_t *)malloc((size_t)(nb > 0 ? nb : 1) * 34);
+    if (!xq) return ORC_EINVAL;
+    orc_quantize_row_q8_0(x, K, xq);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < N; ++r) {
+        const uint8_t *row = W + r * rb;
+        float sumf = 0.0f;
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t *wb = row + 18 * b;
+            const uint8_t *qb = xq + 34 * b;
+            int sumi0 = 0, sumi1 = 0;
+            for (int j = 0; j < 16; ++j) {
+                const int v0 = (wb[2 + j] & 0x0f) - 8;
+                const int v1 = (wb[2 + j] >> 4) - 8;
+                sumi0 += v0 * (int)(int8_t)qb[2 + j];
+                sumi1 += v1 * (int)(int8_t)qb[2 + 16 + j];
+            }
+            const int sumi = sumi0 + sumi1;
+            const float dw = orc_fp16_to_f32((uint16_t)(wb[0] | (wb[1] << 8)));
+            const float dx = orc_fp16_to_f32((uint16_t)(qb[0] | (qb[1] << 8)));
+            sumf += (float)sumi * dw * dx;
+        }
+        y[r] = sumf;
+    }
+    free(xq);
     return ORC_OK;
 }

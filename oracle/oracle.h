@@ -97,6 +97,13 @@ int orc_row_norms(int type, const uint8_t *W, int64_t N, int64_t K, double *norm
  * ksigns_iq2xs, external).  Returns the byte for index i in [0,128). */
 uint8_t orc_ksigns_iq2xs(int i);
 
+/* ggml-cpu's Q4_0 x Q8_0 path (external restatement, parity unpinned; see
+ * oracle.c): f32 -> fp16 round to even, Q8_0 quantization of an activation
+ * row (K/32 blocks of [fp16 d][int8 q[32]]), and the Q4_0 x Q8_0 GEMV. */
+uint16_t orc_f32_to_fp16(float f);
+int orc_quantize_row_q8_0(const float *x, int64_t K, uint8_t *out);
+int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, float *y);
+
 #ifdef __cplusplus
 }
 #endif

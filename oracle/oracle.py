@@ -67,7 +67,30 @@ class Oracle:
                                       ctypes.POINTER(ctypes.c_double), ctypes.c_void_p]
         lib.orc_ksigns_iq2xs.restype = ctypes.c_uint8
         lib.orc_ksigns_iq2xs.argtypes = [ctypes.c_int]
+        lib.orc_f32_to_fp16.restype = ctypes.c_uint16
+        lib.orc_f32_to_fp16.argtypes = [ctypes.c_float]
+        lib.orc_quantize_row_q8_0.argtypes = [_f32p, ctypes.c_int64, _u8p]
+        lib.orc_gemv_q4_0_q8_0.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, _f32p, _f32p]
         self.lib = lib
+
+    # ggml-cpu numerics (external restatement; see oracle.c)
+    def f32_to_fp16(self, f: float) -> int:
+        return self.lib.orc_f32_to_fp16(f)
+
+    def quantize_q8_0(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+        if self.lib.orc_quantize_row_q8_0(_ptr(x, _f32p), x.size, _ptr(out, _u8p)) != 0:
+            raise ValueError("orc_quantize_row_q8_0 rejected the row")
+        return out
+
+    def gemv_q4_0_q8_0(self, W: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
+        W = np.ascontiguousarray(W, dtype=np.uint8).reshape(-1)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(N, dtype=np.float32)
+        if self.lib.orc_gemv_q4_0_q8_0(_ptr(W, _u8p), N, K, _ptr(x, _f32p), _ptr(y, _f32p)) != 0:
+            raise ValueError("orc_gemv_q4_0_q8_0 rejected the shape")
+        return y
 
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.orc_fp16_to_f32(h)
@@ -231,7 +254,9 @@ def decode_gemv(kind: str = "reference"):
 
     kind "reference": the reference's AVX2+OpenMP Q4GemvEngine
     (src/cpu-q4-gemv-engine.cpp), from oracle/_ref;
-    kind "oracle": the scalar C restatement (liboracle.so)."""
+    kind "oracle": the scalar C restatement (liboracle.so);
+    kind "ggml_q8": ggml-cpu's Q8_0-activation numerics, restated in
+    liboracle.so (external, parity unpinned; OpenMP over rows)."""
     if kind == "reference":
         ref = RefLib()
         eng = RefCpuEngine(ref)
@@ -253,4 +278,13 @@ def decode_gemv(kind: str = "reference"):
             if rc != 0:
                 raise ValueError(f"orc_gemv_f32 rc={rc}")
         return f, 1
+    if kind == "ggml_q8":
+        o = Oracle()
+        gemv = o.lib.orc_gemv_q4_0_q8_0
+
+        def f(i, w, N, K, x, y):
+            rc = gemv(ctypes.cast(w, _u8p), N, K, ctypes.cast(x, _f32p), ctypes.cast(y, _f32p))
+            if rc != 0:
+                raise ValueError(f"orc_gemv_q4_0_q8_0 rc={rc}")
+        return f, os.cpu_count() or 1
     raise ValueError(kind)

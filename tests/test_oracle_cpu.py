@@ -485,3 +485,84 @@ def test_quantize_q4_0_invariants(oracle):
     idx = np.argmax(np.abs(blk), axis=2)
     at = np.take_along_axis(dq, idx[..., None], axis=2)[..., 0]
     assert np.array_equal(at, -8 * d)
+
+
+# ---- ggml-cpu Q4_0 x Q8_0 numerics (external restatement) -------------------
+# ggml is not vendored in the reference, so this path cannot be compared with
+# ggml itself here ("parity unpinned"); what the mathematics fixes is pinned.
+
+def test_f32_to_fp16_matches_numpy_round_to_even(oracle):
+    # every fp16 value round-trips, and every midpoint between neighbours
+    # rounds to the even one -- numpy's float16 conversion is independent
+    h = np.arange(0x10000, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(f)
+    got = np.array([oracle.f32_to_fp16(float(v)) for v in f[finite]], dtype=np.uint16)
+    assert np.array_equal(got, h[finite])
+    pos = np.arange(0x0000, 0x7bff, dtype=np.uint16)
+    lo = pos.view(np.float16).astype(np.float64)
+    hi = (pos + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)  # exact in f32
+    want = mid.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_fp16(float(v)) for v in mid], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    for v, bits in ((65520.0, 0x7C00), (65519.0, 0x7BFF), (-1e30, 0xFC00), (2.0 ** -25, 0x0000),
+                    (2.0 ** -24, 0x0001), (float("inf"), 0x7C00)):
+        assert oracle.f32_to_fp16(v) == bits, v
+
+
+def test_q8_0_quantization_invariants(oracle):
+    rng = np.random.default_rng(77)
+    x = (rng.standard_normal(32 * 64) * np.repeat(10.0 ** rng.uniform(-6, 6, 64), 32)).astype(np.float32)
+    x[32:64] = 0.0
+    q = oracle.quantize_q8_0(x).reshape(-1, 34)
+    codes = q[:, 2:].view(np.int8).astype(np.int32)
+    d16 = q[:, 0:2].copy().view(np.uint16).reshape(-1)
+    xb = x.reshape(-1, 32).astype(np.float64)
+    amax = np.abs(xb).max(axis=1)
+    d = (amax.astype(np.float32) / np.float32(127)).astype(np.float64)
+    assert np.all(np.abs(codes) <= 127)
+    # the absmax element is +-127; every value within half a step of q * d
+    for b in range(len(xb)):
+        if amax[b] == 0:
+            assert np.all(codes[b] == 0) and d16[b] == 0
+            continue
+        j = int(np.argmax(np.abs(xb[b])))
+        assert codes[b, j] == (127 if xb[b, j] > 0 else -127)
+        assert np.all(np.abs(xb[b] - codes[b] * d[b]) <= 0.5 * d[b] * (1 + 1e-6))
+        assert d16[b] == np.float32(d[b]).astype(np.float16).view(np.uint16)
+
+
+def test_gemv_q4_0_q8_0_against_f32_path_on_dequantized_activation(oracle):
+    # the blocked integer form equals the f32 GEMV of the same weights against
+    # the dequantized Q8_0 activation, up to f32 rounding of the two orders
+    N, K = 96, 2048
+    raw = synth.random_q4_0(N, K, seed=31)
+    x = synth.activations(K, seed=32)
+    y8 = oracle.gemv_q4_0_q8_0(raw, N, K, x)
+    q = oracle.quantize_q8_0(x).reshape(-1, 34)
+    dx = np.array([oracle.fp16_to_f32(int(v)) for v in q[:, 0:2].copy().view(np.uint16).reshape(-1)], np.float32)
+    xd = (q[:, 2:].view(np.int8).astype(np.float32) * dx[:, None]).reshape(-1)
+    yf = oracle.gemv(2, raw, N, K, xd)
+    norms = oracle.row_norms(2, raw, N, K)
+    assert np.all(np.abs(y8 - yf) <= 1e-5 * norms * np.linalg.norm(xd))
+    # and both are close to the f32-activation GEMV (what Q8_0 costs)
+    y32 = oracle.gemv(2, raw, N, K, x)
+    assert np.all(np.abs(y8 - y32) <= 2e-2 * norms * np.linalg.norm(x))
+
+
+def test_gemv_q4_0_q8_0_known_answer(oracle):
+    # codes 9 (+1) with d = 1 against x = 1: Q8_0 gives d_x = fp16(1/127),
+    # q = 127, so each block adds 32 * 127 * fp16(1/127)
+    N, K = 3, 96
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:] = 0x99
+    raw = np.tile(blk, N * K // 32)
+    y = oracle.gemv_q4_0_q8_0(raw, N, K, np.ones(K, dtype=np.float32))
+    dx = np.float32(np.float32(1.0) / np.float32(127)).astype(np.float16).astype(np.float32)
+    per = np.float32(4064) * np.float32(1.0) * dx
+    want = np.float32(0)
+    for _ in range(K // 32):
+        want = np.float32(want + per)
+    assert np.array_equal(y, np.full(N, want, dtype=np.float32))
