@@ -233,8 +233,23 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                 "note": "every GEMV with ggml-cpu's Q8_0-activation arithmetic (quantize_row_q8_0 + "
                         "vec_dot_q4_0_q8_0, restated from ggml's generic C path; ggml is not in this build)",
             }
-            log(f"bench: decode: ggml Q8_0 numerics: token-identical {q8_same}"
-                + ("" if q8_same else f", first mismatch at {int(q8_diff[0])}"))
+            # the GPU in ggml-cpu numerics (MI355X_VARIANT_GGML_Q8) against it
+            model.set_variant(mi355x.VARIANT_GGML_Q8)
+            g8_toks, tg8 = model.generate(prompt, n_gen)
+            model.set_variant(mi355x.VARIANT_AUTO)
+            g8_same = np.array_equal(g8_toks, q8_toks)
+            g8_diff = np.nonzero(g8_toks != q8_toks)[0]
+            res["ggml_q8_numerics"].update({
+                "gpu_tok_s": round(passes / tg8["gen_s"], 2),
+                "gpu_token_identical": bool(g8_same),
+                "gpu_first_mismatch": None if g8_same else int(g8_diff[0]),
+                "gpu_note": "the GPU decode with MI355X_VARIANT_GGML_Q8 (activations quantized to Q8_0 in the "
+                            "kernel, integer block dots) against the CPU decode with the restated ggml arithmetic",
+            })
+            log(f"bench: decode: ggml Q8_0 numerics: f32-path tokens identical {q8_same}"
+                + ("" if q8_same else f" (first mismatch at {int(q8_diff[0])})")
+                + f"; GPU GGML_Q8 variant {passes / tg8['gen_s']:.1f} tok/s, tokens identical {g8_same}"
+                + ("" if g8_same else f" (first mismatch at {int(g8_diff[0])})"))
     finally:
         model.close()
     return res

@@ -84,7 +84,12 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
- *       for the K/IQ types with int8 dot4 products).
+ *       for the K/IQ types with int8 dot4 products),
+ *     MI355X_VARIANT_GGML_Q8 (Q4_0 only: the arithmetic of ggml's CPU backend
+ *       -- the activation row quantized to Q8_0 per 32-value block, integer
+ *       block dot products scaled by d_w * d_x -- so that results follow
+ *       ggml-cpu rather than the f32 references; other types return
+ *       MI355X_EUNSUPPORTED in this variant).
  *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step
  *     (rows and K-split forms); 4, 8 or 16 rows per step (stream form).
  *   MI355X_OPT_WAVES_PER_GROUP: 0 (auto), 8 or 16 wavefronts per workgroup
@@ -107,6 +112,7 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 #define MI355X_VARIANT_AUTO 0
 #define MI355X_VARIANT_EXACT_F32 1
 #define MI355X_VARIANT_DIGITS 2
+#define MI355X_VARIANT_GGML_Q8 3
 #define MI355X_FORM_AUTO 0
 #define MI355X_FORM_ROWS 1
 #define MI355X_FORM_KSPLIT 2

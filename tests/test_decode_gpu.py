@@ -97,3 +97,28 @@ def test_mapped_io_matches_staged_io():
         assert np.array_equal(lm, m.last_logits())
         with pytest.raises(RuntimeError, match="unknown mode"):
             m.set_io(7)
+
+
+@pytest.mark.parametrize("cfg", [TINY, SHAPE_3B_2L], ids=["tiny", "3b_2layers"])
+def test_ggml_numerics_decode_token_identical_to_cpu(cfg):
+    """With the GGML_Q8 kernel variant (activations quantized to Q8_0 as
+    ggml-cpu does) the GPU decode picks the tokens of the CPU decode that uses
+    the oracle's restatement of ggml-cpu's Q4_0 x Q8_0 arithmetic."""
+    import mi355x
+    with decode.Model(threads=8, **cfg) as m:
+        p = decode.prompt_tokens(9, cfg["vocab"], 3)
+        f, _ = orc.decode_gemv("ggml_q8")
+        cpu_toks, _ = m.generate(p, 8, f)
+        cpu_logits = m.last_logits()
+        m.attach_gpu(0)
+        m.set_variant(mi355x.VARIANT_GGML_Q8)
+        gpu_toks, _ = m.generate(p, 8)
+        gpu_logits = m.last_logits()
+        m.set_variant(mi355x.VARIANT_AUTO)
+    # every GEMV is bit-identical to the restatement and the host ops are the
+    # same code, so the whole decode is: tokens and logits alike.  (Q8_0
+    # codes are discrete -- any upstream rounding difference could move an
+    # activation across a code boundary and grow from layer to layer -- so
+    # anything short of bit-identical GEMVs would not hold the tokens.)
+    assert np.array_equal(gpu_toks, cpu_toks), (gpu_toks, cpu_toks)
+    assert np.array_equal(gpu_logits, cpu_logits)

@@ -290,3 +290,63 @@ def test_stream_form_edges(ctx, oracle):
         check_gemv(y, oracle.gemv(Q4_0, raw, N, K, x), oracle.row_norms(Q4_0, raw, N, K), x, "stream misaligned x")
     finally:
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+
+
+def check_q8(ctx, oracle, raw, N, K, x, what):
+    """GGML_Q8 variant against the oracle's ggml-cpu restatement: the same
+    quantization, the same per-block products ((sumi * d_w) * d_x, sumi
+    exact) and the same sequential block sum -- bit-identical."""
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_GGML_Q8)
+    try:
+        y = run_gpu(ctx, raw, N, K, x)
+    finally:
+        ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+    ref = oracle.gemv_q4_0_q8_0(raw, N, K, x)
+    bad = np.nonzero(y.view(np.uint32) != ref.view(np.uint32))[0]
+    assert bad.size == 0, f"{what}: {bad.size} rows differ, first {bad[:5]} y={y[bad[:3]]} ref={ref[bad[:3]]}"
+    return y, ref
+
+
+def test_ggml_q8_single_block_rows(ctx, oracle, variant):
+    if variant != "digits":
+        pytest.skip("one run is enough")
+    N, K = 1000, 32
+    raw = synth.random_q4_0(N, K, seed=61)
+    x = synth.activations(K, seed=62)
+    check_q8(ctx, oracle, raw, N, K, x, "K=32")
+
+
+@pytest.mark.parametrize("N,K", [(1, 64), (33, 96), (127, 128), (513, 2048), (4096, 4096), (300, 5120),
+                                 (2048, 11008), (64, 16384), (8192, 8192), (151936, 2048)])
+def test_ggml_q8_matches_oracle(ctx, oracle, variant, N, K):
+    if variant != "digits":
+        pytest.skip("one run is enough")
+    raw = synth.quantize_q4_0(synth.normal_weights(N, K, seed=N + K))
+    x = synth.activations(K, seed=K + 1)
+    x[::97] *= np.float32(40.0)  # blocks with a dominant value
+    x[5:37] = 0.0  # an all-zero block (d = 0, id = 0)
+    check_q8(ctx, oracle, raw, N, K, x, f"{N}x{K}")
+
+
+def test_ggml_q8_is_not_the_f32_path(ctx, oracle, variant):
+    """Q8_0 activations are coarser than the f32 path: the variant must land
+    on the ggml-cpu numbers, not on the f32 reference."""
+    if variant != "digits":
+        pytest.skip("one run is enough")
+    N, K = 256, 4096
+    raw = synth.random_q4_0(N, K, seed=71)
+    x = synth.activations(K, seed=72)
+    y, ref8 = check_q8(ctx, oracle, raw, N, K, x, "q8 vs f32")
+    ref32 = oracle.gemv(Q4_0, raw, N, K, x)
+    assert np.max(np.abs(y - ref8)) < 0.05 * np.max(np.abs(ref8 - ref32))
+
+
+def test_ggml_q8_rejects_other_inputs(ctx):
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_GGML_Q8)
+    buf = ctx.alloc(1 << 16)
+    try:
+        assert ctx.gemv_ptr(Q4_0, buf.ptr, 4, 256, buf.ptr, buf.ptr + 4096, bf16=True) == mi355x.EUNSUPPORTED
+        assert ctx.gemv_ptr(mi355x.Q4_K, buf.ptr, 4, 256, buf.ptr, buf.ptr + 4096) == mi355x.EUNSUPPORTED
+    finally:
+        buf.free()
+        ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)

@@ -1033,6 +1033,8 @@ __global__ void bf16_to_f32_kernel(const uint16_t *__restrict__ in, float *__res
 }  // namespace
 
 int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
+    if (ctx->kernel_variant == MI355X_VARIANT_GGML_Q8)
+        return set_error(MI355X_EUNSUPPORTED, "the ggml-cpu numerics variant covers Q4_0 weights only");
     const KqLayout L = kq_layout(a.type);
     if (L.block_bytes == 0) return set_error(MI355X_EUNSUPPORTED, "unsupported weight type for the K/IQ kernels");
     const int64_t B = a.K / 256;

@@ -195,6 +195,12 @@ int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a) {
         return set_error(MI355X_EUNSUPPORTED, "Q4_0 GEMV: N or K beyond 32-bit kernel indexing");
     if (reinterpret_cast<uintptr_t>(a.W) % 2 != 0)
         return set_error(MI355X_EINVAL, "Q4_0 GEMV: weight pointer must be 2-byte aligned");
+    if (ctx->kernel_variant == MI355X_VARIANT_GGML_Q8) {
+        if (!q4_0_q8_supports(ctx, a))
+            return set_error(MI355X_EUNSUPPORTED,
+                             "Q4_0 GEMV: the ggml-cpu numerics variant takes f32 activations and K <= 16384");
+        return launch_gemv_q4_0_q8(ctx, a);
+    }
     if (ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && ctx->form_override == MI355X_FORM_STREAM &&
         q4_0_st_supports(ctx, a))
         return launch_gemv_q4_0_st(ctx, a);

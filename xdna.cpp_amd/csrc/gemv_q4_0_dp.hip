@@ -486,6 +486,164 @@ dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail, bool pf) {
     }
 }
 
+// ---- ggml-cpu numerics ------------------------------------------------------
+// ggml's CPU backend does not multiply Q4_0 weights by f32 activations: it
+// quantizes the activation row to Q8_0 and takes integer block dot
+// products (quantize_row_q8_0 and ggml_vec_dot_q4_0_q8_0 of ggml, llama.cpp
+// 0ec4027a2; ggml is not part of the reference).  This kernel reproduces
+// that arithmetic so that decode can pick ggml-cpu's tokens:
+//   staging, per 32-value block (a DPP quad of 4 threads, as the digit
+//   staging): amax = max|x_j|, d = amax / 127, id = d ? 1/d : 0,
+//   q_j = roundf(x_j * id), d_x = f32(fp16(d)) (round to even), S = sum q_j;
+//   LDS holds the codes as two planes Q[h][b] (uint4; byte e of dword k is
+//   value 16h + 4k + e, the nibble order of the Q4_0 code dwords), d_x and S;
+//   per block: sumi = sum_j (q4_j - 8) q8_j  (exact: v_dot4_i32_i8 on the
+//   unsigned nibbles, minus 8 S), contribution (float(sumi) * d_w) * d_x,
+//   ggml's expression order.  Blocks are summed per lane, then across the
+//   wavefront: the same products as ggml's generic path, re-associated.
+template <int XI>
+__device__ __forceinline__ void q8_stage(const XTile<XI> &xt, int B, uint32_t *Q, float *dx, int *sx) {
+#pragma unroll
+    for (int it = 0; it < XI; ++it) {
+        const int i = threadIdx.x + it * blockDim.x;
+        const int ic = min(i, 4 * B - 1);
+        const int b = ic >> 2, k = ic & 3;
+        // XTile order: v[2e] = value 4k+e, v[2e+1] = value 16+4k+e
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xt.v[it][e]));
+        amax = fmaxf(amax, dpp_mov<0xB1>(amax));
+        amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+        // correctly rounded division, reciprocal and products, as ggml's C
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        uint32_t lo = 0, hi = 0;
+        int sum = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int ql = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e], id)));
+            const int qh = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e + 1], id)));
+            lo |= (static_cast<uint32_t>(ql) & 0xFFu) << (8 * e);
+            hi |= (static_cast<uint32_t>(qh) & 0xFFu) << (8 * e);
+            sum += ql + qh;
+        }
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, false);
+        if (i < 4 * B) {
+            Q[b * 4 + k] = lo;
+            Q[(B + b) * 4 + k] = hi;
+            if (k == 0) {
+                dx[b] = static_cast<float>(static_cast<_Float16>(d));
+                sx[b] = sum;
+            }
+        }
+    }
+}
+
+// Block contributions (float(sumi) * d_w) * d_x of R rows into cs[r * B + b]
+// (blocks past the row end are not written).
+template <int NBL, int R, bool A16, bool TAIL>
+__device__ __forceinline__ void q8_blocks(const RowGroup<NBL, R, A16, TAIL> &g, float *cs, const uint4 *Q,
+                                          const float *dx, const int *sx, int B, int lane, const int bc[NBL],
+                                          uint32_t tail_mask) {
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) {
+        if (j > 0) __builtin_amdgcn_sched_barrier(0);
+        const uint4 q0 = Q[bc[j]], q1 = Q[B + bc[j]];
+        const float d_x = dx[bc[j]];
+        const int s8 = sx[bc[j]];
+        const uint32_t a[4] = {q0.x, q0.y, q0.z, q0.w};
+        const uint32_t c[4] = {q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int dot = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // resident code bytes hold q - 8 per nibble; XOR 8 gives q
+                const uint32_t u = g.q[r][j][k] ^ 0x88888888u;
+                dot = __builtin_amdgcn_sdot4(static_cast<int>(u & 0x0F0F0F0Fu), static_cast<int>(a[k]), dot, false);
+                dot = __builtin_amdgcn_sdot4(static_cast<int>((u >> 4) & 0x0F0F0F0Fu), static_cast<int>(c[k]), dot,
+                                             false);
+            }
+            const int sumi = dot - 8 * s8;
+            const float dw = half_bits_to_float(static_cast<uint16_t>(g.d_bits(r, j, tail_mask)));
+            if (lane + 64 * j < B) cs[r * B + lane + 64 * j] = __fmul_rn(__fmul_rn(static_cast<float>(sumi), dw), d_x);
+        }
+    }
+}
+
+// LDS: Q planes (2 * B uint4), d_x (B floats), S (B ints), then the block
+// contributions of every wavefront's rows (WAVES * R * B floats).  Each row
+// is summed by one lane in block order, ggml's sequential f32 sum, so the
+// result is bit-identical to ggml's generic path for the same activations.
+template <int NBL, int R, bool A16, bool TAIL>
+__global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                           float *__restrict__ y, int N, int B, int64_t row_bytes,
+                                                           int x_al16) {
+    constexpr int WAVES = 8;
+    extern __shared__ uint4 lds_q8[];
+    uint4 *Q = lds_q8;
+    float *dx = reinterpret_cast<float *>(lds_q8 + 2 * B);
+    int *sx = reinterpret_cast<int *>(dx + B);
+    float *cs_all = reinterpret_cast<float *>(sx + B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    constexpr int ROWS = WAVES * R;
+    const int n_groups = (N + ROWS - 1) / ROWS;
+    int bc[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
+    const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
+
+    // activation loads, then the first group's weights, then the staging
+    // math (loads retire in order)
+    constexpr int XI = (4 * NBL + WAVES - 1) / WAVES;
+    XTile<XI> xt;
+    xt.load(x, B, x_al16 != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    int g = blockIdx.x;
+    RowGroup<NBL, R, A16, TAIL> grp;
+    grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+    q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dx, sx);
+    __syncthreads();
+
+    float *cs = cs_all + wave * R * B;
+    while (g < n_groups) {
+        const int row0 = g * ROWS + wave * R;
+        q8_blocks<NBL, R, A16, TAIL>(grp, cs, Q, dx, sx, B, lane, bc, tail_mask);
+        g += gridDim.x;
+        grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+        __syncthreads();
+        if (lane < R) {
+            float sumf = 0.0f;
+            for (int b = 0; b < B; ++b) sumf = __fadd_rn(sumf, cs[lane * B + b]);
+            if (row0 + lane < N) y[row0 + lane] = sumf;
+        }
+        __syncthreads();
+    }
+}
+
+template <int NBL, int R>
+dp_kernel_t pick_q8_at(bool a16, bool tail) {
+    if (a16) return tail ? gemv_q4_0_q8_kernel<NBL, R, true, true> : gemv_q4_0_q8_kernel<NBL, R, true, false>;
+    return tail ? gemv_q4_0_q8_kernel<NBL, R, false, true> : gemv_q4_0_q8_kernel<NBL, R, false, false>;
+}
+
+// rows per wavefront as the digit kernel's defaults: 4 for one block
+// column, 2 for two, 1 beyond
+dp_kernel_t pick_q8(int nbl, bool a16, bool tail) {
+    switch (nbl) {
+    case 1: return pick_q8_at<1, 4>(a16, tail);
+    case 2: return pick_q8_at<2, 2>(a16, tail);
+    case 3: return pick_q8_at<3, 1>(a16, tail);
+    case 4: return pick_q8_at<4, 1>(a16, tail);
+    case 5: return pick_q8_at<5, 1>(a16, tail);
+    case 6: return pick_q8_at<6, 1>(a16, tail);
+    case 7: return pick_q8_at<7, 1>(a16, tail);
+    default: return pick_q8_at<8, 1>(a16, tail);
+    }
+}
+
 }  // namespace
 
 // Largest blocks-per-row the digit-plane kernel takes (8 blocks per lane).
@@ -546,6 +704,43 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds, ctx->stream, a.W,
                        static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),
                        row_bytes, x_al16 ? 1 : 0);
+    MI355X_HIP(hipGetLastError());
+    return MI355X_OK;
+}
+
+}  // namespace mi355x
+
+namespace mi355x {
+
+size_t q8_lds_bytes(int64_t B) {
+    const int nbl = static_cast<int>((B + 63) / 64);
+    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
+    return static_cast<size_t>(B) * (2 * sizeof(uint4) + sizeof(float) + sizeof(int) + 8 * R * sizeof(float));
+}
+
+bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a) {
+    const int64_t B = a.K / 32;
+    const size_t lds = q8_lds_bytes(B);
+    return !a.x_bf16 && B > 0 && B <= kDpMaxBlocks && lds <= ctx->max_lds_per_block && a.N <= INT32_MAX &&
+           static_cast<int64_t>(a.N) * 18 * B < (int64_t(1) << 40);
+}
+
+int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a) {
+    const int64_t B = a.K / 32;
+    const int64_t row_bytes = 18 * B;
+    const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
+    const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
+    const int nbl = static_cast<int>((B + 63) / 64);
+    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
+    const dp_kernel_t k = pick_q8(nbl, a16, B % 64 != 0);
+    const size_t lds = q8_lds_bytes(B);
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, lds);
+    const int64_t n_groups = (a.N + 8 * R - 1) / (8 * R);
+    int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
+    if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(grid, 1))), dim3(512), lds, ctx->stream, a.W,
+                       static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B), row_bytes,
+                       x_al16 ? 1 : 0);
     MI355X_HIP(hipGetLastError());
     return MI355X_OK;
 }

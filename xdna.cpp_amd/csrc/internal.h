@@ -64,6 +64,8 @@ int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_st_supports(const mi355x_ctx *ctx, const GemvArgs &a);
+bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a);
+int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_st(mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a);
 

@@ -259,7 +259,8 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: null context");
     switch (option) {
     case MI355X_OPT_VARIANT:
-        if (value != MI355X_VARIANT_AUTO && value != MI355X_VARIANT_EXACT_F32 && value != MI355X_VARIANT_DIGITS)
+        if (value != MI355X_VARIANT_AUTO && value != MI355X_VARIANT_EXACT_F32 && value != MI355X_VARIANT_DIGITS &&
+            value != MI355X_VARIANT_GGML_Q8)
             return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: unknown kernel variant");
         ctx->kernel_variant = static_cast<int>(value);
         return MI355X_OK;

@@ -52,6 +52,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_last_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_quantize_q4_0.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
     lib.qd_set_fuse.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_set_variant.restype = C.c_int
+    lib.qd_set_variant.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_io.restype = C.c_int
     lib.qd_set_io.argtypes = [C.c_void_p, C.c_int]
     lib.qd_last_launches.restype = C.c_int64
@@ -126,6 +128,11 @@ class Model:
 
     def set_fuse(self, on: bool) -> None:
         self.lib.qd_set_fuse(self.h, 1 if on else 0)
+
+    def set_variant(self, variant: int) -> None:
+        """GEMV kernel variant on the GPU path (mi355x.VARIANT_*)."""
+        if self.lib.qd_set_variant(self.h, variant) != 0:
+            raise RuntimeError(self.lib.qd_last_error().decode())
 
     IO_STAGED, IO_MAPPED = 0, 1
 

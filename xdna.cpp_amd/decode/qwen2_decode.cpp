@@ -433,6 +433,13 @@ void qd_set_fuse(qd_model *m, int on) {
     if (m) m->fuse = on != 0;
 }
 
+int qd_set_variant(qd_model *m, int variant) {
+    if (!m || !m->ctx) return fail("qd_set_variant: qd_attach_gpu first");
+    if (mi355x_ctx_set_option(m->ctx, MI355X_OPT_VARIANT, variant) != MI355X_OK)
+        return fail(std::string("qd_set_variant: ") + mi355x_last_error());
+    return 0;
+}
+
 int qd_set_io(qd_model *m, int mode) {
     if (!m) return fail("qd_set_io: null model");
     if (mode != QD_IO_STAGED && mode != QD_IO_MAPPED) return fail("qd_set_io: unknown mode");

@@ -85,6 +85,9 @@ QD_API void qd_set_fuse(qd_model *m, int on);
 #define QD_IO_STAGED 0
 #define QD_IO_MAPPED 1
 QD_API int qd_set_io(qd_model *m, int mode);
+/* Kernel variant of the GPU GEMVs (MI355X_OPT_VARIANT of mi355x-gemv.h):
+ * MI355X_VARIANT_GGML_Q8 gives ggml-cpu's Q8_0-activation arithmetic. */
+QD_API int qd_set_variant(qd_model *m, int variant);
 /* GPU GEMV launches in the generation phase of the last qd_generate. */
 QD_API int64_t qd_last_launches(const qd_model *m);
 
