@@ -102,7 +102,11 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     rows), MI355X_FORM_KSPLIT (a wavefront owns one 64-block column of 2 or
  *     4 rows; needs rows of a multiple of 8 blocks), MI355X_FORM_STREAM (one
  *     workgroup per CU; a lane owns one block of every row of its team and
- *     keeps that block's activation digits in registers; K <= 16384). */
+ *     keeps that block's activation digits in registers; K <= 16384),
+ *     MI355X_FORM_PIPE (one workgroup of four wavefronts per CU, each
+ *     wavefront owning a run of consecutive rows whose loads are issued
+ *     three rows ahead of their dot products; K a multiple of 2048 up to
+ *     16384, 16-byte aligned weights and activation row). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3
@@ -117,6 +121,7 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 #define MI355X_FORM_ROWS 1
 #define MI355X_FORM_KSPLIT 2
 #define MI355X_FORM_STREAM 3
+#define MI355X_FORM_PIPE 4
 MI355X_API int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value);
 
 /* ---- memory ----------------------------------------------------------------

@@ -350,3 +350,81 @@ def test_ggml_q8_rejects_other_inputs(ctx):
     finally:
         buf.free()
         ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+
+
+def gemv_with_form(ctx, raw, N, K, x, form, rows=0):
+    ctx.set_option(mi355x.OPT_FORM, form)
+    ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, rows)
+    try:
+        return run_gpu(ctx, raw, N, K, x)
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+
+
+@pytest.mark.parametrize("N,K", [(1, 2048), (5, 2048), (1023, 2048), (2560, 2048), (4097, 4096), (8192, 8192),
+                                 (17, 6144), (1000, 10240), (999, 12288), (2048, 14336), (300, 16384),
+                                 (1024, 8192), (3000, 8192), (17408, 4096), (151936, 2048)])
+def test_pipelined_form(ctx, oracle, variant, N, K):
+    """The pipelined work split (one workgroup of four wavefronts per CU,
+    runs of consecutive rows per wavefront, loads three rows ahead, digit
+    planes in registers) against the oracle, and bit for bit against the row
+    form with one row per wavefront, whose per-row arithmetic it shares:
+    every block-column count 1..8, row counts that leave the last wavefronts
+    partly or wholly empty, each compiled rows-per-wavefront count and the
+    run-time count (17408 and 151936 rows)."""
+    if variant != "digits":
+        pytest.skip("the pipelined form is a digit-plane kernel")
+    raw = synth.random_q4_0(N, K, seed=N + 3 * K)
+    x = synth.activations(K, seed=K + 7)
+    y = gemv_with_form(ctx, raw, N, K, x, mi355x.FORM_PIPE)
+    check_gemv(y, oracle.gemv(Q4_0, raw, N, K, x), oracle.row_norms(Q4_0, raw, N, K), x, f"pipelined {N}x{K}")
+    y_rows = gemv_with_form(ctx, raw, N, K, x, mi355x.FORM_ROWS, rows=1)
+    bad = np.nonzero(y.view(np.uint32) != y_rows.view(np.uint32))[0]
+    assert bad.size == 0, f"pipelined {N}x{K}: {bad.size} rows differ from the row form, first {bad[:5]}"
+
+
+def test_pipelined_form_edges(ctx, oracle):
+    """Known answer, non-finite activations poisoning every row, and the
+    shapes the pipelined form does not take (K not a multiple of 2048, a
+    misaligned activation row), which go to the other forms."""
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE)
+    try:
+        N, K = 128, 2048
+        blk = np.zeros(18, dtype=np.uint8)
+        blk[0:2] = [0x00, 0x3C]
+        blk[2:] = 0x99
+        y = run_gpu(ctx, np.tile(blk, N * K // 32), N, K, np.full(K, 0.5, dtype=np.float32))
+        assert np.array_equal(y, np.full(N, 1024.0, dtype=np.float32))
+
+        N, K = 64, 4096
+        raw = synth.random_q4_0(N, K, seed=3)
+        x = synth.activations(K, seed=4)
+        x[40] = np.inf
+        x[3000] = np.nan
+        assert np.all(np.isnan(run_gpu(ctx, raw, N, K, x)))
+
+        for N, K in ((300, 5120), (64, 256), (33, 11008)):
+            raw = synth.random_q4_0(N, K, seed=N + K)
+            x = synth.activations(K, seed=K)
+            parity(ctx, oracle, raw, N, K, x, f"pipelined fallback {N}x{K}")
+
+        N, K = 300, 2048
+        raw = synth.random_q4_0(N, K, seed=5)
+        x = synth.activations(K, seed=6)
+        w = ctx.resident(Q4_0, raw, N, K)
+        xb = ctx.alloc(4 * K + 16)
+        yb = ctx.alloc(4 * N)
+        try:
+            xb.upload(x, offset=4)
+            mi355x.check(ctx.gemv_ptr(Q4_0, w.ptr, N, K, xb.ptr + 4, yb.ptr))
+            ctx.sync()
+            y = yb.download(np.float32, N)
+        finally:
+            w.free()
+            xb.free()
+            yb.free()
+        check_gemv(y, oracle.gemv(Q4_0, raw, N, K, x), oracle.row_norms(Q4_0, raw, N, K), x,
+                   "pipelined misaligned x")
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)

@@ -429,6 +429,139 @@ __global__ __launch_bounds__(64 * G * NBL) void gemv_q4_0_ks_kernel(const uint8_
     }
 }
 
+// ---- pipelined form ---------------------------------------------------------
+// Measured on MI355X, a wavefront that issues every load of its rows before
+// it stages the activation row stalls at the loads: the CU accepts vector
+// memory requests only as earlier ones drain, so the staging math and the
+// first dot products wait until most of the matrix has streamed in, and
+// the dot products then run after the stream instead of under it.  Here:
+//  * one workgroup of four wavefronts per CU (the grid never exceeds the CU
+//    count, so every workgroup is resident from the start); wavefront v owns
+//    the consecutive rows [v*RW, v*RW + RW);
+//  * the activation loads go first, then the weight loads of the first two
+//    rows, then the staging math (which waits only for the activations),
+//    then the loads of row 3; a row's loads are issued D rows ahead of its
+//    dot product, so at most D rows per wavefront are in flight;
+//  * after staging, each lane copies the digit planes of its NBL blocks
+//    from LDS into registers once (20 * NBL VGPRs), so the dot products read
+//    no LDS;
+//  * rows are full 64-block columns (B = 64 * NBL) of 16-byte aligned rows.
+// Per row the arithmetic is the row form's (R = 1): same block order, same
+// expressions, so the results are bit-identical to it.
+// RW > 0: RW rows per wavefront, fully unrolled.  RW == 0: the row count is
+// the argument rw (loop unrolled by D; loads past the wavefront's rows are
+// issued against an empty range and read nothing).
+constexpr int kPlWaves = 4;
+constexpr int kPlDepth = 3;
+
+template <int NBL, int RW>
+__global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
+    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int B,
+    int64_t row_bytes, int x_al16, int rw) {
+    constexpr int D = (RW > 0 && RW < kPlDepth) ? RW : kPlDepth;
+    constexpr int ND0 = D < 2 ? D : 2;  // rows requested before the staging math
+    extern __shared__ uint4 lds_pl[];
+    uint4 *planes = lds_pl;
+    float *ub = reinterpret_cast<float *>(lds_pl + kPlanes * B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int rows = RW > 0 ? RW : rw;
+    const int row0 = (blockIdx.x * kPlWaves + wave) * rows;
+    // rows of this wavefront that exist; loads past them read nothing
+    const int lim = min(N, row0 + rows);
+    const int nrows = max(0, lim - row0);
+
+    constexpr int XI = (4 * NBL + kPlWaves - 1) / kPlWaves;
+    XTile<XI> xt;
+    xt.load(x, B, x_al16 != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    RowGroup<NBL, 1, true, false> g[D];
+#pragma unroll
+    for (int s = 0; s < ND0; ++s) g[s].load(W, row0 + s, lim, B, row_bytes, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = ND0; s < D; ++s) g[s].load(W, row0 + s, lim, B, row_bytes, lane);
+    __syncthreads();
+
+    uint4 P[NBL][kPlanes];
+    float u[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) {
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) P[j][p] = planes[p * B + lane + 64 * j];
+        u[j] = ub[lane + 64 * j];
+    }
+
+    auto row_dot = [&](const RowGroup<NBL, 1, true, false> &grp) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NBL; ++j) {
+            const int T = block_dot_digits(grp.q[0][j], P[j]);
+            const float dr = half_bits_to_float(static_cast<uint16_t>(grp.d_bits(0, j, 0xFFFFu)));
+            acc = fmaf(dr * u[j], static_cast<float>(T), acc);
+        }
+        return acc;
+    };
+
+    if constexpr (RW > 0) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const float acc = row_dot(g[r % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (r + D < RW) g[r % D].load(W, row0 + r + D, lim, B, row_bytes, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            const float s = wave_sum(acc);
+            if (lane == 0 && r < nrows) y[row0 + r] = s;
+        }
+    } else {
+        for (int r0 = 0; r0 < nrows; r0 += D) {
+#pragma unroll
+            for (int s = 0; s < D; ++s) {
+                const int r = r0 + s;
+                const float acc = row_dot(g[s]);
+                __builtin_amdgcn_sched_barrier(0);
+                g[s].load(W, row0 + r + D, lim, B, row_bytes, lane);
+                __builtin_amdgcn_sched_barrier(0);
+                const float sum = wave_sum(acc);
+                if (lane == 0 && r < nrows) y[row0 + r] = sum;
+            }
+        }
+    }
+}
+
+typedef void (*pl_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int, int);
+
+// compiled rows-per-wavefront counts of the unrolled kernel
+constexpr int kPlRows[] = {1, 2, 3, 4, 6, 8};
+
+template <int NBL>
+pl_kernel_t pick_pl_rw(int rw) {
+    switch (rw) {
+    case 1: return gemv_q4_0_pl_kernel<NBL, 1>;
+    case 2: return gemv_q4_0_pl_kernel<NBL, 2>;
+    case 3: return gemv_q4_0_pl_kernel<NBL, 3>;
+    case 4: return gemv_q4_0_pl_kernel<NBL, 4>;
+    case 6: return gemv_q4_0_pl_kernel<NBL, 6>;
+    case 8: return gemv_q4_0_pl_kernel<NBL, 8>;
+    default: return gemv_q4_0_pl_kernel<NBL, 0>;
+    }
+}
+
+pl_kernel_t pick_pl(int nbl, int rw) {
+    switch (nbl) {
+    case 1: return pick_pl_rw<1>(rw);
+    case 2: return pick_pl_rw<2>(rw);
+    case 3: return pick_pl_rw<3>(rw);
+    case 4: return pick_pl_rw<4>(rw);
+    case 5: return pick_pl_rw<5>(rw);
+    case 6: return pick_pl_rw<6>(rw);
+    case 7: return pick_pl_rw<7>(rw);
+    default: return pick_pl_rw<8>(rw);
+    }
+}
+
 typedef void (*ks_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int);
 
 template <int R>
@@ -662,6 +795,30 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
     const int nbl = static_cast<int>((B + 63) / 64);
+    // Pipelined form: full 64-block columns, 16-byte aligned rows and
+    // activation row.  By default wherever each wavefront gets at most 8 rows
+    // (one workgroup per CU; sweeps on MI355X: 8192x8192 7.8 vs 8.1 us).
+    const bool pl_ok = a16 && x_al16 && B % 64 == 0 && nbl <= 8;
+    const int64_t pl_need = (a.N + static_cast<int64_t>(ctx->num_cus) * kPlWaves - 1) /
+                            (static_cast<int64_t>(ctx->num_cus) * kPlWaves);
+    if (pl_ok && (ctx->form_override == MI355X_FORM_PIPE ||
+                  (ctx->form_override == MI355X_FORM_AUTO && pl_need <= kPlRows[5]))) {
+        int rw = 0;  // runtime row count unless a compiled count covers pl_need
+        for (int c : kPlRows)
+            if (c >= pl_need) {
+                rw = c;
+                break;
+            }
+        const int rows = rw > 0 ? rw : static_cast<int>(pl_need);
+        const pl_kernel_t k = pick_pl(nbl, rw);
+        const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float));
+        const int64_t grid = (a.N + static_cast<int64_t>(rows) * kPlWaves - 1) / (static_cast<int64_t>(rows) * kPlWaves);
+        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * kPlWaves), lds, ctx->stream, a.W,
+                           static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B), row_bytes,
+                           1, rows);
+        MI355X_HIP(hipGetLastError());
+        return MI355X_OK;
+    }
     // K-split form: 16-byte aligned rows.  By default (sweeps on MI355X) for
     // tall matrices with 1 or 3 block columns (151936x2048: 26.9 vs 27.8 us,
     // 17408x5120: 9.8 vs 10.1 us), with 2 rows per wavefront; the row form

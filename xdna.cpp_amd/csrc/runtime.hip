@@ -281,9 +281,9 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
         return MI355X_OK;
     case MI355X_OPT_FORM:
         if (value != MI355X_FORM_AUTO && value != MI355X_FORM_ROWS && value != MI355X_FORM_KSPLIT &&
-            value != MI355X_FORM_STREAM)
+            value != MI355X_FORM_STREAM && value != MI355X_FORM_PIPE)
             return set_error(MI355X_EINVAL,
-                             "mi355x_ctx_set_option: form must be 0 (auto), 1 (rows), 2 (K-split) or 3 (stream)");
+                             "mi355x_ctx_set_option: form must be 0 (auto), 1 (rows), 2 (K-split), 3 (stream) or 4 (pipelined)");
         ctx->form_override = static_cast<int>(value);
         return MI355X_OK;
     case MI355X_OPT_GRID:
