@@ -80,7 +80,8 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 /* Per-context options.
  *   MI355X_OPT_VARIANT: which kernel family computes GEMVs --
  *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply,
- *       for the K/IQ types f32 activations),
+ *       for the K/IQ types f32 activations, except Q4_K/Q5_K/Q6_K rows of at
+ *       most 4096 values, which take the pipelined form's 22-bit digits),
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
@@ -97,7 +98,8 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups.
  *   MI355X_OPT_PREFETCH: 0 (auto), 1 (each wavefront requests its next row
  *     group before reducing the current one), 2 (off).
- *   MI355X_OPT_FORM: work split of the digit-plane Q4_0 kernel --
+ *   MI355X_OPT_FORM: work split of the digit-plane kernels (Q4_0; the
+ *     pipelined form also for the K/IQ types) --
  *     MI355X_FORM_AUTO (default), MI355X_FORM_ROWS (a wavefront owns whole
  *     rows), MI355X_FORM_KSPLIT (a wavefront owns one 64-block column of 2 or
  *     4 rows; needs rows of a multiple of 8 blocks), MI355X_FORM_STREAM (one
@@ -105,8 +107,9 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     keeps that block's activation digits in registers; K <= 16384),
  *     MI355X_FORM_PIPE (one workgroup of four wavefronts per CU, each
  *     wavefront owning a run of consecutive rows whose loads are issued
- *     three rows ahead of their dot products; K a multiple of 2048 up to
- *     16384, 16-byte aligned weights and activation row). */
+ *     three rows ahead of their dot products; Q4_0: K a multiple of 2048
+ *     up to 16384, 16-byte aligned weights and activation row; K/IQ types:
+ *     22-bit digit arithmetic, any K). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3

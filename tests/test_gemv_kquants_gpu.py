@@ -40,15 +40,19 @@ def install_grids():
     yield
 
 
-@pytest.fixture(params=["digits", "exact_f32"], autouse=True)
+@pytest.fixture(params=["digits", "exact_f32", "pipelined"], autouse=True)
 def variant(request, ctx):
-    """Every test runs on both kernel families: activations as 22-bit digit
-    planes with integer dot products, and f32 activations as given (the
-    default for these types)."""
-    v = mi355x.VARIANT_DIGITS if request.param == "digits" else mi355x.VARIANT_EXACT_F32
+    """Every test runs on the three kernel families: activations as 22-bit
+    digit planes with integer dot products (several workgroups per CU), f32
+    activations as given, and the pipelined form (digit arithmetic, one
+    workgroup per CU, each lane's digit slices kept in registers)."""
+    v = mi355x.VARIANT_EXACT_F32 if request.param == "exact_f32" else mi355x.VARIANT_DIGITS
     ctx.set_option(mi355x.OPT_VARIANT, v)
+    if request.param == "pipelined":
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE)
     yield request.param
     ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
 
 
 def blocks(t, N, K, seed):
@@ -165,3 +169,26 @@ def test_grid_types_refuse_without_grid_or_bad_table(ctx):
     bad = np.zeros(7, dtype=np.uint8)
     with pytest.raises(mi355x.Mi355xError):
         mi355x.set_iq_grid(18, bad)
+
+
+@pytest.mark.parametrize("name", list(ALL))
+@pytest.mark.parametrize("N,K", [(1, 256), (5, 2048), (1023, 4096), (4096, 8192), (14336, 4096), (300, 14336),
+                                 (2000, 16384), (777, 11008)])
+def test_pipelined_matches_digit_kernel(ctx, name, variant, N, K):
+    """The pipelined form shares the digit kernel's per-row arithmetic (same
+    slices, step order and expressions), so the two agree bit for bit: every
+    step count 1..8 (registers or LDS for the slices), rows that leave the
+    last wavefronts partly or wholly empty, K beyond one LDS chunk (16384)."""
+    if variant != "digits":
+        pytest.skip("one run per shape is enough")
+    t = ALL[name]
+    raw = blocks(t, N, K, N + K)
+    x = np.random.default_rng(K).uniform(-0.5, 0.5, K).astype(np.float32)
+    y_dg = run(ctx, t, raw, N, K, x)
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE)
+    try:
+        y_pl = run(ctx, t, raw, N, K, x)
+    finally:
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+    bad = np.nonzero(y_pl.view(np.uint32) != y_dg.view(np.uint32))[0]
+    assert bad.size == 0, f"{name} {N}x{K}: {bad.size} rows differ, first {bad[:5]} {y_pl[bad[:3]]} {y_dg[bad[:3]]}"

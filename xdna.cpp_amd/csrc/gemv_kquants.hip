@@ -974,6 +974,186 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     }
 }
 
+// ---- pipelined form -----------------------------------------------------------
+// The kernel above re-reads each lane's activation slice from LDS for every
+// row and stages the activations once per workgroup, with several
+// workgroups per CU: measured on MI355X, its time hardly depends on the
+// weight bytes (12-16 us from 21 to 48 MB), i.e. LDS and VALU, not HBM, set
+// it.  This form applies what the Q4_0 pipelined form does:
+//  * one workgroup of four wavefronts per CU (grid <= CU count); wavefront v
+//    owns the consecutive rows [v*rows, v*rows + rows) of the launch;
+//  * activations as 22-bit digits (the digit path's arithmetic, v_dot4 on
+//    three signed-byte planes), staged once per CU; with XREG each lane then
+//    copies the digit slices of its NIT steps into registers once, so the
+//    row loop reads no LDS (32 VGPRs per step; NIT <= 4);
+//  * a row's loads are issued kPlqDepth rows ahead of its decode, the first
+//    two rows' before the staging math;
+//  * loads of rows past the wavefront's range use an empty buffer range and
+//    read nothing.
+// Per row the arithmetic is the digit kernel's (R = 1): same slices, same
+// step order, same expressions.
+constexpr int kPlqWaves = 4;
+constexpr int kPlqThreads = 64 * kPlqWaves;
+constexpr int kPlqDepth = 3;
+constexpr int kPlqStageBlocks = 2;  // 32-value blocks staged per thread (<= 512 per chunk)
+static_assert(kChunkBlocks * 8 <= kPlqThreads * kPlqStageBlocks, "staging covers a chunk");
+
+// Buffer view of one row; rows at or past `lim` get an empty range.
+template <int TYPE>
+__device__ __forceinline__ Row make_row_pl(const KqArgs &a, int64_t row, int64_t lim) {
+    constexpr KqLayout L = kq_layout(TYPE);
+    const uint8_t *base = a.W + row * a.row_bytes;
+    Row r;
+    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
+                                               row < lim ? static_cast<uint32_t>(a.row_bytes) : 0u, kBufferWord3);
+    const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+        r.P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+    return r;
+}
+
+template <int TYPE, int NIT, bool XREG>
+__global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int rows) {
+    using K = Kq<TYPE>;
+    using KD = KqDg<TYPE>;
+    constexpr int D = kPlqDepth;
+    extern __shared__ float4 lds_plq[];
+    uint8_t *lds = reinterpret_cast<uint8_t *>(lds_plq);
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int s = lane / kBlocksPerStep;
+    const int bl = lane % kBlocksPerStep;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kPlqWaves + wave) * rows;
+    const int64_t lim = row0 + rows < a.N ? row0 + rows : a.N;
+    const int nrows = lim > row0 ? static_cast<int>(lim - row0) : 0;
+
+    // 1. activation loads: 32-value blocks threadIdx.x + 256 j (clamped)
+    const int n32 = a.nb * 8;
+    float xv[kPlqStageBlocks][32];
+#pragma unroll
+    for (int j = 0; j < kPlqStageBlocks; ++j) {
+        const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
+        const int tc = t < n32 ? t : n32 - 1;
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(a.b0) * 256 + 32 * tc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 f = src[i];
+            xv[j][4 * i] = f.x;
+            xv[j][4 * i + 1] = f.y;
+            xv[j][4 * i + 2] = f.z;
+            xv[j][4 * i + 3] = f.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. weight loads of the first two rows
+    typename K::Regs regs[D][NIT];
+    auto load_row = [&](int slot, int64_t row) {
+        const Row rr = make_row_pl<TYPE>(a, row, lim);
+#pragma unroll
+        for (int t = 0; t < NIT; ++t) {
+            const int bloc = kBlocksPerStep * t + bl;
+            const int bc = bloc < a.nb ? bloc : a.nb - 1;
+            regs[slot][t] = K::load(rr, static_cast<uint32_t>(a.b0 + bc), s);
+        }
+    };
+    load_row(0, row0);
+    load_row(1, row0 + 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. digits into LDS (waits for the activation loads only); codebook
+#pragma unroll
+    for (int j = 0; j < kPlqStageBlocks; ++j) {
+        const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
+        if (t < n32) stage_digits(xv[j], lds + kDgStride * (t >> 3), t & 7);
+    }
+    if constexpr (K::kGrid > 0) {
+        const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
+        for (int i = threadIdx.x; i < K::kGrid; i += kPlqThreads) grid[i] = src[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_row(2, row0 + 2);
+    __syncthreads();
+
+    // 4. this lane's digit slices (registers with XREG)
+    bool valid[NIT];
+    int bcs[NIT];
+#pragma unroll
+    for (int t = 0; t < NIT; ++t) {
+        const int bloc = kBlocksPerStep * t + bl;
+        valid[t] = bloc < a.nb;
+        bcs[t] = valid[t] ? bloc : a.nb - 1;
+    }
+    XDig xr[XREG ? NIT : 1];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int t = 0; t < NIT; ++t) KD::x_slice(s, lds + kDgStride * bcs[t], xr[t]);
+    }
+
+    // 5. rows, D loads ahead
+    for (int r0 = 0; r0 < nrows; r0 += D) {
+#pragma unroll
+        for (int slot = 0; slot < D; ++slot) {
+            const int r = r0 + slot;
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < NIT; ++t) {
+                float p;
+                if constexpr (XREG) {
+                    p = KD::compute(regs[slot][t], s, xr[t], grid);
+                } else {
+                    XDig x;
+                    KD::x_slice(s, lds + kDgStride * bcs[t], x);
+                    p = KD::compute(regs[slot][t], s, x, grid);
+                    // one step's activations live at a time
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                acc += valid[t] ? p : 0.f;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(slot, row0 + r + D);
+            __builtin_amdgcn_sched_barrier(0);
+            const float tot = wave_sum(acc);
+            if (lane == 0 && r < nrows) {
+                const int64_t row = row0 + r;
+                a.y[row] = a.accumulate ? a.y[row] + tot : tot;
+            }
+        }
+    }
+}
+
+typedef void (*kq_pl_fn)(KqArgs, int);
+
+template <int TYPE>
+kq_pl_fn pick_pl_type(int nit) {
+    switch (nit) {
+    case 1: return gemv_kq_pl_kernel<TYPE, 1, true>;
+    case 2: return gemv_kq_pl_kernel<TYPE, 2, true>;
+    case 3: return gemv_kq_pl_kernel<TYPE, 3, true>;
+    case 4: return gemv_kq_pl_kernel<TYPE, 4, true>;
+    case 5: return gemv_kq_pl_kernel<TYPE, 5, false>;
+    case 6: return gemv_kq_pl_kernel<TYPE, 6, false>;
+    case 7: return gemv_kq_pl_kernel<TYPE, 7, false>;
+    default: return gemv_kq_pl_kernel<TYPE, 8, false>;
+    }
+}
+
+kq_pl_fn pick_pl_kernel(int type, int nit) {
+    switch (type) {
+    case MI355X_TYPE_Q4_K: return pick_pl_type<MI355X_TYPE_Q4_K>(nit);
+    case MI355X_TYPE_Q5_K: return pick_pl_type<MI355X_TYPE_Q5_K>(nit);
+    case MI355X_TYPE_Q3_K: return pick_pl_type<MI355X_TYPE_Q3_K>(nit);
+    case MI355X_TYPE_Q6_K: return pick_pl_type<MI355X_TYPE_Q6_K>(nit);
+    case MI355X_TYPE_IQ4_XS: return pick_pl_type<MI355X_TYPE_IQ4_XS>(nit);
+    case MI355X_TYPE_IQ3_S: return pick_pl_type<MI355X_TYPE_IQ3_S>(nit);
+    case MI355X_TYPE_IQ3_XXS: return pick_pl_type<MI355X_TYPE_IQ3_XXS>(nit);
+    case MI355X_TYPE_IQ2_S: return pick_pl_type<MI355X_TYPE_IQ2_S>(nit);
+    default: return nullptr;
+    }
+}
+
 typedef void (*kq_kernel_fn)(KqArgs);
 
 // R = 2 rows per wavefront only for short rows (NIT <= 2), where both rows'
@@ -1085,9 +1265,33 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
     // equal chunks of at most kChunkBlocks superblocks
     const int64_t n_chunks = (B + kChunkBlocks - 1) / kChunkBlocks;
     const int64_t per_chunk = (B + n_chunks - 1) / n_chunks;
+    // Pipelined form (digit numerics).  By default (sweeps on MI355X) for
+    // Q4_K, Q5_K and Q6_K with at most two steps per row (K <= 4096):
+    // 14336x4096 Q4_K 10.2 vs 11.7 us, Q5_K 12.2 vs 12.9, Q6_K 13.6 vs 15.8.
+    // Longer rows, Q3_K and the IQ types stay on the kernel above, whose
+    // several workgroups per CU hide more of their heavier decode.
+    const bool pl_types = a.type == MI355X_TYPE_Q4_K || a.type == MI355X_TYPE_Q5_K || a.type == MI355X_TYPE_Q6_K;
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
         const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
+        const bool pl = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 &&
+                        (ctx->form_override == MI355X_FORM_PIPE ||
+                         (ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO &&
+                          pl_types && nit <= 2));
+        if (pl) {
+            const kq_pl_fn k = pick_pl_kernel(a.type, nit);
+            const size_t lds = static_cast<size_t>(nb) * kDgStride + grid_words(a.type) * 4u;
+            if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
+            const int64_t slots = static_cast<int64_t>(ctx->num_cus) * kPlqWaves;
+            const int64_t rows = (a.N + slots - 1) / slots;
+            const int64_t wgs = (a.N + rows * kPlqWaves - 1) / (rows * kPlqWaves);
+            KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, x, a.y, b0 > 0 ? 1 : 0,
+                        grid};
+            hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(wgs)), dim3(kPlqThreads), lds, ctx->stream, args,
+                               static_cast<int>(rows));
+            MI355X_HIP(hipGetLastError());
+            continue;
+        }
         int R = a.N >= 8192 && nit <= kMaxNitR2 ? 2 : 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= kMaxNitR2)) R = ctx->rows_override;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
