@@ -5,7 +5,9 @@ north-star shape) over one f32 activation row, with the weights already
 resident in HBM.  Launches rotate through enough resident weight copies
 (>= 1 GiB) that the 256 MB Infinity Cache cannot serve them, so the figure is
 HBM bandwidth.  Timing: HIP events around `--steps` back-to-back launches on
-the library's own stream (mi355x_time_gemv), after `--warmup` launches.
+the library's own stream (mi355x_time_gemv), after `--warmup` launches; before
+those, `--settle` seconds of the same launches, untimed, bring the GPU's
+clocks out of idle.
 
 Prints one JSON line (see README of the driver contract):
   value      = algorithmic GB/s of the whole job (one GPU)
@@ -47,8 +49,11 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes):
-    """Returns (ms_per_launch, copies, y) for `steps` launches over resident copies."""
+def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes, settle_s=0.0):
+    """Returns (ms_per_launch, copies, y) for `steps` launches over resident
+    copies.  With settle_s > 0 the same launches first run untimed for about
+    that long, so the GPU's clocks have left their idle state before the
+    warm-up and the timed launches (a cold GPU adds ~0.3 us per launch)."""
     wbytes = N * mi355x.row_bytes(t, K)
     copies = max(1, -(-rotate_bytes // wbytes)) if rotate_bytes else 1
     first = ctx.resident(t, raw, N, K)
@@ -60,6 +65,9 @@ def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes):
     xb = ctx.to_device(x)
     yb = ctx.alloc(4 * N)
     try:
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < settle_s:
+            ctx.time_gemv(t, [b.ptr for b in bufs], N, K, xb.ptr, yb.ptr, 0, 1000)
         ms = ctx.time_gemv(t, [b.ptr for b in bufs], N, K, xb.ptr, yb.ptr, warmup, steps)
         y = yb.download(np.float32, N)
     finally:
@@ -105,7 +113,7 @@ KQ_TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 IQ_TYPES = {"IQ2_S": 22, "IQ3_S": 21, "IQ3_XXS": 18, "IQ4_XS": 23}
 
 
-def kquant_sweep(ctx, steps, warmup):
+def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
     """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
     (rotated) weights.  Inputs are random valid blocks (any encoding is a
     valid input for a dequant-dot kernel); IQ3_XXS / IQ2_S run with a
@@ -120,7 +128,7 @@ def kquant_sweep(ctx, steps, warmup):
     for name, t, N, K in shapes:
         raw = synth.random_blocks(t, N, K, seed=7)
         x = synth.activations(K, seed=43)
-        ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES)
+        ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
         gbs = algorithmic_bytes(t, N, K) / (ms * 1e-3) / 1e9
         res[f"{name} {N}x{K}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
@@ -263,6 +271,8 @@ def main() -> int:
     ap.add_argument("--N", type=int, default=8192)
     ap.add_argument("--K", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed launches before the warm-up (GPU clocks out of idle)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
     ap.add_argument("--kquants", action="store_true",
@@ -300,16 +310,16 @@ def main() -> int:
             log(f"bench: copy calibration: one {nbytes} B device-to-device copy done")
         name, pci = ctx.describe()
         log(f"bench: device {name} at {pci}; timing {args.steps} launches after {args.warmup} warmup")
-        ms, copies, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES)
+        ms, copies, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle)
         log(f"bench: {ms * 1e3:.2f} us/launch over {copies} resident copies")
-        ms_hot, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, 0)
+        ms_hot, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, 0, args.settle)
         log(f"bench: cache-hot (one copy) {ms_hot * 1e3:.2f} us/launch")
         sweep = {}
         if args.sweep:
             for (n2, k2) in ((4096, 4096), (17408, 5120), (151936, 2048)):
                 raw2 = synth.quantize_q4_0(synth.normal_weights(n2, k2, seed=42))
                 x2 = synth.activations(k2, seed=43)
-                ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES)
+                ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle)
                 gbs2 = algorithmic_bytes(t, n2, k2) / (ms2 * 1e-3) / 1e9
                 sweep[f"{n2}x{k2}"] = {"us": round(ms2 * 1e3, 3), "GB/s": round(gbs2, 1),
                                        "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2}
@@ -317,7 +327,7 @@ def main() -> int:
 
         kq = {}
         if args.kquants:
-            kq = kquant_sweep(ctx, args.steps, args.warmup)
+            kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle)
 
     # the timed output must still be the right answer (checked, not measured)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -351,7 +361,11 @@ def main() -> int:
                    "N": N, "K": K, "weight_type": "Q4_0", "rotate_copies": copies,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "note": "achieved = algorithmic bytes / mean time per launch of the timed back-to-back "
+                             "launches (HIP events on the library's stream), so it includes the gap between "
+                             "consecutive kernels; a kernel trace of the same command reports the kernels "
+                             "alone (see the profile summary)"},
         "cache_hot": {"us_per_launch": round(ms_hot * 1e3, 3),
                       "GB/s": round(alg / (ms_hot * 1e-3) / 1e9, 2),
                       "note": "single resident copy, served partly from MALL/L2; not the HBM figure"},

@@ -26,6 +26,7 @@
 #include "device_common.h"
 #include "internal.h"
 #include "q4_0_layout.h"
+#include "wave_rows.h"
 
 #include <algorithm>
 
@@ -102,16 +103,19 @@ struct XTile {
         // power-of-two block scale 2^e0 with max|x|/2^e0 in (kZmax/2, kZmax]:
         // scaling is exact, so activations with <= 19 significant bits are
         // represented exactly
-        int ex;
-        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
+        // m in [2^(ex-1), 2^ex) (hardware frexp: exact for every finite m)
+        const int ex = __builtin_amdgcn_frexp_expf(m);
         int e0 = ex - 19;
-        if (ldexpf(m, -e0) > kZmax) e0 += 1;
+        if (__builtin_amdgcn_ldexpf(m, -e0) > kZmax) e0 += 1;
+        // blocks below 2^-108 keep the largest finite scale 2^127 (their
+        // digits then resolve 2^-128 absolute instead of 19 bits relative)
+        e0 = max(e0, -127);
         const bool live = m > 0.0f && poison == 0.0f;
         // One FMA per value gives rint(v * 2^-e0) + 0x88888 in the low 20 bits
         // of a float in [2^23, 2^24) (ulp 1, round-to-nearest-even); XOR 0x88888
         // turns its five nibbles into the balanced signed digits.  |v| <= m
         // and m * 2^-e0 <= kZmax keep the value inside the 20-bit field.
-        const float s = live ? ldexpf(1.0f, -e0) : 0.0f;
+        const float s = live ? __builtin_amdgcn_ldexpf(1.0f, -e0) : 0.0f;
         uint32_t L[4], H[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -140,7 +144,7 @@ struct XTile {
         w[1] = __builtin_amdgcn_perm(n23, n01, 0x05040100u);
         w[3] = __builtin_amdgcn_perm(n23, n01, 0x07060302u);
         // non-finite activations poison the block the way f32 arithmetic would
-        const float scale = live ? ldexpf(1.0f, e0) : poison;
+        const float scale = live ? __builtin_amdgcn_ldexpf(1.0f, e0) : poison;
         if (write) {
 #pragma unroll
             for (int p = 0; p < kPlanes; ++p) planes[(p * B + b) * 4 + k] = w[p];
@@ -194,14 +198,24 @@ struct RowGroup {
     // row and block-column parts go in the scalar soffset operand.
     __device__ __forceinline__ void load(const uint8_t *__restrict__ W, int row0, int N, int B,
                                          int64_t row_bytes, int lane) {
+        load_at(row_rsrc(W, row0, N, row_bytes), 0, B, row_bytes, lane);
+    }
+
+    // Descriptor based at row row0 whose range ends with row N; a group past
+    // the last row gets an empty range: every access is out of range and
+    // returns 0 without touching memory.
+    __device__ __forceinline__ static __amdgpu_buffer_rsrc_t row_rsrc(const uint8_t *__restrict__ W, int row0, int N,
+                                                                      int64_t row_bytes) {
         const uint8_t *base = W + static_cast<int64_t>(row0) * row_bytes;
-        // a group past the last row gets an empty descriptor: every access is
-        // out of range and returns 0 without touching memory
         const int64_t left = static_cast<int64_t>(N - row0) * row_bytes;
         const uint32_t records =
             left <= 0 ? 0u : static_cast<uint32_t>(left < 0xFFFFFFFFll ? left : 0xFFFFFFFFll);
-        const __amdgpu_buffer_rsrc_t rsrc =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
+    }
+
+    // The R rows starting at byte offset roff0 of the descriptor's range.
+    __device__ __forceinline__ void load_at(__amdgpu_buffer_rsrc_t rsrc, int roff0, int B, int64_t row_bytes,
+                                            int lane) {
         const int scale_off = 16 * B;
         const int qv = 16 * lane;
         const int dv = 2 * F * lane;
@@ -210,7 +224,7 @@ struct RowGroup {
         // accumulate() consumes them (block column major)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int roff = r * static_cast<int>(row_bytes);
+            const int roff = roff0 + r * static_cast<int>(row_bytes);
             if constexpr (F == 1) {
                 dw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, dv, roff + scale_off, 0);
             } else if constexpr (F == 2) {
@@ -235,7 +249,7 @@ struct RowGroup {
         for (int j = 0; j < NBL; ++j) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const int roff = r * static_cast<int>(row_bytes);
+                const int roff = roff0 + r * static_cast<int>(row_bytes);
                 if constexpr (A16) {
                     q[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, qv, roff + 1024 * j, kNonTemporal);
                 } else {
@@ -435,34 +449,38 @@ __global__ __launch_bounds__(64 * G * NBL) void gemv_q4_0_ks_kernel(const uint8_
 // memory requests only as earlier ones drain, so the staging math and the
 // first dot products wait until most of the matrix has streamed in, and
 // the dot products then run after the stream instead of under it.  Here:
-//  * one workgroup of four wavefronts per CU (the grid never exceeds the CU
+//  * one workgroup of eight wavefronts per CU (the grid never exceeds the CU
 //    count, so every workgroup is resident from the start); wavefront v owns
 //    the consecutive rows [v*RW, v*RW + RW);
 //  * the activation loads go first, then the weight loads of the first two
-//    rows, then the staging math (which waits only for the activations),
-//    then the loads of row 3; a row's loads are issued D rows ahead of its
-//    dot product, so at most D rows per wavefront are in flight;
+//    rows, then the staging math (which waits only for the activations);
+//    a row's loads are issued two rows ahead of its dot products;
 //  * after staging, each lane copies the digit planes of its NBL blocks
 //    from LDS into registers once (20 * NBL VGPRs), so the dot products read
 //    no LDS;
+//  * the per-lane partials of all RW rows are folded across the wavefront in
+//    one batched butterfly (wave_rows.h) at the end, a few instructions per
+//    row instead of a DPP reduction per row;
 //  * rows are full 64-block columns (B = 64 * NBL) of 16-byte aligned rows.
-// Per row the arithmetic is the row form's (R = 1): same block order, same
-// expressions, so the results are bit-identical to it.
+// Per row and lane the arithmetic is the row form's; only the order in which
+// the 64 lane partials are added differs.
 // RW > 0: RW rows per wavefront, fully unrolled.  RW == 0: the row count is
-// the argument rw (loop unrolled by D; loads past the wavefront's rows are
-// issued against an empty range and read nothing).
-constexpr int kPlWaves = 4;
-constexpr int kPlDepth = 3;
+// the argument rw (loop unrolled by three rows, one DPP reduction per row;
+// loads past the wavefront's rows are issued against an empty range and read
+// nothing).
+constexpr int kPlWaves = 8;
 
 template <int NBL, int RW>
 __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
-    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int B,
-    int64_t row_bytes, int x_al16, int rw) {
-    constexpr int D = (RW > 0 && RW < kPlDepth) ? RW : kPlDepth;
+    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int, int64_t, int,
+    int rw) {
+    // rows are NBL full 64-block columns: B and the row length are constants
+    constexpr int B = 64 * NBL;
+    constexpr int64_t row_bytes = 18 * B;
+    constexpr int D = RW == 0 ? 3 : (RW < 2 ? RW : 2);
     constexpr int ND0 = D < 2 ? D : 2;  // rows requested before the staging math
-    extern __shared__ uint4 lds_pl[];
-    uint4 *planes = lds_pl;
-    float *ub = reinterpret_cast<float *>(lds_pl + kPlanes * B);
+    __shared__ uint4 planes[kPlanes * B];
+    __shared__ float ub[B];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int rows = RW > 0 ? RW : rw;
@@ -473,16 +491,20 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
 
     constexpr int XI = (4 * NBL + kPlWaves - 1) / kPlWaves;
     XTile<XI> xt;
-    xt.load(x, B, x_al16 != 0);
+    xt.load(x, B, true);  // the activation row is 16-byte aligned
     __builtin_amdgcn_sched_barrier(0);
-    RowGroup<NBL, 1, true, false> g[D];
+    // one descriptor over the wavefront's rows; row r at byte offset r * row_bytes
+    using Grp = RowGroup<NBL, 1, true, false>;
+    const __amdgpu_buffer_rsrc_t rs = Grp::row_rsrc(W, row0, lim, row_bytes);
+    constexpr int rb = static_cast<int>(row_bytes);
+    Grp g[D];
 #pragma unroll
-    for (int s = 0; s < ND0; ++s) g[s].load(W, row0 + s, lim, B, row_bytes, lane);
+    for (int s = 0; s < ND0; ++s) g[s].load_at(rs, s * rb, B, row_bytes, lane);
     __builtin_amdgcn_sched_barrier(0);
     xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = ND0; s < D; ++s) g[s].load(W, row0 + s, lim, B, row_bytes, lane);
+    for (int s = ND0; s < D; ++s) g[s].load_at(rs, s * rb, B, row_bytes, lane);
     __syncthreads();
 
     uint4 P[NBL][kPlanes];
@@ -494,7 +516,7 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
         u[j] = ub[lane + 64 * j];
     }
 
-    auto row_dot = [&](const RowGroup<NBL, 1, true, false> &grp) {
+    auto row_dot = [&](const Grp &grp) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < NBL; ++j) {
@@ -506,15 +528,22 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
     };
 
     if constexpr (RW > 0) {
+        // partials of all rows, reduced together (a batch of 4 or 8)
+        constexpr int RP = RW <= 4 ? 4 : 8;
+        float part[RP];
+#pragma unroll
+        for (int r = RW; r < RP; ++r) part[r] = 0.0f;
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
-            const float acc = row_dot(g[r % D]);
+            part[r] = row_dot(g[r % D]);
             __builtin_amdgcn_sched_barrier(0);
-            if (r + D < RW) g[r % D].load(W, row0 + r + D, lim, B, row_bytes, lane);
+            if (r + D < RW) g[r % D].load_at(rs, (r + D) * rb, B, row_bytes, lane);
             __builtin_amdgcn_sched_barrier(0);
-            const float s = wave_sum(acc);
-            if (lane == 0 && r < nrows) y[row0 + r] = s;
         }
+        const float tot = st_reduce<RP>(part, lane);
+        constexpr int lgS = RP == 4 ? 2 : 3;
+        const int r = lane >> (6 - lgS);
+        if ((lane & ((64 >> lgS) - 1)) == 0 && r < nrows) y[row0 + r] = tot;
     } else {
         for (int r0 = 0; r0 < nrows; r0 += D) {
 #pragma unroll
@@ -522,7 +551,7 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
                 const int r = r0 + s;
                 const float acc = row_dot(g[s]);
                 __builtin_amdgcn_sched_barrier(0);
-                g[s].load(W, row0 + r + D, lim, B, row_bytes, lane);
+                g[s].load_at(rs, (r + D) * rb, B, row_bytes, lane);
                 __builtin_amdgcn_sched_barrier(0);
                 const float sum = wave_sum(acc);
                 if (lane == 0 && r < nrows) y[row0 + r] = sum;
@@ -536,6 +565,9 @@ typedef void (*pl_kernel_t)(const uint8_t *, const float *, float *, int, int, i
 // compiled rows-per-wavefront counts of the unrolled kernel
 constexpr int kPlRows[] = {1, 2, 3, 4, 6, 8};
 
+// Rows of 7 or 8 block columns keep 140-160 VGPRs of digit planes; with more
+// than four rows per wavefront (or the run-time count) the kernel would
+// spill, so those combinations are not compiled (null: other forms).
 template <int NBL>
 pl_kernel_t pick_pl_rw(int rw) {
     switch (rw) {
@@ -543,10 +575,16 @@ pl_kernel_t pick_pl_rw(int rw) {
     case 2: return gemv_q4_0_pl_kernel<NBL, 2>;
     case 3: return gemv_q4_0_pl_kernel<NBL, 3>;
     case 4: return gemv_q4_0_pl_kernel<NBL, 4>;
-    case 6: return gemv_q4_0_pl_kernel<NBL, 6>;
-    case 8: return gemv_q4_0_pl_kernel<NBL, 8>;
-    default: return gemv_q4_0_pl_kernel<NBL, 0>;
+    default: break;
     }
+    if constexpr (NBL <= 6) {
+        switch (rw) {
+        case 6: return gemv_q4_0_pl_kernel<NBL, 6>;
+        case 8: return gemv_q4_0_pl_kernel<NBL, 8>;
+        default: return gemv_q4_0_pl_kernel<NBL, 0>;
+        }
+    }
+    return nullptr;
 }
 
 pl_kernel_t pick_pl(int nbl, int rw) {
@@ -797,7 +835,7 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     const int nbl = static_cast<int>((B + 63) / 64);
     // Pipelined form: full 64-block columns, 16-byte aligned rows and
     // activation row.  By default wherever each wavefront gets at most 8 rows
-    // (one workgroup per CU; sweeps on MI355X: 8192x8192 7.8 vs 8.1 us).
+    // (one workgroup per CU; sweeps on MI355X: 8192x8192 7.5 vs 8.1 us).
     const bool pl_ok = a16 && x_al16 && B % 64 == 0 && nbl <= 8;
     const int64_t pl_need = (a.N + static_cast<int64_t>(ctx->num_cus) * kPlWaves - 1) /
                             (static_cast<int64_t>(ctx->num_cus) * kPlWaves);
@@ -811,13 +849,15 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
             }
         const int rows = rw > 0 ? rw : static_cast<int>(pl_need);
         const pl_kernel_t k = pick_pl(nbl, rw);
-        const size_t lds = static_cast<size_t>(B) * (kPlanes * sizeof(uint4) + sizeof(float));
-        const int64_t grid = (a.N + static_cast<int64_t>(rows) * kPlWaves - 1) / (static_cast<int64_t>(rows) * kPlWaves);
-        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * kPlWaves), lds, ctx->stream, a.W,
-                           static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B), row_bytes,
-                           1, rows);
-        MI355X_HIP(hipGetLastError());
-        return MI355X_OK;
+        if (k) {  // null: this row length and count are left to the other forms
+            const int64_t grid =
+                (a.N + static_cast<int64_t>(rows) * kPlWaves - 1) / (static_cast<int64_t>(rows) * kPlWaves);
+            hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * kPlWaves), 0, ctx->stream, a.W,
+                               static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),
+                               row_bytes, 1, rows);
+            MI355X_HIP(hipGetLastError());
+            return MI355X_OK;
+        }
     }
     // K-split form: 16-byte aligned rows.  By default (sweeps on MI355X) for
     // tall matrices with 1 or 3 block columns (151936x2048: 26.9 vs 27.8 us,
