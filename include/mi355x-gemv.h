@@ -68,6 +68,15 @@ MI355X_API int mi355x_ctx_create(int device, mi355x_ctx **out);
 MI355X_API void mi355x_ctx_destroy(mi355x_ctx *ctx);
 /* Waits for all work queued on the context's stream. */
 MI355X_API int mi355x_ctx_sync(mi355x_ctx *ctx);
+/* Lower-latency wait for a host loop that issues one GEMV group at a time
+ * (no counterpart in the reference, whose engine calls block): queues a
+ * one-wave kernel that stores a sequence number into pinned host memory and
+ * spins until it arrives (falling back to mi355x_ctx_sync after 2 ms).  On
+ * return every kernel and copy queued before the call has completed and its
+ * writes to device memory and to pinned (hipHostMalloc) host memory are
+ * visible to the caller.  Copies into pageable host memory queued directly
+ * with HIP need mi355x_ctx_sync. */
+MI355X_API int mi355x_ctx_fence(mi355x_ctx *ctx);
 /* The context's hipStream_t, as an opaque pointer. */
 MI355X_API void *mi355x_ctx_stream(mi355x_ctx *ctx);
 MI355X_API int mi355x_ctx_device(mi355x_ctx *ctx);

@@ -449,3 +449,37 @@ def test_pipelined_form_edges(ctx, oracle):
                    "pipelined misaligned x")
     finally:
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+
+
+def test_fence_covers_pinned_outputs(ctx, oracle):
+    """mi355x_ctx_fence: GEMVs write into pinned host memory and the host reads
+    it right after the fence, 40 times in a row with changing activations and
+    shapes; every result equals the same GEMV waited for with mi355x_ctx_sync."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    rng = np.random.default_rng(41)
+    shapes = [(2560, 2048), (2048, 11008), (256, 4096)]
+    ws = [(ctx.resident(Q4_0, synth.random_q4_0(N, K, 50 + i), N, K), N, K) for i, (N, K) in enumerate(shapes)]
+    nmax = max(N for N, _ in shapes)
+    hptr = ctypes.c_void_p()
+    mi355x.check(ctx.lib.mi355x_host_malloc(4 * nmax, ctypes.byref(hptr)))
+    dptr = ctypes.c_void_p()
+    try:
+        assert hip.hipHostGetDevicePointer(ctypes.byref(dptr), hptr, 0) == 0
+        host_y = np.ctypeslib.as_array(ctypes.cast(hptr, ctypes.POINTER(ctypes.c_float)), shape=(nmax,))
+        for it in range(40):
+            w, N, K = ws[it % len(ws)]
+            x = rng.standard_normal(K).astype(np.float32)
+            want = ctx.gemv(w, x)
+            host_y[:] = np.nan
+            xb = ctx.to_device(x)
+            try:
+                mi355x.check(ctx.gemv_ptr(Q4_0, w.ptr, N, K, xb.ptr, dptr.value))
+                ctx.fence()
+                assert np.array_equal(host_y[:N], want), (it, N, K)
+            finally:
+                xb.free()
+    finally:
+        mi355x.check(ctx.lib.mi355x_host_free(hptr))
+        for w, _, _ in ws:
+            w.free()

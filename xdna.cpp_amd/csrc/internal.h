@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -34,6 +35,11 @@ struct mi355x_ctx {
     int64_t grid_override = 0;
     int form_override = MI355X_FORM_AUTO;
     std::mutex mu;  // serialises calls that share the staging buffer
+    // completion word for mi355x_ctx_fence: pinned host memory the signal
+    // kernel writes, and the last value handed out
+    uint32_t *fence_host = nullptr;
+    uint32_t *fence_dev = nullptr;
+    std::atomic<uint32_t> fence_seq{0};
 };
 
 namespace mi355x {

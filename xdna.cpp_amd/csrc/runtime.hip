@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -231,6 +232,20 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
         delete ctx;
         return hip_error(e, "hipStreamCreateWithFlags");
     }
+    void *word = nullptr, *word_dev = nullptr;
+    e = hipHostMalloc(&word, 64, hipHostMallocMapped);
+    if (e == hipSuccess) {
+        std::memset(word, 0, 64);
+        e = hipHostGetDevicePointer(&word_dev, word, 0);
+    }
+    if (e != hipSuccess) {
+        if (word) (void)hipHostFree(word);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_error(e, "completion word allocation");
+    }
+    ctx->fence_host = static_cast<uint32_t *>(word);
+    ctx->fence_dev = static_cast<uint32_t *>(word_dev);
     *out = ctx;
     return MI355X_OK;
 }
@@ -243,6 +258,7 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     if (ctx->xconv) (void)hipFree(ctx->xconv);
     if (ctx->iq3xxs_grid) (void)hipFree(ctx->iq3xxs_grid);
     if (ctx->iq2s_grid) (void)hipFree(ctx->iq2s_grid);
+    if (ctx->fence_host) (void)hipHostFree(ctx->fence_host);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -251,6 +267,42 @@ int mi355x_ctx_sync(mi355x_ctx *ctx) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_sync: null context");
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    return MI355X_OK;
+}
+
+namespace {
+
+// One lane stores the sequence number with release semantics at system
+// scope: everything the stream ran before this kernel is visible to the host
+// once the host reads the number.
+__global__ void fence_signal_kernel(uint32_t *word, uint32_t value) {
+    if (threadIdx.x == 0) __hip_atomic_store(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Host spin budget before falling back to hipStreamSynchronize.
+constexpr double kFenceSpinSeconds = 2e-3;
+
+}  // namespace
+
+int mi355x_ctx_fence(mi355x_ctx *ctx) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_fence: null context");
+    DeviceGuard dg(ctx->device);
+    const uint32_t v = ctx->fence_seq.fetch_add(1) + 1;
+    fence_signal_kernel<<<1, 64, 0, ctx->stream>>>(ctx->fence_dev, v);
+    MI355X_HIP(hipGetLastError());
+    // values are handed out in order; a later one also covers this call
+    auto reached = [&] {
+        return static_cast<int32_t>(__atomic_load_n(ctx->fence_host, __ATOMIC_ACQUIRE) - v) >= 0;
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; !reached(); ++i) {
+        if ((i & 255) == 255 &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kFenceSpinSeconds) {
+            MI355X_HIP(hipStreamSynchronize(ctx->stream));
+            return MI355X_OK;
+        }
+    }
     return MI355X_OK;
 }
 

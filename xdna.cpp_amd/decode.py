@@ -56,6 +56,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_set_variant.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_io.restype = C.c_int
     lib.qd_set_io.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_set_wait.restype = C.c_int
+    lib.qd_set_wait.argtypes = [C.c_void_p, C.c_int]
     lib.qd_last_launches.restype = C.c_int64
     lib.qd_last_launches.argtypes = [C.c_void_p]
     lib.qd_attach_gpu.restype = C.c_int
@@ -140,6 +142,14 @@ class Model:
         """IO_STAGED: activations/outputs copied through HBM around each GEMV
         group; IO_MAPPED (default): kernels read/write pinned host memory."""
         if self.lib.qd_set_io(self.h, mode) != 0:
+            raise RuntimeError(self.lib.qd_last_error().decode())
+
+    WAIT_STREAM, WAIT_FENCE = 0, 1
+
+    def set_wait(self, mode: int) -> None:
+        """WAIT_FENCE (default): spin on a completion word after each GEMV
+        group; WAIT_STREAM: hipStreamSynchronize."""
+        if self.lib.qd_set_wait(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 
     def last_launches(self) -> int:

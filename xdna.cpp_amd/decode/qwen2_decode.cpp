@@ -183,6 +183,7 @@ struct qd_model {
     const float *hx_dev = nullptr;
     float *hy_dev = nullptr;
     int io_mode = QD_IO_MAPPED;
+    int wait_mode = QD_WAIT_FENCE;
 
     ~qd_model() {
         if (ctx) {
@@ -447,6 +448,13 @@ int qd_set_io(qd_model *m, int mode) {
     return 0;
 }
 
+int qd_set_wait(qd_model *m, int mode) {
+    if (!m) return fail("qd_set_wait: null model");
+    if (mode != QD_WAIT_STREAM && mode != QD_WAIT_FENCE) return fail("qd_set_wait: unknown mode");
+    m->wait_mode = mode;
+    return 0;
+}
+
 int64_t qd_last_launches(const qd_model *m) { return m ? m->last_launches : 0; }
 
 int qd_last_logits(const qd_model *m, float *out, int n) {
@@ -573,7 +581,9 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             if (!map_y &&
                 hipMemcpyAsync(m->hy, m->dy, static_cast<size_t>(off) * 4, hipMemcpyDeviceToHost, st) != hipSuccess)
                 return -1;
-            if (hipStreamSynchronize(st) != hipSuccess) return -1;
+            // the outputs are in pinned host memory, which the fence covers
+            if ((m->wait_mode == QD_WAIT_FENCE ? mi355x_ctx_fence(m->ctx) : mi355x_ctx_sync(m->ctx)) != MI355X_OK)
+                return -1;
             off = 0;
             auto oi = outs.begin();
             for (int id : ids) {

@@ -45,6 +45,7 @@ _SIGNATURES = {
     "mi355x_ctx_create": (_c.c_int, [_c.c_int, _c.POINTER(_vp)]),
     "mi355x_ctx_destroy": (None, [_vp]),
     "mi355x_ctx_sync": (_c.c_int, [_vp]),
+    "mi355x_ctx_fence": (_c.c_int, [_vp]),
     "mi355x_ctx_set_option": (_c.c_int, [_vp, _c.c_int, _c.c_int64]),
     "mi355x_ctx_stream": (_vp, [_vp]),
     "mi355x_ctx_device": (_c.c_int, [_vp]),
@@ -210,6 +211,11 @@ class Context:
 
     def sync(self) -> None:
         check(self.lib.mi355x_ctx_sync(self.h))
+
+    def fence(self) -> None:
+        """Spin-wait on the context's completion word (covers device memory
+        and pinned host memory)."""
+        check(self.lib.mi355x_ctx_fence(self.h))
 
     def describe(self) -> tuple[str, str]:
         name = ctypes.create_string_buffer(256)
