@@ -201,7 +201,14 @@ MI355X_API int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_
                                 const uint16_t *x_bf16, float *y);
 /* M activation rows at once (row m at x + m*x_stride floats, output at
  * y + m*y_stride floats); the M-row case the reference admits for weights in
- * its own buffer type (src/ggml-xdna.cpp:110-112, 287-296). */
+ * its own buffer type and computes as M sequential GEMVs
+ * (src/ggml-xdna.cpp:110-112, 287-296).  Q4_0 with the digit-plane
+ * arithmetic (variants AUTO and DIGITS), rows a multiple of 256 values and
+ * 16-byte aligned weights: up to 8 activations per pass over the weights
+ * (one staging launch into a context buffer, one batched launch); an
+ * activation's output does not depend on the batch it is in.  Other cases:
+ * M sequential GEMVs.  Calls on one context serialise on its lock while
+ * they enqueue. */
 MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                                    const float *x, int64_t x_stride, float *y, int64_t y_stride,
                                    int64_t M);

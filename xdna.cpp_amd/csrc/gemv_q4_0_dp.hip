@@ -443,6 +443,140 @@ __global__ __launch_bounds__(64 * G * NBL) void gemv_q4_0_ks_kernel(const uint8_
     }
 }
 
+// ---- batched form: M activation rows, weights read once ---------------------
+// y_m = W x_m for m < M <= MB, reading the weights once.  A staging kernel
+// turns every activation into its digit-plane tile (the row form's staging
+// math, once per call) in a context buffer.  The batched kernel follows the
+// K-split schedule: a wavefront owns one 64-block column (lane = block) of
+// R = 2 rows per step and holds its block's planes of every activation in
+// registers (20 VGPRs each), so each code vector meets all MB plane sets and
+// the main loop touches no LDS but the partial sums.  Code vectors are
+// requested kMbDepth steps ahead.  The R x MB partials of a lane go through
+// one batched cross-lane reduction; the column partials of a (row,
+// activation) are added in column order through LDS.
+constexpr int kMbMax = 8;
+constexpr int kMbRows = 2;   // rows per wavefront step
+constexpr int kMbDepth = 3;  // steps whose code vectors are in flight
+
+// uint4 units of one activation tile: kPlanes planes of B blocks, then B scales
+__host__ __device__ constexpr int mb_tile(int B) { return kPlanes * B + (B + 3) / 4; }
+// row groups per workgroup: 8 wavefronts at most (register budget of MB = 8)
+__host__ __device__ constexpr int mb_groups(int nbl) { return nbl >= 8 ? 1 : 8 / nbl; }
+
+// One thread per 8-value group f = m * 4B + i of activations 0 .. M-1; 4B
+// and the workgroup size are multiples of 4, so the DPP quad of a block never
+// straddles two activations.
+__global__ __launch_bounds__(256) void q4_0_mb_stage_kernel(const float *__restrict__ x, int64_t x_stride, int M,
+                                                            int B, int x_al16, uint4 *__restrict__ tiles) {
+    const int gpa = 4 * B;
+    const int total = M * gpa;
+    const int fr = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int f = min(fr, total - 1);
+    const int m = f / gpa, i = f - m * gpa;
+    const float *xb = x + m * x_stride + 32 * (i >> 2) + 4 * (i & 3);
+    float v[8];
+    if (x_al16) {
+        const float4 lo = *reinterpret_cast<const float4 *>(xb);
+        const float4 hi = *reinterpret_cast<const float4 *>(xb + 16);
+        v[0] = lo.x; v[1] = hi.x; v[2] = lo.y; v[3] = hi.y;
+        v[4] = lo.z; v[5] = hi.z; v[6] = lo.w; v[7] = hi.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = xb[e];
+            v[2 * e + 1] = xb[16 + e];
+        }
+    }
+    uint4 *t = tiles + static_cast<int64_t>(m) * mb_tile(B);
+    XTile<1>::stage_group(v, i >> 2, i & 3, B, fr < total, reinterpret_cast<uint32_t *>(t),
+                          reinterpret_cast<float *>(t + kPlanes * B));
+}
+
+template <int NBL, int MB>
+__global__ __launch_bounds__(64 * 8) void gemv_q4_0_mb_kernel(const uint8_t *__restrict__ W,
+                                                              const uint4 *__restrict__ tiles,
+                                                              float *__restrict__ y, int64_t y_stride, int N,
+                                                              int B, int64_t row_bytes, int M) {
+    constexpr int R = kMbRows;
+    constexpr int G = mb_groups(NBL);
+    constexpr int ROWS = G * R;  // rows per workgroup step
+    constexpr int S = R * MB;    // partials per lane per step
+    static_assert(S == 4 || S == 8 || S == 16, "batched reduction size");
+    __shared__ float red[G * S * NBL];  // [G][R][MB][NBL]
+    const int tile = mb_tile(B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int gi = wave / NBL;  // row group of this wavefront
+    const int c = wave % NBL;   // block column of this wavefront
+    const int n_groups = (N + ROWS - 1) / ROWS;
+
+    // lane's block (as the K-split form): past the row end a lane reads the
+    // last block and its weight scale is masked to 0
+    const int braw = 64 * c + lane;
+    const bool live = braw < B;
+    const int b = live ? braw : B - 1;
+    const int F = B >> 6;
+    const int slot = b < 64 * F ? (b & 63) * F + (b >> 6) : b;
+    const uint32_t dmask = live ? 0xFFFFu : 0u;
+
+    // the first kMbDepth steps' code vectors (an empty range past the end)
+    int g = blockIdx.x;
+    ColumnGroup<R> ring[kMbDepth];
+#pragma unroll
+    for (int d = 0; d < kMbDepth; ++d)
+        ring[d].load(W, (g + d * static_cast<int>(gridDim.x)) * ROWS + gi * R, N, B, row_bytes, b, slot);
+
+    // this lane's block of every activation; slots m >= M repeat the last
+    // activation (their partials are never stored)
+    uint4 P[MB][kPlanes];
+    float u[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const uint4 *t = tiles + min(m, M - 1) * tile;
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) P[m][p] = t[p * B + b];
+        u[m] = reinterpret_cast<const float *>(t + kPlanes * B)[b];
+    }
+
+    // steps g, g + grid, ... in turns of kMbDepth; a step's slot of the ring
+    // is refilled with the step kMbDepth ahead once its dot products are done
+    for (; g < n_groups; g += kMbDepth * static_cast<int>(gridDim.x)) {
+#pragma unroll
+        for (int d = 0; d < kMbDepth; ++d) {
+            const int gd = g + d * static_cast<int>(gridDim.x);
+            if (gd >= n_groups) break;  // uniform across the workgroup
+            float part[S];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float dr = half_bits_to_float(static_cast<uint16_t>(ring[d].d[r] & dmask));
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    const int T = block_dot_digits(ring[d].q[r], P[m]);
+                    part[r * MB + m] = dr * u[m] * static_cast<float>(T);
+                }
+            }
+            ring[d].load(W, (gd + kMbDepth * static_cast<int>(gridDim.x)) * ROWS + gi * R, N, B, row_bytes, b,
+                         slot);
+            // lane l ends with the column total of partial l >> (6 - log2 S)
+            const float tot = st_reduce<S>(part, lane);
+            constexpr int SPAN = 64 / S;
+            if ((lane & (SPAN - 1)) == 0) red[((gi * S) + lane / SPAN) * NBL + c] = tot;
+            __syncthreads();
+            // one thread per (row, activation) of the step adds the columns in order
+            if (threadIdx.x < ROWS * MB) {
+                const int k = threadIdx.x;  // = (g_i * R + r) * MB + m
+                const int m = k % MB;
+                const int row = gd * ROWS + k / MB;
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NBL; ++j) s += red[k * NBL + j];
+                if (m < M && row < N) y[m * y_stride + row] = s;
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // ---- pipelined form ---------------------------------------------------------
 // Measured on MI355X, a wavefront that issues every load of its rows before
 // it stages the activation row stalls at the loads: the CU accepts vector
@@ -938,6 +1072,83 @@ int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a) {
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(grid, 1))), dim3(512), lds, ctx->stream, a.W,
                        static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B), row_bytes,
                        x_al16 ? 1 : 0);
+    MI355X_HIP(hipGetLastError());
+    return MI355X_OK;
+}
+
+}  // namespace mi355x
+
+namespace mi355x {
+
+typedef void (*mb_kernel_t)(const uint8_t *, const uint4 *, float *, int64_t, int, int, int64_t, int);
+
+template <int NBL>
+mb_kernel_t pick_mb_m(int mb) {
+    switch (mb) {
+    case 2: return gemv_q4_0_mb_kernel<NBL, 2>;
+    case 4: return gemv_q4_0_mb_kernel<NBL, 4>;
+    default: return gemv_q4_0_mb_kernel<NBL, 8>;
+    }
+}
+
+mb_kernel_t pick_mb(int nbl, int mb) {
+    switch (nbl) {
+    case 1: return pick_mb_m<1>(mb);
+    case 2: return pick_mb_m<2>(mb);
+    case 3: return pick_mb_m<3>(mb);
+    case 4: return pick_mb_m<4>(mb);
+    case 5: return pick_mb_m<5>(mb);
+    case 6: return pick_mb_m<6>(mb);
+    case 7: return pick_mb_m<7>(mb);
+    default: return pick_mb_m<8>(mb);
+    }
+}
+
+// Activations per batched launch (kMbMax), or 0 if the batched form does not
+// apply: f32 activations, rows a multiple of 256 values up to the digit
+// kernels' limit, 16-byte aligned weights.
+int q4_0_mb_capacity(const mi355x_ctx *, const GemvArgs &a) {
+    const int64_t B = a.K / 32;
+    if (a.x_bf16 || B <= 0 || B > kDpMaxBlocks || B % 8 != 0 || reinterpret_cast<uintptr_t>(a.W) % 16 != 0 ||
+        a.N > INT32_MAX || static_cast<int64_t>(a.N) * 18 * B >= (int64_t(1) << 40))
+        return 0;
+    return kMbMax;
+}
+
+int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M) {
+    const int64_t B = a.K / 32;
+    const int64_t row_bytes = 18 * B;
+    const int nbl = static_cast<int>((B + 63) / 64);
+    const int mb = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
+    const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && x_stride % 4 == 0;
+    // the tiles stay in place from the staging launch to the batched launch
+    // that reads them (calls on one context share the buffer)
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t need = static_cast<size_t>(M) * 16 * mb_tile(static_cast<int>(B));
+    if (ctx->mbtiles_bytes < need) {
+        MI355X_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->mbtiles) MI355X_HIP(hipFree(ctx->mbtiles));
+        ctx->mbtiles = nullptr;
+        ctx->mbtiles_bytes = 0;
+        MI355X_HIP(hipMalloc(&ctx->mbtiles, need));
+        ctx->mbtiles_bytes = need;
+    }
+    uint4 *tiles = static_cast<uint4 *>(ctx->mbtiles);
+    const int64_t groups = static_cast<int64_t>(M) * 4 * B;
+    hipLaunchKernelGGL(q4_0_mb_stage_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
+                       ctx->stream, static_cast<const float *>(a.x), x_stride, M, static_cast<int>(B),
+                       x_al16 ? 1 : 0, tiles);
+    MI355X_HIP(hipGetLastError());
+    const mb_kernel_t k = pick_mb(nbl, mb);
+    const int waves = mb_groups(nbl) * nbl;
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * waves, 0);
+    const int64_t rows = static_cast<int64_t>(mb_groups(nbl)) * kMbRows;
+    const int64_t n_groups = (a.N + rows - 1) / rows;
+    int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * occ);
+    if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), 0, ctx->stream, a.W,
+                       static_cast<const uint4 *>(tiles), a.y, y_stride, static_cast<int>(a.N), static_cast<int>(B),
+                       row_bytes, M);
     MI355X_HIP(hipGetLastError());
     return MI355X_OK;
 }

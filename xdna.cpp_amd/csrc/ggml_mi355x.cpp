@@ -588,6 +588,22 @@ bool process_mul_mat(BackendCtx *bc, T *node, bool host) {
                 const uint8_t *w = w_base + i3 * src0_stride3 + i2 * src0_stride2;
                 const uint8_t *a = a_base + i3 * src1_stride3 + i2 * src1_stride2;
                 uint8_t *o = o_base + i3 * dst_stride3 + i2 * dst_stride2;
+                // M > 1 (weights in this backend's buffer): one batched call,
+                // which reads the weights once per group of activations where
+                // the rows are whole floats apart, else M single GEMVs
+                // (src/ggml-xdna.cpp:281-297 loops)
+                const bool whole = src1_stride1 % sizeof(float) == 0 && dst_stride1 % sizeof(float) == 0;
+                if (M > 1 && whole) {
+                    if (mi355x_gemv_batched(bc->ctx, type, w, N, K, reinterpret_cast<const float *>(a),
+                                            static_cast<int64_t>(src1_stride1 / sizeof(float)),
+                                            reinterpret_cast<float *>(o),
+                                            static_cast<int64_t>(dst_stride1 / sizeof(float)), M) != MI355X_OK) {
+                        std::fprintf(stderr, "[mi355x error] node '%s' batched GEMV dispatch: %s\n", node->name,
+                                     mi355x_last_error());
+                        return false;
+                    }
+                    continue;
+                }
                 for (int64_t m = 0; m < M; ++m) {
                     if (mi355x_gemv(bc->ctx, type, w, N, K, reinterpret_cast<const float *>(a + m * src1_stride1),
                                     reinterpret_cast<float *>(o + m * dst_stride1)) != MI355X_OK) {

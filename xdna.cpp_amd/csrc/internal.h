@@ -23,6 +23,10 @@ struct mi355x_ctx {
     // 16-byte aligned (grown on demand, freed with the context)
     void *xconv = nullptr;
     size_t xconv_bytes = 0;
+    // digit-plane tiles of the activations of a batched Q4_0 call (grown on
+    // demand, freed with the context)
+    void *mbtiles = nullptr;
+    size_t mbtiles_bytes = 0;
     // per-context copies of the IQ grids (device), valid when non-null
     void *iq3xxs_grid = nullptr;
     void *iq2s_grid = nullptr;
@@ -69,6 +73,10 @@ struct GemvArgs {
 int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
+// Batched form: M activation rows (x + m*x_stride) into y + m*y_stride,
+// M <= q4_0_mb_capacity() (0: form not applicable).
+int q4_0_mb_capacity(const mi355x_ctx *ctx, const GemvArgs &a);
+int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M);
 bool q4_0_st_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a);

@@ -256,6 +256,7 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->xconv) (void)hipFree(ctx->xconv);
+    if (ctx->mbtiles) (void)hipFree(ctx->mbtiles);
     if (ctx->iq3xxs_grid) (void)hipFree(ctx->iq3xxs_grid);
     if (ctx->iq2s_grid) (void)hipFree(ctx->iq2s_grid);
     if (ctx->fence_host) (void)hipHostFree(ctx->fence_host);
@@ -590,6 +591,29 @@ int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int
     if (M < 0) return set_error(MI355X_EINVAL, "mi355x_gemv_batched: negative M");
     if (M > 1 && (x_stride < K || y_stride < N))
         return set_error(MI355X_EINVAL, "mi355x_gemv_batched: strides smaller than a row");
+    // Q4_0 digit-plane arithmetic: up to q4_0_mb_capacity() activations per
+    // launch of the batched form (weights read once per launch)
+    if (ctx && type == MI355X_TYPE_Q4_0 && M >= 2 && N > 0 && W && x && y &&
+        (ctx->kernel_variant == MI355X_VARIANT_AUTO || ctx->kernel_variant == MI355X_VARIANT_DIGITS)) {
+        uint64_t total = 0;
+        int rc = check_tensor(type, N, K, &total, "mi355x_gemv_batched");
+        if (rc) return rc;
+        GemvArgs a{type, static_cast<const uint8_t *>(W), N, K, x, false, y};
+        const int cap = q4_0_mb_capacity(ctx, a);
+        if (cap >= 2) {
+            DeviceGuard dg(ctx->device);
+            for (int64_t m0 = 0; m0 < M;) {
+                const int chunk = static_cast<int>(std::min<int64_t>(cap, M - m0));
+                GemvArgs c{type, static_cast<const uint8_t *>(W), N, K, x + m0 * x_stride, false, y + m0 * y_stride};
+                // a one-activation remainder also runs in this form, so every
+                // output of the call has the same arithmetic
+                rc = launch_gemv_q4_0_mb(ctx, c, x_stride, y_stride, chunk);
+                if (rc) return rc;
+                m0 += chunk;
+            }
+            return MI355X_OK;
+        }
+    }
     for (int64_t m = 0; m < M; ++m) {
         int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, "mi355x_gemv_batched");
         if (rc) return rc;

@@ -245,6 +245,29 @@ class Context:
         fn = self.lib.mi355x_gemv_bf16 if bf16 else self.lib.mi355x_gemv
         return fn(self.h, t, w_ptr, N, K, x_ptr, y_ptr)
 
+    def gemv_batched_ptr(self, t: int, w_ptr: int, N: int, K: int, x_ptr: int, x_stride: int, y_ptr: int,
+                         y_stride: int, M: int) -> int:
+        return self.lib.mi355x_gemv_batched(self.h, t, w_ptr, N, K, x_ptr, x_stride, y_ptr, y_stride, M)
+
+    def gemv_batched(self, w: ResidentWeights, xs: np.ndarray, x_stride: int | None = None,
+                     y_stride: int | None = None) -> np.ndarray:
+        """M GEMVs against the same weights (xs: M x K); activation rows
+        x_stride floats apart and outputs y_stride floats apart on the device."""
+        M = xs.shape[0]
+        xst = x_stride or w.K
+        yst = y_stride or w.N
+        xp = np.zeros((M, xst), np.float32)
+        xp[:, :w.K] = xs
+        xb = self.to_device(xp)
+        yb = self.alloc(4 * max(M * yst, 1))
+        try:
+            check(self.gemv_batched_ptr(w.t, w.ptr, w.N, w.K, xb.ptr, xst, yb.ptr, yst, M))
+            self.sync()
+            return yb.download(np.float32, M * yst).reshape(M, yst)[:, :w.N]
+        finally:
+            xb.free()
+            yb.free()
+
     def gemv(self, w: ResidentWeights, x: np.ndarray) -> np.ndarray:
         """One GEMV with host activations; returns the host output."""
         bf16 = x.dtype == np.uint16
