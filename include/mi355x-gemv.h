@@ -114,11 +114,12 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     4 rows; needs rows of a multiple of 8 blocks), MI355X_FORM_STREAM (one
  *     workgroup per CU; a lane owns one block of every row of its team and
  *     keeps that block's activation digits in registers; K <= 16384),
- *     MI355X_FORM_PIPE (one workgroup of four wavefronts per CU, each
- *     wavefront owning a run of consecutive rows whose loads are issued
- *     three rows ahead of their dot products; Q4_0: K a multiple of 2048
- *     up to 16384, 16-byte aligned weights and activation row; K/IQ types:
- *     22-bit digit arithmetic, any K). */
+ *     MI355X_FORM_PIPE (one workgroup per CU -- eight wavefronts for Q4_0,
+ *     four for the K/IQ types -- each wavefront owning a run of consecutive
+ *     rows whose loads are issued two (Q4_0) or three (K/IQ) rows ahead of
+ *     their dot products; Q4_0: K a multiple of 2048 up to 16384, 16-byte
+ *     aligned weights and activation row; K/IQ types: 22-bit digit
+ *     arithmetic, any K). */
 #define MI355X_OPT_VARIANT 1
 #define MI355X_OPT_ROWS_PER_WAVE 2
 #define MI355X_OPT_WAVES_PER_GROUP 3
