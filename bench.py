@@ -176,9 +176,13 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         # completion-word fence
         model.set_wait(model.WAIT_STREAM)
         sync_toks, tw = model.generate(prompt, n_gen)
+        # every GEMV group as a command to the persistent server kernel
+        model.set_wait(model.WAIT_SERVER)
+        srv_toks, tv = model.generate(prompt, n_gen)
         model.set_wait(model.WAIT_FENCE)
         log(f"bench: decode: staged I/O {passes / ts['gen_s']:.1f} tok/s; per-matrix launches with staged I/O "
-            f"{passes / tn['gen_s']:.1f} tok/s; hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s")
+            f"{passes / tn['gen_s']:.1f} tok/s; hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s; "
+            f"server kernel {passes / tv['gen_s']:.1f} tok/s")
         log(f"bench: decode: GPU {tok_s:.1f} tok/s ({t['gen_s'] / passes * 1e3:.3f} ms/token, "
             f"GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops {t['gen_host_s'] / passes * 1e3:.3f} ms); "
             f"prompt {n_prompt / t['prompt_s']:.1f} tok/s token by token")
@@ -202,6 +206,11 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                             "gemv_ms_per_token": round(tw["gen_gemv_s"] / passes * 1e3, 4),
                             "tokens_match": bool(np.array_equal(sync_toks, gpu_toks)),
                             "note": "hipStreamSynchronize after every GEMV group instead of mi355x_ctx_fence"},
+            "server": {"tok_s": round(passes / tv["gen_s"], 2),
+                       "gemv_ms_per_token": round(tv["gen_gemv_s"] / passes * 1e3, 4),
+                       "tokens_match": bool(np.array_equal(srv_toks, gpu_toks)),
+                       "note": "every GEMV group as a command to a resident server kernel (mi355x_server_*): no "
+                               "launch per group; row-form arithmetic"},
             "per_node": {"tok_s": round(passes / tn["gen_s"], 2), "gemv_launches_per_token": node_launches,
                          "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
                          "tokens_match_fused": bool(np.array_equal(node_toks, gpu_toks)),

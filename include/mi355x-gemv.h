@@ -214,6 +214,33 @@ MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int
                                    const float *x, int64_t x_stride, float *y, int64_t y_stride,
                                    int64_t M);
 
+/* ---- persistent GEMV server (decode loops) ---------------------------------
+ * No counterpart in the reference (its engine calls block, one dispatch
+ * each).  For a host loop that issues one Q4_0 GEMV group at a time -- batch-1
+ * decode -- launch and completion cost more than the kernel.  A server keeps
+ * one workgroup per CU resident (cooperative launch on its own stream) and
+ * takes commands through pinned host memory: mi355x_server_gemv copies x,
+ * publishes the jobs and returns once every output is written.  Jobs share x
+ * and K; outputs are device-visible pointers (device memory, or pinned host
+ * memory through hipHostGetDevicePointer).  Arithmetic per row is the digit
+ * kernel's row form (bit-identical to MI355X_FORM_ROWS).  K: a multiple of
+ * 256 up to max_k (<= 16384); weights 16-byte aligned.  The resident kernel
+ * leaves by itself after 1 s without a command (the next call relaunches it),
+ * on mi355x_server_stop / _destroy, and before mi355x_free or
+ * mi355x_ctx_destroy on its context (a hipFree would wait for it).  One host
+ * thread per server; destroy servers before their context. */
+typedef struct mi355x_server mi355x_server;
+typedef struct mi355x_server_job {
+    const void *W; /* resident Q4_0 tensor of N rows */
+    int64_t N;
+    float *y;      /* N outputs */
+} mi355x_server_job;
+MI355X_API int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out);
+MI355X_API int mi355x_server_gemv(mi355x_server *s, const float *x, int64_t K, int njobs,
+                                  const mi355x_server_job *jobs);
+MI355X_API int mi355x_server_stop(mi355x_server *s);
+MI355X_API void mi355x_server_destroy(mi355x_server *s);
+
 /* ---- measurement -----------------------------------------------------------
  * Times `iters` back-to-back launches of mi355x_gemv on the context's stream
  * with HIP events, rotating through `n_weights` resident copies of W

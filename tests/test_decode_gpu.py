@@ -122,3 +122,24 @@ def test_ggml_numerics_decode_token_identical_to_cpu(cfg):
     # anything short of bit-identical GEMVs would not hold the tokens.)
     assert np.array_equal(gpu_toks, cpu_toks), (gpu_toks, cpu_toks)
     assert np.array_equal(gpu_logits, cpu_logits)
+
+
+@pytest.mark.parametrize("cfg,n_prompt,n_gen", [(TINY, 16, 12), (SHAPE_3B_2L, 8, 6)], ids=["tiny", "3b_2layers"])
+def test_server_decode_token_identical(cfg, n_prompt, n_gen):
+    """Every GEMV group as a command to the persistent server kernel: same
+    tokens as the CPU engine, and the same as launch-per-group decode."""
+    with decode.Model(threads=8, **cfg) as m:
+        p = decode.prompt_tokens(n_prompt, cfg["vocab"], 3)
+        f, _ = orc.decode_gemv("oracle")
+        cpu_toks, _ = m.generate(p, n_gen, f)
+        cpu_logits = m.last_logits()
+        m.attach_gpu(0)
+        launch_toks, _ = m.generate(p, n_gen)
+        m.set_wait(m.WAIT_SERVER)
+        srv_toks, t = m.generate(p, n_gen)
+        srv_logits = m.last_logits()
+        again, _ = m.generate(p, n_gen)  # a second decode relaunches the server
+        m.set_wait(m.WAIT_FENCE)
+    check(cpu_toks, cpu_logits, srv_toks, srv_logits)
+    assert np.array_equal(srv_toks, launch_toks) and np.array_equal(again, srv_toks)
+    assert t["gen_passes"] == n_gen - 1

@@ -29,6 +29,9 @@
 #include "wave_rows.h"
 
 #include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <new>
 
 namespace mi355x {
 namespace {
@@ -573,6 +576,282 @@ __global__ __launch_bounds__(64 * 8) void gemv_q4_0_mb_kernel(const uint8_t *__r
                 if (m < M && row < N) y[m * y_stride + row] = s;
             }
             __syncthreads();
+        }
+    }
+}
+
+// ---- persistent server form (decode loops) ------------------------------------
+// A decode loop issues one GEMV group at a time and waits for it; launch and
+// completion then cost more than the kernel.  The server form keeps one
+// workgroup per CU resident (cooperative launch) and takes commands from
+// pinned host memory:
+//   host: x -> pinned buffer, jobs -> command record, then the command number
+//         (seq, with K) last; waits for the completion word to reach seq;
+//   workgroup 0: polls seq over PCIe and republishes it in device memory,
+//         where the other workgroups poll it;
+//   every workgroup: reads the command and x through system-coherent
+//         accesses (never a stale cached line; polls carry no fences, as a
+//         fence at agent or system scope invalidates the whole L2), stages
+//         x's digit planes in LDS, computes its contiguous share of
+//         each job's rows with the row form's arithmetic (bit-identical to
+//         MI355X_FORM_ROWS), writes outputs through to memory and waits for
+//         them, then one arrival on a
+//         per-XCD counter in device memory; the last arrival of a group
+//         arrives on the top counter, and the last of those stores seq into
+//         the completion word.
+// Every wait is bounded: the kernel exits on an exit command or after
+// kSrvIdleTicks without one (workgroup 0 then tells the others), so the grid
+// always drains.
+constexpr int kSrvMaxJobs = 4;
+constexpr int kSrvWaves = 8;
+constexpr uint64_t kSrvClockHz = 100000000ull;  // s_memrealtime
+
+struct SrvJob {
+    const uint8_t *W;
+    float *y;
+    int64_t N;
+};
+
+struct SrvCmd {
+    uint64_t seqk;  // command number | K << 32, written last by the host
+    uint32_t exit;
+    int32_t K;
+    int32_t njobs;
+    int32_t pad;
+    SrvJob jobs[kSrvMaxJobs];
+};
+
+// device-memory state, one 128-byte line per word that is polled or counted
+struct SrvDev {
+    uint32_t seq[32];
+    uint32_t quit[32];
+    uint64_t group[8][16];
+    uint64_t top[16];
+    SrvCmd cmd;  // copy of the current command record
+};
+
+__device__ __forceinline__ uint64_t srv_clock() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Cache policy sc0 sc1 (system coherent): the load reads host memory itself,
+// never a line a GPU cache kept from an earlier command.
+constexpr int kSysCoherent = 1 | 16;
+constexpr int kSrvCopyDepth = 8;  // 16-byte pieces of x in flight per thread (K <= 16384)
+
+// XTile::load for the device copy of the activation, through the system-
+// coherent path, so no L2 line kept from an earlier command is read (group i
+// of this thread: block i / 4, dword i % 4, clamped).
+template <int XI>
+__device__ __forceinline__ void srv_load_x(XTile<XI> &xt, const float *x, int B) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(x), 0, static_cast<uint32_t>(128 * B), kBufferWord3);
+#pragma unroll
+    for (int it = 0; it < XI; ++it) {
+        const int i = min(static_cast<int>(threadIdx.x + it * blockDim.x), 4 * B - 1);
+        const int off = 4 * (32 * (i >> 2) + 4 * (i & 3));
+        const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kSysCoherent);
+        const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 64, 0, kSysCoherent);
+        // copy the elements out before bit-casting: clang lowers a bit cast
+        // of a vector element lvalue as a load from the vector's base
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t l = lo[e], h = hi[e];
+            xt.v[it][2 * e] = __builtin_bit_cast(float, l);
+            xt.v[it][2 * e + 1] = __builtin_bit_cast(float, h);
+        }
+    }
+}
+
+// Outputs of one job are gathered in LDS and written out together: one
+// workgroup's rows are contiguous, so the stores of a wavefront cover 256
+// contiguous bytes (written through to memory one 4-byte row at a time they
+// would cost a PCIe transaction each when y is host memory).
+constexpr int kSrvOutMax = 4096;  // rows of one job per workgroup
+
+template <int NBL, bool TAIL>
+__device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                         float *out) {
+    constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
+    constexpr int ROWS = kSrvWaves * R;
+    constexpr int XI = (4 * NBL + kSrvWaves - 1) / kSrvWaves;
+    uint4 *planes = lds;
+    float *ub = reinterpret_cast<float *>(lds + kPlanes * B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t row_bytes = 18 * static_cast<int64_t>(B);
+    int bc[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
+    const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
+    const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
+
+    // the first job's first rows are requested before the staging math
+    const int lo0 = static_cast<int>(c.jobs[0].N * g / G), hi0 = static_cast<int>(c.jobs[0].N * (g + 1) / G);
+    XTile<XI> xt;
+    srv_load_x(xt, x, B);
+    __builtin_amdgcn_sched_barrier(0);
+    RowGroup<NBL, R, true, TAIL> grp;
+    grp.load(c.jobs[0].W, lo0 + wave * R, hi0, B, row_bytes, lane);
+    xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
+    __syncthreads();
+
+    for (int j = 0; j < c.njobs; ++j) {
+        const SrvJob &job = c.jobs[j];
+        const int lo = static_cast<int>(job.N * g / G), hi = static_cast<int>(job.N * (g + 1) / G);
+        if (j > 0) grp.load(job.W, lo + wave * R, hi, B, row_bytes, lane);
+        for (int row0 = lo + wave * R; row0 < hi; row0 += ROWS) {
+            RowGroup<NBL, R, true, TAIL> nxt;
+            nxt.load(job.W, row0 + ROWS, hi, B, row_bytes, lane);  // empty range past hi
+            float acc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+            grp.accumulate(acc, planes, ub, B, bc, tail_mask);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float s = wave_sum(acc[r]);
+                if (lane == 0 && row0 + r < hi) out[row0 + r - lo] = s;
+            }
+            grp = nxt;
+        }
+        __syncthreads();
+        // system-scope stores: written through to memory, so the command
+        // completes without an L2 write-back
+        for (int i = threadIdx.x; i < hi - lo; i += blockDim.x)
+            __hip_atomic_store(&job.y[lo + i], out[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __syncthreads();  // `out` is reused by the next job
+    }
+}
+
+// Command-record fields as 32-bit words (the record is copied word by word).
+constexpr int kSrvCmdWords = static_cast<int>(sizeof(SrvCmd) / 4);
+static_assert(sizeof(SrvCmd) % 4 == 0, "command record in words");
+
+__global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd *cmd, const float *hx,
+                                                                            SrvDev *dev, float *dx,
+                                                                            uint32_t *done, uint32_t first,
+                                                                            uint64_t idle_ticks) {
+    extern __shared__ uint4 lds_dp[];
+    __shared__ uint32_t verdict;  // 0 run, 1 leave
+    __shared__ int32_t shk;       // K of this command (workgroup 0)
+    __shared__ SrvCmd cs;         // this command
+    __shared__ float outb[kSrvOutMax];
+    const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
+    uint32_t *csw = reinterpret_cast<uint32_t *>(&cs);
+    for (uint32_t expect = first;; ++expect) {
+        if (g == 0) {
+            // workgroup 0: wait for the host, then copy the command record
+            // and x into device memory (read from and written through to
+            // memory itself), and only then publish the command number
+            if (threadIdx.x == 0) {
+                const uint64_t t0 = srv_clock();
+                uint32_t leave = 0;
+                for (;;) {
+                    const uint64_t s = __hip_atomic_load(&cmd->seqk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    if (static_cast<int32_t>(static_cast<uint32_t>(s) - expect) >= 0) {
+                        shk = static_cast<int32_t>(s >> 32);
+                        break;
+                    }
+                    if (srv_clock() - t0 > idle_ticks) {
+                        leave = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                verdict = leave;
+            }
+            __syncthreads();
+            if (verdict) {
+                if (threadIdx.x == 0) __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+            // the record and x in one round trip: K came with the command
+            // number; x in 16-byte pieces, kSrvCopyDepth loads in flight per
+            // thread (K is a multiple of 256, so K / 4 pieces)
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(cmd);
+            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
+                csw[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const int K4 = shk / 4;
+            const __amdgpu_buffer_rsrc_t hs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(hx), 0, static_cast<uint32_t>(16 * K4), kBufferWord3);
+            const __amdgpu_buffer_rsrc_t ds =
+                __builtin_amdgcn_make_buffer_rsrc(dx, 0, static_cast<uint32_t>(16 * K4), kBufferWord3);
+            for (int base = 0; base < K4; base += kSrvCopyDepth * 64 * kSrvWaves) {
+                u32x4 v[kSrvCopyDepth];
+#pragma unroll
+                for (int k = 0; k < kSrvCopyDepth; ++k)
+                    v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                        hs, 16 * (base + k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)), 0, kSysCoherent);
+#pragma unroll
+                for (int k = 0; k < kSrvCopyDepth; ++k)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        v[k], ds, 16 * (base + k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)), 0, kSysCoherent);
+            }
+            uint32_t *dcw = reinterpret_cast<uint32_t *>(&dev->cmd);
+            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
+                __hip_atomic_store(&dcw[i], csw[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __builtin_amdgcn_s_waitcnt(0);  // every copy store has completed
+            __syncthreads();  // and the record is in LDS
+            if (threadIdx.x == 0) __hip_atomic_store(&dev->seq[0], expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (cs.exit) return;
+        } else {
+            if (threadIdx.x == 0) {
+                const uint64_t t0 = srv_clock();
+                uint32_t leave = 0;
+                for (;;) {
+                    const uint32_t s = __hip_atomic_load(&dev->seq[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (static_cast<int32_t>(s - expect) >= 0) break;
+                    if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                        srv_clock() - t0 > 2 * idle_ticks) {
+                        leave = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                verdict = leave;
+            }
+            __syncthreads();
+            if (verdict) return;
+            const uint32_t *dcw = reinterpret_cast<const uint32_t *>(&dev->cmd);
+            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
+                csw[i] = __hip_atomic_load(&dcw[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __syncthreads();
+            if (cs.exit) return;
+        }
+        const SrvCmd &c = cs;
+        const int B = c.K / 32;
+        switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
+        case 2: srv_rows<1, false>(c, B, lds_dp, dx, outb); break;
+        case 3: srv_rows<1, true>(c, B, lds_dp, dx, outb); break;
+        case 4: srv_rows<2, false>(c, B, lds_dp, dx, outb); break;
+        case 5: srv_rows<2, true>(c, B, lds_dp, dx, outb); break;
+        case 6: srv_rows<3, false>(c, B, lds_dp, dx, outb); break;
+        case 7: srv_rows<3, true>(c, B, lds_dp, dx, outb); break;
+        case 8: srv_rows<4, false>(c, B, lds_dp, dx, outb); break;
+        case 9: srv_rows<4, true>(c, B, lds_dp, dx, outb); break;
+        case 10: srv_rows<5, false>(c, B, lds_dp, dx, outb); break;
+        case 11: srv_rows<5, true>(c, B, lds_dp, dx, outb); break;
+        case 12: srv_rows<6, false>(c, B, lds_dp, dx, outb); break;
+        case 13: srv_rows<6, true>(c, B, lds_dp, dx, outb); break;
+        case 14: srv_rows<7, false>(c, B, lds_dp, dx, outb); break;
+        case 15: srv_rows<7, true>(c, B, lds_dp, dx, outb); break;
+        default: srv_rows<8, false>(c, B, lds_dp, dx, outb); break;  // B = 512 (the host checks K)
+        }
+        // every wave's output stores have completed (they write through) before
+        // the barrier, and so before thread 0 counts the arrival; no fence:
+        // a release fence writes back the whole L2, once per workgroup
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // also: LDS planes are rewritten by the next command
+        if (threadIdx.x == 0) {
+            const int gi = g & 7;
+            const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
+            const uint64_t n = expect - first + 1;  // commands this launch has completed
+            const uint64_t a =
+                __hip_atomic_fetch_add(&dev->group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+            if (a == n * members) {
+                const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
+                const uint64_t t =
+                    __hip_atomic_fetch_add(&dev->top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+                if (t == n * groups) __hip_atomic_store(done, expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         }
     }
 }
@@ -1154,3 +1433,238 @@ int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, in
 }
 
 }  // namespace mi355x
+
+// ---- persistent server: host side ----------------------------------------------
+namespace mi355x {
+namespace {
+
+struct DeviceScope {
+    int prev = -1;
+    explicit DeviceScope(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceScope() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+struct ServerImpl {
+    mi355x_ctx *ctx = nullptr;
+    hipStream_t stream = nullptr;
+    int64_t max_k = 0;
+    int grid = 0;
+    size_t lds = 0;
+    SrvCmd *cmd_h = nullptr, *cmd_d = nullptr;  // pinned, mapped
+    float *hx_h = nullptr, *hx_d = nullptr;
+    uint32_t *done_h = nullptr, *done_d = nullptr;
+    SrvDev *dev = nullptr;
+    float *dx = nullptr;   // device copy of x (written by workgroup 0)
+    uint32_t seq = 0;      // last command number handed out
+    bool running = false;
+    std::chrono::steady_clock::time_point last{};
+};
+
+// The kernel leaves after kSrvIdleSeconds without a command; the host
+// relaunches once it has been idle for half that, so a command never meets a
+// kernel that is about to leave.
+constexpr double kSrvIdleSeconds = 1.0;
+constexpr double kSrvWaitSeconds = 5.0;  // host wait for one command
+
+int server_launch(ServerImpl *s) {
+    MI355X_HIP(hipMemsetAsync(s->dev, 0, sizeof(SrvDev), s->stream));
+    const uint32_t first = s->seq + 1;
+    __hip_atomic_store(s->done_h, s->seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    uint64_t idle = static_cast<uint64_t>(kSrvIdleSeconds * kSrvClockHz);
+    const SrvCmd *cmd = s->cmd_d;
+    const float *hx = s->hx_d;
+    SrvDev *dev = s->dev;
+    float *dx = s->dx;
+    uint32_t *done = s->done_d;
+    void *args[] = {&cmd, &hx, &dev, &dx, &done, const_cast<uint32_t *>(&first), &idle};
+    MI355X_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(gemv_q4_0_server_kernel), dim3(s->grid),
+                                          dim3(64 * kSrvWaves), args, s->lds, s->stream));
+    s->running = true;
+    s->last = std::chrono::steady_clock::now();
+    return MI355X_OK;
+}
+
+int server_stop(ServerImpl *s) {
+    if (!s->running) return MI355X_OK;
+    s->cmd_h->exit = 1;
+    s->cmd_h->K = 0;
+    __hip_atomic_store(&s->cmd_h->seqk, static_cast<uint64_t>(++s->seq), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    s->running = false;
+    MI355X_HIP(hipStreamSynchronize(s->stream));
+    s->cmd_h->exit = 0;
+    return MI355X_OK;
+}
+
+}  // namespace
+}  // namespace mi355x
+
+struct mi355x_server {
+    mi355x::ServerImpl impl;
+};
+
+namespace mi355x {
+
+int stop_servers(mi355x_ctx *ctx) {
+    std::lock_guard<std::mutex> lk(ctx->srv_mu);
+    for (mi355x_server *srv : ctx->servers) {
+        DeviceScope dg(ctx->device);
+        const int rc = server_stop(&srv->impl);
+        if (rc) return rc;
+    }
+    return MI355X_OK;
+}
+
+}  // namespace mi355x
+
+using mi355x::set_error;
+using mi355x::hip_error;
+using mi355x::clear_error;
+
+extern "C" {
+
+int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
+    clear_error();
+    if (!ctx || !out) return set_error(MI355X_EINVAL, "mi355x_server_create: null pointer");
+    *out = nullptr;
+    if (max_k <= 0 || max_k % 256 != 0 || max_k > 64 * 8 * 32)
+        return set_error(MI355X_EINVAL, "mi355x_server_create: max_k must be a multiple of 256 up to 16384");
+    mi355x::DeviceScope dg(ctx->device);
+    int coop = 0;
+    MI355X_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device));
+    if (!coop) return set_error(MI355X_EUNSUPPORTED, "mi355x_server_create: no cooperative launch on this device");
+    auto *srv = new (std::nothrow) mi355x_server();
+    if (!srv) return set_error(MI355X_ENOMEM, "mi355x_server_create: out of memory");
+    mi355x::ServerImpl &s = srv->impl;
+    s.ctx = ctx;
+    s.max_k = max_k;
+    const int64_t B = max_k / 32;
+    s.lds = static_cast<size_t>(B) * (mi355x::kPlanes * sizeof(uint4) + sizeof(float));
+    hipError_t e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking);
+    void *p = nullptr;
+    if (e == hipSuccess) e = hipHostMalloc(&p, sizeof(mi355x::SrvCmd), hipHostMallocMapped);
+    if (e == hipSuccess) {
+        s.cmd_h = static_cast<mi355x::SrvCmd *>(p);
+        std::memset(p, 0, sizeof(mi355x::SrvCmd));
+        e = hipHostGetDevicePointer(&p, s.cmd_h, 0);
+        s.cmd_d = static_cast<mi355x::SrvCmd *>(p);
+    }
+    if (e == hipSuccess) e = hipHostMalloc(&p, static_cast<size_t>(max_k) * sizeof(float), hipHostMallocMapped);
+    if (e == hipSuccess) {
+        s.hx_h = static_cast<float *>(p);
+        e = hipHostGetDevicePointer(&p, s.hx_h, 0);
+        s.hx_d = static_cast<float *>(p);
+    }
+    if (e == hipSuccess) e = hipHostMalloc(&p, 64, hipHostMallocMapped);
+    if (e == hipSuccess) {
+        s.done_h = static_cast<uint32_t *>(p);
+        std::memset(p, 0, 64);
+        e = hipHostGetDevicePointer(&p, s.done_h, 0);
+        s.done_d = static_cast<uint32_t *>(p);
+    }
+    if (e == hipSuccess) e = hipMalloc(&p, sizeof(mi355x::SrvDev));
+    if (e == hipSuccess) s.dev = static_cast<mi355x::SrvDev *>(p);
+    if (e == hipSuccess) e = hipMalloc(&p, static_cast<size_t>(max_k) * sizeof(float));
+    if (e == hipSuccess) s.dx = static_cast<float *>(p);
+    int per_cu = 0;
+    if (e == hipSuccess)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(mi355x::gemv_q4_0_server_kernel), 64 * mi355x::kSrvWaves, s.lds);
+    if (e != hipSuccess || per_cu < 1) {
+        mi355x_server_destroy(srv);
+        return e != hipSuccess ? hip_error(e, "mi355x_server_create")
+                               : set_error(MI355X_EUNSUPPORTED, "mi355x_server_create: kernel does not fit a CU");
+    }
+    s.grid = ctx->num_cus;
+    {
+        std::lock_guard<std::mutex> lk(ctx->srv_mu);
+        ctx->servers.push_back(srv);
+    }
+    *out = srv;
+    return MI355X_OK;
+}
+
+int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs, const mi355x_server_job *jobs) {
+    clear_error();
+    if (!srv || !x || !jobs) return set_error(MI355X_EINVAL, "mi355x_server_gemv: null pointer");
+    mi355x::ServerImpl &s = srv->impl;
+    if (njobs < 1 || njobs > mi355x::kSrvMaxJobs)
+        return set_error(MI355X_EINVAL, "mi355x_server_gemv: 1 to 4 jobs per call");
+    if (K <= 0 || K % 256 != 0 || K > s.max_k)
+        return set_error(MI355X_EINVAL, "mi355x_server_gemv: K must be a multiple of 256 up to the server's max_k");
+    for (int j = 0; j < njobs; ++j) {
+        if (!jobs[j].W || !jobs[j].y || jobs[j].N <= 0)
+            return set_error(MI355X_EINVAL, "mi355x_server_gemv: bad job");
+        if (jobs[j].N > static_cast<int64_t>(mi355x::kSrvOutMax) * s.grid - s.grid)
+            return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: job of more rows than the server holds");
+        if (reinterpret_cast<uintptr_t>(jobs[j].W) % 16 != 0)
+            return set_error(MI355X_EINVAL, "mi355x_server_gemv: weights must be 16-byte aligned");
+    }
+    mi355x::DeviceScope dg(s.ctx->device);
+    const auto now = std::chrono::steady_clock::now();
+    if (s.running && std::chrono::duration<double>(now - s.last).count() > mi355x::kSrvIdleSeconds / 2) {
+        int rc = mi355x::server_stop(&s);
+        if (rc) return rc;
+    }
+    if (!s.running) {
+        int rc = mi355x::server_launch(&s);
+        if (rc) return rc;
+    }
+    std::memcpy(s.hx_h, x, static_cast<size_t>(K) * sizeof(float));
+    s.cmd_h->K = static_cast<int32_t>(K);
+    s.cmd_h->njobs = njobs;
+    for (int j = 0; j < njobs; ++j)
+        s.cmd_h->jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
+    const uint32_t v = ++s.seq;
+    __hip_atomic_store(&s.cmd_h->seqk, static_cast<uint64_t>(v) | (static_cast<uint64_t>(K) << 32), __ATOMIC_RELEASE,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0;; ++i) {
+        if (static_cast<int32_t>(__hip_atomic_load(s.done_h, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) - v) >= 0)
+            break;
+        if ((i & 1023) == 1023 &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > mi355x::kSrvWaitSeconds) {
+            // the kernel leaves by its idle rule; collect it and report
+            s.running = false;
+            (void)hipStreamSynchronize(s.stream);
+            return set_error(MI355X_EHIP, "mi355x_server_gemv: no completion within 5 s");
+        }
+    }
+    s.last = std::chrono::steady_clock::now();
+    return MI355X_OK;
+}
+
+int mi355x_server_stop(mi355x_server *srv) {
+    clear_error();
+    if (!srv) return set_error(MI355X_EINVAL, "mi355x_server_stop: null pointer");
+    mi355x::DeviceScope dg(srv->impl.ctx->device);
+    return mi355x::server_stop(&srv->impl);
+}
+
+void mi355x_server_destroy(mi355x_server *srv) {
+    if (!srv) return;
+    mi355x::ServerImpl &s = srv->impl;
+    if (s.ctx) {
+        {
+            std::lock_guard<std::mutex> lk(s.ctx->srv_mu);
+            auto &v = s.ctx->servers;
+            v.erase(std::remove(v.begin(), v.end(), srv), v.end());
+        }
+        mi355x::DeviceScope dg(s.ctx->device);
+        (void)mi355x::server_stop(&s);
+        if (s.stream) (void)hipStreamDestroy(s.stream);
+        if (s.dev) (void)hipFree(s.dev);
+        if (s.dx) (void)hipFree(s.dx);
+    }
+    if (s.cmd_h) (void)hipHostFree(s.cmd_h);
+    if (s.hx_h) (void)hipHostFree(s.hx_h);
+    if (s.done_h) (void)hipHostFree(s.done_h);
+    delete srv;
+}
+
+}  // extern "C"

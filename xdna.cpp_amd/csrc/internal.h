@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "mi355x-gemv.h"
 
@@ -44,6 +45,10 @@ struct mi355x_ctx {
     uint32_t *fence_host = nullptr;
     uint32_t *fence_dev = nullptr;
     std::atomic<uint32_t> fence_seq{0};
+    // persistent GEMV servers on this context (stopped before any hipFree,
+    // which would otherwise wait for their resident kernel)
+    std::mutex srv_mu;
+    std::vector<mi355x_server *> servers;
 };
 
 namespace mi355x {
@@ -73,6 +78,9 @@ struct GemvArgs {
 int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
+// Stops the resident kernel of every server on the context (they relaunch on
+// their next call).
+int stop_servers(mi355x_ctx *ctx);
 // Batched form: M activation rows (x + m*x_stride) into y + m*y_stride,
 // M <= q4_0_mb_capacity() (0: form not applicable).
 int q4_0_mb_capacity(const mi355x_ctx *ctx, const GemvArgs &a);

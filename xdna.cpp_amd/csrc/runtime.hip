@@ -253,6 +253,7 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
 void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     if (!ctx) return;
     DeviceGuard dg(ctx->device);
+    (void)stop_servers(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->xconv) (void)hipFree(ctx->xconv);
@@ -391,6 +392,8 @@ int mi355x_free(mi355x_ctx *ctx, void *dptr) {
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_free: null context");
     if (!dptr) return MI355X_OK;
     DeviceGuard dg(ctx->device);
+    int rc = stop_servers(ctx);
+    if (rc) return rc;
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
     MI355X_HIP(hipFree(dptr));
     return MI355X_OK;

@@ -144,11 +144,12 @@ class Model:
         if self.lib.qd_set_io(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 
-    WAIT_STREAM, WAIT_FENCE = 0, 1
+    WAIT_STREAM, WAIT_FENCE, WAIT_SERVER = 0, 1, 2
 
     def set_wait(self, mode: int) -> None:
-        """WAIT_FENCE (default): spin on a completion word after each GEMV
-        group; WAIT_STREAM: hipStreamSynchronize."""
+        """WAIT_FENCE (default): one launch per GEMV group, then a spin on a
+        completion word; WAIT_STREAM: hipStreamSynchronize instead;
+        WAIT_SERVER: GEMV groups as commands to a persistent server kernel."""
         if self.lib.qd_set_wait(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 

@@ -185,7 +185,10 @@ struct qd_model {
     int io_mode = QD_IO_MAPPED;
     int wait_mode = QD_WAIT_FENCE;
 
+    mi355x_server *server = nullptr;
+
     ~qd_model() {
+        if (server) mi355x_server_destroy(server);
         if (ctx) {
             if (weights) mi355x_free(ctx, weights);
             if (dx) mi355x_free(ctx, dx);
@@ -450,7 +453,8 @@ int qd_set_io(qd_model *m, int mode) {
 
 int qd_set_wait(qd_model *m, int mode) {
     if (!m) return fail("qd_set_wait: null model");
-    if (mode != QD_WAIT_STREAM && mode != QD_WAIT_FENCE) return fail("qd_set_wait: unknown mode");
+    if (mode != QD_WAIT_STREAM && mode != QD_WAIT_FENCE && mode != QD_WAIT_SERVER)
+        return fail("qd_set_wait: unknown mode");
     m->wait_mode = mode;
     return 0;
 }
@@ -523,6 +527,12 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     const int H = c.hidden, QD = m->q_dim(), KVD = m->kv_dim(), hd = c.head_dim;
     const int L = c.n_layers, T = n_prompt + std::max(n_gen, 1);
     omp_set_num_threads(m->threads);
+    if (backend == 0 && m->wait_mode == QD_WAIT_SERVER && !m->server) {
+        int64_t max_k = 0;
+        for (const Matrix &mat : m->mats) max_k = std::max<int64_t>(max_k, mat.K);
+        if (mi355x_server_create(m->ctx, (max_k + 255) / 256 * 256, &m->server) != MI355X_OK)
+            return fail(std::string("qd_generate: ") + mi355x_last_error());
+    }
 
     // per layer: keys [g][t / 8][i][t % 8], values [g][t][i] (see attention())
     const int tcap = (T + 7) / 8 * 8;
@@ -544,7 +554,34 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     constexpr int64_t kMappedOutMax = 65536;
     auto gemvs = [&](const float *x, int64_t K, std::initializer_list<int> ids, std::initializer_list<float *> outs) {
         const double t0 = now();
-        if (backend == 0) {
+        if (backend == 0 && m->wait_mode == QD_WAIT_SERVER) {
+            // one server command per group: runs of matrices adjacent in HBM
+            // with the same K are one job, outputs land in pinned memory
+            mi355x_server_job jobs[4];
+            int nj = 0;
+            int64_t off = 0;
+            const Matrix *run = nullptr;
+            for (int id : ids) {
+                const Matrix &mat = m->mats[id];
+                if (run && m->fuse && mat.K == run->K &&
+                    mat.dev == static_cast<const uint8_t *>(jobs[nj - 1].W) + jobs[nj - 1].N * (run->K / 32) * 18) {
+                    jobs[nj - 1].N += mat.N;
+                } else {
+                    if (nj == 4) return -1;
+                    jobs[nj++] = {mat.dev, mat.N, m->hy_dev + off};
+                }
+                off += mat.N;
+                run = &mat;
+            }
+            if (mi355x_server_gemv(m->server, x, K, nj, jobs) != MI355X_OK) return -1;
+            launches += nj;
+            off = 0;
+            auto oi = outs.begin();
+            for (int id : ids) {
+                std::memcpy(*oi++, m->hy + off, static_cast<size_t>(m->mats[id].N) * 4);
+                off += m->mats[id].N;
+            }
+        } else if (backend == 0) {
             // all on the context's stream: one wait per group
             const hipStream_t st = static_cast<hipStream_t>(mi355x_ctx_stream(m->ctx));
             int64_t n_out = 0;
@@ -671,6 +708,8 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     }
     if (n_gen > 0 && n_pos == n_prompt) t_gen0 = now();  // n_gen == 1: no generation-phase passes
     const double t_end = now();
+    // the resident server kernel leaves with the decode loop
+    if (m->server && mi355x_server_stop(m->server) != MI355X_OK && !rc) rc = -1;
     if (rc) return fail(std::string("qd_generate: GEMV failed: ") + (backend == 0 ? mi355x_last_error() : "callback"));
     if (n_gen > 0) m->last_logits = logits;
     m->last_launches = backend == 0 ? launches : 0;

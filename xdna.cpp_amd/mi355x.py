@@ -46,6 +46,10 @@ _SIGNATURES = {
     "mi355x_ctx_destroy": (None, [_vp]),
     "mi355x_ctx_sync": (_c.c_int, [_vp]),
     "mi355x_ctx_fence": (_c.c_int, [_vp]),
+    "mi355x_server_create": (_c.c_int, [_vp, _c.c_int64, _c.POINTER(_vp)]),
+    "mi355x_server_gemv": (_c.c_int, [_vp, _vp, _c.c_int64, _c.c_int, _vp]),
+    "mi355x_server_stop": (_c.c_int, [_vp]),
+    "mi355x_server_destroy": (None, [_vp]),
     "mi355x_ctx_set_option": (_c.c_int, [_vp, _c.c_int, _c.c_int64]),
     "mi355x_ctx_stream": (_vp, [_vp]),
     "mi355x_ctx_device": (_c.c_int, [_vp]),
@@ -184,6 +188,43 @@ class ResidentWeights:
 
     def free(self) -> None:
         self.buf.free()
+
+
+class ServerJob(ctypes.Structure):
+    _fields_ = [("W", ctypes.c_void_p), ("N", ctypes.c_int64), ("y", ctypes.c_void_p)]
+
+
+class Server:
+    """Persistent Q4_0 GEMV server (mi355x_server_*) on a Context's device."""
+
+    def __init__(self, ctx: "Context", max_k: int):
+        self.lib = ctx.lib
+        h = ctypes.c_void_p()
+        check(self.lib.mi355x_server_create(ctx.h, max_k, ctypes.byref(h)))
+        self.h = h.value
+
+    def gemv_ptr(self, x: np.ndarray, jobs) -> int:
+        """jobs: [(W device pointer, N, y device-visible pointer)]; x: host f32."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        arr = (ServerJob * len(jobs))(*[ServerJob(w, n, y) for w, n, y in jobs])
+        return self.lib.mi355x_server_gemv(self.h, x.ctypes.data, x.size, len(jobs), arr)
+
+    def gemv(self, x: np.ndarray, jobs) -> None:
+        check(self.gemv_ptr(x, jobs))
+
+    def stop(self) -> None:
+        check(self.lib.mi355x_server_stop(self.h))
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.mi355x_server_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class Context:
