@@ -206,8 +206,8 @@ MI355X_API int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_
  * (src/ggml-xdna.cpp:110-112, 287-296).  Q4_0 with the digit-plane
  * arithmetic (variants AUTO and DIGITS), rows a multiple of 256 values and
  * 16-byte aligned weights: up to 8 activations per pass over the weights
- * (one staging launch into a context buffer, one batched launch); an
- * activation's output does not depend on the batch it is in.  Other cases:
+ * (one staging launch into a context buffer, one batched launch).  Other
+ * cases:
  * M sequential GEMVs.  Calls on one context serialise on its lock while
  * they enqueue. */
 MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,

@@ -1,11 +1,11 @@
 """Batched Q4_0 GEMV (mi355x_gemv_batched): M activation rows against the same
 resident weights, the M>1 case the reference admits for weights in its own
 buffer type and computes as M sequential GEMVs (src/ggml-xdna.cpp:110-112,
-287-296).  The batched form reads the weights once per launch.  Every output
+287-296).  The batched forms read the weights once per launch.  Every output
 must be within the GEMV tolerance of the oracle, and an activation's output
-must not depend on the batch it came in (bit-identical across batch sizes
-and positions: the per-(row, activation) arithmetic and reduction tree are
-the same in every batch configuration)."""
+must agree across batch sizes and positions to float rounding (the form --
+pipelined or K-split -- depends on the batch size, the arithmetic per block
+does not)."""
 import numpy as np
 import pytest
 
@@ -46,7 +46,7 @@ def test_batched_matches_oracle(ctx, oracle, N, K, M):
 @pytest.mark.parametrize("N,K", [(300, 2048), (777, 5120), (512, 8192), (128, 16384)])
 def test_batched_output_independent_of_batch(ctx, N, K):
     """Activation j alone (a one-activation remainder), in a pair, in a batch
-    of 4 and in a batch of 8 at another position: identical bits."""
+    of 4 and in a batch of 8 at another position: the same values."""
     raw = synth.random_q4_0(N, K, seed=11)
     xs = np.stack([synth.activations(K, seed=400 + m) for m in range(9)])
     w = ctx.resident(Q4_0, raw, N, K)
@@ -57,8 +57,9 @@ def test_batched_output_independent_of_batch(ctx, N, K):
         y4 = ctx.gemv_batched(w, xs[4:8])
     finally:
         w.free()
-    assert np.array_equal(y9[:8], y8)
-    assert np.array_equal(y2, y8[6:8]) and np.array_equal(y4, y8[4:8])
+    scale = np.abs(y8).max()
+    for a, b in ((y9[:8], y8), (y2, y8[6:8]), (y4, y8[4:8])):
+        np.testing.assert_allclose(a, b, rtol=2e-6, atol=2e-6 * scale)
 
 
 def test_batched_strides_and_misaligned_rows(ctx, oracle):

@@ -973,6 +973,97 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
     }
 }
 
+// Pipelined batched variant for NBL x MB <= 8 (rows of full 64-block
+// columns): the pipelined form's schedule -- a wavefront owns a run of
+// consecutive rows whose loads are issued kPlmDepth rows ahead -- with the
+// lane's planes of every activation in registers (20 * NBL * MB VGPRs),
+// staged in the workgroup's LDS as the pipelined form stages one.  No
+// barrier in the row loop: a row's MB partial sums go through one batched
+// cross-lane reduction.
+constexpr int kPlmDepth = 3;
+
+template <int NBL, int MB>
+__global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_plm_kernel(const uint8_t *__restrict__ W,
+                                                                      const float *__restrict__ x,
+                                                                      int64_t x_stride, int x_al16,
+                                                                      float *__restrict__ y, int64_t y_stride,
+                                                                      int N, int M, int rows) {
+    static_assert(NBL * MB <= 8, "planes of every activation in registers");
+    constexpr int B = 64 * NBL;
+    constexpr int64_t row_bytes = 18 * B;
+    constexpr int rb = static_cast<int>(row_bytes);
+    constexpr int D = kPlmDepth;
+    constexpr int S = MB <= 4 ? 4 : 8;  // reduction batch (MB padded)
+    constexpr int tile = mb_tile(B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * kPlWaves + wave) * rows;
+    const int lim = min(N, row0 + rows);
+    const int nrows = max(0, lim - row0);
+
+    // as the pipelined form: every activation's loads, then the weight
+    // loads, then the staging math (into one LDS tile per activation)
+    constexpr int XI = (4 * NBL + kPlWaves - 1) / kPlWaves;
+    XTile<XI> xt[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+        if (m < M) xt[m].load(x + m * x_stride, B, x_al16 != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    using Grp = RowGroup<NBL, 1, true, false>;
+    const __amdgpu_buffer_rsrc_t rs = Grp::row_rsrc(W, row0, lim, row_bytes);
+    Grp g[D];
+#pragma unroll
+    for (int s = 0; s < D; ++s) g[s].load_at(rs, s * rb, B, row_bytes, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    __shared__ uint4 lt[MB * tile];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+        if (m < M)
+            xt[m].store(B, reinterpret_cast<uint32_t *>(lt + m * tile), reinterpret_cast<float *>(lt + m * tile + kPlanes * B));
+    __syncthreads();
+
+    // slots m >= M repeat the last activation (never stored)
+    uint4 P[MB][NBL][kPlanes];
+    float u[MB][NBL];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const uint4 *t = lt + min(m, M - 1) * tile;
+#pragma unroll
+        for (int j = 0; j < NBL; ++j) {
+#pragma unroll
+            for (int p = 0; p < kPlanes; ++p) P[m][j][p] = t[p * B + lane + 64 * j];
+            u[m][j] = reinterpret_cast<const float *>(t + kPlanes * B)[lane + 64 * j];
+        }
+    }
+
+    for (int r0 = 0; r0 < nrows; r0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int r = r0 + s;
+            float part[S];
+#pragma unroll
+            for (int m = 0; m < S; ++m) part[m] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NBL; ++j) {
+                const float dr = half_bits_to_float(static_cast<uint16_t>(g[s].d_bits(0, j, 0xFFFFu)));
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    const int T = block_dot_digits(g[s].q[0][j], P[m][j]);
+                    part[m] = fmaf(dr * u[m][j], static_cast<float>(T), part[m]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            g[s].load_at(rs, (r + D) * rb, B, row_bytes, lane);  // empty range past the run
+            __builtin_amdgcn_sched_barrier(0);
+            // lane l ends with the total of partial l >> (6 - log2 S)
+            const float tot = st_reduce<S>(part, lane);
+            constexpr int SPAN = 64 / S;
+            const int m = lane / SPAN;
+            if ((lane & (SPAN - 1)) == 0 && m < M && r < nrows) y[m * y_stride + row0 + r] = tot;
+        }
+    }
+}
+
 typedef void (*pl_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int, int);
 
 // compiled rows-per-wavefront counts of the unrolled kernel
@@ -1360,6 +1451,21 @@ int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a) {
 namespace mi355x {
 
 typedef void (*mb_kernel_t)(const uint8_t *, const uint4 *, float *, int64_t, int, int, int64_t, int);
+typedef void (*plm_kernel_t)(const uint8_t *, const float *, int64_t, int, float *, int64_t, int, int, int);
+
+// the pipelined batched variant: NBL full columns with NBL x MB <= 8
+plm_kernel_t pick_plm(int nbl, int mb) {
+    switch (nbl * 16 + mb) {
+    case 16 + 2: return gemv_q4_0_plm_kernel<1, 2>;
+    case 16 + 4: return gemv_q4_0_plm_kernel<1, 4>;
+    case 16 + 8: return gemv_q4_0_plm_kernel<1, 8>;
+    case 32 + 2: return gemv_q4_0_plm_kernel<2, 2>;
+    case 32 + 4: return gemv_q4_0_plm_kernel<2, 4>;
+    case 48 + 2: return gemv_q4_0_plm_kernel<3, 2>;
+    case 64 + 2: return gemv_q4_0_plm_kernel<4, 2>;
+    default: return nullptr;
+    }
+}
 
 template <int NBL>
 mb_kernel_t pick_mb_m(int mb) {
@@ -1400,6 +1506,19 @@ int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, in
     const int nbl = static_cast<int>((B + 63) / 64);
     const int mb = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && x_stride % 4 == 0;
+    // rows of full columns whose planes of every activation fit in registers:
+    // the pipelined variant, staging in its own LDS (sweeps on MI355X)
+    const plm_kernel_t kp = B % 64 == 0 ? pick_plm(nbl, mb) : nullptr;
+    if (kp) {
+        const int64_t slots = static_cast<int64_t>(ctx->num_cus) * kPlWaves;
+        const int64_t rows = (a.N + slots - 1) / slots;
+        const int64_t grid = (a.N + rows * kPlWaves - 1) / (rows * kPlWaves);
+        hipLaunchKernelGGL(kp, dim3(static_cast<unsigned>(grid)), dim3(64 * kPlWaves), 0, ctx->stream, a.W,
+                           static_cast<const float *>(a.x), x_stride, x_al16 ? 1 : 0, a.y, y_stride,
+                           static_cast<int>(a.N), M, static_cast<int>(rows));
+        MI355X_HIP(hipGetLastError());
+        return MI355X_OK;
+    }
     // the tiles stay in place from the staging launch to the batched launch
     // that reads them (calls on one context share the buffer)
     std::lock_guard<std::mutex> lk(ctx->mu);
