@@ -62,11 +62,13 @@ def test_gpu_decode_repeatable():
         assert one[0] == a[0]
 
 
-def test_fused_launches_match_per_matrix_launches():
-    """q|k|v and gate|up as one launch each (adjacent in HBM) against one
-    launch per matrix: same tokens, logits equal to float rounding."""
+@pytest.mark.parametrize("wait", ["fence", "server"])
+def test_fused_launches_match_per_matrix_launches(wait):
+    """q|k|v and gate|up as one launch (one server job) each, adjacent in
+    HBM, against one per matrix: same tokens, logits equal to float rounding."""
     with decode.Model(threads=4, **TINY) as m:
         m.attach_gpu(0)
+        m.set_wait(m.WAIT_FENCE if wait == "fence" else m.WAIT_SERVER)
         p = decode.prompt_tokens(9, 1000, 4)
         fused, _ = m.generate(p, 6)
         lf = m.last_logits()
@@ -77,6 +79,7 @@ def test_fused_launches_match_per_matrix_launches():
         assert m.last_launches() == 5 * (7 * TINY["n_layers"] + 1)
         assert np.array_equal(fused, single)
         assert np.abs(lf - ls).max() <= 1e-5 * np.abs(ls).max()
+        assert m.last_wait() == (m.WAIT_FENCE if wait == "fence" else m.WAIT_SERVER)
 
 
 def test_mapped_io_matches_staged_io():
@@ -88,6 +91,7 @@ def test_mapped_io_matches_staged_io():
     cfg = dict(TINY, vocab=70000)
     with decode.Model(threads=4, **cfg) as m:
         m.attach_gpu(0)
+        m.set_wait(m.WAIT_FENCE)  # I/O modes are those of the launch path
         p = decode.prompt_tokens(7, cfg["vocab"], 5)
         mapped, _ = m.generate(p, 5)
         lm = m.last_logits()
@@ -114,6 +118,7 @@ def test_ggml_numerics_decode_token_identical_to_cpu(cfg):
         m.set_variant(mi355x.VARIANT_GGML_Q8)
         gpu_toks, _ = m.generate(p, 8)
         gpu_logits = m.last_logits()
+        assert m.last_wait() == m.WAIT_FENCE  # the server does not take this variant
         m.set_variant(mi355x.VARIANT_AUTO)
     # every GEMV is bit-identical to the restatement and the host ops are the
     # same code, so the whole decode is: tokens and logits alike.  (Q8_0
@@ -134,9 +139,12 @@ def test_server_decode_token_identical(cfg, n_prompt, n_gen):
         cpu_toks, _ = m.generate(p, n_gen, f)
         cpu_logits = m.last_logits()
         m.attach_gpu(0)
+        m.set_wait(m.WAIT_FENCE)
         launch_toks, _ = m.generate(p, n_gen)
+        assert m.last_wait() == m.WAIT_FENCE
         m.set_wait(m.WAIT_SERVER)
         srv_toks, t = m.generate(p, n_gen)
+        assert m.last_wait() == m.WAIT_SERVER
         srv_logits = m.last_logits()
         again, _ = m.generate(p, n_gen)  # a second decode relaunches the server
         m.set_wait(m.WAIT_FENCE)

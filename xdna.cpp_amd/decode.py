@@ -58,6 +58,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_set_io.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_wait.restype = C.c_int
     lib.qd_set_wait.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_last_wait.restype = C.c_int
+    lib.qd_last_wait.argtypes = [C.c_void_p]
     lib.qd_last_launches.restype = C.c_int64
     lib.qd_last_launches.argtypes = [C.c_void_p]
     lib.qd_attach_gpu.restype = C.c_int
@@ -147,11 +149,16 @@ class Model:
     WAIT_STREAM, WAIT_FENCE, WAIT_SERVER = 0, 1, 2
 
     def set_wait(self, mode: int) -> None:
-        """WAIT_FENCE (default): one launch per GEMV group, then a spin on a
-        completion word; WAIT_STREAM: hipStreamSynchronize instead;
-        WAIT_SERVER: GEMV groups as commands to a persistent server kernel."""
+        """WAIT_SERVER (default): GEMV groups as commands to a persistent
+        server kernel (where it applies, else WAIT_FENCE); WAIT_FENCE: one
+        launch per GEMV group, then a spin on a completion word; WAIT_STREAM:
+        hipStreamSynchronize instead."""
         if self.lib.qd_set_wait(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
+
+    def last_wait(self) -> int:
+        """The wait mode the last GPU decode used."""
+        return self.lib.qd_last_wait(self.h)
 
     def last_launches(self) -> int:
         return self.lib.qd_last_launches(self.h)

@@ -183,7 +183,9 @@ struct qd_model {
     const float *hx_dev = nullptr;
     float *hy_dev = nullptr;
     int io_mode = QD_IO_MAPPED;
-    int wait_mode = QD_WAIT_FENCE;
+    int wait_mode = QD_WAIT_SERVER;
+    int variant = MI355X_VARIANT_AUTO;
+    int last_wait = QD_WAIT_FENCE;  // the mode the last GPU decode used
 
     mi355x_server *server = nullptr;
 
@@ -441,6 +443,7 @@ int qd_set_variant(qd_model *m, int variant) {
     if (!m || !m->ctx) return fail("qd_set_variant: qd_attach_gpu first");
     if (mi355x_ctx_set_option(m->ctx, MI355X_OPT_VARIANT, variant) != MI355X_OK)
         return fail(std::string("qd_set_variant: ") + mi355x_last_error());
+    m->variant = variant;
     return 0;
 }
 
@@ -460,6 +463,8 @@ int qd_set_wait(qd_model *m, int mode) {
 }
 
 int64_t qd_last_launches(const qd_model *m) { return m ? m->last_launches : 0; }
+
+int qd_last_wait(const qd_model *m) { return m ? m->last_wait : -1; }
 
 int qd_last_logits(const qd_model *m, float *out, int n) {
     if (!m || !out || n != m->c.vocab || m->last_logits.size() != static_cast<size_t>(n))
@@ -527,12 +532,18 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     const int H = c.hidden, QD = m->q_dim(), KVD = m->kv_dim(), hd = c.head_dim;
     const int L = c.n_layers, T = n_prompt + std::max(n_gen, 1);
     omp_set_num_threads(m->threads);
-    if (backend == 0 && m->wait_mode == QD_WAIT_SERVER && !m->server) {
-        int64_t max_k = 0;
-        for (const Matrix &mat : m->mats) max_k = std::max<int64_t>(max_k, mat.K);
-        if (mi355x_server_create(m->ctx, (max_k + 255) / 256 * 256, &m->server) != MI355X_OK)
-            return fail(std::string("qd_generate: ") + mi355x_last_error());
+    // the server computes the digit-plane arithmetic on rows of multiples of
+    // 256 values; other variants and shapes take launch + fence
+    bool use_server = backend == 0 && m->wait_mode == QD_WAIT_SERVER &&
+                      (m->variant == MI355X_VARIANT_AUTO || m->variant == MI355X_VARIANT_DIGITS);
+    int64_t max_k = 0;
+    for (const Matrix &mat : m->mats) {
+        max_k = std::max<int64_t>(max_k, mat.K);
+        if (mat.K % 256 != 0) use_server = false;
     }
+    if (use_server && !m->server && mi355x_server_create(m->ctx, max_k, &m->server) != MI355X_OK)
+        use_server = false;  // e.g. no cooperative launch: one launch per group
+    const int wait = !use_server && m->wait_mode == QD_WAIT_SERVER ? QD_WAIT_FENCE : m->wait_mode;
 
     // per layer: keys [g][t / 8][i][t % 8], values [g][t][i] (see attention())
     const int tcap = (T + 7) / 8 * 8;
@@ -554,7 +565,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     constexpr int64_t kMappedOutMax = 65536;
     auto gemvs = [&](const float *x, int64_t K, std::initializer_list<int> ids, std::initializer_list<float *> outs) {
         const double t0 = now();
-        if (backend == 0 && m->wait_mode == QD_WAIT_SERVER) {
+        if (backend == 0 && use_server) {
             // one server command per group: runs of matrices adjacent in HBM
             // with the same K are one job, outputs land in pinned memory
             mi355x_server_job jobs[4];
@@ -619,7 +630,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
                 hipMemcpyAsync(m->hy, m->dy, static_cast<size_t>(off) * 4, hipMemcpyDeviceToHost, st) != hipSuccess)
                 return -1;
             // the outputs are in pinned host memory, which the fence covers
-            if ((m->wait_mode == QD_WAIT_FENCE ? mi355x_ctx_fence(m->ctx) : mi355x_ctx_sync(m->ctx)) != MI355X_OK)
+            if ((wait == QD_WAIT_FENCE ? mi355x_ctx_fence(m->ctx) : mi355x_ctx_sync(m->ctx)) != MI355X_OK)
                 return -1;
             off = 0;
             auto oi = outs.begin();
@@ -713,6 +724,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     if (rc) return fail(std::string("qd_generate: GEMV failed: ") + (backend == 0 ? mi355x_last_error() : "callback"));
     if (n_gen > 0) m->last_logits = logits;
     m->last_launches = backend == 0 ? launches : 0;
+    if (backend == 0) m->last_wait = use_server ? QD_WAIT_SERVER : wait;
     if (timings) {
         timings[0] = t_gen0 - t_start;
         timings[1] = t_end - t_gen0;

@@ -86,15 +86,19 @@ QD_API void qd_set_fuse(qd_model *m, int on);
 #define QD_IO_MAPPED 1
 QD_API int qd_set_io(qd_model *m, int mode);
 /* How GEMV groups reach the GPU on the GPU path:
- * QD_WAIT_FENCE (default): one launch per group, then mi355x_ctx_fence (spin
- * on a completion word in pinned memory); QD_WAIT_STREAM: one launch per
- * group, then mi355x_ctx_sync (hipStreamSynchronize); QD_WAIT_SERVER: every
- * group is a command to a persistent GEMV server (mi355x_server_*), outputs
- * in pinned memory, no launch per group. */
+ * QD_WAIT_SERVER (default): every group is a command to a persistent GEMV
+ * server (mi355x_server_*), outputs in pinned memory, no launch per group --
+ * for the AUTO and DIGITS variants with rows of multiples of 256 values on a
+ * device with cooperative launch, else as QD_WAIT_FENCE;
+ * QD_WAIT_FENCE: one launch per group, then mi355x_ctx_fence (spin on a
+ * completion word in pinned memory); QD_WAIT_STREAM: one launch per group,
+ * then mi355x_ctx_sync (hipStreamSynchronize).  qd_last_wait gives the mode
+ * the last GPU decode used. */
 #define QD_WAIT_STREAM 0
 #define QD_WAIT_FENCE 1
 #define QD_WAIT_SERVER 2
 QD_API int qd_set_wait(qd_model *m, int mode);
+QD_API int qd_last_wait(const qd_model *m);
 /* Kernel variant of the GPU GEMVs (MI355X_OPT_VARIANT of mi355x-gemv.h):
  * MI355X_VARIANT_GGML_Q8 gives ggml-cpu's Q8_0-activation arithmetic. */
 QD_API int qd_set_variant(qd_model *m, int variant);
