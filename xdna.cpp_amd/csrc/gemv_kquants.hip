@@ -501,6 +501,30 @@ __device__ __forceinline__ float combine(const int (&s)[3]) {
     return fmaf(static_cast<float>(s[2]), 65536.0f, fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0])));
 }
 
+// The same sum formed in int32 before one conversion.  It equals
+// sum_i code_i * Z_i with |Z_i| < 2^22, so for 16 values of codes below 32
+// (Q4_K, Q5_K) it stays below 16 * 31 * 2^22 < 2^31, as do the partial
+// terms (|s2| <= 16 * 31 * 64).
+__device__ __forceinline__ float combine_i(const int (&s)[3]) {
+    return static_cast<float>(s[0] + s[1] * 256 + s[2] * 65536);
+}
+
+// (scale, min) of sub-blocks 2c and 2c+1 of a Q4_K/Q5_K block at once: their
+// bytes are adjacent in each of the three scale words (w0 = bytes 0-3,
+// w1 = 4-7, w2 = 8-11), so both 6-bit pairs come out of 16-bit lanes
+// (include/xdna/kquants.h:204-212 per sub-block).
+__device__ __forceinline__ void scale_min_pair_k4(int c, uint32_t w0, uint32_t w1, uint32_t w2, float &sc0,
+                                                  float &m0, float &sc1, float &m1) {
+    const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
+    const uint32_t a2 = (w0 >> sh) & 0xFFFFu, b2 = (w1 >> sh) & 0xFFFFu, c2 = (w2 >> sh) & 0xFFFFu;
+    const uint32_t sc = c < 2 ? (a2 & 0x3F3Fu) : ((c2 & 0x0F0Fu) | ((a2 >> 2) & 0x3030u));
+    const uint32_t mn = c < 2 ? (b2 & 0x3F3Fu) : (((c2 >> 4) & 0x0F0Fu) | ((b2 >> 2) & 0x3030u));
+    sc0 = static_cast<float>(sc & 0xFFu);
+    sc1 = static_cast<float>(sc >> 8);
+    m0 = static_cast<float>(mn & 0xFFu);
+    m1 = static_cast<float>(mn >> 8);
+}
+
 // Accumulates code dword `c` (4 values) against dword `i` of the 3 planes.
 __device__ __forceinline__ void dot3(uint32_t c, const XDig &x, int i, int (&s)[3]) {
     s[0] = sdot4(c, x.z[0][i], s[0]);
@@ -594,11 +618,10 @@ struct KqDg<MI355X_TYPE_Q4_K> {
         }
         const int c = s >> 1;
         float sc0, m0, sc1, m1;
-        scale_min_k4(2 * c, g.hd[1], g.hd[2], g.hd[3], sc0, m0);
-        scale_min_k4(2 * c + 1, g.hd[1], g.hd[2], g.hd[3], sc1, m1);
+        scale_min_pair_k4(c, g.hd[1], g.hd[2], g.hd[3], sc0, m0, sc1, m1);
         const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
-        return ldexpf((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
-               ldexpf((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+        return ldexpf((d * sc0) * combine_i(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
+               ldexpf((d * sc1) * combine_i(sb) - (dmin * m1) * x.zs[1], x.e[1]);
     }
 };
 
@@ -614,11 +637,10 @@ struct KqDg<MI355X_TYPE_Q5_K> {
             dot3(((g.q[i] >> 4) & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c + 1)) & 0x01010101u) << 4), x, 4 + i, sb);
         }
         float sc0, m0, sc1, m1;
-        scale_min_k4(2 * c, g.hd[1], g.hd[2], g.hd[3], sc0, m0);
-        scale_min_k4(2 * c + 1, g.hd[1], g.hd[2], g.hd[3], sc1, m1);
+        scale_min_pair_k4(c, g.hd[1], g.hd[2], g.hd[3], sc0, m0, sc1, m1);
         const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
-        return ldexpf((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
-               ldexpf((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+        return ldexpf((d * sc0) * combine_i(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
+               ldexpf((d * sc1) * combine_i(sb) - (dmin * m1) * x.zs[1], x.e[1]);
     }
 };
 
