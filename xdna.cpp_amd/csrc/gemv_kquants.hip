@@ -502,9 +502,10 @@ __device__ __forceinline__ float combine(const int (&s)[3]) {
 }
 
 // The same sum formed in int32 before one conversion.  It equals
-// sum_i code_i * Z_i with |Z_i| < 2^22, so for 16 values of codes below 32
-// (Q4_K, Q5_K) it stays below 16 * 31 * 2^22 < 2^31, as do the partial
-// terms (|s2| <= 16 * 31 * 64).
+// sum_i code_i * Z_i with |Z_i| <= 2^22, so it stays below 2^31 for 16
+// values of codes below 32 (Q4_K, Q5_K) and 8 values of codes below 64
+// (Q6_K, Q3_K), as do the partial terms (|s2| <= 8 * 63 * 64 or 16 * 31 * 64:
+// |s2| * 2^16 + |s1| * 2^8 + |s0| < 2.14e9).
 __device__ __forceinline__ float combine_i(const int (&s)[3]) {
     return static_cast<float>(s[0] + s[1] * 256 + s[2] * 65536);
 }
@@ -664,7 +665,7 @@ struct KqDg<MI355X_TYPE_Q6_K> {
             const uint32_t word = j < 2 ? g.sw[0] : g.sw[1];
             const int idx = 2 * (j & 1) + kk;
             const float sc = static_cast<float>(static_cast<int32_t>(word << (24 - 8 * idx)) >> 24);
-            acc = fmaf(sc, ldexpf(combine(sg[j]) - 32.0f * x.zs[j], x.e[j]), acc);
+            acc = fmaf(sc, ldexpf(combine_i(sg[j]) - 32.0f * x.zs[j], x.e[j]), acc);
         }
         return half_f(g.d) * acc;
     }
@@ -694,7 +695,7 @@ struct KqDg<MI355X_TYPE_Q3_K> {
             const uint32_t lo = (byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u;
             const uint32_t hi = (byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
             const float sc = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
-            acc = fmaf(sc, ldexpf(combine(sg[j]) - 4.0f * x.zs[j], x.e[j]), acc);
+            acc = fmaf(sc, ldexpf(combine_i(sg[j]) - 4.0f * x.zs[j], x.e[j]), acc);
         }
         return half_f(g.d) * acc;
     }
