@@ -38,6 +38,28 @@ def test_forward_matches_numpy_qwen2(oracle, cfg):
         assert t["gen_passes"] == 5 and t["gen_s"] > 0
 
 
+# long enough for the threaded attention (>= 64 positions: two 64-position
+# score blocks, the second partial), 12 query heads on one KV head (blocks of
+# 8 and 4 heads) and a head dimension of 5 eight-wide slices
+LONG = dict(n_layers=2, hidden=480, n_heads=12, n_kv_heads=1, head_dim=40, ffn=256, vocab=300,
+            rope_theta=1e4, norm_eps=1e-6, seed=5)
+
+
+def test_long_context_matches_numpy_and_thread_count(oracle):
+    p = decode.prompt_tokens(70, LONG["vocab"], 4)
+    f, _ = orc.decode_gemv("oracle")
+    runs = []
+    for threads in (1, 5):
+        with decode.Model(threads=threads, **LONG) as m:
+            runs.append((m.generate(p, 5, f)[0], m.last_logits()))
+            if threads == 1:
+                rt, rl = Qwen2Numpy(m, oracle).generate(p, 5)
+    assert np.array_equal(runs[0][0], rt)
+    assert np.abs(runs[0][1] - rl).max() <= 1e-5 * np.abs(rl).max()
+    # the attention's split of the work does not depend on the team size
+    assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+
+
 def test_model_shapes_and_vectors():
     with decode.Model(threads=2, **TINY) as m:
         assert m.n_matrices() == 7 * 2 + 1

@@ -235,8 +235,19 @@ void fill_vector(std::vector<float> &v, int64_t n, uint64_t seed, uint64_t strea
 }
 
 void rmsnorm(const float *x, const float *w, float *out, int n, float eps) {
-    double ss = 0.0;
-    for (int i = 0; i < n; ++i) ss += static_cast<double>(x[i]) * x[i];
+    // sum of squares in double (a float's square is exact there), in 16
+    // interleaved partial sums so the loop runs at vector throughput
+    __m256d acc[4] = {_mm256_setzero_pd(), _mm256_setzero_pd(), _mm256_setzero_pd(), _mm256_setzero_pd()};
+    int i0 = 0;
+    for (; i0 + 16 <= n; i0 += 16)
+        for (int j = 0; j < 4; ++j) {
+            const __m256d v = _mm256_cvtps_pd(_mm_loadu_ps(x + i0 + 4 * j));
+            acc[j] = _mm256_fmadd_pd(v, v, acc[j]);
+        }
+    alignas(32) double lanes[4];
+    _mm256_store_pd(lanes, _mm256_add_pd(_mm256_add_pd(acc[0], acc[1]), _mm256_add_pd(acc[2], acc[3])));
+    double ss = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
+    for (int i = i0; i < n; ++i) ss += static_cast<double>(x[i]) * x[i];
     const float s = 1.0f / std::sqrt(static_cast<float>(ss / n) + eps);
     for (int i = 0; i < n; ++i) out[i] = x[i] * s * w[i];
 }
@@ -366,6 +377,50 @@ void attention(const float *q, const float *K, const float *V, int n_t, int tcap
                                 tcap, n_t, att + static_cast<size_t>(h0) * hd + 8 * sl);
                 }
     }
+}
+
+// index of the first largest element, as std::max_element: 32 lanes (four
+// independent registers, so the compare-select chains overlap) each keep
+// their first maximum above -inf (strict >), then ties go to the lowest
+// index.  NaNs never win, except at index 0, where max_element keeps them.
+int argmax(const float *x, int n) {
+    if (n < 64 || std::isnan(x[0])) return static_cast<int>(std::max_element(x, x + n) - x);
+    __m256 best[4];
+    __m256i bi[4], idx[4];
+    for (int a = 0; a < 4; ++a) {
+        best[a] = _mm256_set1_ps(-INFINITY);
+        bi[a] = _mm256_set1_epi32(-1);
+        idx[a] = _mm256_add_epi32(_mm256_setr_epi32(0, 1, 2, 3, 4, 5, 6, 7), _mm256_set1_epi32(8 * a));
+    }
+    const __m256i step = _mm256_set1_epi32(32);
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int a = 0; a < 4; ++a) {
+            const __m256 v = _mm256_loadu_ps(x + i + 8 * a);
+            const __m256 gt = _mm256_cmp_ps(v, best[a], _CMP_GT_OQ);
+            best[a] = _mm256_blendv_ps(best[a], v, gt);
+            bi[a] = _mm256_blendv_epi8(bi[a], idx[a], _mm256_castps_si256(gt));
+            idx[a] = _mm256_add_epi32(idx[a], step);
+        }
+    alignas(32) float bv[32];
+    alignas(32) int32_t bx[32];
+    for (int a = 0; a < 4; ++a) {
+        _mm256_store_ps(bv + 8 * a, best[a]);
+        _mm256_store_si256(reinterpret_cast<__m256i *>(bx + 8 * a), bi[a]);
+    }
+    int r = -1;
+    float rv = -INFINITY;
+    for (int l = 0; l < 32; ++l)
+        if (bx[l] >= 0 && (r < 0 || bv[l] > rv || (bv[l] == rv && bx[l] < r))) {
+            rv = bv[l];
+            r = bx[l];
+        }
+    for (; i < n; ++i)
+        if (x[i] > rv) {
+            rv = x[i];
+            r = i;
+        }
+    return r < 0 ? 0 : r;  // nothing above -inf: max_element keeps index 0
 }
 
 double now() {
@@ -713,7 +768,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
         if (pos + 1 < n_prompt || n_gen == 0) continue;  // only the last prompt token needs logits
         if ((rc = gemvs(xn.data(), H, {7 * L}, {logits.data()}))) break;
         th = now();
-        tok = static_cast<int32_t>(std::max_element(logits.begin(), logits.end()) - logits.begin());
+        tok = argmax(logits.data(), c.vocab);
         t_host += now() - th;
         out_tokens[pos + 1 - n_prompt] = tok;
     }
