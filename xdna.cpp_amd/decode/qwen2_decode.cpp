@@ -297,7 +297,7 @@ inline float fast_exp(float x) {
 //      a score pass covers 8 positions per AVX2 register for up to 8 heads
 //      that share K_g, reading 4 KB contiguous blocks (unused slots zero);
 //   V: [g][t][i].
-// Passes: scores (in blocks of 64 positions), softmax per head, then P V in
+// Passes: scores (in blocks of 32 positions), softmax per head, then P V in
 // 8-wide slices of the head dimension.  sc has n_heads * tcap floats.
 template <int NJ>
 void scores_block(const float *q, const float *Kg, int hd, int tcap, int t0, int t1, float scale, float *sc) {
@@ -338,7 +338,7 @@ void attention(const float *q, const float *K, const float *V, int n_t, int tcap
     const int group = n_heads / n_kv;
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
     const int hb_count = (group + 7) / 8;  // blocks of up to 8 heads per KV head
-    const int n_chunks = (n_t + 63) / 64;
+    const int n_chunks = (n_t + 31) / 32;  // score blocks: enough tasks for a 16-thread team
     const int n_slices = hd / 8;
     // a thread team pays off only for long contexts
 #pragma omp parallel if (n_t >= 64)
@@ -349,7 +349,7 @@ void attention(const float *q, const float *K, const float *V, int n_t, int tcap
                 for (int ch = 0; ch < n_chunks; ++ch) {
                     const int h0 = g * group + 8 * hb, nj = std::min(8, group - 8 * hb);
                     kScores[nj - 1](q + static_cast<size_t>(h0) * hd, K + static_cast<size_t>(g) * hd * tcap, hd,
-                                    tcap, 64 * ch, std::min(n_t, 64 * ch + 64), scale,
+                                    tcap, 32 * ch, std::min(n_t, 32 * ch + 32), scale,
                                     sc + static_cast<size_t>(h0) * tcap);
                 }
 #pragma omp for schedule(static)
