@@ -315,7 +315,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding plan is described in DESIGN.md", file=sys.stderr)
+              "across GPUs the GEMV would shard by output rows (activation broadcast, outputs "
+              "all-gathered), which is not built here", file=sys.stderr)
         return 2
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: run without torch.distributed; one GPU only", file=sys.stderr)
