@@ -13,8 +13,10 @@ Four independent sources:
      K/IQ format's decode against an independent *encoder* written from ggml's
      quantizer packing (the inverse direction), so a wrong shift, index or
      nibble order in the oracle's decoder fails.
-IQ3_XXS / IQ2_S have no reference code, vectors or tests: only the structural
-invariants at the end apply to them (parity unpinned).
+IQ3_XXS / IQ2_S have no reference code, vectors or tests: their layouts are
+pinned by encoders from ggml's quantizer packing and known answers for every
+sign bit, parity bit, scale nibble and scale factor, on synthetic grids (the
+grid contents themselves stay ggml's).
 """
 import hashlib
 import os
@@ -418,7 +420,16 @@ def test_ksigns_table_structure(oracle):
     assert all(bin(int(v)).count("1") % 2 == 0 for v in k)
 
 
-# ---- IQ3_XXS / IQ2_S: parity unpinned; structural invariants only -------------
+# ---- IQ3_XXS / IQ2_S ------------------------------------------------------------
+# The reference reaches these two types only through ggml
+# (src/xdna-gemv-engine.cpp:1395-1396), so their block layouts are pinned here
+# from ggml's published quantizer packing (quantize_row_iq3_xxs_impl,
+# quantize_row_iq2_s_impl of ggml-quants.c, llama.cpp 0ec4027a2): an encoder
+# written in that direction must round-trip through the oracle's decoder, and
+# known answers fix every sign bit, the parity bit, the scale nibbles and the
+# scale factors.  The grid *contents* are ggml's and absent here; these tests
+# use synthetic grids (the library checks the real ones against the host's
+# ggml at run time).
 
 def synthetic_grid(t, seed=0):
     rng = np.random.default_rng(seed)
@@ -459,6 +470,178 @@ def test_iq2_s_probe_reads_back_the_grid(oracle):
         v = oracle.dequant_row(IQ2_S, blk, 256, grid=grid) * 8  # db = 0.125
         want = grid[32 * b:32 * (b + 1)].view(np.uint8).astype(np.float32)
         assert np.array_equal(v, want)
+
+
+def sign8(idx7):
+    """Full 8-bit sign pattern of a 7-bit IQ3_XXS sign index: ggml's
+    quantizer makes the number of negative values in a group of 8 even and
+    stores the low 7 bits, so bit 7 is the parity of the other seven."""
+    return idx7 | ((bin(idx7).count("1") & 1) << 7)
+
+
+def enc_iq3_xxs(d, gidx, signs7, ls):
+    """ggml's IQ3_XXS packing: gidx[8][8] grid indices (q3[8*ib + k]),
+    signs7[8][4] 7-bit sign indices and ls[8] 4-bit scales per 32-value
+    sub-block; scales_and_signs[ib] = s0 | s1 << 7 | s2 << 14 | s3 << 21 |
+    ls << 28 (little-endian u32 after the 64 index bytes)."""
+    blk = np.zeros(98, dtype=np.uint8)
+    blk[0:2] = half(d)
+    for ib in range(8):
+        for k in range(8):
+            blk[2 + 8 * ib + k] = gidx[ib][k]
+        w = 0
+        for l in range(4):
+            w |= int(signs7[ib][l]) << (7 * l)
+        w |= int(ls[ib]) << 28
+        blk[66 + 4 * ib:70 + 4 * ib] = np.array([w], dtype=np.uint32).view(np.uint8)
+    return blk
+
+
+def want_iq3_xxs(d, gidx, signs7, ls, grid):
+    """Values of a block built by enc_iq3_xxs: ggml's dequantize_row_iq3_xxs
+    formula db = d * (0.5 + ls) * 0.5 on magnitude bytes of the grid entry,
+    value 8l + j of sub-block ib negated where bit j of sign8(signs7[ib][l])
+    is set; lookups 2l and 2l + 1 give values 8l..8l+3 and 8l+4..8l+7."""
+    mags = grid.view(np.uint8).reshape(256, 4)
+    out = np.zeros(256, dtype=np.float32)
+    for ib in range(8):
+        db = np.float32(d) * (np.float32(0.5) + np.float32(ls[ib])) * np.float32(0.5)
+        for l in range(4):
+            sg = sign8(int(signs7[ib][l]))
+            for j in range(8):
+                m = np.float32(mags[gidx[ib][2 * l + j // 4]][j % 4])
+                v = db * m
+                out[32 * ib + 8 * l + j] = -v if (sg >> j) & 1 else v
+    return out
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_iq3_xxs_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(100 + seed)
+    grid = synthetic_grid(IQ3_XXS, seed)
+    gidx = rng.integers(0, 256, (8, 8))
+    signs7 = rng.integers(0, 128, (8, 4))
+    ls = rng.integers(0, 16, 8)
+    d = f32(0.0625)
+    got = oracle.dequant_row(IQ3_XXS, enc_iq3_xxs(d, gidx, signs7, ls), 256, grid=grid)
+    assert np.array_equal(bits(got), bits(want_iq3_xxs(d, gidx, signs7, ls, grid)))
+
+
+def test_iq3_xxs_every_sign_index_and_parity_bit(oracle):
+    """All 128 sign indices in every one of the 32 groups of 8: value j of the
+    group is negative exactly where bit j of idx | parity << 7 is set."""
+    grid = np.full(256, 0x01010101, dtype=np.uint32)  # every magnitude 1
+    gidx = np.zeros((8, 8), dtype=np.int64)
+    ls = np.zeros(8, dtype=np.int64)  # db = 0.25 at d = 1
+    for idx in range(128):
+        for l in range(4):
+            signs7 = np.zeros((8, 4), dtype=np.int64)
+            signs7[:, l] = idx
+            v = oracle.dequant_row(IQ3_XXS, enc_iq3_xxs(f32(1.0), gidx, signs7, ls), 256, grid=grid)
+            want = np.full(256, 0.25, dtype=np.float32)
+            for ib in range(8):
+                for j in range(8):
+                    if (sign8(idx) >> j) & 1:
+                        want[32 * ib + 8 * l + j] = -0.25
+            assert np.array_equal(v, want), (idx, l)
+
+
+def test_iq3_xxs_scale_factor_known_answers(oracle):
+    """db = d * (0.5 + s) * 0.5 for s = 0..15 (0.25, 0.75, ..., 7.75 at d = 1
+    and magnitude 1), one scale per 32-value sub-block, from bits 28-31."""
+    grid = np.full(256, 0x01010101, dtype=np.uint32)
+    gidx = np.zeros((8, 8), dtype=np.int64)
+    signs7 = np.zeros((8, 4), dtype=np.int64)
+    for lo in (0, 8):
+        ls = np.arange(lo, lo + 8)
+        v = oracle.dequant_row(IQ3_XXS, enc_iq3_xxs(f32(1.0), gidx, signs7, ls), 256, grid=grid)
+        assert np.array_equal(v, np.repeat(0.25 + 0.5 * ls, 32).astype(np.float32))
+    # d scales everything: d = 2^-3 -> 1/8 of the values above (exact)
+    v = oracle.dequant_row(IQ3_XXS, enc_iq3_xxs(f32(0.125), gidx, signs7, np.full(8, 15)), 256, grid=grid)
+    assert np.array_equal(v, np.full(256, 7.75 / 8, dtype=np.float32))
+
+
+def enc_iq2_s(d, gidx, signs, l1, l2):
+    """ggml's IQ2_S packing: per group of 8 values i8 = 0..31, qs[i8] = grid
+    index & 255, qh[i8 / 4] |= (index >> 8) << 2 * (i8 % 4), signs at
+    qs[32 + i8] (8 free bits); scales[ib] = l1 | l2 << 4 (l1 for the first 16
+    values of 32-value sub-block ib, l2 for the next 16)."""
+    blk = np.zeros(82, dtype=np.uint8)
+    blk[0:2] = half(d)
+    for i8 in range(32):
+        g = int(gidx[i8])
+        blk[2 + i8] = g & 0xFF
+        blk[66 + i8 // 4] |= (g >> 8) << (2 * (i8 % 4))
+        blk[34 + i8] = signs[i8]
+    for ib in range(8):
+        blk[74 + ib] = int(l1[ib]) | (int(l2[ib]) << 4)
+    return blk
+
+
+def want_iq2_s(d, gidx, signs, l1, l2, grid):
+    mags = grid.view(np.uint8).reshape(1024, 8)
+    out = np.zeros(256, dtype=np.float32)
+    for i8 in range(32):
+        ib, half16 = i8 // 4, (i8 % 4) // 2
+        s = (l1 if half16 == 0 else l2)[ib]
+        db = np.float32(d) * (np.float32(0.5) + np.float32(s)) * np.float32(0.25)
+        for j in range(8):
+            v = db * np.float32(mags[gidx[i8]][j])
+            out[8 * i8 + j] = -v if (int(signs[i8]) >> j) & 1 else v
+    return out
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_iq2_s_decode_inverts_ggml_packing(oracle, seed):
+    rng = np.random.default_rng(200 + seed)
+    grid = synthetic_grid(IQ2_S, seed)
+    gidx = rng.integers(0, 1024, 32)
+    signs = rng.integers(0, 256, 32)
+    l1, l2 = rng.integers(0, 16, 8), rng.integers(0, 16, 8)
+    d = f32(0.5)
+    got = oracle.dequant_row(IQ2_S, enc_iq2_s(d, gidx, signs, l1, l2), 256, grid=grid)
+    assert np.array_equal(bits(got), bits(want_iq2_s(d, gidx, signs, l1, l2, grid)))
+
+
+def test_iq2_s_every_sign_bit(oracle):
+    grid = np.full(1024, 0x0101010101010101, dtype=np.uint64)
+    z = np.zeros(32, dtype=np.int64)
+    zs = np.zeros(8, dtype=np.int64)
+    for i8 in range(32):
+        for j in range(8):
+            signs = np.zeros(32, dtype=np.int64)
+            signs[i8] = 1 << j
+            v = oracle.dequant_row(IQ2_S, enc_iq2_s(f32(1.0), z, signs, zs, zs), 256, grid=grid)
+            want = np.full(256, 0.125, dtype=np.float32)
+            want[8 * i8 + j] = -0.125
+            assert np.array_equal(v, want), (i8, j)
+
+
+def test_iq2_s_scale_nibbles_known_answers(oracle):
+    """db = d * (0.5 + s) * 0.25: the low nibble of scales[ib] scales values
+    32ib..32ib+15, the high nibble 32ib+16..32ib+31, for s = 0..15 each."""
+    grid = np.full(1024, 0x0101010101010101, dtype=np.uint64)
+    z = np.zeros(32, dtype=np.int64)
+    for rot in range(16):
+        l1 = (np.arange(8) + rot) % 16
+        l2 = (np.arange(8) * 3 + rot + 5) % 16
+        v = oracle.dequant_row(IQ2_S, enc_iq2_s(f32(1.0), z, z, l1, l2), 256, grid=grid)
+        want = np.concatenate([np.concatenate([np.full(16, 0.125 + 0.25 * a), np.full(16, 0.125 + 0.25 * b)])
+                               for a, b in zip(l1, l2)]).astype(np.float32)
+        assert np.array_equal(v, want), rot
+
+
+def test_iq2_s_index_high_bits(oracle):
+    """The two high index bits of lookup i8 sit at bits 2 * (i8 % 4) of
+    qh[i8 / 4]: indices 256 apart read different grid entries."""
+    grid = np.zeros(1024, dtype=np.uint64)
+    for q in range(4):  # entry 256 q + 7 has every magnitude q + 1
+        grid[256 * q + 7] = np.uint64(0x0101010101010101 * (q + 1))
+    zs = np.zeros(8, dtype=np.int64)
+    rng = np.random.default_rng(9)
+    hi = rng.integers(0, 4, 32)
+    v = oracle.dequant_row(IQ2_S, enc_iq2_s(f32(1.0), 256 * hi + 7, np.zeros(32, np.int64), zs, zs), 256, grid=grid)
+    assert np.array_equal(v, np.repeat(0.125 * (hi + 1), 8).astype(np.float32))
 
 
 # ---- the Q4_0 quantizer used to build the BASELINE configs ------------------
