@@ -222,13 +222,17 @@ MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int
  * takes commands through pinned host memory: mi355x_server_gemv copies x,
  * publishes the jobs and returns once every output is written.  Jobs share x
  * and K; outputs are device-visible pointers (device memory, or pinned host
- * memory through hipHostGetDevicePointer).  Arithmetic per row is the digit
- * kernel's row form (bit-identical to MI355X_FORM_ROWS).  K: a multiple of
+ * memory through hipHostGetDevicePointer).  The variant of the server's
+ * context at the call picks the arithmetic per row: AUTO and DIGITS the digit
+ * kernel's row form (bit-identical to MI355X_FORM_ROWS), GGML_Q8 ggml-cpu's
+ * Q8_0 numerics (bit-identical to mi355x_gemv in that variant); EXACT_F32 is
+ * MI355X_EUNSUPPORTED.  K: a multiple of
  * 256 up to max_k (<= 16384); weights 16-byte aligned.  The resident kernel
  * leaves by itself after 1 s without a command (the next call relaunches it),
- * on mi355x_server_stop / _destroy, and before mi355x_free or
- * mi355x_ctx_destroy on its context (a hipFree would wait for it).  One host
- * thread per server; destroy servers before their context. */
+ * on mi355x_server_stop / _destroy, and before any mi355x_free or
+ * mi355x_ctx_destroy on its device, from any context or thread (a hipFree
+ * would wait for it; such a stop waits for the command in flight).  Calls on
+ * one server serialise on its lock; destroy servers before their context. */
 typedef struct mi355x_server mi355x_server;
 typedef struct mi355x_server_job {
     const void *W; /* resident Q4_0 tensor of N rows */
@@ -239,6 +243,9 @@ MI355X_API int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_serve
 MI355X_API int mi355x_server_gemv(mi355x_server *s, const float *x, int64_t K, int njobs,
                                   const mi355x_server_job *jobs);
 MI355X_API int mi355x_server_stop(mi355x_server *s);
+/* 1 while the server's resident kernel is running, 0 once it has left (after
+ * its idle time, a stop, or before the first command); < 0 on error. */
+MI355X_API int mi355x_server_running(mi355x_server *s);
 MI355X_API void mi355x_server_destroy(mi355x_server *s);
 
 /* ---- measurement -----------------------------------------------------------

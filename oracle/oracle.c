@@ -483,19 +483,28 @@ int orc_gemv_f32(int type, const uint8_t *W, int64_t N, int64_t K,
     if ((type == ORC_IQ3_XXS || type == ORC_IQ2_S) && !grid) return ORC_ENOGRID;
     if (N == 0) return ORC_OK;
     if (!W || !y || (K > 0 && !x)) return ORC_EINVAL;
-    float *w = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
-    if (!w) return ORC_EINVAL;
-    for (int64_t r = 0; r < N; ++r) {
-        orc_dequant_row(type, W + r * rb, K, w, grid);
-        float s = 0.0f;
-        for (int64_t c = 0; c < K; ++c) {
-            float p = w[c] * x[c];
-            s = s + p;
+    int failed = 0;
+    /* rows are independent: threads split them, each row's sum stays sequential */
+#pragma omp parallel reduction(| : failed)
+    {
+        float *w = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+        if (!w) {
+            failed = 1;
+        } else {
+#pragma omp for schedule(static)
+            for (int64_t r = 0; r < N; ++r) {
+                orc_dequant_row(type, W + r * rb, K, w, grid);
+                float s = 0.0f;
+                for (int64_t c = 0; c < K; ++c) {
+                    float p = w[c] * x[c];
+                    s = s + p;
+                }
+                y[r] = s;
+            }
+            free(w);
         }
-        y[r] = s;
     }
-    free(w);
-    return ORC_OK;
+    return failed ? ORC_EINVAL : ORC_OK;
 }
 
 int orc_gemv_bf16(int type, const uint8_t *W, int64_t N, int64_t K,

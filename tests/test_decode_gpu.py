@@ -118,8 +118,14 @@ def test_ggml_numerics_decode_token_identical_to_cpu(cfg):
         m.set_variant(mi355x.VARIANT_GGML_Q8)
         gpu_toks, _ = m.generate(p, 8)
         gpu_logits = m.last_logits()
-        assert m.last_wait() == m.WAIT_FENCE  # the server does not take this variant
+        assert m.last_wait() == m.WAIT_SERVER  # the server's Q8_0 job form
+        m.set_wait(m.WAIT_FENCE)
+        launch_toks, _ = m.generate(p, 8)
+        launch_logits = m.last_logits()
+        assert m.last_wait() == m.WAIT_FENCE
+        m.set_wait(m.WAIT_SERVER)
         m.set_variant(mi355x.VARIANT_AUTO)
+    assert np.array_equal(launch_toks, cpu_toks) and np.array_equal(launch_logits, cpu_logits)
     # every GEMV is bit-identical to the restatement and the host ops are the
     # same code, so the whole decode is: tokens and logits alike.  (Q8_0
     # codes are discrete -- any upstream rounding difference could move an
@@ -151,3 +157,41 @@ def test_server_decode_token_identical(cfg, n_prompt, n_gen):
     check(cpu_toks, cpu_logits, srv_toks, srv_logits)
     assert np.array_equal(srv_toks, launch_toks) and np.array_equal(again, srv_toks)
     assert t["gen_passes"] == n_gen - 1
+
+
+@pytest.mark.timeout(900)
+def test_config5_full_decode_token_identical():
+    """BASELINE config 5 at full size: the Qwen2.5-3B shape (36 layers), a
+    512-token uniform-random prompt, then 128 greedy tokens.
+      * default GPU decode (digit-plane GEMVs, persistent server) against the
+        same decoder with every GEMV on the reference's own CPU engine
+        (oracle/_ref, else the C oracle): the same 128 tokens;
+      * GGML_Q8 GPU decode (server Q8_0 job form) against the CPU decode with
+        the oracle's restatement of ggml-cpu's Q4_0 x Q8_0 arithmetic: the
+        same 128 tokens and bit-identical last logits."""
+    import mi355x
+    cfg = decode.QWEN25_3B
+    p = decode.prompt_tokens(512, cfg["vocab"], 1)
+    with decode.Model(threads=16, **cfg) as m:
+        kind = "reference" if orc.RefLib.available() else "oracle"
+        f, _ = orc.decode_gemv(kind)
+        cpu_toks, _ = m.generate(p, 128, f)
+        cpu_logits = m.last_logits()
+        fq, _ = orc.decode_gemv("ggml_q8")
+        q8_toks, _ = m.generate(p, 128, fq)
+        q8_logits = m.last_logits()
+        m.attach_gpu(0)
+        gpu_toks, t = m.generate(p, 128)
+        gpu_logits = m.last_logits()
+        assert m.last_wait() == m.WAIT_SERVER
+        m.set_variant(mi355x.VARIANT_GGML_Q8)
+        gq_toks, tq = m.generate(p, 128)
+        gq_logits = m.last_logits()
+        assert m.last_wait() == m.WAIT_SERVER
+        m.set_variant(mi355x.VARIANT_AUTO)
+    print(f"config 5: default {127 / t['gen_s']:.1f} tok/s, GGML_Q8 {127 / tq['gen_s']:.1f} tok/s "
+          f"(CPU GEMVs: {kind})", flush=True)
+    check(cpu_toks, cpu_logits, gpu_toks, gpu_logits)
+    assert np.array_equal(gq_toks, q8_toks), (gq_toks, q8_toks)
+    assert np.array_equal(gq_logits, q8_logits)
+    assert t["gen_passes"] == 127 and tq["gen_passes"] == 127

@@ -1,9 +1,13 @@
 """Persistent Q4_0 GEMV server (mi355x_server_*): a resident kernel that takes
 GEMV commands through pinned host memory, for decode loops.  Every output is
-bit-identical to the row form (MI355X_FORM_ROWS) on the same inputs and within
-the GEMV tolerance of the oracle; commands run back to back, with several
-jobs per command, outputs in device or pinned host memory, across stops,
-idle relaunches and rejected arguments."""
+bit-identical to the launch path's arithmetic of the context's variant (the
+row form MI355X_FORM_ROWS for the digit planes, mi355x_gemv for GGML_Q8) and
+within the GEMV tolerance of the oracle.
+
+Any free on the device stops the resident kernel (a hipFree waits for it), so
+the tests that run several commands on one launch make their references and
+buffers first and free nothing until the end; mi355x_server_running tells
+whether the resident kernel is still there."""
 import ctypes
 import time
 
@@ -32,6 +36,25 @@ def rows_form(ctx, w, x):
         return ctx.gemv(w, x)
     finally:
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+
+
+def ggml_q8(ctx, w, x):
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_GGML_Q8)
+    try:
+        return ctx.gemv(w, x)
+    finally:
+        ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+
+
+class variant:
+    def __init__(self, ctx, v):
+        self.ctx, self.v = ctx, v
+
+    def __enter__(self):
+        self.ctx.set_option(mi355x.OPT_VARIANT, self.v)
+
+    def __exit__(self, *exc):
+        self.ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
 
 
 def run_server(ctx, server, ws, x):
@@ -66,22 +89,52 @@ def test_server_matches_row_form_and_oracle(ctx, server, oracle, N, K):
         check_gemv(y, oracle.gemv(Q4_0, raw, N, K, x), oracle.row_norms(Q4_0, raw, N, K), x, f"server {N}x{K}")
 
 
-def test_server_several_jobs_and_back_to_back_commands(ctx, server):
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_server_ggml_q8_bit_identical(ctx, server, oracle, N, K):
+    """The Q8_0 job form (context variant GGML_Q8): bit-identical to
+    mi355x_gemv in that variant and to the oracle's restatement of ggml-cpu's
+    Q4_0 x Q8_0 arithmetic (blocks summed in order per row)."""
+    raw = synth.random_q4_0(N, K, seed=N ^ K ^ 5)
+    x = synth.activations(K, seed=K + 2)
+    w = ctx.resident(Q4_0, raw, N, K)
+    try:
+        with variant(ctx, mi355x.VARIANT_GGML_Q8):
+            (y,) = run_server(ctx, server, [w], x)
+        ref = ggml_q8(ctx, w, x)
+    finally:
+        w.free()
+    assert np.array_equal(y, ref), (N, K, np.abs(y - ref).max())
+    if N * K <= 50_000_000:
+        assert np.array_equal(y, oracle.gemv_q4_0_q8_0(raw, N, K, x)), (N, K)
+
+
+def test_server_many_commands_per_launch(ctx, server):
+    """24 commands on one resident kernel, 1-4 jobs each, alternating the
+    digit and Q8_0 job forms: every output equals its launch-path reference
+    and the kernel stays resident throughout."""
     K = 2048
     shapes = [700, 64, 3000, 129]
     raws = [synth.random_q4_0(N, K, seed=10 + i) for i, N in enumerate(shapes)]
     ws = [ctx.resident(Q4_0, r, N, K) for r, N in zip(raws, shapes)]
+    xs = [synth.activations(K, seed=500 + it) for it in range(24)]
+    modes = [mi355x.VARIANT_AUTO if it % 3 else mi355x.VARIANT_GGML_Q8 for it in range(24)]
+    refs = [[(rows_form if m == mi355x.VARIANT_AUTO else ggml_q8)(ctx, w, x) for w in ws]
+            for x, m in zip(xs, modes)]
+    ys = [ctx.alloc(4 * w.N) for w in ws]
     try:
-        for it in range(60):
-            x = synth.activations(K, seed=500 + it)
-            sel = ws[it % 4:] + ws[:it % 4]
-            sel = sel[:1 + it % 4]
-            ys = run_server(ctx, server, sel, x)
-            for w, y in zip(sel, ys):
-                assert np.array_equal(y, rows_form(ctx, w, x)), (it, w.N)
+        server.stop()
+        assert not server.running()
+        for it, (x, m) in enumerate(zip(xs, modes)):
+            sel = [(it + j) % 4 for j in range(1 + it % 4)]
+            with variant(ctx, m):
+                server.gemv(x, [(ws[i].ptr, ws[i].N, ys[i].ptr) for i in sel])
+            assert server.running(), it
+            for i in sel:
+                assert np.array_equal(ys[i].download(np.float32, ws[i].N), refs[it][i]), (it, i)
     finally:
-        for w in ws:
-            w.free()
+        for b in ys + ws:
+            b.free()
+    assert not server.running()  # the frees stopped it
 
 
 def test_server_pinned_outputs(ctx, server):
@@ -89,39 +142,77 @@ def test_server_pinned_outputs(ctx, server):
     N, K = 4096, 2048
     raw = synth.random_q4_0(N, K, seed=77)
     w = ctx.resident(Q4_0, raw, N, K)
+    xs = [synth.activations(K, seed=900 + it) for it in range(30)]
+    refs = [rows_form(ctx, w, x) for x in xs]
     hptr = ctypes.c_void_p()
     mi355x.check(ctx.lib.mi355x_host_malloc(4 * N, ctypes.byref(hptr)))
     dptr = ctypes.c_void_p()
     try:
         assert hip.hipHostGetDevicePointer(ctypes.byref(dptr), hptr, 0) == 0
         host_y = np.ctypeslib.as_array(ctypes.cast(hptr, ctypes.POINTER(ctypes.c_float)), shape=(N,))
-        for it in range(30):
-            x = synth.activations(K, seed=900 + it)
+        for it, x in enumerate(xs):
             host_y[:] = np.nan
             server.gemv(x, [(w.ptr, N, dptr.value)])
-            assert np.array_equal(host_y, rows_form(ctx, w, x)), it
+            assert np.array_equal(host_y, refs[it]), it
     finally:
         mi355x.check(ctx.lib.mi355x_host_free(hptr))
         w.free()
 
 
 def test_server_stop_and_idle_relaunch(ctx, server):
+    """The host's relaunch after 0.5 s idle (inside the next call) and the
+    kernel's own exit after 1 s without a command."""
     N, K = 1000, 4096
     raw = synth.random_q4_0(N, K, seed=3)
     w = ctx.resident(Q4_0, raw, N, K)
+    x = synth.activations(K, seed=4)
+    ref = rows_form(ctx, w, x)
+    y = ctx.alloc(4 * N)
+    out = []
     try:
-        x = synth.activations(K, seed=4)
-        ref = rows_form(ctx, w, x)
-        (a,) = run_server(ctx, server, [w], x)
+        job = [(w.ptr, N, y.ptr)]
+        server.gemv(x, job)
+        out.append(y.download(np.float32, N))
+        assert server.running()
         server.stop()
-        (b,) = run_server(ctx, server, [w], x)  # relaunch after a stop
-        time.sleep(0.7)  # past the host's idle limit: stop and relaunch inside the call
-        (c,) = run_server(ctx, server, [w], x)
+        assert not server.running()
+        server.gemv(x, job)  # relaunch after a stop
+        out.append(y.download(np.float32, N))
+        assert server.running()
+        time.sleep(0.7)  # past the host's idle limit, before the kernel's
+        assert server.running()
+        server.gemv(x, job)  # the call stops and relaunches the kernel
+        out.append(y.download(np.float32, N))
+        assert server.running()
         time.sleep(2.5)  # past the kernel's own idle exit
-        (d,) = run_server(ctx, server, [w], x)
-        for y in (a, b, c, d):
-            assert np.array_equal(y, ref)
+        assert not server.running()
+        server.gemv(x, job)  # relaunch after the kernel left by itself
+        out.append(y.download(np.float32, N))
     finally:
+        y.free()
+        w.free()
+    for i, o in enumerate(out):
+        assert np.array_equal(o, ref), i
+
+
+def test_free_on_another_context_stops_the_server(ctx, server):
+    """A free through a second context on the same device stops this
+    server's resident kernel first (hipFree would otherwise wait for it)."""
+    N, K = 512, 2048
+    w = ctx.resident(Q4_0, synth.random_q4_0(N, K, seed=21), N, K)
+    y = ctx.alloc(4 * N)
+    try:
+        x = synth.activations(K, seed=22)
+        server.gemv(x, [(w.ptr, N, y.ptr)])
+        assert server.running()
+        with mi355x.Context(0) as other:
+            b = other.alloc(1 << 20)
+            t0 = time.perf_counter()
+            b.free()
+            assert time.perf_counter() - t0 < 0.5  # no wait for the idle exit
+        assert not server.running()
+    finally:
+        y.free()
         w.free()
 
 
@@ -137,6 +228,8 @@ def test_server_rejects_bad_arguments(ctx, server):
         assert server.gemv_ptr(x, [(w.ptr, N, y.ptr)] * 5) == mi355x.EINVAL
         assert server.gemv_ptr(x, [(w.ptr + 2, N, y.ptr)]) == mi355x.EINVAL  # alignment
         assert server.gemv_ptr(x, [(w.ptr, 0, y.ptr)]) == mi355x.EINVAL
+        with variant(ctx, mi355x.VARIANT_EXACT_F32):
+            assert server.gemv_ptr(x, [(w.ptr, N, y.ptr)]) == mi355x.EUNSUPPORTED
         server.gemv(x, [(w.ptr, N, y.ptr)])  # still serves
     finally:
         y.free()

@@ -153,3 +153,18 @@ def test_struct_layouts():
     assert gh.Tensor.data.offset == 248 and gh.Tensor.op.offset == 80
     assert C.sizeof(gh.CompatTensor) == 304
     assert gh.CompatTensor.data.offset == 224
+
+
+def test_compat_batch_broadcast_rule(plib):
+    # weight batches must divide the activation batches (ggml's broadcast);
+    # otherwise the weight index would run past the tensor
+    o, w, x = compat_op(Q["Q4_0"], 2048, 256)
+    for w2, x2, claimed in [(1, 1, True), (1, 4, True), (2, 4, True), (4, 4, True), (2, 3, False),
+                            (3, 1, False), (4, 2, False)]:
+        w.ne[2], x.ne[2], o.ne[2] = w2, x2, x2
+        assert claims(plib, o) == claimed, (w2, x2)
+    w.ne[2], x.ne[2], o.ne[2] = 1, 1, 1
+    w.ne[3], x.ne[3], o.ne[3] = 2, 3, 3
+    assert not claims(plib, o)
+    w.ne[3], x.ne[3], o.ne[3] = 1, 2, 1  # output batches must be the activation batches
+    assert not claims(plib, o)

@@ -1261,8 +1261,8 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         lk.lock();
         const size_t need = static_cast<size_t>(a.K) * sizeof(float);
         if (ctx->xconv_bytes < need) {
-            MI355X_HIP(hipStreamSynchronize(ctx->stream));
-            if (ctx->xconv) MI355X_HIP(hipFree(ctx->xconv));
+            const int rc = free_device(ctx, ctx->xconv);
+            if (rc) return rc;
             ctx->xconv = nullptr;
             ctx->xconv_bytes = 0;
             MI355X_HIP(hipMalloc(&ctx->xconv, need));

@@ -580,6 +580,94 @@ __global__ __launch_bounds__(64 * 8) void gemv_q4_0_mb_kernel(const uint8_t *__r
     }
 }
 
+// ---- ggml-cpu numerics ------------------------------------------------------
+// ggml's CPU backend does not multiply Q4_0 weights by f32 activations: it
+// quantizes the activation row to Q8_0 and takes integer block dot
+// products (quantize_row_q8_0 and ggml_vec_dot_q4_0_q8_0 of ggml, llama.cpp
+// 0ec4027a2; ggml is not part of the reference).  gemv_q4_0_q8_kernel and
+// the server's Q8_0 job form reproduce that arithmetic so that decode can
+// pick ggml-cpu's tokens:
+//   staging, per 32-value block (a DPP quad of 4 threads, as the digit
+//   staging): amax = max|x_j|, d = amax / 127, id = d ? 1/d : 0,
+//   q_j = roundf(x_j * id), d_x = f32(fp16(d)) (round to even), S = sum q_j;
+//   LDS holds the codes as two planes Q[h][b] (uint4; byte e of dword k is
+//   value 16h + 4k + e, the nibble order of the Q4_0 code dwords), d_x and S;
+//   per block: sumi = sum_j (q4_j - 8) q8_j  (exact: v_dot4_i32_i8 on the
+//   unsigned nibbles, minus 8 S), contribution (float(sumi) * d_w) * d_x,
+//   ggml's expression order.  Blocks are summed per lane, then across the
+//   wavefront: the same products as ggml's generic path, re-associated.
+template <int XI>
+__device__ __forceinline__ void q8_stage(const XTile<XI> &xt, int B, uint32_t *Q, float *dx, int *sx) {
+#pragma unroll
+    for (int it = 0; it < XI; ++it) {
+        const int i = threadIdx.x + it * blockDim.x;
+        const int ic = min(i, 4 * B - 1);
+        const int b = ic >> 2, k = ic & 3;
+        // XTile order: v[2e] = value 4k+e, v[2e+1] = value 16+4k+e
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xt.v[it][e]));
+        amax = fmaxf(amax, dpp_mov<0xB1>(amax));
+        amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+        // correctly rounded division, reciprocal and products, as ggml's C
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        uint32_t lo = 0, hi = 0;
+        int sum = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int ql = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e], id)));
+            const int qh = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e + 1], id)));
+            lo |= (static_cast<uint32_t>(ql) & 0xFFu) << (8 * e);
+            hi |= (static_cast<uint32_t>(qh) & 0xFFu) << (8 * e);
+            sum += ql + qh;
+        }
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, false);
+        if (i < 4 * B) {
+            Q[b * 4 + k] = lo;
+            Q[(B + b) * 4 + k] = hi;
+            if (k == 0) {
+                dx[b] = static_cast<float>(static_cast<_Float16>(d));
+                sx[b] = sum;
+            }
+        }
+    }
+}
+
+// Block contributions (float(sumi) * d_w) * d_x of R rows into
+// cs[r * cs_stride + b] (blocks past the row end are not written).
+template <int NBL, int R, bool A16, bool TAIL>
+__device__ __forceinline__ void q8_blocks(const RowGroup<NBL, R, A16, TAIL> &g, float *cs, int cs_stride,
+                                          const uint4 *Q, const float *dx, const int *sx, int B, int lane,
+                                          const int bc[NBL], uint32_t tail_mask) {
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) {
+        if (j > 0) __builtin_amdgcn_sched_barrier(0);
+        const uint4 q0 = Q[bc[j]], q1 = Q[B + bc[j]];
+        const float d_x = dx[bc[j]];
+        const int s8 = sx[bc[j]];
+        const uint32_t a[4] = {q0.x, q0.y, q0.z, q0.w};
+        const uint32_t c[4] = {q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int dot = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // resident code bytes hold q - 8 per nibble; XOR 8 gives q
+                const uint32_t u = g.q[r][j][k] ^ 0x88888888u;
+                dot = __builtin_amdgcn_sdot4(static_cast<int>(u & 0x0F0F0F0Fu), static_cast<int>(a[k]), dot, false);
+                dot = __builtin_amdgcn_sdot4(static_cast<int>((u >> 4) & 0x0F0F0F0Fu), static_cast<int>(c[k]), dot,
+                                             false);
+            }
+            const int sumi = dot - 8 * s8;
+            const float dw = half_bits_to_float(static_cast<uint16_t>(g.d_bits(r, j, tail_mask)));
+            if (lane + 64 * j < B)
+                cs[r * cs_stride + lane + 64 * j] = __fmul_rn(__fmul_rn(static_cast<float>(sumi), dw), d_x);
+        }
+    }
+}
+
 // ---- persistent server form (decode loops) ------------------------------------
 // A decode loop issues one GEMV group at a time and waits for it; launch and
 // completion then cost more than the kernel.  The server form keeps one
@@ -617,9 +705,12 @@ struct SrvCmd {
     uint32_t exit;
     int32_t K;
     int32_t njobs;
-    int32_t pad;
+    int32_t mode;  // kSrvDigits or kSrvGgmlQ8
     SrvJob jobs[kSrvMaxJobs];
 };
+// job arithmetic: the row form's digit planes, or ggml-cpu's Q8_0 numerics
+constexpr int32_t kSrvDigits = 0;
+constexpr int32_t kSrvGgmlQ8 = 1;
 
 // device-memory state, one 128-byte line per word that is polled or counted
 struct SrvDev {
@@ -721,6 +812,85 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
     }
 }
 
+// ggml-cpu numerics job form (MI355X_VARIANT_GGML_Q8): the arithmetic of
+// gemv_q4_0_q8_kernel, bit for bit.  The activation row is staged as Q8_0
+// codes; a workgroup takes its rows of a job in chunks whose block
+// contributions fit kSrvCsFloats of LDS; within a chunk wavefront v computes
+// rows v, v+8, ... one at a time (lane = block, the next row's loads in
+// flight) and stores (float(sumi) * d_w) * d_x per block; then one thread per
+// row adds its row's contributions in block order (ggml's sequential sum).
+// Rows of a chunk sit B + 1 floats apart, so those threads read distinct
+// banks.
+constexpr int kSrvCsFloats = 8192;
+
+template <int NBL, bool TAIL>
+__device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                            float *out, float *csb) {
+    constexpr int XI = (4 * NBL + kSrvWaves - 1) / kSrvWaves;
+    uint4 *Q = lds;
+    float *dxs = reinterpret_cast<float *>(lds + 2 * B);
+    int *sxs = reinterpret_cast<int *>(dxs + B);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t row_bytes = 18 * static_cast<int64_t>(B);
+    const int stride = B + 1;
+    // rows per chunk: a multiple of the wavefront count, so a wavefront's
+    // rows continue v, v+8, ... from one chunk into the next (>= 8: B <= 512)
+    // and at most one per thread
+    const int chunk = min((kSrvCsFloats / stride) & ~(kSrvWaves - 1), 64 * kSrvWaves);
+    int bc[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
+    const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
+    const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
+
+    const int lo0 = static_cast<int>(c.jobs[0].N * g / G), hi0 = static_cast<int>(c.jobs[0].N * (g + 1) / G);
+    XTile<XI> xt;
+    srv_load_x(xt, x, B);
+    __builtin_amdgcn_sched_barrier(0);
+    using Grp = RowGroup<NBL, 1, true, TAIL>;
+    Grp grp;
+    grp.load(c.jobs[0].W, lo0 + wave, hi0, B, row_bytes, lane);
+    q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dxs, sxs);
+    __syncthreads();
+
+    for (int j = 0; j < c.njobs; ++j) {
+        const SrvJob &job = c.jobs[j];
+        const int lo = static_cast<int>(job.N * g / G), hi = static_cast<int>(job.N * (g + 1) / G);
+        if (j > 0) grp.load(job.W, lo + wave, hi, B, row_bytes, lane);
+        for (int c0 = lo; c0 < hi; c0 += chunk) {
+            const int c1 = min(hi, c0 + chunk);
+            for (int row = c0 + wave; row < c1; row += kSrvWaves) {
+                Grp nxt;
+                nxt.load(job.W, row + kSrvWaves, hi, B, row_bytes, lane);  // empty range past hi
+                q8_blocks<NBL, 1, true, TAIL>(grp, csb + (row - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
+                                              tail_mask);
+                grp = nxt;
+            }
+            __syncthreads();
+            const int t = static_cast<int>(threadIdx.x);
+            if (t < c1 - c0) {
+                const float *cr = csb + t * stride;
+                float sumf = 0.0f;
+#pragma unroll 8
+                for (int b = 0; b < B; ++b) sumf = __fadd_rn(sumf, cr[b]);
+                out[c0 - lo + t] = sumf;
+            }
+            __syncthreads();  // csb is rewritten by the next chunk
+        }
+        for (int i = threadIdx.x; i < hi - lo; i += blockDim.x)
+            __hip_atomic_store(&job.y[lo + i], out[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __syncthreads();  // `out` is reused by the next job
+    }
+}
+
+template <int NBL, bool TAIL>
+__device__ __forceinline__ void srv_job(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                        float *out, float *csb) {
+    if (c.mode == kSrvGgmlQ8) srv_rows_q8<NBL, TAIL>(c, B, lds, x, out, csb);
+    else srv_rows<NBL, TAIL>(c, B, lds, x, out);
+}
+
 // Command-record fields as 32-bit words (the record is copied word by word).
 constexpr int kSrvCmdWords = static_cast<int>(sizeof(SrvCmd) / 4);
 static_assert(sizeof(SrvCmd) % 4 == 0, "command record in words");
@@ -734,6 +904,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
     __shared__ int32_t shk;       // K of this command (workgroup 0)
     __shared__ SrvCmd cs;         // this command
     __shared__ float outb[kSrvOutMax];
+    __shared__ float csb[kSrvCsFloats];  // block contributions (Q8_0 jobs)
     const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
     uint32_t *csw = reinterpret_cast<uint32_t *>(&cs);
     for (uint32_t expect = first;; ++expect) {
@@ -819,21 +990,21 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
         const SrvCmd &c = cs;
         const int B = c.K / 32;
         switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
-        case 2: srv_rows<1, false>(c, B, lds_dp, dx, outb); break;
-        case 3: srv_rows<1, true>(c, B, lds_dp, dx, outb); break;
-        case 4: srv_rows<2, false>(c, B, lds_dp, dx, outb); break;
-        case 5: srv_rows<2, true>(c, B, lds_dp, dx, outb); break;
-        case 6: srv_rows<3, false>(c, B, lds_dp, dx, outb); break;
-        case 7: srv_rows<3, true>(c, B, lds_dp, dx, outb); break;
-        case 8: srv_rows<4, false>(c, B, lds_dp, dx, outb); break;
-        case 9: srv_rows<4, true>(c, B, lds_dp, dx, outb); break;
-        case 10: srv_rows<5, false>(c, B, lds_dp, dx, outb); break;
-        case 11: srv_rows<5, true>(c, B, lds_dp, dx, outb); break;
-        case 12: srv_rows<6, false>(c, B, lds_dp, dx, outb); break;
-        case 13: srv_rows<6, true>(c, B, lds_dp, dx, outb); break;
-        case 14: srv_rows<7, false>(c, B, lds_dp, dx, outb); break;
-        case 15: srv_rows<7, true>(c, B, lds_dp, dx, outb); break;
-        default: srv_rows<8, false>(c, B, lds_dp, dx, outb); break;  // B = 512 (the host checks K)
+        case 2: srv_job<1, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 3: srv_job<1, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 4: srv_job<2, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 5: srv_job<2, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 6: srv_job<3, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 7: srv_job<3, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 8: srv_job<4, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 9: srv_job<4, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 10: srv_job<5, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 11: srv_job<5, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 12: srv_job<6, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 13: srv_job<6, true>(c, B, lds_dp, dx, outb, csb); break;
+        case 14: srv_job<7, false>(c, B, lds_dp, dx, outb, csb); break;
+        case 15: srv_job<7, true>(c, B, lds_dp, dx, outb, csb); break;
+        default: srv_job<8, false>(c, B, lds_dp, dx, outb, csb); break;  // B = 512 (the host checks K)
         }
         // every wave's output stores have completed (they write through) before
         // the barrier, and so before thread 0 counts the arrival; no fence:
@@ -1161,92 +1332,6 @@ dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail, bool pf) {
     }
 }
 
-// ---- ggml-cpu numerics ------------------------------------------------------
-// ggml's CPU backend does not multiply Q4_0 weights by f32 activations: it
-// quantizes the activation row to Q8_0 and takes integer block dot
-// products (quantize_row_q8_0 and ggml_vec_dot_q4_0_q8_0 of ggml, llama.cpp
-// 0ec4027a2; ggml is not part of the reference).  This kernel reproduces
-// that arithmetic so that decode can pick ggml-cpu's tokens:
-//   staging, per 32-value block (a DPP quad of 4 threads, as the digit
-//   staging): amax = max|x_j|, d = amax / 127, id = d ? 1/d : 0,
-//   q_j = roundf(x_j * id), d_x = f32(fp16(d)) (round to even), S = sum q_j;
-//   LDS holds the codes as two planes Q[h][b] (uint4; byte e of dword k is
-//   value 16h + 4k + e, the nibble order of the Q4_0 code dwords), d_x and S;
-//   per block: sumi = sum_j (q4_j - 8) q8_j  (exact: v_dot4_i32_i8 on the
-//   unsigned nibbles, minus 8 S), contribution (float(sumi) * d_w) * d_x,
-//   ggml's expression order.  Blocks are summed per lane, then across the
-//   wavefront: the same products as ggml's generic path, re-associated.
-template <int XI>
-__device__ __forceinline__ void q8_stage(const XTile<XI> &xt, int B, uint32_t *Q, float *dx, int *sx) {
-#pragma unroll
-    for (int it = 0; it < XI; ++it) {
-        const int i = threadIdx.x + it * blockDim.x;
-        const int ic = min(i, 4 * B - 1);
-        const int b = ic >> 2, k = ic & 3;
-        // XTile order: v[2e] = value 4k+e, v[2e+1] = value 16+4k+e
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xt.v[it][e]));
-        amax = fmaxf(amax, dpp_mov<0xB1>(amax));
-        amax = fmaxf(amax, dpp_mov<0x4E>(amax));
-        // correctly rounded division, reciprocal and products, as ggml's C
-        const float d = __fdiv_rn(amax, 127.0f);
-        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-        uint32_t lo = 0, hi = 0;
-        int sum = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int ql = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e], id)));
-            const int qh = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e + 1], id)));
-            lo |= (static_cast<uint32_t>(ql) & 0xFFu) << (8 * e);
-            hi |= (static_cast<uint32_t>(qh) & 0xFFu) << (8 * e);
-            sum += ql + qh;
-        }
-        sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
-        sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, false);
-        if (i < 4 * B) {
-            Q[b * 4 + k] = lo;
-            Q[(B + b) * 4 + k] = hi;
-            if (k == 0) {
-                dx[b] = static_cast<float>(static_cast<_Float16>(d));
-                sx[b] = sum;
-            }
-        }
-    }
-}
-
-// Block contributions (float(sumi) * d_w) * d_x of R rows into cs[r * B + b]
-// (blocks past the row end are not written).
-template <int NBL, int R, bool A16, bool TAIL>
-__device__ __forceinline__ void q8_blocks(const RowGroup<NBL, R, A16, TAIL> &g, float *cs, const uint4 *Q,
-                                          const float *dx, const int *sx, int B, int lane, const int bc[NBL],
-                                          uint32_t tail_mask) {
-#pragma unroll
-    for (int j = 0; j < NBL; ++j) {
-        if (j > 0) __builtin_amdgcn_sched_barrier(0);
-        const uint4 q0 = Q[bc[j]], q1 = Q[B + bc[j]];
-        const float d_x = dx[bc[j]];
-        const int s8 = sx[bc[j]];
-        const uint32_t a[4] = {q0.x, q0.y, q0.z, q0.w};
-        const uint32_t c[4] = {q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int dot = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                // resident code bytes hold q - 8 per nibble; XOR 8 gives q
-                const uint32_t u = g.q[r][j][k] ^ 0x88888888u;
-                dot = __builtin_amdgcn_sdot4(static_cast<int>(u & 0x0F0F0F0Fu), static_cast<int>(a[k]), dot, false);
-                dot = __builtin_amdgcn_sdot4(static_cast<int>((u >> 4) & 0x0F0F0F0Fu), static_cast<int>(c[k]), dot,
-                                             false);
-            }
-            const int sumi = dot - 8 * s8;
-            const float dw = half_bits_to_float(static_cast<uint16_t>(g.d_bits(r, j, tail_mask)));
-            if (lane + 64 * j < B) cs[r * B + lane + 64 * j] = __fmul_rn(__fmul_rn(static_cast<float>(sumi), dw), d_x);
-        }
-    }
-}
-
 // LDS: Q planes (2 * B uint4), d_x (B floats), S (B ints), then the block
 // contributions of every wavefront's rows (WAVES * R * B floats).  Each row
 // is summed by one lane in block order, ggml's sequential f32 sum, so the
@@ -1285,7 +1370,7 @@ __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__rest
     float *cs = cs_all + wave * R * B;
     while (g < n_groups) {
         const int row0 = g * ROWS + wave * R;
-        q8_blocks<NBL, R, A16, TAIL>(grp, cs, Q, dx, sx, B, lane, bc, tail_mask);
+        q8_blocks<NBL, R, A16, TAIL>(grp, cs, B, Q, dx, sx, B, lane, bc, tail_mask);
         g += gridDim.x;
         grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
         __syncthreads();
@@ -1524,8 +1609,8 @@ int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, in
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t need = static_cast<size_t>(M) * 16 * mb_tile(static_cast<int>(B));
     if (ctx->mbtiles_bytes < need) {
-        MI355X_HIP(hipStreamSynchronize(ctx->stream));
-        if (ctx->mbtiles) MI355X_HIP(hipFree(ctx->mbtiles));
+        const int rc = free_device(ctx, ctx->mbtiles);
+        if (rc) return rc;
         ctx->mbtiles = nullptr;
         ctx->mbtiles_bytes = 0;
         MI355X_HIP(hipMalloc(&ctx->mbtiles, need));
@@ -1570,6 +1655,10 @@ struct DeviceScope {
 };
 
 struct ServerImpl {
+    // held by every call that talks to the resident kernel; a stop from
+    // another thread (a free on the same device) waits for the command in
+    // flight
+    std::mutex mu;
     mi355x_ctx *ctx = nullptr;
     hipStream_t stream = nullptr;
     int64_t max_k = 0;
@@ -1628,12 +1717,22 @@ struct mi355x_server {
 };
 
 namespace mi355x {
+namespace {
+// Every server of the process.  A hipFree waits for every kernel running on
+// its device, so a free stops the resident kernels of all servers on that
+// device, whichever context created them.  Lock order: registry, then server.
+std::mutex g_srv_mu;
+std::vector<mi355x_server *> g_servers;
+}  // namespace
 
 int stop_servers(mi355x_ctx *ctx) {
-    std::lock_guard<std::mutex> lk(ctx->srv_mu);
-    for (mi355x_server *srv : ctx->servers) {
-        DeviceScope dg(ctx->device);
-        const int rc = server_stop(&srv->impl);
+    std::lock_guard<std::mutex> lk(g_srv_mu);
+    for (mi355x_server *srv : g_servers) {
+        ServerImpl &s = srv->impl;
+        if (s.ctx->device != ctx->device) continue;
+        std::lock_guard<std::mutex> sl(s.mu);
+        DeviceScope dg(s.ctx->device);
+        const int rc = server_stop(&s);
         if (rc) return rc;
     }
     return MI355X_OK;
@@ -1701,8 +1800,8 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
     }
     s.grid = ctx->num_cus;
     {
-        std::lock_guard<std::mutex> lk(ctx->srv_mu);
-        ctx->servers.push_back(srv);
+        std::lock_guard<std::mutex> lk(mi355x::g_srv_mu);
+        mi355x::g_servers.push_back(srv);
     }
     *out = srv;
     return MI355X_OK;
@@ -1716,6 +1815,11 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
         return set_error(MI355X_EINVAL, "mi355x_server_gemv: 1 to 4 jobs per call");
     if (K <= 0 || K % 256 != 0 || K > s.max_k)
         return set_error(MI355X_EINVAL, "mi355x_server_gemv: K must be a multiple of 256 up to the server's max_k");
+    // the context's kernel variant picks the arithmetic of every job
+    const int variant = s.ctx->kernel_variant;
+    if (variant == MI355X_VARIANT_EXACT_F32)
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: no exact-f32 form in the server");
+    const int32_t mode = variant == MI355X_VARIANT_GGML_Q8 ? mi355x::kSrvGgmlQ8 : mi355x::kSrvDigits;
     for (int j = 0; j < njobs; ++j) {
         if (!jobs[j].W || !jobs[j].y || jobs[j].N <= 0)
             return set_error(MI355X_EINVAL, "mi355x_server_gemv: bad job");
@@ -1724,6 +1828,7 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
         if (reinterpret_cast<uintptr_t>(jobs[j].W) % 16 != 0)
             return set_error(MI355X_EINVAL, "mi355x_server_gemv: weights must be 16-byte aligned");
     }
+    std::lock_guard<std::mutex> sl(s.mu);
     mi355x::DeviceScope dg(s.ctx->device);
     const auto now = std::chrono::steady_clock::now();
     if (s.running && std::chrono::duration<double>(now - s.last).count() > mi355x::kSrvIdleSeconds / 2) {
@@ -1737,6 +1842,7 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
     std::memcpy(s.hx_h, x, static_cast<size_t>(K) * sizeof(float));
     s.cmd_h->K = static_cast<int32_t>(K);
     s.cmd_h->njobs = njobs;
+    s.cmd_h->mode = mode;
     for (int j = 0; j < njobs; ++j)
         s.cmd_h->jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
     const uint32_t v = ++s.seq;
@@ -1761,8 +1867,21 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
 int mi355x_server_stop(mi355x_server *srv) {
     clear_error();
     if (!srv) return set_error(MI355X_EINVAL, "mi355x_server_stop: null pointer");
+    std::lock_guard<std::mutex> sl(srv->impl.mu);
     mi355x::DeviceScope dg(srv->impl.ctx->device);
     return mi355x::server_stop(&srv->impl);
+}
+
+int mi355x_server_running(mi355x_server *srv) {
+    clear_error();
+    if (!srv) return set_error(MI355X_EINVAL, "mi355x_server_running: null pointer");
+    std::lock_guard<std::mutex> sl(srv->impl.mu);
+    mi355x::DeviceScope dg(srv->impl.ctx->device);
+    // the server's stream holds nothing but the resident kernel
+    const hipError_t e = hipStreamQuery(srv->impl.stream);
+    if (e == hipErrorNotReady) return 1;
+    if (e == hipSuccess) return 0;
+    return hip_error(e, "hipStreamQuery");
 }
 
 void mi355x_server_destroy(mi355x_server *srv) {
@@ -1770,10 +1889,11 @@ void mi355x_server_destroy(mi355x_server *srv) {
     mi355x::ServerImpl &s = srv->impl;
     if (s.ctx) {
         {
-            std::lock_guard<std::mutex> lk(s.ctx->srv_mu);
-            auto &v = s.ctx->servers;
+            std::lock_guard<std::mutex> lk(mi355x::g_srv_mu);
+            auto &v = mi355x::g_servers;
             v.erase(std::remove(v.begin(), v.end(), srv), v.end());
         }
+        std::lock_guard<std::mutex> sl(s.mu);
         mi355x::DeviceScope dg(s.ctx->device);
         (void)mi355x::server_stop(&s);
         if (s.stream) (void)hipStreamDestroy(s.stream);

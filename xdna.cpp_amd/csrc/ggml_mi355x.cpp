@@ -142,6 +142,63 @@ size_t tensor_nbytes(const ggml_tensor *t) {
 }
 
 // ---------------------------------------------------------------------------
+// batch geometry of a MUL_MAT node
+// ---------------------------------------------------------------------------
+// A node multiplies activation batch (i2, i3) -- ne[2] x ne[3] of them, each
+// M rows -- by weight matrix (i2 / r2, i3 / r3), r = activation batches per
+// weight matrix (ggml's broadcast).  Byte strides left at 0 (the
+// compatibility struct) mean densely packed.
+inline int64_t extent(int64_t ne) { return ne > 0 ? ne : 1; }
+inline size_t stride_or(size_t nb, size_t dense) { return nb != 0 ? nb : dense; }
+
+template <typename T>
+bool broadcast_ok(const T *op) {
+    const auto *w = op->src[0];
+    const auto *a = op->src[1];
+    const int64_t b2 = extent(a->ne[2]), b3 = extent(a->ne[3]);
+    return b2 % extent(w->ne[2]) == 0 && b3 % extent(w->ne[3]) == 0 && extent(op->ne[2]) == b2 &&
+           extent(op->ne[3]) == b3;
+}
+
+struct BatchGeometry {
+    int64_t batches2 = 1, batches3 = 1;   // activation batches
+    int64_t per_w2 = 1, per_w3 = 1;       // activation batches per weight matrix
+    size_t w_b2 = 0, w_b3 = 0;            // weight matrix strides
+    size_t a_row = 0, a_b2 = 0, a_b3 = 0; // activation row / batch strides
+    size_t o_row = 0, o_b2 = 0, o_b3 = 0; // output row / batch strides
+
+    size_t weight_at(int64_t i2, int64_t i3) const {
+        return static_cast<size_t>(i2 / per_w2) * w_b2 + static_cast<size_t>(i3 / per_w3) * w_b3;
+    }
+    size_t act_at(int64_t i2, int64_t i3) const {
+        return static_cast<size_t>(i2) * a_b2 + static_cast<size_t>(i3) * a_b3;
+    }
+    size_t out_at(int64_t i2, int64_t i3) const {
+        return static_cast<size_t>(i2) * o_b2 + static_cast<size_t>(i3) * o_b3;
+    }
+};
+
+template <typename T>
+BatchGeometry batch_geometry(const T *node, int64_t N, int64_t K, int64_t M, size_t row_bytes) {
+    const auto *w = node->src[0];
+    const auto *a = node->src[1];
+    BatchGeometry g;
+    g.batches2 = extent(a->ne[2]);
+    g.batches3 = extent(a->ne[3]);
+    g.per_w2 = g.batches2 / extent(w->ne[2]);
+    g.per_w3 = g.batches3 / extent(w->ne[3]);
+    g.w_b2 = stride_or(w->nb[2], static_cast<size_t>(N) * row_bytes);
+    g.w_b3 = stride_or(w->nb[3], g.w_b2 * static_cast<size_t>(extent(w->ne[2])));
+    g.a_row = stride_or(a->nb[1], static_cast<size_t>(K) * sizeof(float));
+    g.a_b2 = stride_or(a->nb[2], g.a_row * static_cast<size_t>(M));
+    g.a_b3 = stride_or(a->nb[3], g.a_b2 * static_cast<size_t>(g.batches2));
+    g.o_row = stride_or(node->nb[1], static_cast<size_t>(N) * sizeof(float));
+    g.o_b2 = stride_or(node->nb[2], g.o_row * static_cast<size_t>(M));
+    g.o_b3 = stride_or(node->nb[3], g.o_b2 * static_cast<size_t>(g.batches2));
+    return g;
+}
+
+// ---------------------------------------------------------------------------
 // claim rule (src/ggml-xdna.cpp:95-147) on any tensor-like struct
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -159,6 +216,10 @@ bool claim_mul_mat(const T *op, int mul_mat_id, bool weights_resident) {
     // this plugin's buffer (src/ggml-xdna.cpp:110-112)
     if (N < 32 || N % 4 != 0) return false;
     if (!weights_resident && M != 1) return false;
+    // weight batches broadcast over activation batches as in ggml (each
+    // weight matrix serves a whole number of them); anything else would
+    // index weights past the tensor
+    if (!broadcast_ok(op)) return false;
     const int bv = block_values(src0->type);
     if (bv == 0 || K % bv != 0) return false;
     if (!mi355x_type_ready(src0->type)) return false;
@@ -566,28 +627,25 @@ bool process_mul_mat(BackendCtx *bc, T *node, bool host) {
         std::fprintf(stderr, "[mi355x error] node '%s' src1 rows are not contiguous\n", node->name);
         return false;
     }
+    if (!broadcast_ok(node)) {
+        std::fprintf(stderr, "[mi355x error] node '%s' weight batches do not divide the activation batches\n",
+                     node->name);
+        return false;
+    }
     const size_t total_weight_bytes = static_cast<size_t>(N) * row_bytes;
-    const int64_t ne2 = node->ne[2] > 0 ? node->ne[2] : 1;
-    const int64_t ne3 = node->ne[3] > 0 ? node->ne[3] : 1;
-    const size_t dst_stride1 = node->nb[1] > 0 ? node->nb[1] : static_cast<size_t>(N) * sizeof(float);
-    const size_t dst_stride2 = node->nb[2] > 0 ? node->nb[2] : dst_stride1 * M;
-    const size_t dst_stride3 = node->nb[3] > 0 ? node->nb[3] : dst_stride2 * ne2;
-    const size_t src1_stride1 = src1->nb[1] > 0 ? src1->nb[1] : static_cast<size_t>(K) * sizeof(float);
-    const size_t src1_stride2 = src1->ne[2] > 1 ? (src1->nb[2] > 0 ? src1->nb[2] : src1_stride1 * M) : 0;
-    const size_t src1_stride3 = src1->ne[3] > 1 ? (src1->nb[3] > 0 ? src1->nb[3] : src1_stride2 * ne2) : 0;
-    const size_t src0_stride2 = src0->ne[2] > 1 ? (src0->nb[2] > 0 ? src0->nb[2] : total_weight_bytes) : 0;
-    const size_t src0_stride3 = src0->ne[3] > 1 ? (src0->nb[3] > 0 ? src0->nb[3] : src0_stride2 * ne2) : 0;
+    const BatchGeometry bg = batch_geometry(node, N, K, M, row_bytes);
+    const size_t src1_stride1 = bg.a_row, dst_stride1 = bg.o_row;
 
     const auto *w_base = static_cast<const uint8_t *>(src0->data);
     const auto *a_base = static_cast<const uint8_t *>(src1->data);
     auto *o_base = static_cast<uint8_t *>(node->data);
 
     if (!host) {
-        for (int64_t i3 = 0; i3 < ne3; ++i3) {
-            for (int64_t i2 = 0; i2 < ne2; ++i2) {
-                const uint8_t *w = w_base + i3 * src0_stride3 + i2 * src0_stride2;
-                const uint8_t *a = a_base + i3 * src1_stride3 + i2 * src1_stride2;
-                uint8_t *o = o_base + i3 * dst_stride3 + i2 * dst_stride2;
+        for (int64_t i3 = 0; i3 < bg.batches3; ++i3) {
+            for (int64_t i2 = 0; i2 < bg.batches2; ++i2) {
+                const uint8_t *w = w_base + bg.weight_at(i2, i3);
+                const uint8_t *a = a_base + bg.act_at(i2, i3);
+                uint8_t *o = o_base + bg.out_at(i2, i3);
                 // M > 1 (weights in this backend's buffer): one batched call,
                 // which reads the weights once per group of activations where
                 // the rows are whole floats apart, else M single GEMVs
@@ -630,15 +688,15 @@ bool process_mul_mat(BackendCtx *bc, T *node, bool host) {
     uint8_t *dw = scratch;
     float *dx = reinterpret_cast<float *>(scratch + w_al);
     float *dy = reinterpret_cast<float *>(scratch + w_al + ((x_bytes + 255) & ~size_t(255)));
-    for (int64_t i3 = 0; i3 < ne3; ++i3) {
-        for (int64_t i2 = 0; i2 < ne2; ++i2) {
-            const uint8_t *w = w_base + i3 * src0_stride3 + i2 * src0_stride2;
+    for (int64_t i3 = 0; i3 < bg.batches3; ++i3) {
+        for (int64_t i2 = 0; i2 < bg.batches2; ++i2) {
+            const uint8_t *w = w_base + bg.weight_at(i2, i3);
             if (mi355x_prepack_from_host(bc->ctx, type, N, K, dw, w, 0, total_weight_bytes) != MI355X_OK) {
                 std::fprintf(stderr, "[mi355x error] node '%s' weight upload: %s\n", node->name, mi355x_last_error());
                 return false;
             }
-            const uint8_t *a = a_base + i3 * src1_stride3 + i2 * src1_stride2;
-            uint8_t *o = o_base + i3 * dst_stride3 + i2 * dst_stride2;
+            const uint8_t *a = a_base + bg.act_at(i2, i3);
+            uint8_t *o = o_base + bg.out_at(i2, i3);
             for (int64_t m = 0; m < M; ++m) {
                 if (mi355x_memcpy_h2d(bc->ctx, dx, a + m * src1_stride1, x_bytes) != MI355X_OK ||
                     mi355x_gemv(bc->ctx, type, dw, N, K, dx, dy) != MI355X_OK ||

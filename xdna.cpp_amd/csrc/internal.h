@@ -45,10 +45,6 @@ struct mi355x_ctx {
     uint32_t *fence_host = nullptr;
     uint32_t *fence_dev = nullptr;
     std::atomic<uint32_t> fence_seq{0};
-    // persistent GEMV servers on this context (stopped before any hipFree,
-    // which would otherwise wait for their resident kernel)
-    std::mutex srv_mu;
-    std::vector<mi355x_server *> servers;
 };
 
 namespace mi355x {
@@ -78,9 +74,13 @@ struct GemvArgs {
 int launch_gemv_q4_0(mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_dp_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a);
-// Stops the resident kernel of every server on the context (they relaunch on
-// their next call).
+// Stops the resident kernel of every server on the context's device, whatever
+// context created it (they relaunch on their next call): a hipFree on a
+// device waits for every kernel still running there.
 int stop_servers(mi355x_ctx *ctx);
+// hipFree of a device allocation of the library: stops the device's servers,
+// waits for the context's stream, then frees.  Null is a no-op.
+int free_device(mi355x_ctx *ctx, void *p);
 // Batched form: M activation rows (x + m*x_stride) into y + m*y_stride,
 // M <= q4_0_mb_capacity() (0: form not applicable).
 int q4_0_mb_capacity(const mi355x_ctx *ctx, const GemvArgs &a);

@@ -90,8 +90,8 @@ int ensure_staging(mi355x_ctx *ctx, size_t want) {
     want = std::min(want, kStagingMax);
     if (ctx->staging_bytes >= want) return MI355X_OK;
     if (ctx->staging) {
-        MI355X_HIP(hipStreamSynchronize(ctx->stream));
-        MI355X_HIP(hipFree(ctx->staging));
+        int rc = free_device(ctx, ctx->staging);
+        if (rc) return rc;
         ctx->staging = nullptr;
         ctx->staging_bytes = 0;
     }
@@ -153,6 +153,15 @@ int hip_error(hipError_t e, const char *what) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+int free_device(mi355x_ctx *ctx, void *p) {
+    if (!p) return MI355X_OK;
+    int rc = stop_servers(ctx);
+    if (rc) return rc;
+    MI355X_HIP(hipStreamSynchronize(ctx->stream));
+    MI355X_HIP(hipFree(p));
+    return MI355X_OK;
+}
 
 int occupancy(const void *kernel, int block_threads, size_t lds_bytes) {
     static std::mutex mu;
@@ -253,13 +262,10 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
 void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     if (!ctx) return;
     DeviceGuard dg(ctx->device);
+    for (void *p : {ctx->staging, ctx->xconv, ctx->mbtiles, ctx->iq3xxs_grid, ctx->iq2s_grid})
+        (void)free_device(ctx, p);
     (void)stop_servers(ctx);
     (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->staging) (void)hipFree(ctx->staging);
-    if (ctx->xconv) (void)hipFree(ctx->xconv);
-    if (ctx->mbtiles) (void)hipFree(ctx->mbtiles);
-    if (ctx->iq3xxs_grid) (void)hipFree(ctx->iq3xxs_grid);
-    if (ctx->iq2s_grid) (void)hipFree(ctx->iq2s_grid);
     if (ctx->fence_host) (void)hipHostFree(ctx->fence_host);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -392,11 +398,7 @@ int mi355x_free(mi355x_ctx *ctx, void *dptr) {
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_free: null context");
     if (!dptr) return MI355X_OK;
     DeviceGuard dg(ctx->device);
-    int rc = stop_servers(ctx);
-    if (rc) return rc;
-    MI355X_HIP(hipStreamSynchronize(ctx->stream));
-    MI355X_HIP(hipFree(dptr));
-    return MI355X_OK;
+    return free_device(ctx, dptr);
 }
 
 int mi355x_host_malloc(size_t bytes, void **hptr) {

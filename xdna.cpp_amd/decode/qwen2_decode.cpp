@@ -587,10 +587,10 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     const int H = c.hidden, QD = m->q_dim(), KVD = m->kv_dim(), hd = c.head_dim;
     const int L = c.n_layers, T = n_prompt + std::max(n_gen, 1);
     omp_set_num_threads(m->threads);
-    // the server computes the digit-plane arithmetic on rows of multiples of
-    // 256 values; other variants and shapes take launch + fence
-    bool use_server = backend == 0 && m->wait_mode == QD_WAIT_SERVER &&
-                      (m->variant == MI355X_VARIANT_AUTO || m->variant == MI355X_VARIANT_DIGITS);
+    // the server computes the digit-plane arithmetic or ggml-cpu's Q8_0
+    // numerics on rows of multiples of 256 values; the exact-f32 variant and
+    // other shapes take launch + fence
+    bool use_server = backend == 0 && m->wait_mode == QD_WAIT_SERVER && m->variant != MI355X_VARIANT_EXACT_F32;
     int64_t max_k = 0;
     for (const Matrix &mat : m->mats) {
         max_k = std::max<int64_t>(max_k, mat.K);

@@ -88,8 +88,8 @@ QD_API int qd_set_io(qd_model *m, int mode);
 /* How GEMV groups reach the GPU on the GPU path:
  * QD_WAIT_SERVER (default): every group is a command to a persistent GEMV
  * server (mi355x_server_*), outputs in pinned memory, no launch per group --
- * for the AUTO and DIGITS variants with rows of multiples of 256 values on a
- * device with cooperative launch, else as QD_WAIT_FENCE;
+ * for the AUTO, DIGITS and GGML_Q8 variants with rows of multiples of 256
+ * values on a device with cooperative launch, else as QD_WAIT_FENCE;
  * QD_WAIT_FENCE: one launch per group, then mi355x_ctx_fence (spin on a
  * completion word in pinned memory); QD_WAIT_STREAM: one launch per group,
  * then mi355x_ctx_sync (hipStreamSynchronize).  qd_last_wait gives the mode

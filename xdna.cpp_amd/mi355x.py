@@ -49,6 +49,7 @@ _SIGNATURES = {
     "mi355x_server_create": (_c.c_int, [_vp, _c.c_int64, _c.POINTER(_vp)]),
     "mi355x_server_gemv": (_c.c_int, [_vp, _vp, _c.c_int64, _c.c_int, _vp]),
     "mi355x_server_stop": (_c.c_int, [_vp]),
+    "mi355x_server_running": (_c.c_int, [_vp]),
     "mi355x_server_destroy": (None, [_vp]),
     "mi355x_ctx_set_option": (_c.c_int, [_vp, _c.c_int, _c.c_int64]),
     "mi355x_ctx_stream": (_vp, [_vp]),
@@ -214,6 +215,13 @@ class Server:
 
     def stop(self) -> None:
         check(self.lib.mi355x_server_stop(self.h))
+
+    def running(self) -> bool:
+        """True while the resident kernel runs (it leaves after 1 s idle)."""
+        rc = self.lib.mi355x_server_running(self.h)
+        if rc < 0:
+            check(rc)
+        return rc == 1
 
     def close(self) -> None:
         if self.h:
