@@ -78,22 +78,26 @@ def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes, settle_s=0.0):
     return ms / steps, copies, y
 
 
-def cpu_baseline(raw, N, K, x, budget_s: float):
-    """Time the reference's Q4GemvEngine (oracle/_ref) -- or the C oracle when
-    the reference build is absent -- on the same bytes for ~budget_s seconds."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as orc
+def host_topology():
+    """(logical CPUs this process may use, physical cores among them): the
+    cores come from each allowed CPU's (package, core) id in sysfs, the same
+    topology lscpu prints."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    return len(cpus), len(cores)
 
-    raw = np.ascontiguousarray(raw.reshape(-1))
-    y = np.empty(N, dtype=np.float32)
-    if orc.RefLib.available():
-        eng = orc.RefCpuEngine(orc.RefLib())
-        run = lambda: eng.run(raw, N, K, x, y)  # noqa: E731
-        kind, cores, what = "reference", orc.RefCpuEngine.THREADS, "xdna::Q4GemvEngine::run (AVX2+OpenMP)"
-    else:
-        o = orc.Oracle()
-        run = lambda: o.gemv(2, raw, N, K, x)  # noqa: E731
-        kind, cores, what = "port", 1, "scalar C oracle (port of gemv_f32)"
+
+def timed(run, budget_s):
     run()
     n, t0 = 0, time.perf_counter()
     while True:
@@ -101,12 +105,55 @@ def cpu_baseline(raw, N, K, x, budget_s: float):
         n += 1
         dt = time.perf_counter() - t0
         if dt >= budget_s:
-            break
+            return n, dt
+
+
+def cpu_baseline(raw, N, K, x, budget_s: float):
+    """Time the reference's Q4GemvEngine (oracle/_ref) -- or the C oracle when
+    the reference build is absent -- on the same bytes for ~budget_s seconds.
+    The engine runs its rows on 4 OpenMP threads (num_threads(4) in
+    src/cpu-q4-gemv-engine.cpp:166); to use every physical core of the host,
+    cores / 4 host threads each run the engine on an equal slice of the rows
+    (rows are independent, so the outputs are the engine's own)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    logical, physical = host_topology()
+    raw = np.ascontiguousarray(raw.reshape(-1))
+    y = np.empty(N, dtype=np.float32)
+    rb = mi355x.row_bytes(mi355x.Q4_0, K)
+    if orc.RefLib.available():
+        ref = orc.RefLib()
+        teams = max(1, physical // orc.RefCpuEngine.THREADS)
+        engines = [orc.RefCpuEngine(ref) for _ in range(teams)]
+        bounds = [N * i // teams for i in range(teams + 1)]
+        pool = ThreadPoolExecutor(max_workers=teams)
+
+        def part(i):
+            r0, r1 = bounds[i], bounds[i + 1]
+            engines[i].run(raw[r0 * rb:r1 * rb], r1 - r0, K, x, y[r0:r1])
+
+        run = lambda: list(pool.map(part, range(teams)))  # noqa: E731
+        kind, cores = "reference", teams * orc.RefCpuEngine.THREADS
+        what = (f"xdna::Q4GemvEngine::run (AVX2+OpenMP, 4 threads each) in {teams} concurrent row slices")
+    else:
+        o = orc.Oracle()
+        run = lambda: o.gemv(2, raw, N, K, x)  # noqa: E731
+        pool = None
+        kind, cores, what = "port", physical, "C oracle (port of gemv_f32, OpenMP over rows)"
+    try:
+        n, dt = timed(run, budget_s)
+    finally:
+        if pool:
+            pool.shutdown()
     sec = dt / n
     return {"value": round(algorithmic_bytes(mi355x.Q4_0, N, K) / sec / 1e9, 3), "unit": "GB/s",
             "cores": cores, "kind": kind,
             "sample": f"{n} GEMVs of Q4_0 {N}x{K} (same bytes and x) in {dt:.1f} s, {what}, "
-                      f"{sec * 1e3:.3f} ms/GEMV; host has {os.cpu_count()} logical CPUs"}
+                      f"{sec * 1e3:.3f} ms/GEMV; {cores} threads on a host share of {physical} physical cores "
+                      f"({logical} logical CPUs)"}
 
 
 KQ_TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
@@ -140,62 +187,82 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
     """greedy decode of the Qwen2.5-3B-shaped Q4_0 model,
     every matrix-vector product on the GPU (weights resident in HBM), the
     rest of the step on the host.  tok/s = generation-phase passes / their
-    wall time.  With `cpu`, the same decode with the reference's CPU GEMV
-    engine is the baseline and the token-identity check."""
+    wall time.
+
+    The headline runs in ggml-cpu's numerics (MI355X_VARIANT_GGML_Q8: the
+    activation row quantized to Q8_0, integer block dots, blocks summed in
+    order), the configuration whose tokens follow ggml's CPU path, with every
+    GEMV group a command to the persistent server kernel.  The digit-plane
+    f32-activation mode (the library's default arithmetic) is reported
+    beside it.  With `cpu`, the same decode with the oracle's restatement of
+    ggml-cpu's arithmetic is the baseline and the headline's token check, and
+    the decode with the reference's own CPU engine checks the digit mode."""
     import decode
 
     cfg = decode.QWEN25_3B
-    threads = min(16, os.cpu_count() or 1)
+    logical, physical = host_topology()
+    threads = min(16, logical)
     t0 = time.perf_counter()
     model = decode.Model(threads=threads, **cfg)
     gemv_bytes = sum(algorithmic_bytes(mi355x.Q4_0, *model.matrix(i)[1:]) for i in range(model.n_matrices()))
     log(f"bench: decode: built the 3B-shape model ({model.weight_bytes() / 2**30:.2f} GiB Q4_0) "
         f"in {time.perf_counter() - t0:.1f} s with {threads} threads")
     prompt = decode.prompt_tokens(n_prompt, cfg["vocab"], seed=512)
+
+    def run():
+        toks, t = model.generate(prompt, n_gen)
+        passes = t["gen_passes"]
+        return toks, t, passes / t["gen_s"]
+
     try:
         t0 = time.perf_counter()
         model.attach_gpu(0)
         log(f"bench: decode: weights prepacked into HBM in {time.perf_counter() - t0:.1f} s")
+        model.set_variant(mi355x.VARIANT_GGML_Q8)
         model.generate(prompt[:8], 4)  # warm-up: first launches of each kernel form
-        # default: every GEMV group a command to the persistent server kernel
         try:
-            gpu_toks, t = model.generate(prompt, n_gen)
+            gq_toks, t, tok_s = run()
             mode = {0: "stream", 1: "fence", 2: "server"}.get(model.last_wait(), "?")
         except RuntimeError as e:
             log(f"bench: decode: server mode failed ({e}); one launch per group instead")
             model.set_wait(model.WAIT_FENCE)
-            gpu_toks, t = model.generate(prompt, n_gen)
+            gq_toks, t, tok_s = run()
             mode = f"fence (server failed: {e})"
         passes = t["gen_passes"]
-        tok_s = passes / t["gen_s"]
         launches = model.last_launches() / passes
-        # one launch per group, the host spinning on a completion word ...
+        # the same numerics with one launch per group, the host spinning on a
+        # completion word or waiting with hipStreamSynchronize
         model.set_wait(model.WAIT_FENCE)
-        fence_toks, tf = model.generate(prompt, n_gen)
-        # ... or waiting with hipStreamSynchronize
+        fence_toks, tf, _ = run()
         model.set_wait(model.WAIT_STREAM)
-        sync_toks, tw = model.generate(prompt, n_gen)
+        sync_toks, tw, _ = run()
         # launch + fence with activations and outputs copied through HBM
-        # (staged I/O) ...
+        # (staged I/O), then also one launch per weight matrix: the traffic
+        # of a ggml graph with one MUL_MAT node per weight
         model.set_wait(model.WAIT_FENCE)
         model.set_io(model.IO_STAGED)
-        staged_toks, ts = model.generate(prompt, n_gen)
-        # ... and, in addition, one launch per weight matrix: the traffic of a
-        # ggml graph with one MUL_MAT node per weight on a device-memory backend
+        staged_toks, ts, _ = run()
         model.set_fuse(False)
-        node_toks, tn = model.generate(prompt, n_gen)
+        node_toks, tn, _ = run()
         node_launches = model.last_launches() / passes
         model.set_fuse(True)
         model.set_io(model.IO_MAPPED)
         model.set_wait(model.WAIT_SERVER)
-        log(f"bench: decode: launch + fence {passes / tf['gen_s']:.1f} tok/s; hipStreamSynchronize waits "
-            f"{passes / tw['gen_s']:.1f} tok/s; staged I/O {passes / ts['gen_s']:.1f} tok/s; per-matrix launches "
-            f"with staged I/O {passes / tn['gen_s']:.1f} tok/s")
-        log(f"bench: decode: GPU {tok_s:.1f} tok/s ({t['gen_s'] / passes * 1e3:.3f} ms/token, "
-            f"GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops {t['gen_host_s'] / passes * 1e3:.3f} ms); "
-            f"prompt {n_prompt / t['prompt_s']:.1f} tok/s token by token")
+        # the digit-plane f32-activation arithmetic (library default)
+        model.set_variant(mi355x.VARIANT_AUTO)
+        dg_toks, td, dg_tok_s = run()
+        log(f"bench: decode (ggml Q8_0 numerics): launch + fence {passes / tf['gen_s']:.1f} tok/s; "
+            f"hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s; staged I/O {passes / ts['gen_s']:.1f} "
+            f"tok/s; per-matrix launches with staged I/O {passes / tn['gen_s']:.1f} tok/s")
+        log(f"bench: decode: GPU {tok_s:.1f} tok/s in ggml Q8_0 numerics ({t['gen_s'] / passes * 1e3:.3f} "
+            f"ms/token, GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops "
+            f"{t['gen_host_s'] / passes * 1e3:.3f} ms); digit-plane mode {dg_tok_s:.1f} tok/s; prompt "
+            f"{n_prompt / t['prompt_s']:.1f} tok/s token by token")
         res = {
             "tok_s": round(tok_s, 2), "unit": "tok/s",
+            "numerics": "ggml-cpu Q4_0 x Q8_0 (MI355X_VARIANT_GGML_Q8): activations quantized to Q8_0 per "
+                        "32-value block, exact integer block dots, (sumi * d_w) * d_x summed in block order per "
+                        "row -- the arithmetic of ggml's generic CPU path",
             "workload": f"Qwen2.5-3B shape (36 layers, hidden 2048, 16q/2kv x 128, FFN 11008, vocab 151936, "
                         f"tied), Q4_0 of N(0,0.02), {n_prompt}-token uniform-random prompt then {n_gen} "
                         f"greedy tokens; tok/s over the {passes} generation-phase forward passes",
@@ -207,24 +274,32 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
             "prompt_tok_s": round(n_prompt / t["prompt_s"], 2),
             "gemv_launches_per_token": launches,
             "mode": mode,
-            "staged_io": {"tok_s": round(passes / ts["gen_s"], 2),
-                          "gemv_ms_per_token": round(ts["gen_gemv_s"] / passes * 1e3, 4),
-                          "tokens_match": bool(np.array_equal(staged_toks, gpu_toks)),
-                          "note": "activation copied host->HBM and outputs HBM->host around every GEMV group"},
             "fence": {"tok_s": round(passes / tf["gen_s"], 2),
                       "gemv_ms_per_token": round(tf["gen_gemv_s"] / passes * 1e3, 4),
-                      "tokens_match": bool(np.array_equal(fence_toks, gpu_toks)),
+                      "tokens_match": bool(np.array_equal(fence_toks, gq_toks)),
                       "note": "one launch per GEMV group, the host spinning on a completion word "
                               "(mi355x_ctx_fence)"},
             "stream_wait": {"tok_s": round(passes / tw["gen_s"], 2),
                             "gemv_ms_per_token": round(tw["gen_gemv_s"] / passes * 1e3, 4),
-                            "tokens_match": bool(np.array_equal(sync_toks, gpu_toks)),
+                            "tokens_match": bool(np.array_equal(sync_toks, gq_toks)),
                             "note": "one launch per GEMV group, then hipStreamSynchronize"},
+            "staged_io": {"tok_s": round(passes / ts["gen_s"], 2),
+                          "gemv_ms_per_token": round(ts["gen_gemv_s"] / passes * 1e3, 4),
+                          "tokens_match": bool(np.array_equal(staged_toks, gq_toks)),
+                          "note": "launch + fence with the activation copied host->HBM and outputs HBM->host "
+                                  "around every GEMV group"},
             "per_node": {"tok_s": round(passes / tn["gen_s"], 2), "gemv_launches_per_token": node_launches,
                          "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
-                         "tokens_match_fused": bool(np.array_equal(node_toks, gpu_toks)),
+                         "tokens_match_fused": bool(np.array_equal(node_toks, gq_toks)),
                          "note": "one GEMV launch per weight matrix (q, k, v, gate, up separately) with staged I/O: "
                                  "the pattern of a ggml graph with one MUL_MAT node per weight on this backend"},
+            "digit_mode": {"tok_s": round(dg_tok_s, 2),
+                           "gemv_ms_per_token": round(td["gen_gemv_s"] / passes * 1e3, 4),
+                           "host_ms_per_token": round(td["gen_host_s"] / passes * 1e3, 4),
+                           "numerics": "the library's default arithmetic: f32 activations as 20-bit fixed point "
+                                       "per 32-value block, int4 dot8 block dots, f32 row sums (within 1e-4 "
+                                       "||w|| ||x|| of the reference's f32 GEMV)",
+                           "mode": {0: "stream", 1: "fence", 2: "server"}.get(model.last_wait(), "?")},
             "split": "the 253 weight GEMVs per token on the GPU (q|k|v and gate|up, adjacent in HBM, as one "
                      "job each); norms, RoPE, attention, SwiGLU, argmax on the host; mode 'server': each GEMV "
                      "group is a command to a resident server kernel (mi355x_server_*) that reads the activation "
@@ -235,57 +310,43 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
             sys.path.insert(0, os.path.join(ROOT, "oracle"))
             import oracle as orc
 
-            kind = "reference" if orc.RefLib.available() else "oracle"
-            f, cores = orc.decode_gemv(kind)
-            log(f"bench: decode: CPU run ({kind} GEMV) for the baseline and the token-identity check")
-            cpu_toks, tc = model.generate(prompt, n_gen, f)
-            same = np.array_equal(cpu_toks, gpu_toks)
-            diff = np.nonzero(cpu_toks != gpu_toks)[0]
+            # the headline's check and baseline: every GEMV with ggml-cpu's
+            # Q8_0 arithmetic, restated in the oracle (ggml itself is not in
+            # this build), OpenMP over rows
+            fq, _ = orc.decode_gemv("ggml_q8")
+            log("bench: decode: CPU run with the restated ggml Q8_0 arithmetic (baseline, token check)")
+            q8_toks, tq = model.generate(prompt, n_gen, fq)
+            same = np.array_equal(q8_toks, gq_toks)
+            diff = np.nonzero(q8_toks != gq_toks)[0]
             res["token_identical"] = bool(same)
             res["first_mismatch"] = None if same else int(diff[0])
+            res["token_check"] = ("the same decode on the CPU with ggml-cpu's Q4_0 x Q8_0 arithmetic restated from "
+                                  "ggml's generic C path (quantize_row_q8_0, ggml_vec_dot_q4_0_q8_0); identity "
+                                  "with a real ggml build is not checked here (ggml is not in this build)")
             res["cpu_baseline"] = {
-                "tok_s": round(passes / tc["gen_s"], 3), "unit": "tok/s", "cores": cores, "kind": kind,
-                "sample": f"the same {n_prompt}+{n_gen}-token decode with every GEMV on "
-                          + ("the reference's AVX2+OpenMP Q4GemvEngine (src/cpu-q4-gemv-engine.cpp)"
-                             if kind == "reference" else "the scalar C oracle")
-                          + f" and the same host ops ({threads} OpenMP threads for attention); "
-                            "not ggml-cpu, which is not in this build",
-                "ms_per_token": round(tc["gen_s"] / passes * 1e3, 3),
+                "tok_s": round(passes / tq["gen_s"], 3), "unit": "tok/s", "cores": logical, "kind": "port",
+                "sample": f"the same {n_prompt}+{n_gen}-token decode with every GEMV in the restated ggml-cpu "
+                          f"Q4_0 x Q8_0 arithmetic (oracle/oracle.c, OpenMP over rows on {logical} threads of a "
+                          f"host share of {physical} physical cores) and the same host ops",
+                "ms_per_token": round(tq["gen_s"] / passes * 1e3, 3),
             }
-            log(f"bench: decode: CPU {passes / tc['gen_s']:.2f} tok/s; token-identical: {same}")
-            # ggml-cpu does not multiply by f32 activations: it quantizes them
-            # to Q8_0 first.  The same decode with that arithmetic (restated
-            # in the oracle; ggml itself is not part of this build) shows
-            # whether the GPU's f32-activation tokens survive it.
-            fq, qcores = orc.decode_gemv("ggml_q8")
-            q8_toks, tq = model.generate(prompt, n_gen, fq)
-            q8_same = np.array_equal(q8_toks, gpu_toks)
-            q8_diff = np.nonzero(q8_toks != gpu_toks)[0]
-            res["ggml_q8_numerics"] = {
-                "token_identical": bool(q8_same),
-                "first_mismatch": None if q8_same else int(q8_diff[0]),
-                "matching_tokens": int(np.sum(q8_toks == gpu_toks)),
-                "tok_s": round(passes / tq["gen_s"], 3), "cores": qcores,
-                "note": "every GEMV with ggml-cpu's Q8_0-activation arithmetic (quantize_row_q8_0 + "
-                        "vec_dot_q4_0_q8_0, restated from ggml's generic C path; ggml is not in this build)",
-            }
-            # the GPU in ggml-cpu numerics (MI355X_VARIANT_GGML_Q8) against it
-            model.set_variant(mi355x.VARIANT_GGML_Q8)
-            g8_toks, tg8 = model.generate(prompt, n_gen)
-            model.set_variant(mi355x.VARIANT_AUTO)
-            g8_same = np.array_equal(g8_toks, q8_toks)
-            g8_diff = np.nonzero(g8_toks != q8_toks)[0]
-            res["ggml_q8_numerics"].update({
-                "gpu_tok_s": round(passes / tg8["gen_s"], 2),
-                "gpu_token_identical": bool(g8_same),
-                "gpu_first_mismatch": None if g8_same else int(g8_diff[0]),
-                "gpu_note": "the GPU decode with MI355X_VARIANT_GGML_Q8 (activations quantized to Q8_0 in the "
-                            "kernel, integer block dots) against the CPU decode with the restated ggml arithmetic",
+            log(f"bench: decode: CPU {passes / tq['gen_s']:.2f} tok/s; GPU tokens identical: {same}")
+            # the digit mode against the reference's own CPU GEMV engine
+            kind = "reference" if orc.RefLib.available() else "oracle"
+            f, cores = orc.decode_gemv(kind)
+            ref_toks, tc = model.generate(prompt, n_gen, f)
+            d_same = np.array_equal(ref_toks, dg_toks)
+            d_diff = np.nonzero(ref_toks != dg_toks)[0]
+            res["digit_mode"].update({
+                "token_identical_vs_cpu_engine": bool(d_same),
+                "first_mismatch": None if d_same else int(d_diff[0]),
+                "cpu_engine": ("the reference's AVX2+OpenMP Q4GemvEngine (src/cpu-q4-gemv-engine.cpp)"
+                               if kind == "reference" else "the C oracle"),
+                "cpu_engine_tok_s": round(passes / tc["gen_s"], 3), "cpu_engine_cores": cores,
+                "matching_tokens_vs_ggml_numerics": int(np.sum(q8_toks == dg_toks)),
             })
-            log(f"bench: decode: ggml Q8_0 numerics: f32-path tokens identical {q8_same}"
-                + ("" if q8_same else f" (first mismatch at {int(q8_diff[0])})")
-                + f"; GPU GGML_Q8 variant {passes / tg8['gen_s']:.1f} tok/s, tokens identical {g8_same}"
-                + ("" if g8_same else f" (first mismatch at {int(g8_diff[0])})"))
+            log(f"bench: decode: digit mode vs the {kind} CPU engine: tokens identical {d_same}; CPU engine "
+                f"{passes / tc['gen_s']:.2f} tok/s")
     finally:
         model.close()
     return res
@@ -343,6 +404,18 @@ def main() -> int:
         log(f"bench: {ms * 1e3:.2f} us/launch over {copies} resident copies")
         ms_hot, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, 0, args.settle)
         log(f"bench: cache-hot (one copy) {ms_hot * 1e3:.2f} us/launch")
+        # the other arithmetic variants on the same workload
+        variants = {}
+        for vname, v in (("exact_f32", mi355x.VARIANT_EXACT_F32), ("ggml_q8", mi355x.VARIANT_GGML_Q8)):
+            ctx.set_option(mi355x.OPT_VARIANT, v)
+            try:
+                msv, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle)
+            finally:
+                ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+            gv = alg / (msv * 1e-3) / 1e9
+            variants[vname] = {"us_per_launch": round(msv * 1e3, 3), "GB/s": round(gv, 1),
+                               "frac": round(gv / HBM_PEAK_GBS, 4)}
+            log(f"bench: variant {vname}: {msv * 1e3:.2f} us/launch, {gv:.1f} GB/s")
         sweep = {}
         if args.sweep:
             for (n2, k2) in ((4096, 4096), (17408, 5120), (151936, 2048)):
@@ -382,7 +455,11 @@ def main() -> int:
         "vs_baseline": round(gbs / REFERENCE_GBS, 2),
         "baseline_note": f"value / {REFERENCE_GBS} GB/s, the reference's published Q4_0 8192x8192 GEMV rate "
                          "(README.md:98, host CPU, weight bytes only)",
-        "dtype": "f32",
+        "dtype": "q4_0 x fx20 (int4 dot8)",
+        "arithmetic": "Q4_0 weights (4-bit codes, fp16 block scales) times f32 activations: each 32-value "
+                      "activation block as 20-bit fixed point (5 signed 4-bit digit planes, power-of-two block "
+                      "scale), block dots exact in int32 with v_dot8_i32_i4, f32 scale-and-sum per row; inputs "
+                      "and outputs f32",
         "data": "synthetic: f32 N(0,0.02) weights (seed 42) quantized to Q4_0, x ~ N(0,1) (seed 43)",
         "config": {"workload": f"Q4_0 GEMV {N}x{K} (N rows x K), 1 f32 activation row, "
                                f"weights rotated over {copies} resident copies "
@@ -399,6 +476,10 @@ def main() -> int:
                       "GB/s": round(alg / (ms_hot * 1e-3) / 1e9, 2),
                       "note": "single resident copy, served partly from MALL/L2; not the HBM figure"},
         "parity": {"cosine_vs_oracle": cos},
+        "variants": {**variants,
+                     "note": "the same workload in the library's other arithmetic variants: exact_f32 (codes to "
+                             "f32, fp32 FMA, activations exactly as given) and ggml_q8 (ggml-cpu's Q8_0 "
+                             "activation numerics, blocks summed in order)"},
     }
     if sweep:
         out["sweep"] = sweep
