@@ -214,6 +214,25 @@ MI355X_API int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int
                                    const float *x, int64_t x_stride, float *y, int64_t y_stride,
                                    int64_t M);
 
+/* Allocation-free form of mi355x_gemv_batched, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  No counterpart in the reference.  Same arguments and the
+ * same outputs, bit for bit; the K-split batched form keeps its activation
+ * tiles in the library's static device scratch of
+ * MI355X_NOALLOC_SCRATCH_BYTES (336 KiB per device, held until the process
+ * ends; enough for 8 activations of K = 16384 per pass, the most the form
+ * stages) instead of a context buffer grown with hipMalloc.  Every call on
+ * one device shares that scratch: calls that overlap on one device (two
+ * streams or contexts of the same device) race.  Nothing else allocates:
+ * K/IQ weights need 16-byte aligned activation rows (x and x_stride a
+ * multiple of 4 floats), IQ3_XXS / IQ2_S need their grid already on the
+ * context (one mi355x_gemv of the type first); otherwise MI355X_EINVAL /
+ * MI355X_EUNSUPPORTED with a message. */
+#define MI355X_NOALLOC_SCRATCH_BYTES 344064
+MI355X_API int mi355x_gemv_batched_noalloc(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                                           const float *x, int64_t x_stride, float *y, int64_t y_stride,
+                                           int64_t M);
+
 /* ---- persistent GEMV server (decode loops) ---------------------------------
  * No counterpart in the reference (its engine calls block, one dispatch
  * each).  For a host loop that issues one Q4_0 GEMV group at a time -- batch-1

@@ -31,7 +31,9 @@
 #include <algorithm>
 #include <chrono>
 #include <cstring>
+#include <mutex>
 #include <new>
+#include <string>
 
 namespace mi355x {
 namespace {
@@ -1585,7 +1587,42 @@ int q4_0_mb_capacity(const mi355x_ctx *, const GemvArgs &a) {
     return kMbMax;
 }
 
-int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M) {
+// ---- static scratch of the allocation-free batched entry point --------------
+// The activation tiles of one K-split batched launch, for callers that cannot
+// allocate (graph capture, serving loops): kMbMax activations of the longest
+// row the batched form stages (kDpMaxBlocks blocks) -- 336 KiB, held by every
+// device the library runs on until the process ends.  In host code `scratch`
+// names a host-side stand-in: its device address, per device, comes from
+// hipGetSymbolAddress (resolve_scratch) and only that address is used.
+constexpr size_t kScratchBytes = static_cast<size_t>(kMbMax) * 16 * mb_tile(static_cast<int>(kDpMaxBlocks));
+static_assert(kScratchBytes == MI355X_NOALLOC_SCRATCH_BYTES, "static scratch size as declared in the C-ABI");
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+int resolve_scratch(int device, void **out) {
+    *out = nullptr;
+    if (device < 0 || device >= kScratchDevices)
+        return set_error(MI355X_EUNSUPPORTED, "static scratch: device index beyond the library's table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return MI355X_OK;
+}
+
+size_t scratch_bytes() { return kScratchBytes; }
+
+int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M,
+                        void *fixed_tiles) {
     const int64_t B = a.K / 32;
     const int64_t row_bytes = 18 * B;
     const int nbl = static_cast<int>((B + 63) / 64);
@@ -1605,18 +1642,29 @@ int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, in
         return MI355X_OK;
     }
     // the tiles stay in place from the staging launch to the batched launch
-    // that reads them (calls on one context share the buffer)
-    std::lock_guard<std::mutex> lk(ctx->mu);
+    // that reads them (calls on one context share the buffer; with
+    // fixed_tiles, the device's static scratch, calls on any context of the
+    // device share it and overlapping calls race)
+    std::unique_lock<std::mutex> lk(ctx->mu, std::defer_lock);
     const size_t need = static_cast<size_t>(M) * 16 * mb_tile(static_cast<int>(B));
-    if (ctx->mbtiles_bytes < need) {
-        const int rc = free_device(ctx, ctx->mbtiles);
-        if (rc) return rc;
-        ctx->mbtiles = nullptr;
-        ctx->mbtiles_bytes = 0;
-        MI355X_HIP(hipMalloc(&ctx->mbtiles, need));
-        ctx->mbtiles_bytes = need;
+    uint4 *tiles = static_cast<uint4 *>(fixed_tiles);
+    if (tiles) {
+        if (need > kScratchBytes)
+            return set_error(MI355X_EINVAL, "batched GEMV needs " + std::to_string(need) +
+                                                " bytes of activation tiles, the static scratch holds " +
+                                                std::to_string(kScratchBytes));
+    } else {
+        lk.lock();
+        if (ctx->mbtiles_bytes < need) {
+            const int rc = free_device(ctx, ctx->mbtiles);
+            if (rc) return rc;
+            ctx->mbtiles = nullptr;
+            ctx->mbtiles_bytes = 0;
+            MI355X_HIP(hipMalloc(&ctx->mbtiles, need));
+            ctx->mbtiles_bytes = need;
+        }
+        tiles = static_cast<uint4 *>(ctx->mbtiles);
     }
-    uint4 *tiles = static_cast<uint4 *>(ctx->mbtiles);
     const int64_t groups = static_cast<int64_t>(M) * 4 * B;
     hipLaunchKernelGGL(q4_0_mb_stage_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
                        ctx->stream, static_cast<const float *>(a.x), x_stride, M, static_cast<int>(B),

@@ -28,6 +28,9 @@ struct mi355x_ctx {
     // demand, freed with the context)
     void *mbtiles = nullptr;
     size_t mbtiles_bytes = 0;
+    // device address of the library's static scratch on this device
+    // (allocation-free entry point)
+    void *scratch = nullptr;
     // per-context copies of the IQ grids (device), valid when non-null
     void *iq3xxs_grid = nullptr;
     void *iq2s_grid = nullptr;
@@ -84,7 +87,14 @@ int free_device(mi355x_ctx *ctx, void *p);
 // Batched form: M activation rows (x + m*x_stride) into y + m*y_stride,
 // M <= q4_0_mb_capacity() (0: form not applicable).
 int q4_0_mb_capacity(const mi355x_ctx *ctx, const GemvArgs &a);
-int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M);
+// fixed_tiles: the device's static scratch (allocation-free entry point), or
+// null for the context's own tile buffer (grown with hipMalloc on demand).
+int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, int64_t y_stride, int M,
+                        void *fixed_tiles);
+// Device address of the static scratch on `device` (the device must be
+// current); resolved once per device with hipGetSymbolAddress.
+int resolve_scratch(int device, void **out);
+size_t scratch_bytes();
 bool q4_0_st_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a);

@@ -6,11 +6,9 @@
 #include <atomic>
 #include <chrono>
 #include <cstring>
-#include <map>
 #include <mutex>
 #include <new>
 #include <string>
-#include <tuple>
 #include <vector>
 
 namespace mi355x {
@@ -163,18 +161,28 @@ int free_device(mi355x_ctx *ctx, void *p) {
     return MI355X_OK;
 }
 
+// Fixed-size cache (no heap allocation: the allocation-free entry point goes
+// through here); a full table just recomputes.
 int occupancy(const void *kernel, int block_threads, size_t lds_bytes) {
+    struct Entry {
+        const void *kernel;
+        int threads;
+        size_t lds;
+        int occ;
+    };
+    constexpr int kSlots = 512;
     static std::mutex mu;
-    static std::map<std::tuple<const void *, int, size_t>, int> cache;
+    static Entry cache[kSlots];
+    static int used = 0;
     std::lock_guard<std::mutex> lk(mu);
-    auto key = std::make_tuple(kernel, block_threads, lds_bytes);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
+    for (int i = 0; i < used; ++i)
+        if (cache[i].kernel == kernel && cache[i].threads == block_threads && cache[i].lds == lds_bytes)
+            return cache[i].occ;
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block_threads, lds_bytes) != hipSuccess ||
         occ < 1)
         occ = 1;
-    cache.emplace(key, occ);
+    if (used < kSlots) cache[used++] = {kernel, block_threads, lds_bytes, occ};
     return occ;
 }
 
@@ -255,6 +263,14 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
     }
     ctx->fence_host = static_cast<uint32_t *>(word);
     ctx->fence_dev = static_cast<uint32_t *>(word_dev);
+    // the device address of the static scratch, once per device, with the
+    // device current (the allocation-free entry point uses only this address)
+    rc = resolve_scratch(device, &ctx->scratch);
+    if (rc) {
+        const std::string msg = mi355x_last_error();
+        mi355x_ctx_destroy(ctx);
+        return set_error(rc, msg);
+    }
     *out = ctx;
     return MI355X_OK;
 }
@@ -590,18 +606,36 @@ int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_
     return gemv_common(ctx, type, W, N, K, x_bf16, true, y, "mi355x_gemv_bf16");
 }
 
-int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x,
-                        int64_t x_stride, float *y, int64_t y_stride, int64_t M) {
+namespace {
+
+// mi355x_gemv_batched and its allocation-free form (noalloc: activation tiles
+// in the device's static scratch; no path that would allocate).
+int gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x, int64_t x_stride,
+                 float *y, int64_t y_stride, int64_t M, bool noalloc, const char *who) {
     clear_error();
-    if (M < 0) return set_error(MI355X_EINVAL, "mi355x_gemv_batched: negative M");
+    if (M < 0) return set_error(MI355X_EINVAL, std::string(who) + ": negative M");
     if (M > 1 && (x_stride < K || y_stride < N))
-        return set_error(MI355X_EINVAL, "mi355x_gemv_batched: strides smaller than a row");
+        return set_error(MI355X_EINVAL, std::string(who) + ": strides smaller than a row");
+    if (noalloc && ctx && M > 0 && N > 0) {
+        if (!ctx->scratch) return set_error(MI355X_EUNSUPPORTED, std::string(who) + ": no static scratch on the device");
+        // the K/IQ kernels copy unaligned activations into a context buffer,
+        // and IQ3_XXS / IQ2_S grids reach a context on its first such GEMV:
+        // both would allocate
+        if (type != MI355X_TYPE_Q4_0 &&
+            ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (M > 1 && (x_stride & 3) != 0)))
+            return set_error(MI355X_EINVAL, std::string(who) +
+                                                ": K/IQ weights need 16-byte aligned activation rows here");
+        if ((type == MI355X_TYPE_IQ3_XXS && !ctx->iq3xxs_grid) || (type == MI355X_TYPE_IQ2_S && !ctx->iq2s_grid))
+            return set_error(MI355X_EUNSUPPORTED, std::string(who) +
+                                                      ": the grid is not on this context yet (one mi355x_gemv of "
+                                                      "this type on the context first)");
+    }
     // Q4_0 digit-plane arithmetic: up to q4_0_mb_capacity() activations per
     // launch of the batched form (weights read once per launch)
     if (ctx && type == MI355X_TYPE_Q4_0 && M >= 2 && N > 0 && W && x && y &&
         (ctx->kernel_variant == MI355X_VARIANT_AUTO || ctx->kernel_variant == MI355X_VARIANT_DIGITS)) {
         uint64_t total = 0;
-        int rc = check_tensor(type, N, K, &total, "mi355x_gemv_batched");
+        int rc = check_tensor(type, N, K, &total, who);
         if (rc) return rc;
         GemvArgs a{type, static_cast<const uint8_t *>(W), N, K, x, false, y};
         const int cap = q4_0_mb_capacity(ctx, a);
@@ -612,7 +646,7 @@ int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int
                 GemvArgs c{type, static_cast<const uint8_t *>(W), N, K, x + m0 * x_stride, false, y + m0 * y_stride};
                 // a one-activation remainder also runs in this form, so every
                 // output of the call has the same arithmetic
-                rc = launch_gemv_q4_0_mb(ctx, c, x_stride, y_stride, chunk);
+                rc = launch_gemv_q4_0_mb(ctx, c, x_stride, y_stride, chunk, noalloc ? ctx->scratch : nullptr);
                 if (rc) return rc;
                 m0 += chunk;
             }
@@ -620,10 +654,22 @@ int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int
         }
     }
     for (int64_t m = 0; m < M; ++m) {
-        int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, "mi355x_gemv_batched");
+        int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, who);
         if (rc) return rc;
     }
     return MI355X_OK;
+}
+
+}  // namespace
+
+int mi355x_gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x,
+                        int64_t x_stride, float *y, int64_t y_stride, int64_t M) {
+    return gemv_batched(ctx, type, W, N, K, x, x_stride, y, y_stride, M, false, "mi355x_gemv_batched");
+}
+
+int mi355x_gemv_batched_noalloc(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x,
+                                int64_t x_stride, float *y, int64_t y_stride, int64_t M) {
+    return gemv_batched(ctx, type, W, N, K, x, x_stride, y, y_stride, M, true, "mi355x_gemv_batched_noalloc");
 }
 
 int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int n_weights, int64_t N, int64_t K,

@@ -77,6 +77,8 @@ _SIGNATURES = {
     "mi355x_gemv_bf16": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _vp]),
     "mi355x_gemv_batched": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _c.c_int64, _vp,
                                        _c.c_int64, _c.c_int64]),
+    "mi355x_gemv_batched_noalloc": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _c.c_int64, _vp,
+                                               _c.c_int64, _c.c_int64]),
     "mi355x_time_gemv": (_c.c_int, [_vp, _c.c_int, _c.POINTER(_vp), _c.c_int, _c.c_int64, _c.c_int64, _vp,
                                     _vp, _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
 }
