@@ -223,200 +223,172 @@ static void scale_min_k4(int j, const uint8_t *q, int *sc, int *m) {
     }
 }
 
+/* Integer form of one 256-value superblock: a[p] is the integer every value
+ * multiplies (its code, or its signed grid magnitude), sc[g] the integer
+ * scale of its group of `group` values (16 or 32), mn[] the Q4_K/Q5_K mins,
+ * d/dmin the fp16 block scales.  Both the f32 dequantizers below and the
+ * ggml Q8_K dot products further down read blocks through these, so the
+ * dequantizers' golden vectors from the reference build also pin the
+ * integers the dot products use. */
+typedef struct {
+    int a[256];
+    uint8_t neg[256]; /* grid types: sign bit of value p (a zero magnitude keeps it) */
+    int sc[16];
+    int mn[8];
+    int group;
+    float d, dmin;
+} kq_int;
+
 /* Q4_K: d, dmin (fp16), 12 scale bytes, 128 quant bytes.  Each 64-value
- * chunk uses two sub-blocks: low nibbles with (sc0,m0), high nibbles with
- * (sc1,m1): w = (d*sc)*q - dmin*m (include/xdna/kquants.h:290-315). */
-static void dq_q4_k(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 144 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        float dmin = orc_fp16_to_f32(rd16(blk + 2));
-        const uint8_t *sc = blk + 4;
-        const uint8_t *q = blk + 16;
-        for (int c = 0; c < 4; ++c) {
-            int s0, m0, s1, m1;
-            scale_min_k4(2 * c, sc, &s0, &m0);
-            scale_min_k4(2 * c + 1, sc, &s1, &m1);
-            float d0 = d * (float)s0, n0 = dmin * (float)m0;
-            float d1 = d * (float)s1, n1 = dmin * (float)m1;
-            for (int l = 0; l < 32; ++l) *y++ = d0 * (float)(q[l] & 15) - n0;
-            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] >> 4) - n1;
-            q += 32;
+ * chunk c uses two sub-blocks: low nibbles (sub-block 2c), high nibbles
+ * (2c+1) (include/xdna/kquants.h:290-315). */
+static void int_q4_k(const uint8_t *blk, kq_int *k) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = orc_fp16_to_f32(rd16(blk + 2));
+    k->group = 32;
+    for (int j = 0; j < 8; ++j) scale_min_k4(j, blk + 4, &k->sc[j], &k->mn[j]);
+    const uint8_t *q = blk + 16;
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) {
+            k->a[64 * c + l] = q[32 * c + l] & 15;
+            k->a[64 * c + 32 + l] = q[32 * c + l] >> 4;
         }
-    }
 }
 
 /* Q5_K: as Q4_K plus a fifth bit from qh[32]; chunk c takes bit 2c for the
  * low-nibble half and bit 2c+1 for the high half (include/xdna/kquants.h:317-348). */
-static void dq_q5_k(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 176 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        float dmin = orc_fp16_to_f32(rd16(blk + 2));
-        const uint8_t *sc = blk + 4;
-        const uint8_t *qh = blk + 16;
-        const uint8_t *ql = blk + 48;
-        for (int c = 0; c < 4; ++c) {
-            int s0, m0, s1, m1;
-            scale_min_k4(2 * c, sc, &s0, &m0);
-            scale_min_k4(2 * c + 1, sc, &s1, &m1);
-            float d0 = d * (float)s0, n0 = dmin * (float)m0;
-            float d1 = d * (float)s1, n1 = dmin * (float)m1;
-            unsigned lo_bit = 1u << (2 * c), hi_bit = 2u << (2 * c);
-            for (int l = 0; l < 32; ++l)
-                *y++ = d0 * (float)((ql[l] & 15) + ((qh[l] & lo_bit) ? 16 : 0)) - n0;
-            for (int l = 0; l < 32; ++l)
-                *y++ = d1 * (float)((ql[l] >> 4) + ((qh[l] & hi_bit) ? 16 : 0)) - n1;
-            ql += 32;
+static void int_q5_k(const uint8_t *blk, kq_int *k) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = orc_fp16_to_f32(rd16(blk + 2));
+    k->group = 32;
+    for (int j = 0; j < 8; ++j) scale_min_k4(j, blk + 4, &k->sc[j], &k->mn[j]);
+    const uint8_t *qh = blk + 16;
+    const uint8_t *ql = blk + 48;
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) {
+            k->a[64 * c + l] = (ql[32 * c + l] & 15) + (((qh[l] >> (2 * c)) & 1) ? 16 : 0);
+            k->a[64 * c + 32 + l] = (ql[32 * c + l] >> 4) + (((qh[l] >> (2 * c + 1)) & 1) ? 16 : 0);
         }
-    }
 }
 
 /* Q3_K: hmask[32], qs[64], 12 packed bytes of sixteen 6-bit scales, fp16 d
  * at byte 108.  Scale s (0..15): low 4 bits from byte s%8 (nibble s/8), high
- * 2 bits from byte 8 + s%4 (bit pair s/4).  Value = 2-bit q minus 4 when the
- * hmask bit is clear; w = (d*(s-32)) * v (include/xdna/kquants.h:350-389). */
-static void q3_k_scales(const uint8_t *p, int out[16]) {
+ * 2 bits from byte 8 + s%4 (bit pair s/4), minus 32.  Value = 2-bit q minus 4
+ * when its hmask bit is clear (include/xdna/kquants.h:350-389). */
+static void int_q3_k(const uint8_t *blk, kq_int *k) {
+    const uint8_t *hm = blk;
+    const uint8_t *q = blk + 32;
+    const uint8_t *p = blk + 96;
+    k->d = orc_fp16_to_f32(rd16(blk + 108));
+    k->dmin = 0.0f;
+    k->group = 16;
     for (int s = 0; s < 16; ++s) {
         int lo = (p[s % 8] >> (4 * (s / 8))) & 15;
         int hi = (p[8 + s % 4] >> (2 * (s / 4))) & 3;
-        out[s] = lo | (hi << 4);
+        k->sc[s] = (lo | (hi << 4)) - 32;
     }
-}
-
-static void dq_q3_k(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 110 * b;
-        const uint8_t *hm = blk;
-        const uint8_t *q = blk + 32;
-        int sc[16];
-        q3_k_scales(blk + 96, sc);
-        float dall = orc_fp16_to_f32(rd16(blk + 108));
-        int is = 0;
-        unsigned mbit = 1;
-        for (int half = 0; half < 2; ++half) {
-            for (int shift = 0; shift < 8; shift += 2) {
-                for (int g = 0; g < 2; ++g) {
-                    float dl = dall * ((float)sc[is++] - 32.0f);
-                    for (int l = 0; l < 16; ++l) {
-                        int idx = 16 * g + l;
-                        float v = (float)((q[idx] >> shift) & 3) -
-                                  ((hm[idx] & mbit) ? 0.0f : 4.0f);
-                        *y++ = dl * v;
-                    }
-                }
-                mbit <<= 1;
+    /* position 128 half + 32 j + i: bits 2j of qs[32 half + i], hmask bit 4 half + j */
+    for (int half = 0; half < 2; ++half)
+        for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < 32; ++i) {
+                int v = (q[32 * half + i] >> (2 * j)) & 3;
+                k->a[128 * half + 32 * j + i] = v - (((hm[i] >> (4 * half + j)) & 1) ? 0 : 4);
             }
-            q += 32;
-        }
-    }
 }
 
 /* Q6_K: ql[128], qh[64], int8 scales[16], fp16 d at byte 208.  Per 128-value
  * half: four 32-value groups (ql low, ql+32 low, ql high, ql+32 high) with
- * qh bit pairs 0,2,4,6; q = 6-bit - 32; w = (d*sc)*q
- * (include/xdna/kquants.h:391-419). */
-static void dq_q6_k(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 210 * b;
-        const uint8_t *ql = blk;
-        const uint8_t *qh = blk + 128;
-        const int8_t *sc = (const int8_t *)(blk + 192);
-        float d = orc_fp16_to_f32(rd16(blk + 208));
-        for (int half = 0; half < 2; ++half) {
-            for (int l = 0; l < 32; ++l) {
-                int is = l / 16;
-                int q1 = (int)(int8_t)((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
-                int q2 = (int)(int8_t)((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
-                int q3 = (int)(int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
-                int q4 = (int)(int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
-                y[l] = d * (float)sc[is] * (float)q1;
-                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
-                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
-                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
-            }
-            y += 128;
-            ql += 64;
-            qh += 32;
-            sc += 8;
+ * qh bit pairs 0,2,4,6; q = 6-bit - 32 (include/xdna/kquants.h:391-419). */
+static void int_q6_k(const uint8_t *blk, kq_int *k) {
+    k->d = orc_fp16_to_f32(rd16(blk + 208));
+    k->dmin = 0.0f;
+    k->group = 16;
+    for (int s = 0; s < 16; ++s) k->sc[s] = (int8_t)blk[192 + s];
+    for (int half = 0; half < 2; ++half) {
+        const uint8_t *ql = blk + 64 * half;
+        const uint8_t *qh = blk + 128 + 32 * half;
+        int *a = k->a + 128 * half;
+        for (int l = 0; l < 32; ++l) {
+            a[l] = ((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            a[l + 32] = ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            a[l + 64] = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            a[l + 96] = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
         }
     }
 }
 
 /* IQ4_XS: fp16 d, scales_h (u16), scales_l[4], qs[128].  Sub-block ib of 32:
- * 6-bit ls = nibble ib of scales_l | 2 bits ib of scales_h; dl = d*(ls-32);
+ * 6-bit ls = nibble ib of scales_l | 2 bits ib of scales_h, scale ls - 32;
  * first 16 values from low nibbles, next 16 from high nibbles through the
  * IQ4_NL codebook (include/xdna/kquants.h:421-441). */
-static void dq_iq4_xs(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 136 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        unsigned sh = rd16(blk + 2);
-        const uint8_t *sl = blk + 4;
-        const uint8_t *qs = blk + 8;
-        for (int ib = 0; ib < 8; ++ib) {
-            int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
-            float dl = d * (float)(ls - 32);
-            for (int j = 0; j < 16; ++j) {
-                y[j] = dl * (float)k_iq4nl[qs[j] & 15];
-                y[j + 16] = dl * (float)k_iq4nl[qs[j] >> 4];
-            }
-            y += 32;
-            qs += 16;
+static void int_iq4_xs(const uint8_t *blk, kq_int *k) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = 0.0f;
+    k->group = 32;
+    unsigned sh = rd16(blk + 2);
+    const uint8_t *sl = blk + 4;
+    const uint8_t *qs = blk + 8;
+    for (int ib = 0; ib < 8; ++ib) {
+        int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+        k->sc[ib] = ls - 32;
+        for (int j = 0; j < 16; ++j) {
+            k->a[32 * ib + j] = k_iq4nl[qs[16 * ib + j] & 15];
+            k->a[32 * ib + 16 + j] = k_iq4nl[qs[16 * ib + j] >> 4];
         }
     }
 }
 
 /* IQ3_S: fp16 d, qs[64], qh[8], signs[32], scales[4].  Eight groups of 32;
- * group g uses scale nibble g of scales (db = d*(1+2*nib)), qh[g] supplies
- * the 9th index bit of its eight grid lookups (bit k for lookup k), signs
- * bytes 4g..4g+3 one bit per value (include/xdna/kquants.h:443-490). */
-static void dq_iq3_s(const uint8_t *row, int64_t K, float *y) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 110 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        const uint8_t *qs = blk + 2;
-        const uint8_t *qh = blk + 66;
-        const uint8_t *signs = blk + 74;
-        const uint8_t *scales = blk + 106;
-        for (int g = 0; g < 8; ++g) {
-            int nib = (scales[g / 2] >> (4 * (g % 2))) & 15;
-            float db = d * (1.0f + 2.0f * (float)nib);
-            for (int k = 0; k < 8; ++k) {
-                unsigned idx = qs[8 * g + k] | (((unsigned)qh[g] >> k & 1u) << 8);
-                uint32_t gv = k_iq3s_grid[idx];
-                uint8_t sb = signs[4 * g + k / 2];
-                for (int j = 0; j < 4; ++j) {
-                    float mag = (float)((gv >> (8 * j)) & 0xffu);
-                    int bit = 4 * (k & 1) + j;
-                    *y++ = db * mag * (((sb >> bit) & 1) ? -1.0f : 1.0f);
-                }
+ * group g uses scale nibble g of scales (1 + 2 * nib), qh[g] supplies the 9th
+ * index bit of its eight grid lookups (bit k for lookup k), signs bytes
+ * 4g..4g+3 one bit per value (include/xdna/kquants.h:443-490). */
+static void int_iq3_s(const uint8_t *blk, kq_int *k) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = 0.0f;
+    k->group = 32;
+    const uint8_t *qs = blk + 2;
+    const uint8_t *qh = blk + 66;
+    const uint8_t *signs = blk + 74;
+    const uint8_t *scales = blk + 106;
+    for (int g = 0; g < 8; ++g) {
+        k->sc[g] = 1 + 2 * ((scales[g / 2] >> (4 * (g % 2))) & 15);
+        for (int kk = 0; kk < 8; ++kk) {
+            unsigned idx = qs[8 * g + kk] | (((unsigned)qh[g] >> kk & 1u) << 8);
+            uint32_t gv = k_iq3s_grid[idx];
+            uint8_t sb = signs[4 * g + kk / 2];
+            for (int j = 0; j < 4; ++j) {
+                int mag = (int)((gv >> (8 * j)) & 0xffu);
+                int neg = (sb >> (4 * (kk & 1) + j)) & 1;
+                k->neg[32 * g + 4 * kk + j] = (uint8_t)neg;
+                k->a[32 * g + 4 * kk + j] = neg ? -mag : mag;
             }
         }
     }
 }
 
 /* IQ3_XXS (ggml, external): fp16 d, qs[64] grid indices, then eight u32
- * words (one per 32-value group): bits 0..27 four 7-bit sign indices, bits
- * 28..31 the scale; db = (d*(0.5+ls))*0.5.  Parity unpinned. */
-static void dq_iq3_xxs(const uint8_t *row, int64_t K, float *y, const uint32_t *grid) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 98 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        const uint8_t *qs = blk + 2;
-        const uint8_t *ss = blk + 66;
-        for (int g = 0; g < 8; ++g) {
-            uint32_t aux = (uint32_t)ss[4 * g] | ((uint32_t)ss[4 * g + 1] << 8) |
-                           ((uint32_t)ss[4 * g + 2] << 16) | ((uint32_t)ss[4 * g + 3] << 24);
-            float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
-            for (int l = 0; l < 4; ++l) {
-                uint8_t sg = orc_ksigns_iq2xs((aux >> (7 * l)) & 127);
-                for (int h = 0; h < 2; ++h) {
-                    uint32_t gv = grid[qs[8 * g + 2 * l + h]];
-                    for (int j = 0; j < 4; ++j) {
-                        float mag = (float)((gv >> (8 * j)) & 0xffu);
-                        *y++ = db * mag * (((sg >> (4 * h + j)) & 1) ? -1.0f : 1.0f);
-                    }
+ * words (one per 32-value group): bits 0..27 four 7-bit sign indices (bit 7
+ * of each sign byte: even parity), bits 28..31 the scale s (integer 2s + 1;
+ * ggml's dequantizer computes (d*(0.5+s))*0.5). */
+static void int_iq3_xxs(const uint8_t *blk, kq_int *k, const uint32_t *grid) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = 0.0f;
+    k->group = 32;
+    const uint8_t *qs = blk + 2;
+    const uint8_t *ss = blk + 66;
+    for (int g = 0; g < 8; ++g) {
+        uint32_t aux = (uint32_t)ss[4 * g] | ((uint32_t)ss[4 * g + 1] << 8) |
+                       ((uint32_t)ss[4 * g + 2] << 16) | ((uint32_t)ss[4 * g + 3] << 24);
+        k->sc[g] = 1 + 2 * (int)(aux >> 28);
+        for (int l = 0; l < 4; ++l) {
+            uint8_t sg = orc_ksigns_iq2xs((aux >> (7 * l)) & 127);
+            for (int h = 0; h < 2; ++h) {
+                uint32_t gv = grid[qs[8 * g + 2 * l + h]];
+                for (int j = 0; j < 4; ++j) {
+                    int mag = (int)((gv >> (8 * j)) & 0xffu);
+                    int neg = (sg >> (4 * h + j)) & 1;
+                    k->neg[32 * g + 8 * l + 4 * h + j] = (uint8_t)neg;
+                    k->a[32 * g + 8 * l + 4 * h + j] = neg ? -mag : mag;
                 }
             }
         }
@@ -425,30 +397,103 @@ static void dq_iq3_xxs(const uint8_t *row, int64_t K, float *y, const uint32_t *
 
 /* IQ2_S (ggml, external): fp16 d, qs[32] low index bytes, signs[32], qh[8]
  * (two index bits per lookup), scales[8] (two nibbles per 32-value group:
- * low for the first 16 values, high for the next 16); db = (d*(0.5+s))*0.25.
- * Parity unpinned. */
-static void dq_iq2_s(const uint8_t *row, int64_t K, float *y, const uint64_t *grid) {
-    for (int64_t b = 0; b < K / 256; ++b) {
-        const uint8_t *blk = row + 82 * b;
-        float d = orc_fp16_to_f32(rd16(blk));
-        const uint8_t *qs = blk + 2;
-        const uint8_t *signs = blk + 34;
-        const uint8_t *qh = blk + 66;
-        const uint8_t *scales = blk + 74;
-        for (int g = 0; g < 8; ++g) {
-            float db0 = d * (0.5f + (float)(scales[g] & 15)) * 0.25f;
-            float db1 = d * (0.5f + (float)(scales[g] >> 4)) * 0.25f;
-            for (int l = 0; l < 4; ++l) {
-                float dl = l < 2 ? db0 : db1;
-                unsigned idx = qs[4 * g + l] | ((((unsigned)qh[g]) >> (2 * l) & 3u) << 8);
-                uint64_t gv = grid[idx];
-                uint8_t sg = signs[4 * g + l];
-                for (int j = 0; j < 8; ++j) {
-                    float mag = (float)((gv >> (8 * j)) & 0xffu);
-                    *y++ = dl * mag * (((sg >> j) & 1) ? -1.0f : 1.0f);
-                }
+ * low for the first 16 values, high for the next 16), scale 2s + 1 per 16
+ * (ggml's dequantizer: (d*(0.5+s))*0.25). */
+static void int_iq2_s(const uint8_t *blk, kq_int *k, const uint64_t *grid) {
+    k->d = orc_fp16_to_f32(rd16(blk));
+    k->dmin = 0.0f;
+    k->group = 16;
+    const uint8_t *qs = blk + 2;
+    const uint8_t *signs = blk + 34;
+    const uint8_t *qh = blk + 66;
+    const uint8_t *scales = blk + 74;
+    for (int g = 0; g < 8; ++g) {
+        k->sc[2 * g] = 1 + 2 * (scales[g] & 15);
+        k->sc[2 * g + 1] = 1 + 2 * (scales[g] >> 4);
+        for (int l = 0; l < 4; ++l) {
+            unsigned idx = qs[4 * g + l] | ((((unsigned)qh[g]) >> (2 * l) & 3u) << 8);
+            uint64_t gv = grid[idx];
+            uint8_t sg = signs[4 * g + l];
+            for (int j = 0; j < 8; ++j) {
+                int mag = (int)((gv >> (8 * j)) & 0xffu);
+                int neg = (sg >> j) & 1;
+                k->neg[32 * g + 8 * l + j] = (uint8_t)neg;
+                k->a[32 * g + 8 * l + j] = neg ? -mag : mag;
             }
         }
+    }
+}
+
+static int block_int(int type, const uint8_t *blk, kq_int *k, const void *grid) {
+    switch (type) {
+    case ORC_Q4_K: int_q4_k(blk, k); return ORC_OK;
+    case ORC_Q5_K: int_q5_k(blk, k); return ORC_OK;
+    case ORC_Q3_K: int_q3_k(blk, k); return ORC_OK;
+    case ORC_Q6_K: int_q6_k(blk, k); return ORC_OK;
+    case ORC_IQ4_XS: int_iq4_xs(blk, k); return ORC_OK;
+    case ORC_IQ3_S: int_iq3_s(blk, k); return ORC_OK;
+    case ORC_IQ3_XXS:
+        if (!grid) return ORC_ENOGRID;
+        int_iq3_xxs(blk, k, (const uint32_t *)grid);
+        return ORC_OK;
+    case ORC_IQ2_S:
+        if (!grid) return ORC_ENOGRID;
+        int_iq2_s(blk, k, (const uint64_t *)grid);
+        return ORC_OK;
+    default: return ORC_EINVAL;
+    }
+}
+
+/* f32 dequantization of one superblock, in each reference expression's
+ * order:
+ *   Q4_K, Q5_K  (d*sc)*a - dmin*m       (include/xdna/kquants.h:290-348)
+ *   Q3_K        (d*(sc-32))*a           (include/xdna/kquants.h:350-389)
+ *   Q6_K        (d*sc)*a                (include/xdna/kquants.h:391-419)
+ *   IQ4_XS      (d*(ls-32))*kvalue      (include/xdna/kquants.h:421-441)
+ *   IQ3_S       (d*(1+2s))*(+-mag)      (include/xdna/kquants.h:443-490)
+ *   IQ3_XXS     ((d*(0.5+s))*0.5)*(+-mag)   (ggml dequantize_row_iq3_xxs)
+ *   IQ2_S       ((d*(0.5+s))*0.25)*(+-mag)  (ggml dequantize_row_iq2_s)
+ * For the grid types the sign is applied after the product, as the
+ * references do (a zero magnitude with its sign bit set gives -0.0). */
+static void dq_superblock(int type, const kq_int *k, float *y) {
+    for (int g = 0; g < 256 / k->group; ++g) {
+        float dl, ml = 0.0f;
+        switch (type) {
+        case ORC_Q4_K: case ORC_Q5_K:
+            dl = k->d * (float)k->sc[g];
+            ml = k->dmin * (float)k->mn[g];
+            break;
+        case ORC_IQ3_XXS:
+            dl = k->d * (0.5f + (float)((k->sc[g] - 1) / 2)) * 0.5f;
+            break;
+        case ORC_IQ2_S:
+            dl = k->d * (0.5f + (float)((k->sc[g] - 1) / 2)) * 0.25f;
+            break;
+        default:
+            dl = k->d * (float)k->sc[g];
+            break;
+        }
+        const int grid_type = type == ORC_IQ3_S || type == ORC_IQ3_XXS || type == ORC_IQ2_S;
+        for (int i = 0; i < k->group; ++i) {
+            const int p = g * k->group + i;
+            if (type == ORC_Q4_K || type == ORC_Q5_K) {
+                y[p] = dl * (float)k->a[p] - ml;
+            } else if (grid_type) {
+                const float v = dl * (float)(k->a[p] < 0 ? -k->a[p] : k->a[p]);
+                y[p] = k->neg[p] ? -v : v;
+            } else {
+                y[p] = dl * (float)k->a[p];
+            }
+        }
+    }
+}
+
+static void dq_kquant(int type, const uint8_t *row, int64_t K, float *y, const void *grid) {
+    const int64_t bb = orc_block_bytes(type);
+    kq_int k;
+    for (int64_t b = 0; b < K / 256; ++b) {
+        block_int(type, row + bb * b, &k, grid);
+        dq_superblock(type, &k, y + 256 * b);
     }
 }
 
@@ -456,19 +501,12 @@ int orc_dequant_row(int type, const uint8_t *row, int64_t K, float *out, const v
     if (orc_row_bytes(type, K) < 0 || (K > 0 && (!row || !out))) return ORC_EINVAL;
     switch (type) {
     case ORC_Q4_0: dq_q4_0(row, K, out); return ORC_OK;
-    case ORC_Q4_K: dq_q4_k(row, K, out); return ORC_OK;
-    case ORC_Q5_K: dq_q5_k(row, K, out); return ORC_OK;
-    case ORC_Q3_K: dq_q3_k(row, K, out); return ORC_OK;
-    case ORC_Q6_K: dq_q6_k(row, K, out); return ORC_OK;
-    case ORC_IQ4_XS: dq_iq4_xs(row, K, out); return ORC_OK;
-    case ORC_IQ3_S: dq_iq3_s(row, K, out); return ORC_OK;
-    case ORC_IQ3_XXS:
-        if (!grid) return ORC_ENOGRID;
-        dq_iq3_xxs(row, K, out, (const uint32_t *)grid);
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q3_K: case ORC_Q6_K: case ORC_IQ4_XS: case ORC_IQ3_S:
+        dq_kquant(type, row, K, out, NULL);
         return ORC_OK;
-    case ORC_IQ2_S:
+    case ORC_IQ3_XXS: case ORC_IQ2_S:
         if (!grid) return ORC_ENOGRID;
-        dq_iq2_s(row, K, out, (const uint64_t *)grid);
+        dq_kquant(type, row, K, out, grid);
         return ORC_OK;
     default: return ORC_EINVAL;
     }
@@ -625,5 +663,144 @@ int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, f
         y[r] = sumf;
     }
     free(xq);
+    return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml-cpu's K-quant / IQ x Q8_K numerics (EXTERNAL, parity unpinned)       */
+/* ------------------------------------------------------------------------ */
+/* The reference's live path for the eight 256-value types, whenever
+ * ggml-cpu is loaded (src/xdna-gemv-engine.cpp:1382-1399, 1430-1453):
+ * quantize_row_q8_K on the activation row, then per output row
+ * ggml_vec_dot_<type>_q8_K(K, &y[r], 0, row, 0, q8, 0, 1).  Restated from
+ * ggml's published generic C path (llama.cpp 0ec4027a2, the pinned build of
+ * README.md:64; not vendored in the reference):
+ *   Q8_K block of 256: f32 d, int8 qs[256], int16 bsums[16] (292 bytes);
+ *     max = the first value of largest |x|, iscale = -127 / max,
+ *     q = min(127, nearest_int(iscale * x)) (round half to even through
+ *     + 1.5 * 2^23), bsums = sums of 16 codes, d = 1 / iscale; an all-zero
+ *     block stores d = 0 and zero codes (and, here, zero sums).
+ *   Q4_K, Q5_K, Q3_K, Q6_K: per superblock the integers
+ *     aux[l] = sum over values p = l (mod 8) of scale(p) * a[p] * q8[p],
+ *     then lanes[l] += (d_w * d_x) * aux[l]; Q4_K / Q5_K also
+ *     sumf -= (dmin_w * d_x) * sum_j bsums[j] * min[j / 2]; at the end
+ *     sumf += lanes[0..7] in order.
+ *   IQ4_XS: per 32-value sub-block sumf += ((d_w * d_x) * (ls - 32)) * sumi.
+ *   IQ3_S, IQ3_XXS, IQ2_S: per superblock bsum = sum over groups of
+ *     scale * sum(a * q8) (scales 2s + 1), sumf += (d_w * d_x) * bsum; the
+ *     result is sumf (IQ3_S), 0.25 * sumf (IQ3_XXS) or 0.125 * sumf (IQ2_S).
+ * Integers as ggml's generic code forms them (their order does not matter);
+ * every f32 operation in ggml's order (build with -ffp-contract=off). */
+
+static int nearest_int_q8(float f) {
+    float v = f + 12582912.0f;
+    int32_t i;
+    memcpy(&i, &v, sizeof i);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+int orc_quantize_row_q8_K(const float *x, int64_t K, uint8_t *out) {
+    if (K < 0 || K % 256 != 0 || (K > 0 && (!x || !out))) return ORC_EINVAL;
+    for (int64_t b = 0; b < K / 256; ++b) {
+        const float *xb = x + 256 * b;
+        uint8_t *ob = out + ORC_Q8K_BYTES * b;
+        int8_t *qs = (int8_t *)(ob + 4);
+        int16_t bsums[16];
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = xb[j];
+            }
+        }
+        float d = 0.0f;
+        if (amax == 0.0f) {
+            memset(qs, 0, 256);
+        } else {
+            const float iscale = -127.0f / max;
+            for (int j = 0; j < 256; ++j) {
+                const int v = nearest_int_q8(iscale * xb[j]);
+                qs[j] = (int8_t)(v < 127 ? v : 127);
+            }
+            d = 1.0f / iscale;
+        }
+        for (int j = 0; j < 16; ++j) {
+            int sum = 0;
+            for (int i = 0; i < 16; ++i) sum += qs[16 * j + i];
+            bsums[j] = (int16_t)sum;
+        }
+        memcpy(ob, &d, 4);
+        memcpy(ob + 260, bsums, sizeof bsums);
+    }
+    return ORC_OK;
+}
+
+/* One output row: ggml_vec_dot_<type>_q8_K (generic) over nb superblocks. */
+static float dot_row_q8_K(int type, const uint8_t *row, int64_t nb, const uint8_t *q8, const void *grid) {
+    const int64_t bb = orc_block_bytes(type);
+    const int eight_lanes = type == ORC_Q4_K || type == ORC_Q5_K || type == ORC_Q3_K || type == ORC_Q6_K;
+    float lanes[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float sumf = 0.0f;
+    kq_int k;
+    for (int64_t i = 0; i < nb; ++i) {
+        block_int(type, row + bb * i, &k, grid);
+        const uint8_t *yb = q8 + ORC_Q8K_BYTES * i;
+        float yd;
+        memcpy(&yd, yb, 4);
+        const int8_t *yq = (const int8_t *)(yb + 4);
+        int16_t bsums[16];
+        memcpy(bsums, yb + 260, sizeof bsums);
+        if (eight_lanes) {
+            int32_t aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int p = 0; p < 256; ++p) aux[p & 7] += k.sc[p / k.group] * (k.a[p] * (int)yq[p]);
+            const float d = k.d * yd;
+            for (int l = 0; l < 8; ++l) lanes[l] += d * (float)aux[l];
+            if (type == ORC_Q4_K || type == ORC_Q5_K) {
+                int sumi = 0;
+                for (int j = 0; j < 16; ++j) sumi += bsums[j] * k.mn[j / 2];
+                const float dmin = k.dmin * yd;
+                sumf -= dmin * (float)sumi;
+            }
+        } else if (type == ORC_IQ4_XS) {
+            const float d4d8 = k.d * yd;
+            for (int ib = 0; ib < 8; ++ib) {
+                int sumi = 0;
+                for (int p = 32 * ib; p < 32 * ib + 32; ++p) sumi += (int)yq[p] * k.a[p];
+                const float dl = d4d8 * (float)k.sc[ib];
+                sumf += dl * (float)sumi;
+            }
+        } else {
+            const float d = k.d * yd;
+            int bsum = 0;
+            for (int g = 0; g < 256 / k.group; ++g) {
+                int sumi = 0;
+                for (int p = g * k.group; p < (g + 1) * k.group; ++p) sumi += k.a[p] * (int)yq[p];
+                bsum += sumi * k.sc[g];
+            }
+            sumf += d * (float)bsum;
+        }
+    }
+    if (eight_lanes)
+        for (int l = 0; l < 8; ++l) sumf += lanes[l];
+    if (type == ORC_IQ3_XXS) return 0.25f * sumf;
+    if (type == ORC_IQ2_S) return 0.125f * sumf;
+    return sumf;
+}
+
+int orc_gemv_q8_K(int type, const uint8_t *W, int64_t N, int64_t K, const float *x, float *y,
+                  const void *grid) {
+    const int64_t rb = orc_row_bytes(type, K);
+    if (rb < 0 || N < 0 || orc_block_values(type) != 256) return ORC_EINVAL;
+    if ((type == ORC_IQ3_XXS || type == ORC_IQ2_S) && !grid) return ORC_ENOGRID;
+    if (N == 0) return ORC_OK;
+    if (!W || !y || (K > 0 && !x)) return ORC_EINVAL;
+    const int64_t nb = K / 256;
+    uint8_t *q8 = (uint8_t *)malloc((size_t)(nb > 0 ? nb : 1) * ORC_Q8K_BYTES);
+    if (!q8) return ORC_EINVAL;
+    orc_quantize_row_q8_K(x, K, q8);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < N; ++r) y[r] = dot_row_q8_K(type, W + r * rb, nb, q8, grid);
+    free(q8);
     return ORC_OK;
 }

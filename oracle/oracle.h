@@ -104,6 +104,15 @@ uint16_t orc_f32_to_fp16(float f);
 int orc_quantize_row_q8_0(const float *x, int64_t K, uint8_t *out);
 int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, float *y);
 
+/* ggml-cpu's K-quant / IQ x Q8_K path (external restatement, parity
+ * unpinned; see oracle.c): Q8_K quantization of an activation row (K/256
+ * blocks of [f32 d][int8 q[256]][int16 bsums[16]]) and the GEMV of any of
+ * the eight 256-value types against it. */
+#define ORC_Q8K_BYTES 292
+int orc_quantize_row_q8_K(const float *x, int64_t K, uint8_t *out);
+int orc_gemv_q8_K(int type, const uint8_t *W, int64_t N, int64_t K, const float *x, float *y,
+                  const void *grid);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,9 @@ class Oracle:
         lib.orc_f32_to_fp16.argtypes = [ctypes.c_float]
         lib.orc_quantize_row_q8_0.argtypes = [_f32p, ctypes.c_int64, _u8p]
         lib.orc_gemv_q4_0_q8_0.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, _f32p, _f32p]
+        lib.orc_quantize_row_q8_K.argtypes = [_f32p, ctypes.c_int64, _u8p]
+        lib.orc_gemv_q8_K.argtypes = [ctypes.c_int, _u8p, ctypes.c_int64, ctypes.c_int64, _f32p, _f32p,
+                                      ctypes.c_void_p]
         self.lib = lib
 
     # ggml-cpu numerics (external restatement; see oracle.c)
@@ -90,6 +93,31 @@ class Oracle:
         y = np.zeros(N, dtype=np.float32)
         if self.lib.orc_gemv_q4_0_q8_0(_ptr(W, _u8p), N, K, _ptr(x, _f32p), _ptr(y, _f32p)) != 0:
             raise ValueError("orc_gemv_q4_0_q8_0 rejected the shape")
+        return y
+
+    Q8K_BYTES = 292
+
+    def quantize_q8_K(self, x: np.ndarray):
+        """Q8_K blocks of an activation row: (d[nb] f32, qs[nb, 256] int8,
+        bsums[nb, 16] int16)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        nb = x.size // 256
+        out = np.zeros(nb * self.Q8K_BYTES, dtype=np.uint8)
+        if self.lib.orc_quantize_row_q8_K(_ptr(x, _f32p), x.size, _ptr(out, _u8p)) != 0:
+            raise ValueError("orc_quantize_row_q8_K rejected the row")
+        blk = out.reshape(nb, self.Q8K_BYTES)
+        return (blk[:, 0:4].copy().view(np.float32).reshape(nb), blk[:, 4:260].copy().view(np.int8),
+                blk[:, 260:292].copy().view(np.int16))
+
+    def gemv_q8_K(self, t: int, W: np.ndarray, N: int, K: int, x: np.ndarray, grid=None) -> np.ndarray:
+        W = np.ascontiguousarray(W, dtype=np.uint8).reshape(-1)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(N, dtype=np.float32)
+        g = None if grid is None else np.ascontiguousarray(grid)
+        rc = self.lib.orc_gemv_q8_K(t, _ptr(W, _u8p), N, K, _ptr(x, _f32p), _ptr(y, _f32p),
+                                    None if g is None else g.ctypes.data)
+        if rc != 0:
+            raise ValueError(f"orc_gemv_q8_K rc={rc}")
         return y
 
     def fp16_to_f32(self, h: int) -> float:

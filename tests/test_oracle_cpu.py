@@ -749,3 +749,100 @@ def test_gemv_q4_0_q8_0_known_answer(oracle):
     for _ in range(K // 32):
         want = np.float32(want + per)
     assert np.array_equal(y, np.full(N, want, dtype=np.float32))
+
+
+# ---- ggml-cpu K-quant / IQ x Q8_K numerics (external restatement) -----------
+# The reference's live path for the 256-value types (src/xdna-gemv-engine.cpp:
+# 1382-1399, 1430-1453).  ggml itself is not in this build, so the f32 order
+# of ggml's generic code is restated, not compared ("parity unpinned" against
+# ggml); the quantizer, the integers and the sums are pinned here.
+
+KQ_ALL = (Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS, IQ3_S, IQ3_XXS, IQ2_S)
+
+
+def test_q8_K_quantization_invariants(oracle):
+    rng = np.random.default_rng(5)
+    nb = 48
+    x = (rng.standard_normal(256 * nb) * np.repeat(10.0 ** rng.uniform(-8, 8, nb), 256)).astype(np.float32)
+    x[256:512] = 0.0                                   # an all-zero block
+    x[1024 + 3], x[1024 + 9] = 7.0, -7.0               # a tie of |x|: the first wins
+    x[1024:1024 + 256][np.abs(x[1024:1280]) > 6.0] = 0.0
+    x[1024 + 3], x[1024 + 9] = 7.0, -7.0
+    d, qs, bs = oracle.quantize_q8_K(x)
+    xb = x.reshape(nb, 256).astype(np.float64)
+    q = qs.astype(np.int64)
+    assert np.array_equal(bs.astype(np.int64), q.reshape(nb, 16, 16).sum(axis=2))
+    for b in range(nb):
+        if not np.any(xb[b]):
+            assert d[b] == 0 and not np.any(q[b])
+            continue
+        j = int(np.argmax(np.abs(xb[b])))           # first index of the largest |x|
+        mx = np.float32(xb[b, j])
+        iscale = np.float32(-127.0) / mx
+        assert d[b] == np.float32(1.0) / iscale
+        assert q[b, j] == -127                         # the largest value maps to -127 * sign
+        assert np.all(np.abs(q[b]) <= 127)
+        # every value within half a step (plus f32 rounding of iscale * x)
+        assert np.all(np.abs(xb[b] - q[b] * np.float64(d[b])) <= 0.5 * abs(d[b]) * (1 + 1e-5))
+    assert q[4, 3] == -127 and q[4, 9] == 127          # the tie: +7 first, so d < 0
+
+
+def test_q8_K_known_answers(oracle):
+    # x = (127, 64, -32, 0.5, 0, ...): max 127, iscale -1, codes (-127, -64,
+    # 32, 0) (0.5 rounds to even), d = -1
+    x = np.zeros(256, np.float32)
+    x[:4] = [127.0, 64.0, -32.0, 0.5]
+    d, qs, bs = oracle.quantize_q8_K(x)
+    assert d[0] == -1.0 and list(qs[0, :4]) == [-127, -64, 32, 0] and not np.any(qs[0, 4:])
+    assert bs[0, 0] == -159 and not np.any(bs[0, 1:])
+    # a Q6_K superblock with d = 1, every scale 1 and every code 33 (+1):
+    # aux = (-127, -64, 32, 0, ...), lanes = d_w * d_x * aux = (127, 64, -32),
+    # summed in lane order: 159 (the f32 dot is 159.5: 0.5 quantized to 0)
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = 0x11                                   # low nibbles 1
+    blk[128:192] = 0xAA                                 # high 2-bit fields 2 -> code 33
+    blk[192:208] = 1
+    blk[208:210] = half(1.0)
+    assert np.array_equal(oracle.dequant_row(Q6_K, blk, 256), np.ones(256, np.float32))
+    assert oracle.gemv_q8_K(Q6_K, blk, 1, 256, x)[0] == np.float32(159.0)
+    # Q4_K with dmin: codes 1, scale 1, min 1 -> every weight 1*1 - 1*1 = 0:
+    # sumf -= dmin_w * d_x * sum(bsums * min) cancels the lanes exactly
+    b4 = np.zeros(144, np.uint8)
+    b4[0:2], b4[2:4] = half(1.0), half(1.0)
+    b4[4:12] = 1                                        # scales and mins of sub-blocks 0..3 = 1
+    b4[12:16] = 0x11                                    # sub-blocks 4..7: low nibbles 1
+    b4[16:] = 0x11
+    assert np.array_equal(oracle.dequant_row(Q4_K, b4, 256), np.zeros(256, np.float32))
+    assert oracle.gemv_q8_K(Q4_K, b4, 1, 256, x)[0] == 0.0
+
+
+@pytest.mark.parametrize("t", KQ_ALL, ids=[TYPE_NAMES[t] for t in KQ_ALL])
+def test_gemv_q8_K_against_f64_dot_on_dequantized_operands(oracle, t):
+    """The integer blocks and their scales form the same number as the f64
+    dot of the dequantized weights (the reference-pinned dequantizers) with
+    the dequantized Q8_K activation, up to f32 rounding of ggml's sums: a
+    wrong code, scale, sign, min or final factor fails."""
+    N, K = 64, 2048
+    grid = synthetic_grid(t, 3) if t in (IQ3_XXS, IQ2_S) else None
+    raw = synth.random_blocks(t, N, K, seed=11)
+    x = synth.activations(K, seed=12)
+    y = oracle.gemv_q8_K(t, raw, N, K, x, grid=grid)
+    d, qs, _ = oracle.quantize_q8_K(x)
+    xq = (qs.astype(np.float64) * d.astype(np.float64)[:, None]).reshape(-1)
+    rows = raw.reshape(N, -1)
+    for r in range(N):
+        w = oracle.dequant_row(t, rows[r], K, grid=grid).astype(np.float64)
+        want = float(np.dot(w, xq))
+        scale = float(np.dot(np.abs(w), np.abs(xq)))
+        assert abs(float(y[r]) - want) <= 2e-6 * scale + 1e-30, (TYPE_NAMES[t], r, float(y[r]), want)
+
+
+def test_gemv_q8_K_rows_independent_of_threads_and_shape(oracle):
+    # a row's result depends only on its bytes and x (OpenMP split, row count)
+    N, K = 37, 1024
+    raw = synth.random_blocks(Q5_K, N, K, seed=2)
+    x = synth.activations(K, seed=3)
+    y = oracle.gemv_q8_K(Q5_K, raw, N, K, x)
+    rb = raw.reshape(N, -1)
+    for r in (0, 17, 36):
+        assert oracle.gemv_q8_K(Q5_K, rb[r], 1, K, x)[0] == y[r]

@@ -818,16 +818,18 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 // gemv_q4_0_q8_kernel, bit for bit.  The activation row is staged as Q8_0
 // codes; a workgroup takes its rows of a job in chunks whose block
 // contributions fit kSrvCsFloats of LDS; within a chunk wavefront v computes
-// rows v, v+8, ... one at a time (lane = block, the next row's loads in
-// flight) and stores (float(sumi) * d_w) * d_x per block; then one thread per
-// row adds its row's contributions in block order (ggml's sequential sum).
-// Rows of a chunk sit B + 1 floats apart, so those threads read distinct
-// banks.
+// runs of R rows (the row form's R: 4 for one block column, 2 for two, 1
+// beyond) v*R, v*R + 8R, ... (lane = block, the next run's loads in flight)
+// and stores (float(sumi) * d_w) * d_x per block; then one thread per row adds
+// its row's contributions in block order (ggml's sequential sum).  Rows of a
+// chunk sit B + 1 floats apart, so those threads read distinct banks.
 constexpr int kSrvCsFloats = 8192;
 
 template <int NBL, bool TAIL>
 __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                             float *out, float *csb) {
+    constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
+    constexpr int ROWS = kSrvWaves * R;
     constexpr int XI = (4 * NBL + kSrvWaves - 1) / kSrvWaves;
     uint4 *Q = lds;
     float *dxs = reinterpret_cast<float *>(lds + 2 * B);
@@ -836,10 +838,10 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int64_t row_bytes = 18 * static_cast<int64_t>(B);
     const int stride = B + 1;
-    // rows per chunk: a multiple of the wavefront count, so a wavefront's
-    // rows continue v, v+8, ... from one chunk into the next (>= 8: B <= 512)
-    // and at most one per thread
-    const int chunk = min((kSrvCsFloats / stride) & ~(kSrvWaves - 1), 64 * kSrvWaves);
+    // rows per chunk: a multiple of ROWS, so a wavefront's runs continue from
+    // one chunk into the next, and at most one per thread (>= ROWS: B <= 64
+    // for R = 4, B <= 128 for R = 2, B <= 512 for R = 1)
+    const int chunk = min((kSrvCsFloats / stride) / ROWS * ROWS, 64 * kSrvWaves);
     int bc[NBL];
 #pragma unroll
     for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
@@ -850,22 +852,24 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     XTile<XI> xt;
     srv_load_x(xt, x, B);
     __builtin_amdgcn_sched_barrier(0);
-    using Grp = RowGroup<NBL, 1, true, TAIL>;
+    using Grp = RowGroup<NBL, R, true, TAIL>;
     Grp grp;
-    grp.load(c.jobs[0].W, lo0 + wave, hi0, B, row_bytes, lane);
+    grp.load(c.jobs[0].W, lo0 + wave * R, hi0, B, row_bytes, lane);
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dxs, sxs);
     __syncthreads();
 
     for (int j = 0; j < c.njobs; ++j) {
         const SrvJob &job = c.jobs[j];
         const int lo = static_cast<int>(job.N * g / G), hi = static_cast<int>(job.N * (g + 1) / G);
-        if (j > 0) grp.load(job.W, lo + wave, hi, B, row_bytes, lane);
+        if (j > 0) grp.load(job.W, lo + wave * R, hi, B, row_bytes, lane);
         for (int c0 = lo; c0 < hi; c0 += chunk) {
             const int c1 = min(hi, c0 + chunk);
-            for (int row = c0 + wave; row < c1; row += kSrvWaves) {
+            for (int row0 = c0 + wave * R; row0 < c1; row0 += ROWS) {
                 Grp nxt;
-                nxt.load(job.W, row + kSrvWaves, hi, B, row_bytes, lane);  // empty range past hi
-                q8_blocks<NBL, 1, true, TAIL>(grp, csb + (row - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
+                nxt.load(job.W, row0 + ROWS, hi, B, row_bytes, lane);  // empty range past hi
+                // rows past c1 (at most R - 1) land inside the chunk's
+                // buffer and are never summed
+                q8_blocks<NBL, R, true, TAIL>(grp, csb + (row0 - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
                                               tail_mask);
                 grp = nxt;
             }
