@@ -95,10 +95,13 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
  *       for the K/IQ types with int8 dot4 products),
- *     MI355X_VARIANT_GGML_Q8 (Q4_0 only: the arithmetic of ggml's CPU backend
- *       -- the activation row quantized to Q8_0 per 32-value block, integer
- *       block dot products scaled by d_w * d_x -- so that results follow
- *       ggml-cpu rather than the f32 references; other types return
+ *     MI355X_VARIANT_GGML_Q8 (the arithmetic of ggml's CPU backend, so that
+ *       results follow ggml-cpu rather than the f32 references: Q4_0 -- the
+ *       activation row quantized to Q8_0 per 32-value block, integer block
+ *       dot products scaled by d_w * d_x, blocks summed in order; the eight
+ *       256-value types -- the row quantized to Q8_K per superblock and
+ *       ggml's generic vec_dot_<type>_q8_K sums, rows of up to 16384 values;
+ *       BF16 activations for Q4_0 and longer K/IQ rows return
  *       MI355X_EUNSUPPORTED in this variant).
  *   MI355X_OPT_ROWS_PER_WAVE: 0 (auto) or 1, 2, 4 rows per wavefront step
  *     (rows and K-split forms); 4, 8 or 16 rows per step (stream form).

@@ -1233,11 +1233,508 @@ __global__ void bf16_to_f32_kernel(const uint16_t *__restrict__ in, float *__res
         out[i] = bf16_bits_to_float(in[i]);
 }
 
+
+// ---- ggml-cpu numerics: K/IQ weights x Q8_K activations ----------------------
+// MI355X_VARIANT_GGML_Q8 for the eight 256-value types: the reference's live
+// path whenever ggml-cpu is loaded is quantize_row_q8_K on the activation row
+// and ggml_vec_dot_<type>_q8_K per output row (src/xdna-gemv-engine.cpp:
+// 1382-1399, 1430-1453; ggml, llama.cpp 0ec4027a2).  This kernel computes
+// the arithmetic of ggml's generic C path bit for bit:
+//  * each workgroup quantizes the activation row to Q8_K in LDS (one wave per
+//    superblock: the first value of largest |x| gives iscale = -127 / max,
+//    q = min(127, round-half-even(iscale * x)), d = 1 / iscale, sums of 16);
+//  * a wavefront takes one row at a time, 8 lanes per superblock (one
+//    32-value slice each, the slices of the f32 kernel), and forms exact
+//    integer partials; for Q3_K..Q6_K a reduce-scatter across the 8 lanes
+//    leaves ggml's aux[l] (values p = l mod 8, times their scales) in lane l
+//    of the superblock;
+//  * the f32 terms of ggml's sums ((d_w * d_x) * aux[l], (dmin_w * d_x) *
+//    sum(bsums * mins), ((d_w * d_x) * (ls - 32)) * sumi, (d_w * d_x) *
+//    bsum) go to LDS, and after a batch of rows one lane per (row, chain)
+//    adds each chain in ggml's order, then the chains meet as ggml's do.
+// Rows of up to 64 superblocks (K <= 16384).
+constexpr int kQ8kMaxBlocks = 64;
+constexpr int kQ8kTermFloats = 1024;  // per wavefront: the terms of a batch of rows
+constexpr int kQ8kMaxBatch = 16;      // rows per batch
+// LDS bytes per staged superblock's codes: 256 + 16, so the 8 superblocks of
+// a step (lanes of one slice) read 8 different bank groups
+constexpr int kQ8kStride = 272;
+
+// integer max / min / sum across the wavefront (all lanes active)
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ float max_swap32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    const unsigned a = r[0], b = r[1];
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float max_swap16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    const unsigned a = r[0], b = r[1];
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+// maximum over the wavefront, in every lane: lane ^ 32, lane ^ 16 (permlane
+// swaps), then row mirror, half-row mirror and quad swaps
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = max_swap32(v);
+    v = max_swap16(v);
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x140>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x141>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x4E>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0xB1>(__builtin_bit_cast(int, v))));
+    return v;
+}
+
+__device__ __forceinline__ int wave_min_i(int v) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+        const unsigned a = r[0], b = r[1];
+        v = min(static_cast<int>(a), static_cast<int>(b));
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+        const unsigned a = r[0], b = r[1];
+        v = min(static_cast<int>(a), static_cast<int>(b));
+    }
+    v = min(v, dpp_i<0x140>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0xB1>(v));
+    return v;
+}
+
+// ggml's nearest_int: round half to even through + 1.5 * 2^23.  The ggml
+// numerics here use plain operators in functions compiled with contraction
+// off: hipcc contracts by default, and a product feeding this sum would
+// otherwise fuse into one FMA (one rounding instead of ggml's two).  HIP's
+// __fmul_rn / __fadd_rn do not prevent that: they are plain * and + defined
+// where contraction is on.
+__device__ __forceinline__ int nearest_int_rn(float f) {
+#pragma clang fp contract(off)
+    const float v = (f + 12582912.0f);
+    return (__builtin_bit_cast(int, v) & 0x007fffff) - 0x00400000;
+}
+
+// Superblocks [0, nb) of x into Q8_K in LDS: codes qs[kQ8kStride * sb + p],
+// bsums bs[16 * sb + j], scales dq[sb].  Wave w takes superblocks w, w + 8,
+// ...; lane l holds values 4l..4l+3.
+__device__ __forceinline__ void q8k_stage(const float *__restrict__ x, int nb, int8_t *qs, int16_t *bs, float *dq,
+                                          int wave, int lane) {
+#pragma clang fp contract(off)
+    for (int sb = wave; sb < nb; sb += kWaves) {
+        const float4 v4 = reinterpret_cast<const float4 *>(x + 256 * static_cast<int64_t>(sb))[lane];
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[e]));
+        const float amax = wave_max_f(m);
+        int first = 256;
+#pragma unroll
+        for (int e = 3; e >= 0; --e)
+            if (fabsf(v[e]) == amax) first = 4 * lane + e;
+        const int j = wave_min_i(first);
+        int q[4] = {0, 0, 0, 0};
+        float d = 0.0f;
+        if (amax != 0.0f && j < 256) {
+            // the value at j: element j % 4 (a uniform index) of lane j / 4
+            const float sel = v[j & 3];
+            const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sel), j >> 2));
+            const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = min(127, nearest_int_rn((iscale * v[e])));
+            d = __fdiv_rn(1.0f, iscale);
+        }
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed |= (static_cast<uint32_t>(q[e]) & 0xFFu) << (8 * e);
+        reinterpret_cast<uint32_t *>(qs + kQ8kStride * sb)[lane] = packed;
+        int s4 = q[0] + q[1] + q[2] + q[3];
+        s4 += dpp_i<0xB1>(s4);
+        s4 += dpp_i<0x4E>(s4);
+        if ((lane & 3) == 0) bs[16 * sb + (lane >> 2)] = static_cast<int16_t>(s4);
+        if (lane == 0) dq[sb] = d;
+    }
+}
+
+__device__ __forceinline__ int sext8(uint32_t w, int byte) { return static_cast<int>(w << (24 - 8 * byte)) >> 24; }
+
+// (scale, min) integers of sub-blocks 2c and 2c+1 of a Q4_K/Q5_K block from
+// its scale words (include/xdna/kquants.h:204-212 per sub-block)
+__device__ __forceinline__ void scale_min_pair_k4_i(int c, uint32_t w0, uint32_t w1, uint32_t w2, int &sc0, int &m0,
+                                                    int &sc1, int &m1) {
+    const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
+    const uint32_t a2 = (w0 >> sh) & 0xFFFFu, b2 = (w1 >> sh) & 0xFFFFu, c2 = (w2 >> sh) & 0xFFFFu;
+    const uint32_t sc = c < 2 ? (a2 & 0x3F3Fu) : ((c2 & 0x0F0Fu) | ((a2 >> 2) & 0x3030u));
+    const uint32_t mn = c < 2 ? (b2 & 0x3F3Fu) : (((c2 >> 4) & 0x0F0Fu) | ((b2 >> 2) & 0x3030u));
+    sc0 = static_cast<int>(sc & 0xFFu);
+    sc1 = static_cast<int>(sc >> 8);
+    m0 = static_cast<int>(mn & 0xFFu);
+    m1 = static_cast<int>(mn >> 8);
+}
+
+// sum over sub-blocks j of bsums[j] * min[j / 2] of a Q4_K/Q5_K superblock
+__device__ __forceinline__ int k4_min_sum(const u32x4 &hd, const int16_t *bs) {
+    int s = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        int sc0, m0, sc1, m1;
+        scale_min_pair_k4_i(c, hd[1], hd[2], hd[3], sc0, m0, sc1, m1);
+        s += (bs[4 * c] + bs[4 * c + 1]) * m0 + (bs[4 * c + 2] + bs[4 * c + 3]) * m1;
+    }
+    return s;
+}
+
+// Lane partials of aux[0..7] for Q4_K / Q5_K slice s = (c, h): code byte i of
+// the slice holds value 64c + 16h + i (low nibble, sub-block 2c) and 64c + 32
+// + 16h + i (high nibble, 2c + 1); both sit at l = i mod 8.
+template <bool Q5>
+__device__ __forceinline__ void k45_partial(const u32x4 &q, const u32x4 &qh, const u32x4 &hd, int s,
+                                            const int8_t *q8, int (&part)[8]) {
+    const int c = s >> 1, h = s & 1;
+    int sc0, m0, sc1, m1;
+    scale_min_pair_k4_i(c, hd[1], hd[2], hd[3], sc0, m0, sc1, m1);
+    const uint32_t *qa = reinterpret_cast<const uint32_t *>(q8 + 64 * c + 16 * h);
+    const uint32_t *qb = reinterpret_cast<const uint32_t *>(q8 + 64 * c + 32 + 16 * h);
+    int lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t A = qa[w], Bv = qb[w];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * w + e;
+            int cl = static_cast<int>((q[w] >> (8 * e)) & 15u);
+            int ch = static_cast<int>((q[w] >> (8 * e + 4)) & 15u);
+            if constexpr (Q5) {
+                cl += static_cast<int>((qh[w] >> (8 * e + 2 * c)) & 1u) << 4;
+                ch += static_cast<int>((qh[w] >> (8 * e + 2 * c + 1)) & 1u) << 4;
+            }
+            lo[i & 7] += cl * sext8(A, e);
+            hi[i & 7] += ch * sext8(Bv, e);
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < 8; ++l) part[l] = sc0 * lo[l] + sc1 * hi[l];
+}
+
+// Lane partials of aux[0..7] for Q6_K / Q3_K slice s = (hh, k): value
+// 128hh + 32j + 8k + t (j = 0..3, t = 0..7) sits at l = t, scale group
+// 8hh + 2j + k/2.
+__device__ __forceinline__ void k6_partial(const Kq<MI355X_TYPE_Q6_K>::Regs &g, int s, const int8_t *q8,
+                                           int (&part)[8]) {
+    const int hh = s >> 2, k = s & 3;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) part[t] = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int sc = sext8(g.sw[j >> 1], 2 * (j & 1) + (k >> 1));
+        const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 128 * hh + 32 * j + 8 * k);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t A = g.qa[w], Bq = g.qb[w], H = g.qh[w], Q = qv[w];
+            uint32_t code;
+            if (j == 0) code = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+            else if (j == 1) code = (Bq & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+            else if (j == 2) code = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+            else code = ((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                part[4 * w + e] += sc * ((static_cast<int>((code >> (8 * e)) & 0xFFu) - 32) * sext8(Q, e));
+        }
+    }
+}
+
+__device__ __forceinline__ void k3_partial(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const int8_t *q8,
+                                           int (&part)[8]) {
+    const int hh = s >> 2, k = s & 3, kk = k >> 1;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) part[t] = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int lo_byte = 2 * j + kk;
+        const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
+        const int lo = static_cast<int>((byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u);
+        const int hi = static_cast<int>((byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u);
+        const int sc = (lo | (hi << 4)) - 32;
+        const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 128 * hh + 32 * j + 8 * k);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t code =
+                ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
+            const uint32_t Q = qv[w];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                part[4 * w + e] += sc * ((static_cast<int>((code >> (8 * e)) & 0xFFu) - 4) * sext8(Q, e));
+        }
+    }
+}
+
+// Integer sums of one 32-value slice of the IQ types: IQ4_XS the codebook dot
+// (its scale enters in f32), the grid types sumi times their integer scales.
+__device__ __forceinline__ int iq4xs_sumi(const Kq<MI355X_TYPE_IQ4_XS>::Regs &g, int s, const int8_t *q8) {
+    const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 32 * s);
+    int sumi = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        sumi = sdot4(KqDg<MI355X_TYPE_IQ4_XS>::lookup(g.q[w] & 0x0F0F0F0Fu), qv[w], sumi);
+        sumi = sdot4(KqDg<MI355X_TYPE_IQ4_XS>::lookup((g.q[w] >> 4) & 0x0F0F0F0Fu), qv[4 + w], sumi);
+    }
+    return sumi;
+}
+
+__device__ __forceinline__ int iq3s_bsum(const Kq<MI355X_TYPE_IQ3_S>::Regs &g, int s, const int8_t *q8,
+                                         const uint32_t *grid) {
+    const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 32 * s);
+    int sumi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t idx = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
+        sumi = sdot4(apply_signs(grid[idx], sign_mask4(g.sg >> (4 * k))), qv[k], sumi);
+    }
+    return sumi * (1 + 2 * static_cast<int>((g.scb >> (4 * (s & 1))) & 15u));
+}
+
+__device__ __forceinline__ int iq3xxs_bsum(const Kq<MI355X_TYPE_IQ3_XXS>::Regs &g, int s, const int8_t *q8,
+                                           const uint32_t *grid) {
+    const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 32 * s);
+    int sumi = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t sg = ksigns((g.aux >> (7 * l)) & 127u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t gv = grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + h)];
+            sumi = sdot4(apply_signs(gv, sign_mask4(sg >> (4 * h))), qv[2 * l + h], sumi);
+        }
+    }
+    return sumi * (1 + 2 * static_cast<int>(g.aux >> 28));
+}
+
+__device__ __forceinline__ int iq2s_bsum(const Kq<MI355X_TYPE_IQ2_S>::Regs &g, int s, const int8_t *q8,
+                                         const uint32_t *grid) {
+    const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 32 * s);
+    int s1 = 0, s2 = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
+        const uint32_t sb8 = byte_u(g.sg, l);
+        int t = sdot4(apply_signs(grid[2 * idx], sign_mask4(sb8)), qv[2 * l], 0);
+        t = sdot4(apply_signs(grid[2 * idx + 1], sign_mask4(sb8 >> 4)), qv[2 * l + 1], t);
+        if (l < 2) s1 += t;
+        else s2 += t;
+    }
+    return (1 + 2 * static_cast<int>(g.scb & 15u)) * s1 + (1 + 2 * static_cast<int>(g.scb >> 4)) * s2;
+}
+
+// Reduce-scatter of 8 per-lane partials across the 8 slice lanes of a
+// superblock (lanes bl + 8 s): lane (s, bl) ends with the total of partial s.
+// Partners: lane ^ 32 (permlane32 swap), lane ^ 16 (permlane16 swap),
+// lane ^ 8 (DPP row rotate by 8).
+__device__ __forceinline__ int fold32_i(int a, int b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(a), static_cast<unsigned>(b), false, false);
+    const unsigned lo = r[0], hi = r[1];
+    return static_cast<int>(lo) + static_cast<int>(hi);
+}
+__device__ __forceinline__ int fold16_i(int a, int b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(a), static_cast<unsigned>(b), false, false);
+    const unsigned lo = r[0], hi = r[1];
+    return static_cast<int>(lo) + static_cast<int>(hi);
+}
+__device__ __forceinline__ int scatter8(const int (&p)[8], int lane) {
+    int v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v4[i] = fold32_i(p[i], p[i + 4]);   // lanes s < 4: l 0..3; s >= 4: 4..7
+    int v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v2[i] = fold16_i(v4[i], v4[i + 2]); // then by s & 2
+    const bool odd = (lane & 8) != 0;                                // s & 1
+    const int own = odd ? v2[1] : v2[0];
+    const int other = odd ? v2[0] : v2[1];
+    return own + dpp_i<0x128>(other);  // row_ror:8 = lane ^ 8 within a 16-lane row
+}
+// full integer sum over the 8 slice lanes
+__device__ __forceinline__ int sum8(int v) {
+    v = fold32_i(v, v);
+    v = fold16_i(v, v);
+    return v + dpp_i<0x128>(v);
+}
+
+template <int TYPE, int NIT>
+__global__ __launch_bounds__(kThreads) void gemv_kq_q8k_kernel(KqArgs a, int rb) {
+#pragma clang fp contract(off)
+    using K = Kq<TYPE>;
+    constexpr bool EIGHT = TYPE == MI355X_TYPE_Q3_K || TYPE == MI355X_TYPE_Q4_K || TYPE == MI355X_TYPE_Q5_K ||
+                           TYPE == MI355X_TYPE_Q6_K;
+    constexpr bool MINS = TYPE == MI355X_TYPE_Q4_K || TYPE == MI355X_TYPE_Q5_K;
+    constexpr bool IQ4 = TYPE == MI355X_TYPE_IQ4_XS;
+    extern __shared__ float4 lds_q8k[];
+    const int S = a.nb;  // superblocks per row (the whole row: b0 == 0)
+    int8_t *qs = reinterpret_cast<int8_t *>(lds_q8k);
+    int16_t *bs = reinterpret_cast<int16_t *>(qs + kQ8kStride * S);
+    float *dq = reinterpret_cast<float *>(bs + 16 * S);
+    float *terms = dq + S;  // kWaves x kQ8kTermFloats
+    uint32_t *grid = reinterpret_cast<uint32_t *>(terms + kWaves * kQ8kTermFloats);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int s = lane / kBlocksPerStep;
+    const int bl = lane % kBlocksPerStep;
+    float *tw = terms + wave * kQ8kTermFloats;
+    // terms per row: chains of S (8 lanes [+ mins]) or 8S (IQ4_XS) or S
+    const int per_row = EIGHT ? (MINS ? 9 : 8) * S : (IQ4 ? 8 * S : S);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+    int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+
+    // first row's weights in flight while the activations are quantized
+    typename K::Regs regs[1][NIT];
+    load_group<TYPE, 1, NIT>(a, row < a.N ? row : a.N - 1, s, bl, regs);
+    __builtin_amdgcn_sched_barrier(0);
+    q8k_stage(a.x, S, qs, bs, dq, wave, lane);
+    if constexpr (K::kGrid > 0) {
+        const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
+        for (int i = threadIdx.x; i < K::kGrid; i += kThreads) grid[i] = src[i];
+    }
+    __syncthreads();
+
+    while (row < a.N) {
+        // a batch of up to rb rows of this wavefront; their terms in tw
+        const int64_t first = row;  // batch rows first + r * stride
+        int nrow = 0;
+        for (; nrow < rb && row < a.N; ++nrow, row += stride) {
+            float *tr = tw + nrow * per_row;
+#pragma unroll
+            for (int t = 0; t < NIT; ++t) {
+                const int i = kBlocksPerStep * t + bl;  // superblock
+                const bool valid = i < S;
+                const int ic = valid ? i : S - 1;
+                const int8_t *q8 = qs + kQ8kStride * ic;
+                const float dx = dq[ic];
+                const auto &g = regs[0][t];
+                if constexpr (EIGHT) {
+                    int part[8];
+                    float dw;
+                    if constexpr (TYPE == MI355X_TYPE_Q4_K || TYPE == MI355X_TYPE_Q5_K) {
+                        u32x4 qh{0u, 0u, 0u, 0u};
+                        if constexpr (TYPE == MI355X_TYPE_Q5_K) qh = g.qh;
+                        k45_partial<TYPE == MI355X_TYPE_Q5_K>(g.q, qh, g.hd, s, q8, part);
+                        dw = half_f(g.hd[0] & 0xFFFF);
+                    } else if constexpr (TYPE == MI355X_TYPE_Q6_K) {
+                        k6_partial(g, s, q8, part);
+                        dw = half_f(g.d);
+                    } else {
+                        k3_partial(g, s, q8, part);
+                        dw = half_f(g.d);
+                    }
+                    const int aux = scatter8(part, lane);  // aux[s] of superblock i
+                    if (valid) tr[s * S + i] = ((dw * dx) * static_cast<float>(aux));
+                    if constexpr (MINS) {
+                        if (valid && s == 0) {
+                            const int msum = k4_min_sum(g.hd, bs + 16 * ic);
+                            const float dmin = (half_f(g.hd[0] >> 16) * dx);
+                            tr[8 * S + i] = (dmin * static_cast<float>(msum));
+                        }
+                    }
+                } else if constexpr (IQ4) {
+                    const int sumi = iq4xs_sumi(g, s, q8);
+                    const uint32_t sh = g.hd[0] >> 16;
+                    const int ls = static_cast<int>(((g.hd[1] >> (4 * s)) & 15u) | (((sh >> (2 * s)) & 3u) << 4));
+                    const float d4d8 = (half_f(g.hd[0] & 0xFFFF) * dx);
+                    const float dl = (d4d8 * static_cast<float>(ls - 32));
+                    if (valid) tr[8 * i + s] = (dl * static_cast<float>(sumi));
+                } else {
+                    int part;
+                    if constexpr (TYPE == MI355X_TYPE_IQ3_S) part = iq3s_bsum(g, s, q8, grid);
+                    else if constexpr (TYPE == MI355X_TYPE_IQ3_XXS) part = iq3xxs_bsum(g, s, q8, grid);
+                    else part = iq2s_bsum(g, s, q8, grid);
+                    const int bsum = sum8(part);
+                    const float d = (half_f(g.d) * dx);
+                    if (valid && s == 0) tr[i] = (d * static_cast<float>(bsum));
+                }
+            }
+            // the next row's loads before this row's terms are summed
+            load_group<TYPE, 1, NIT>(a, row + stride < a.N ? row + stride : a.N - 1, s, bl, regs);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // chains: one lane per (row, chain), terms in ggml's order
+        if constexpr (EIGHT) {
+            constexpr int C = MINS ? 9 : 8;
+            for (int task = lane; task < nrow * C; task += 64) {
+                const int r = task / C, c = task % C;
+                const float *src = tw + r * per_row + c * S;
+                float acc = 0.0f;
+                if (c < 8) {
+                    for (int i = 0; i < S; ++i) acc = (acc + src[i]);
+                } else {
+                    for (int i = 0; i < S; ++i) acc = (acc - src[i]);
+                }
+                tw[r * per_row + c * S] = acc;  // the chain's first term is no longer needed
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane < nrow) {
+                const float *cr = tw + lane * per_row;
+                float sumf = MINS ? cr[8 * S] : 0.0f;
+#pragma unroll
+                for (int l = 0; l < 8; ++l) sumf = (sumf + cr[l * S]);
+                a.y[first + lane * stride] = sumf;
+            }
+        } else {
+            if (lane < nrow) {
+                const float *src = tw + lane * per_row;
+                float sumf = 0.0f;
+                for (int i = 0; i < per_row; ++i) sumf = (sumf + src[i]);
+                if constexpr (TYPE == MI355X_TYPE_IQ3_XXS) sumf = (0.25f * sumf);
+                if constexpr (TYPE == MI355X_TYPE_IQ2_S) sumf = (0.125f * sumf);
+                a.y[first + lane * stride] = sumf;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+typedef void (*kq_q8k_fn)(KqArgs, int);
+
+template <int TYPE>
+kq_q8k_fn pick_q8k_type(int nit) {
+    switch (nit) {
+    case 1: return gemv_kq_q8k_kernel<TYPE, 1>;
+    case 2: return gemv_kq_q8k_kernel<TYPE, 2>;
+    case 3: return gemv_kq_q8k_kernel<TYPE, 3>;
+    case 4: return gemv_kq_q8k_kernel<TYPE, 4>;
+    case 5: return gemv_kq_q8k_kernel<TYPE, 5>;
+    case 6: return gemv_kq_q8k_kernel<TYPE, 6>;
+    case 7: return gemv_kq_q8k_kernel<TYPE, 7>;
+    default: return gemv_kq_q8k_kernel<TYPE, 8>;
+    }
+}
+
+kq_q8k_fn pick_q8k_kernel(int type, int nit) {
+    switch (type) {
+    case MI355X_TYPE_Q4_K: return pick_q8k_type<MI355X_TYPE_Q4_K>(nit);
+    case MI355X_TYPE_Q5_K: return pick_q8k_type<MI355X_TYPE_Q5_K>(nit);
+    case MI355X_TYPE_Q3_K: return pick_q8k_type<MI355X_TYPE_Q3_K>(nit);
+    case MI355X_TYPE_Q6_K: return pick_q8k_type<MI355X_TYPE_Q6_K>(nit);
+    case MI355X_TYPE_IQ4_XS: return pick_q8k_type<MI355X_TYPE_IQ4_XS>(nit);
+    case MI355X_TYPE_IQ3_S: return pick_q8k_type<MI355X_TYPE_IQ3_S>(nit);
+    case MI355X_TYPE_IQ3_XXS: return pick_q8k_type<MI355X_TYPE_IQ3_XXS>(nit);
+    case MI355X_TYPE_IQ2_S: return pick_q8k_type<MI355X_TYPE_IQ2_S>(nit);
+    default: return nullptr;
+    }
+}
+
 }  // namespace
 
 int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
-    if (ctx->kernel_variant == MI355X_VARIANT_GGML_Q8)
-        return set_error(MI355X_EUNSUPPORTED, "the ggml-cpu numerics variant covers Q4_0 weights only");
     const KqLayout L = kq_layout(a.type);
     if (L.block_bytes == 0) return set_error(MI355X_EUNSUPPORTED, "unsupported weight type for the K/IQ kernels");
     const int64_t B = a.K / 256;
@@ -1278,6 +1775,32 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
             MI355X_HIP(hipMemcpyAsync(dst, a.x, need, hipMemcpyDeviceToDevice, ctx->stream));
         }
         x = dst;
+    }
+
+    // ggml-cpu numerics: the whole row in one launch (ggml's sums run over
+    // every superblock in order)
+    if (ctx->kernel_variant == MI355X_VARIANT_GGML_Q8) {
+        if (B > kQ8kMaxBlocks)
+            return set_error(MI355X_EUNSUPPORTED,
+                             "the ggml-cpu numerics variant takes K/IQ rows of up to 16384 values");
+        const bool eight = a.type == MI355X_TYPE_Q3_K || a.type == MI355X_TYPE_Q4_K || a.type == MI355X_TYPE_Q5_K ||
+                           a.type == MI355X_TYPE_Q6_K;
+        const bool mins = a.type == MI355X_TYPE_Q4_K || a.type == MI355X_TYPE_Q5_K;
+        const int64_t per_row = eight ? (mins ? 9 : 8) * B : (a.type == MI355X_TYPE_IQ4_XS ? 8 * B : B);
+        const int rb = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kQ8kMaxBatch, kQ8kTermFloats / per_row)));
+        const int nit = static_cast<int>((B + kBlocksPerStep - 1) / kBlocksPerStep);
+        const kq_q8k_fn k = pick_q8k_kernel(a.type, nit);
+        const size_t lds = static_cast<size_t>(B) * (kQ8kStride + 32 + 4) +
+                           static_cast<size_t>(kWaves) * kQ8kTermFloats * sizeof(float) + grid_words(a.type) * 4u;
+        if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation row exceeds LDS");
+        const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
+        int64_t wgs = std::min<int64_t>((a.N + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
+        if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);
+        KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), 0, static_cast<int>(B), x, a.y, 0, grid};
+        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(wgs, 1))), dim3(kThreads), lds,
+                           ctx->stream, args, rb);
+        MI355X_HIP(hipGetLastError());
+        return MI355X_OK;
     }
 
     // f32 activations unless the caller asks for the digit path: with the

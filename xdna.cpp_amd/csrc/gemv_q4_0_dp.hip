@@ -600,6 +600,7 @@ __global__ __launch_bounds__(64 * 8) void gemv_q4_0_mb_kernel(const uint8_t *__r
 //   wavefront: the same products as ggml's generic path, re-associated.
 template <int XI>
 __device__ __forceinline__ void q8_stage(const XTile<XI> &xt, int B, uint32_t *Q, float *dx, int *sx) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int it = 0; it < XI; ++it) {
         const int i = threadIdx.x + it * blockDim.x;
@@ -618,8 +619,8 @@ __device__ __forceinline__ void q8_stage(const XTile<XI> &xt, int B, uint32_t *Q
         int sum = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int ql = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e], id)));
-            const int qh = static_cast<int>(roundf(__fmul_rn(xt.v[it][2 * e + 1], id)));
+            const int ql = static_cast<int>(roundf((xt.v[it][2 * e] * id)));
+            const int qh = static_cast<int>(roundf((xt.v[it][2 * e + 1] * id)));
             lo |= (static_cast<uint32_t>(ql) & 0xFFu) << (8 * e);
             hi |= (static_cast<uint32_t>(qh) & 0xFFu) << (8 * e);
             sum += ql + qh;
@@ -643,6 +644,7 @@ template <int NBL, int R, bool A16, bool TAIL>
 __device__ __forceinline__ void q8_blocks(const RowGroup<NBL, R, A16, TAIL> &g, float *cs, int cs_stride,
                                           const uint4 *Q, const float *dx, const int *sx, int B, int lane,
                                           const int bc[NBL], uint32_t tail_mask) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < NBL; ++j) {
         if (j > 0) __builtin_amdgcn_sched_barrier(0);
@@ -665,7 +667,7 @@ __device__ __forceinline__ void q8_blocks(const RowGroup<NBL, R, A16, TAIL> &g, 
             const int sumi = dot - 8 * s8;
             const float dw = half_bits_to_float(static_cast<uint16_t>(g.d_bits(r, j, tail_mask)));
             if (lane + 64 * j < B)
-                cs[r * cs_stride + lane + 64 * j] = __fmul_rn(__fmul_rn(static_cast<float>(sumi), dw), d_x);
+                cs[r * cs_stride + lane + 64 * j] = (static_cast<float>(sumi) * dw) * d_x;
         }
     }
 }
@@ -828,6 +830,7 @@ constexpr int kSrvCsFloats = 8192;
 template <int NBL, bool TAIL>
 __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                             float *out, float *csb) {
+#pragma clang fp contract(off)
     constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
     constexpr int ROWS = kSrvWaves * R;
     constexpr int XI = (4 * NBL + kSrvWaves - 1) / kSrvWaves;
@@ -879,7 +882,7 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
                 const float *cr = csb + t * stride;
                 float sumf = 0.0f;
 #pragma unroll 8
-                for (int b = 0; b < B; ++b) sumf = __fadd_rn(sumf, cr[b]);
+                for (int b = 0; b < B; ++b) sumf = (sumf + cr[b]);
                 out[c0 - lo + t] = sumf;
             }
             __syncthreads();  // csb is rewritten by the next chunk
@@ -1346,6 +1349,7 @@ template <int NBL, int R, bool A16, bool TAIL>
 __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
                                                            float *__restrict__ y, int N, int B, int64_t row_bytes,
                                                            int x_al16) {
+#pragma clang fp contract(off)
     constexpr int WAVES = 8;
     extern __shared__ uint4 lds_q8[];
     uint4 *Q = lds_q8;
@@ -1382,7 +1386,7 @@ __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__rest
         __syncthreads();
         if (lane < R) {
             float sumf = 0.0f;
-            for (int b = 0; b < B; ++b) sumf = __fadd_rn(sumf, cs[lane * B + b]);
+            for (int b = 0; b < B; ++b) sumf = (sumf + cs[lane * B + b]);
             if (row0 + lane < N) y[row0 + lane] = sumf;
         }
         __syncthreads();
