@@ -432,3 +432,112 @@ def test_four_backends_share_resident_weights(plugin, oracle):
             be.free()
         buf.free()
     assert not errors, errors[:3]
+
+
+# ---- K-quant / IQ weights through the plugin --------------------------------
+# The reference claims and dispatches all eight 256-value types through the
+# same process_mul_mat_node (src/ggml-xdna.cpp:185-254;
+# tests/test-kquants-gemv.cpp:351-414).  Rows of an odd number of superblocks
+# of the 2-mod-4 block sizes (Q3_K, Q6_K, IQ3_S, IQ3_XXS, IQ2_S) start 2 mod 4
+# on odd rows, where the resident layout moves the fp16 plane to the front.
+
+KQ = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_XS": 23, "IQ3_S": 21, "IQ3_XXS": 18, "IQ2_S": 22}
+
+
+def iq_grid(t):
+    # the synthetic grids the other K/IQ GPU tests install (process-wide)
+    rng = np.random.default_rng(t)
+    n, w = (256, 4) if t == 18 else (1024, 8)
+    g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
+    return g.view(np.uint32 if w == 4 else np.uint64).reshape(n)
+
+
+def kq_weight(buf, t, raw, N, K, name=b"wk"):
+    bb = mi355x.BLOCK_BYTES[t]
+    rb = mi355x.row_bytes(t, K)
+    w = gh.tensor(t, [K, N], [bb, rb, rb * N, rb * N], name)
+    buf.place(w, N * rb)
+    return w
+
+
+@pytest.mark.parametrize("name", list(KQ))
+def test_kq_weights_set_get_compute_and_views(plugin, oracle, name):
+    t = KQ[name]
+    grid = iq_grid(t) if t in (18, 22) else None
+    if grid is not None:
+        mi355x.set_iq_grid(t, grid)
+    N, K, r0 = 64, 256 * 3, 9  # odd superblock count; a view from an odd row
+    rb = mi355x.row_bytes(t, K)
+    raw = synth.random_blocks(t, N, K, seed=t)
+    new_rows = synth.random_blocks(t, N - r0, K, seed=t + 100)
+    x = synth.activations(K, seed=t + 1)
+    buf = plugin.buft.alloc(N * rb + 8 * K + 8 * N + 8 * 256)
+    try:
+        w = kq_weight(buf, t, raw, N, K)
+        # ragged byte-range uploads, then whole and partial read-backs
+        rng = np.random.default_rng(t)
+        off = 0
+        while off < raw.nbytes:
+            n = int(rng.integers(1, 300))
+            buf.set(w, raw.tobytes()[off:off + n], off)
+            off += n
+        assert buf.get(w, raw.nbytes) == raw.tobytes()
+        for _ in range(6):
+            o = int(rng.integers(0, raw.nbytes))
+            n = int(rng.integers(1, raw.nbytes - o + 1))
+            assert buf.get(w, n, o) == raw.tobytes()[o:o + n], (o, n)
+        assert plugin.dev.supports_op(gh.mul_mat(w, f32_tensor(buf, None, [K, 1], b"probe"), [N, 1]))
+        xt = f32_tensor(buf, x, [K, 1])
+        d = gh.mul_mat(w, xt, [N, 1])
+        buf.place(d, 4 * N)
+        assert plugin.backend.compute([d]) == gh.STATUS_SUCCESS
+        plugin.backend.call("synchronize")
+        y = read_f32(buf, d, N)
+        check_gemv(y, oracle.gemv(t, raw, N, K, x, grid=grid), oracle.row_norms(t, raw, N, K, grid=grid), x,
+                   f"{name} plugin")
+        # a row view from odd row r0: set_tensor through the view lands in
+        # the right resident rows, get_tensor through it reads them back, and
+        # the view computes
+        v = gh.tensor(t, [K, N - r0], [mi355x.BLOCK_BYTES[t], rb, rb * (N - r0), rb * (N - r0)])
+        v.buffer, v.view_src, v.view_offs = w.buffer, C.addressof(w), r0 * rb
+        v.data = w.data + r0 * rb
+        buf.set(v, new_rows)
+        want = raw.copy().reshape(N, -1)
+        want[r0:] = new_rows.reshape(N - r0, -1)
+        assert buf.get(w, raw.nbytes) == want.tobytes()
+        assert buf.get(v, 77, 13) == new_rows.tobytes()[13:90]
+        dv = gh.mul_mat(v, xt, [N - r0, 1])
+        buf.place(dv, 4 * (N - r0))
+        assert plugin.backend.compute([dv]) == gh.STATUS_SUCCESS
+        plugin.backend.call("synchronize")
+        yv = read_f32(buf, dv, N - r0)
+        check_gemv(yv, oracle.gemv(t, new_rows, N - r0, K, x, grid=grid),
+                   oracle.row_norms(t, new_rows, N - r0, K, grid=grid), x, f"{name} view")
+    finally:
+        buf.free()
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "IQ4_XS"])
+def test_kq_batched_rows_through_plugin(plugin, oracle, name):
+    """M = 3 activation rows against K/IQ weights in this buffer (M sequential
+    GEMVs, as the reference's loop)."""
+    t = KQ[name]
+    N, K, M = 128, 1024, 3
+    rb = mi355x.row_bytes(t, K)
+    raw = synth.random_blocks(t, N, K, seed=5)
+    xs = np.stack([synth.activations(K, seed=60 + m) for m in range(M)])
+    buf = plugin.buft.alloc(N * rb + 4 * K * M + 4 * N * M + 4 * 256)
+    try:
+        w = kq_weight(buf, t, raw, N, K)
+        buf.set(w, raw)
+        xt = f32_tensor(buf, xs, [K, M])
+        d = gh.mul_mat(w, xt, [N, M])
+        buf.place(d, 4 * N * M)
+        assert plugin.backend.compute([d]) == gh.STATUS_SUCCESS
+        plugin.backend.call("synchronize")
+        y = read_f32(buf, d, N * M).reshape(M, N)
+        norms = oracle.row_norms(t, raw, N, K)
+        for m in range(M):
+            check_gemv(y[m], oracle.gemv(t, raw, N, K, xs[m]), norms, xs[m], f"{name} row {m}")
+    finally:
+        buf.free()
