@@ -163,7 +163,9 @@ MI355X_API int64_t mi355x_row_bytes(int type, int64_t K);
 MI355X_API int mi355x_type_ready(int type);
 /* Installs the IQ3_XXS (uint32[256]) or IQ2_S (uint64[1024]) grid for every
  * context created afterwards and every existing one.  `bytes` must equal the
- * table size.  Table contents are ggml's; this library does not ship them. */
+ * table size and every byte a magnitude in 1..127 (as in ggml's grids),
+ * else MI355X_EINVAL.  Table contents are ggml's; this library does not ship
+ * them. */
 MI355X_API int mi355x_set_iq_grid(int type, const void *table, size_t bytes);
 
 /* ---- prepack: ggml raw bytes <-> resident layout ----------------------------

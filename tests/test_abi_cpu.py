@@ -48,6 +48,12 @@ def test_type_ready_and_grid_validation():
     assert lib.mi355x_set_iq_grid(mi355x.IQ3_XXS, bad.ctypes.data, bad.nbytes) == mi355x.EINVAL
     assert "1024 bytes" in mi355x.last_error()
     assert lib.mi355x_set_iq_grid(mi355x.Q4_0, bad.ctypes.data, bad.nbytes) == mi355x.EINVAL
+    # magnitudes outside 1..127 (the kernels negate bytes carry-free)
+    for bad_byte in (0, 128, 255):
+        g = np.full(1024, 43, dtype=np.uint8)
+        g[517] = bad_byte
+        assert lib.mi355x_set_iq_grid(mi355x.IQ3_XXS, g.ctypes.data, g.nbytes) == mi355x.EINVAL
+        assert "1..127" in mi355x.last_error()
 
 
 def test_device_count_does_not_crash_without_gpu():

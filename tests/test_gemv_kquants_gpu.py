@@ -171,24 +171,48 @@ def test_grid_types_refuse_without_grid_or_bad_table(ctx):
         mi355x.set_iq_grid(18, bad)
 
 
+@pytest.mark.parametrize("form", ["pipelined", "ksplit"])
 @pytest.mark.parametrize("name", list(ALL))
 @pytest.mark.parametrize("N,K", [(1, 256), (5, 2048), (1023, 4096), (4096, 8192), (14336, 4096), (300, 14336),
-                                 (2000, 16384), (777, 11008)])
-def test_pipelined_matches_digit_kernel(ctx, name, variant, N, K):
-    """The pipelined form shares the digit kernel's per-row arithmetic (same
-    slices, step order and expressions), so the two agree bit for bit: every
-    step count 1..8 (registers or LDS for the slices), rows that leave the
-    last wavefronts partly or wholly empty, K beyond one LDS chunk (16384)."""
+                                 (2000, 16384), (777, 11008), (4096, 14336), (8192, 8192)])
+def test_form_matches_digit_kernel(ctx, name, variant, form, N, K):
+    """The pipelined and activation-stationary (K-split) forms share the digit
+    row kernel's per-row arithmetic (same slices, step order and
+    expressions), so they agree with it bit for bit: every step count 1..8,
+    rows that leave the last wavefronts or tiles partly or wholly empty, K
+    beyond one LDS chunk (16384), the BASELINE shapes."""
     if variant != "digits":
         pytest.skip("one run per shape is enough")
     t = ALL[name]
     raw = blocks(t, N, K, N + K)
     x = np.random.default_rng(K).uniform(-0.5, 0.5, K).astype(np.float32)
-    y_dg = run(ctx, t, raw, N, K, x)
-    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE)
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_ROWS)
     try:
-        y_pl = run(ctx, t, raw, N, K, x)
+        y_dg = run(ctx, t, raw, N, K, x)
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE if form == "pipelined" else mi355x.FORM_KSPLIT)
+        y_f = run(ctx, t, raw, N, K, x)
     finally:
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
-    bad = np.nonzero(y_pl.view(np.uint32) != y_dg.view(np.uint32))[0]
-    assert bad.size == 0, f"{name} {N}x{K}: {bad.size} rows differ, first {bad[:5]} {y_pl[bad[:3]]} {y_dg[bad[:3]]}"
+    bad = np.nonzero(y_f.view(np.uint32) != y_dg.view(np.uint32))[0]
+    assert bad.size == 0, f"{name} {N}x{K}: {bad.size} rows differ, first {bad[:5]} {y_f[bad[:3]]} {y_dg[bad[:3]]}"
+
+
+@pytest.mark.parametrize("name", ["Q5_K", "IQ2_S"])
+def test_ksplit_tile_rows_option(ctx, variant, name):
+    """2 and 4 rows per group and tile (OPT_ROWS_PER_WAVE) give the same bits."""
+    if variant != "digits":
+        pytest.skip("one run per case is enough")
+    t = ALL[name]
+    N, K = 999, 6144
+    raw = blocks(t, N, K, 11)
+    x = np.random.default_rng(3).uniform(-0.5, 0.5, K).astype(np.float32)
+    ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_KSPLIT)
+    try:
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 4)
+        y4 = run(ctx, t, raw, N, K, x)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 2)
+        yr = run(ctx, t, raw, N, K, x)
+    finally:
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
+        ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+    assert np.array_equal(y4.view(np.uint32), yr.view(np.uint32))

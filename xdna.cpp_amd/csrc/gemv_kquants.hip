@@ -71,6 +71,12 @@ __device__ __forceinline__ float byte_f(uint32_t w, int t) { return static_cast<
 
 __device__ __forceinline__ uint32_t byte_u(uint32_t w, int t) { return (w >> (8 * t)) & 0xFFu; }
 
+// One DPP move of an int across lanes (all lanes active).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
 // sum_t byte_t(codes) * x[t] for the 4 bytes of one dword
 __device__ __forceinline__ float dot4(uint32_t codes, const float *x, float acc) {
     acc = fmaf(byte_f(codes, 0), x[0], acc);
@@ -84,7 +90,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct Row {
     __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t P[5];  // plane starts inside the row
+    uint32_t P[5];  // plane types: plane starts in the row; group types: B, flip
 };
 
 __device__ __forceinline__ u32x4 ld128(const Row &r, uint32_t off) {
@@ -101,6 +107,30 @@ __device__ __forceinline__ uint32_t ld16(const Row &r, uint32_t off) {
 }
 __device__ __forceinline__ uint32_t ld8(const Row &r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b8(r.rsrc, static_cast<int>(off), 0, kNonTemporal);
+}
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+__device__ __forceinline__ u32x3 ld96(const Row &r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r.rsrc, static_cast<int>(off), 0, kNonTemporal);
+}
+
+// Group-layout position of superblock b for slice s (kq_layout.h): the
+// group's start, its size g, the lane record index s * g + bl and the fp16
+// d's offset.  Row.P[0] holds B and P[1] the row's flip for these types.
+struct GPos {
+    uint32_t base, g, bl, m, d;
+};
+__device__ __forceinline__ GPos gpos(const Row &r, int bb, uint32_t b, int s) {
+    const uint32_t B = r.P[0];
+    const bool flipped = r.P[1] != 0;
+    const uint32_t t = b >> 3;
+    const uint32_t ng = (B + 7) >> 3;
+    const uint32_t last_g = B - 8 * (ng - 1);
+    const bool last = t + 1 == ng;
+    const uint32_t g = last ? last_g : 8u;
+    const uint32_t bl = b & 7;
+    const uint32_t base = (flipped ? 2 * last_g : 0u) + t * 8 * static_cast<uint32_t>(bb);
+    const uint32_t d = flipped && last ? 2 * bl : base + static_cast<uint32_t>(bb - 2) * g + 2 * bl;
+    return {base, g, bl, static_cast<uint32_t>(s) * g + bl, d};
 }
 
 __device__ __forceinline__ float half_f(uint32_t bits) { return half_bits_to_float(static_cast<uint16_t>(bits)); }
@@ -234,19 +264,21 @@ __device__ __forceinline__ void x_slice_k6(int s, const float *xb, const float *
 template <>
 struct Kq<MI355X_TYPE_Q6_K> {
     static constexpr int kGrid = 0;
+    // sw4: the four scales of this slice, scales[8hh + kk + 2j] in byte j
     struct Regs {
-        u32x2 qa, qb, qh, sw;
-        uint32_t d;
+        u32x2 qa, qb, qh;
+        uint32_t sw4, d;
     };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
+    // lane record (ql, ql, qh runs), the slice pair's scale word, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
-        const int hh = s >> 2, k = s & 3;
-        return {ld64(r, r.P[0] + 128 * b + 64 * hh + 8 * k), ld64(r, r.P[0] + 128 * b + 64 * hh + 32 + 8 * k),
-                ld64(r, r.P[1] + 64 * b + 32 * hh + 8 * k), ld64(r, r.P[2] + 16 * b + 8 * hh),
-                ld16(r, r.P[3] + 2 * b)};
+        const GPos q = gpos(r, 210, b, s);
+        const u32x4 a = ld128(r, q.base + 24 * q.m);
+        const u32x2 h = ld64(r, q.base + 24 * q.m + 16);
+        const uint32_t w = ld32(r, q.base + 192 * q.g + 16 * q.bl + 4 * (s >> 1));
+        return {u32x2{a[0], a[1]}, u32x2{a[2], a[3]}, h, w, ld16(r, q.d)};
     }
-    __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
-        const int k = s & 3;
+    __device__ static float compute(const Regs &g, int, const XSlice &x, const uint32_t *) {
         float sg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
@@ -256,13 +288,10 @@ struct Kq<MI355X_TYPE_Q6_K> {
             sg[2] = dot4(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), &x.v[16 + 4 * w], sg[2]);
             sg[3] = dot4(((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u), &x.v[24 + 4 * w], sg[3]);
         }
-        const int kk = k >> 1;
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t word = j < 2 ? g.sw[0] : g.sw[1];
-            const int idx = 2 * (j & 1) + kk;
-            const float sc = static_cast<float>(static_cast<int32_t>(word << (24 - 8 * idx)) >> 24);
+            const float sc = static_cast<float>(static_cast<int32_t>(g.sw4 << (24 - 8 * j)) >> 24);
             acc = fmaf(sc, sg[j] - 32.0f * x.s[j], acc);
         }
         return half_f(g.d) * acc;
@@ -280,10 +309,18 @@ struct Kq<MI355X_TYPE_Q3_K> {
         uint32_t sw2, d;
     };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
+    // lane record (8 code bytes, this slice's half of the 8 hmask bytes it
+    // shares with slice s ^ 4, whose lane is lane ^ 32: one permlane32 swap
+    // brings the other half), the 12 scale bytes, d.  The swap of the
+    // record's word 2 returns, in every lane, the lower lane's (slice hh = 0)
+    // half first and the upper lane's second: the 8 bytes in order.
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
-        const int hh = s >> 2, k = s & 3;
-        return {ld64(r, r.P[0] + 64 * b + 32 * hh + 8 * k), ld64(r, r.P[1] + 32 * b + 8 * k),
-                ld64(r, r.P[2] + 12 * b), ld32(r, r.P[2] + 12 * b + 8), ld16(r, r.P[3] + 2 * b)};
+        const GPos q = gpos(r, 110, b, s);
+        const u32x3 rec = ld96(r, q.base + 12 * q.m);
+        const u32x3 sc = ld96(r, q.base + 96 * q.g + 12 * q.bl);
+        const auto sw = __builtin_amdgcn_permlane32_swap(rec[2], rec[2], false, false);
+        return {u32x2{rec[0], rec[1]}, u32x2{static_cast<uint32_t>(sw[0]), static_cast<uint32_t>(sw[1])},
+                u32x2{sc[0], sc[1]}, sc[2], ld16(r, q.d)};
     }
     __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
@@ -386,9 +423,12 @@ struct Kq<MI355X_TYPE_IQ3_S> {
         uint32_t sg, qh, scb, d;
     };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
+    // lane record (qs, signs), qh byte, scale byte, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
-        return {ld64(r, r.P[0] + 64 * b + 8 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld8(r, r.P[2] + 8 * b + s),
-                ld8(r, r.P[3] + 4 * b + (s >> 1)), ld16(r, r.P[4] + 2 * b)};
+        const GPos q = gpos(r, 110, b, s);
+        const u32x3 rec = ld96(r, q.base + 12 * q.m);
+        return {u32x2{rec[0], rec[1]}, rec[2], ld8(r, q.base + 96 * q.g + q.m),
+                ld8(r, q.base + 104 * q.g + 4 * q.bl + (s >> 1)), ld16(r, q.d)};
     }
     __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *grid) {
         const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
@@ -417,8 +457,11 @@ struct Kq<MI355X_TYPE_IQ3_XXS> {
         uint32_t aux, d;
     };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
+    // lane record (qs, scales_and_signs word), d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
-        return {ld64(r, r.P[0] + 64 * b + 8 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld16(r, r.P[2] + 2 * b)};
+        const GPos q = gpos(r, 98, b, s);
+        const u32x3 rec = ld96(r, q.base + 12 * q.m);
+        return {u32x2{rec[0], rec[1]}, rec[2], ld16(r, q.d)};
     }
     __device__ static float compute(const Regs &g, int, const XSlice &x, const uint32_t *grid) {
         const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
@@ -447,9 +490,12 @@ struct Kq<MI355X_TYPE_IQ2_S> {
         uint32_t qs, sg, qh, scb, d;
     };
     __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
+    // lane record (qs, signs), the (qh, scale) byte pair, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
-        return {ld32(r, r.P[0] + 32 * b + 4 * s), ld32(r, r.P[1] + 32 * b + 4 * s), ld8(r, r.P[2] + 8 * b + s),
-                ld8(r, r.P[3] + 8 * b + s), ld16(r, r.P[4] + 2 * b)};
+        const GPos q = gpos(r, 82, b, s);
+        const u32x2 rec = ld64(r, q.base + 8 * q.m);
+        const uint32_t p = ld16(r, q.base + 64 * q.g + 2 * q.m);
+        return {rec[0], rec[1], p & 0xFFu, p >> 8, ld16(r, q.d)};
     }
     __device__ static float compute(const Regs &g, int, const XSlice &x, const uint32_t *grid) {
         float part[2] = {0.f, 0.f};
@@ -533,17 +579,21 @@ __device__ __forceinline__ void dot3(uint32_t c, const XDig &x, int i, int (&s)[
     s[2] = sdot4(c, x.z[2][i], s[2]);
 }
 
-// Byte mask 0xFF where bit j (j < 4) of `bits` is set.
-__device__ __forceinline__ uint32_t sign_mask4(uint32_t bits) {
-    const uint32_t m1 = ((bits & 15u) * 0x00204081u) & 0x01010101u;  // bit j -> byte j
-    return (m1 << 8) - m1;
+// The 4 codebook values of grid word g (magnitude bytes, each in 1..127, as
+// every installed grid is) with the signs of nibble n (bit j set: value j
+// negative; n < 16).  n * 0x810204 places copies of n at bits 2, 9, 16, 23
+// (no two overlap, so no carries): bit j of n lands at bit 8j + 2, which
+// with 0x03020100 makes a v_perm selector taking byte j of g (selector j) or
+// of -g (j + 4); -g is 0x01010100 - g, exact per byte while no byte of g is
+// zero.
+__device__ __forceinline__ uint32_t signed4(uint32_t g, uint32_t n) {
+    const uint32_t sel = ((n * 0x810204u) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(0x01010100u - g, g, sel);
 }
-
-// Magnitude bytes g (each <= 127) negated where `mask` is 0xFF; carry-free:
-// (0x80 - g) ^ 0x80 is -g as a signed byte.
-__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t mask) {
-    const uint32_t neg = (0x80808080u - g) ^ 0x80808080u;
-    return (neg & mask) | (g & ~mask);
+// Two grid words with the low and high nibble of sign byte b.
+__device__ __forceinline__ void signed8(uint32_t g_lo, uint32_t g_hi, uint32_t b, uint32_t &lo, uint32_t &hi) {
+    lo = signed4(g_lo, b & 15u);
+    hi = signed4(g_hi, (b >> 4) & 15u);
 }
 
 __device__ __forceinline__ void dg_load_run16(const uint8_t *xb, int off, XDig &x, int slot) {
@@ -658,13 +708,10 @@ struct KqDg<MI355X_TYPE_Q6_K> {
             dot3(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), x, 4 + w, sg[2]);
             dot3(((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u), x, 6 + w, sg[3]);
         }
-        const int kk = (s & 3) >> 1;
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t word = j < 2 ? g.sw[0] : g.sw[1];
-            const int idx = 2 * (j & 1) + kk;
-            const float sc = static_cast<float>(static_cast<int32_t>(word << (24 - 8 * idx)) >> 24);
+            const float sc = static_cast<float>(static_cast<int32_t>(g.sw4 << (24 - 8 * j)) >> 24);
             acc = fmaf(sc, ldexpf(combine_i(sg[j]) - 32.0f * x.zs[j], x.e[j]), acc);
         }
         return half_f(g.d) * acc;
@@ -736,9 +783,13 @@ struct KqDg<MI355X_TYPE_IQ3_S> {
                                     const uint32_t *grid) {
         int sm[3] = {0, 0, 0};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t idx = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
-            dot3(apply_signs(grid[idx], sign_mask4(g.sg >> (4 * k))), x, k, sm);
+        for (int k = 0; k < 8; k += 2) {
+            const uint32_t i0 = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
+            const uint32_t i1 = byte_u(g.qs[k >> 2], (k & 3) + 1) | (((g.qh >> (k + 1)) & 1u) << 8);
+            uint32_t v0, v1;
+            signed8(grid[i0], grid[i1], byte_u(g.sg, k >> 1), v0, v1);
+            dot3(v0, x, k, sm);
+            dot3(v1, x, k + 1, sm);
         }
         const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
         return db * ldexpf(combine(sm), x.e[0]);
@@ -753,12 +804,11 @@ struct KqDg<MI355X_TYPE_IQ3_XXS> {
         int sm[3] = {0, 0, 0};
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t sg = ksigns((g.aux >> (7 * l)) & 127u);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t gv = grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + h)];
-                dot3(apply_signs(gv, sign_mask4(sg >> (4 * h))), x, 2 * l + h, sm);
-            }
+            uint32_t v0, v1;
+            signed8(grid[byte_u(g.qs[l >> 1], 2 * (l & 1))], grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + 1)],
+                    ksigns((g.aux >> (7 * l)) & 127u), v0, v1);
+            dot3(v0, x, 2 * l, sm);
+            dot3(v1, x, 2 * l + 1, sm);
         }
         const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
         return db * ldexpf(combine(sm), x.e[0]);
@@ -774,9 +824,8 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
-            const uint32_t sb8 = byte_u(g.sg, l);
-            const uint32_t g0 = apply_signs(grid[2 * idx], sign_mask4(sb8));
-            const uint32_t g1 = apply_signs(grid[2 * idx + 1], sign_mask4(sb8 >> 4));
+            uint32_t g0, g1;
+            signed8(grid[2 * idx], grid[2 * idx + 1], byte_u(g.sg, l), g0, g1);
             if (l < 2) {
                 dot3(g0, x, 2 * l, s0);
                 dot3(g1, x, 2 * l + 1, s0);
@@ -835,6 +884,37 @@ __device__ __forceinline__ void stage_digits(const float (&v)[32], uint8_t *xb, 
     *reinterpret_cast<float4 *>(xb + kDgZsum + 16 * j) = make_float4(zs[0], zs[1], zs[2], zs[3]);
 }
 
+// ---- codebook staging ----------------------------------------------------------
+// A thread's share of the codebook (words tid + nthr * k) is read into
+// registers before the weight loads and written to LDS after them: vector
+// loads retire in order, so a copy issued after the weight loads would wait
+// for all of them before the workgroup's first barrier.  NMIN is the
+// smallest thread count the kernel runs with.
+template <int TYPE, int NMIN>
+struct GridRegs {
+    static constexpr int kN = Kq<TYPE>::kGrid > 0 ? (Kq<TYPE>::kGrid + NMIN - 1) / NMIN : 1;
+    uint32_t w[kN];
+    __device__ void fetch(const KqArgs &a, int tid, int nthr) {
+        if constexpr (Kq<TYPE>::kGrid > 0) {
+            const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
+#pragma unroll
+            for (int k = 0; k < kN; ++k) {
+                const int i = tid + nthr * k;
+                w[k] = src[i < Kq<TYPE>::kGrid ? i : Kq<TYPE>::kGrid - 1];
+            }
+        }
+    }
+    __device__ void put(uint32_t *grid, int tid, int nthr) const {
+        if constexpr (Kq<TYPE>::kGrid > 0) {
+#pragma unroll
+            for (int k = 0; k < kN; ++k) {
+                const int i = tid + nthr * k;
+                if (i < Kq<TYPE>::kGrid) grid[i] = w[k];
+            }
+        }
+    }
+};
+
 // ---- kernel ------------------------------------------------------------------
 template <int TYPE, int R>
 __device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows)[R]) {
@@ -846,9 +926,14 @@ __device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows
         const uint8_t *base = a.W + row * a.row_bytes;
         rows[r].rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, records, kBufferWord3);
         const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
+        if constexpr (L.grouped) {
+            rows[r].P[0] = static_cast<uint32_t>(a.B);
+            rows[r].P[1] = flipped ? 1u : 0u;
+        } else {
 #pragma unroll
-        for (int i = 0; i < 5; ++i)
-            rows[r].P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+            for (int i = 0; i < 5; ++i)
+                rows[r].P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+        }
     }
 }
 
@@ -912,6 +997,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
         xv[j][0] = reinterpret_cast<const float4 *>(src)[0];
         xv[j][1] = reinterpret_cast<const float4 *>(src)[1];
     }
+    GridRegs<TYPE, kThreads> gr;
+    gr.fetch(a, threadIdx.x, kThreads);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads of the first row group (clamped; results unused past N)
@@ -949,10 +1036,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             }
         }
     }
-    if constexpr (K::kGrid > 0) {
-        const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
-        for (int i = threadIdx.x; i < K::kGrid; i += kThreads) grid[i] = src[i];
-    }
+    gr.put(grid, threadIdx.x, kThreads);
     __syncthreads();
 
     // 4. row groups
@@ -1030,9 +1114,14 @@ __device__ __forceinline__ Row make_row_pl(const KqArgs &a, int64_t row, int64_t
     r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
                                                row < lim ? static_cast<uint32_t>(a.row_bytes) : 0u, kBufferWord3);
     const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
+    if constexpr (L.grouped) {
+        r.P[0] = static_cast<uint32_t>(a.B);
+        r.P[1] = flipped ? 1u : 0u;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 5; ++i)
-        r.P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+        for (int i = 0; i < 5; ++i)
+            r.P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+    }
     return r;
 }
 
@@ -1069,6 +1158,8 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
             xv[j][4 * i + 3] = f.w;
         }
     }
+    GridRegs<TYPE, kPlqThreads> gr;
+    gr.fetch(a, threadIdx.x, kPlqThreads);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads of the first two rows
@@ -1092,10 +1183,7 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
         const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
         if (t < n32) stage_digits(xv[j], lds + kDgStride * (t >> 3), t & 7);
     }
-    if constexpr (K::kGrid > 0) {
-        const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
-        for (int i = threadIdx.x; i < K::kGrid; i += kPlqThreads) grid[i] = src[i];
-    }
+    gr.put(grid, threadIdx.x, kPlqThreads);
     __builtin_amdgcn_sched_barrier(0);
     load_row(2, row0 + 2);
     __syncthreads();
@@ -1175,6 +1263,214 @@ kq_pl_fn pick_pl_kernel(int type, int nit) {
     case MI355X_TYPE_IQ2_S: return pick_pl_type<MI355X_TYPE_IQ2_S>(nit);
     default: return nullptr;
     }
+}
+
+// ---- activation-stationary form ------------------------------------------------
+// The forms above give each wavefront whole rows, so every row re-reads its
+// activation slices from LDS and, at N = 4096 over 256 CUs, a wavefront has
+// a single row: its load latency is exposed and each workgroup stages the
+// whole activation chunk for a few rows.  Here the steps of a row are split
+// over wavefronts instead:
+//  * one workgroup per CU of G groups of S = ceil(nb / 8) wavefronts;
+//    wavefront (g, t) owns step t (superblocks 8t..8t+7 of the chunk) and,
+//    once the digit planes are staged, copies its lanes' slices of that step
+//    into registers for good;
+//  * the workgroup's rows (a contiguous range) go in tiles of G * RB; group g
+//    takes RB consecutive rows of a tile, each wavefront of the group loads
+//    and decodes its step of them and writes its lane partials to LDS;
+//    loads run two tiles ahead (two register sets), so the tile barrier
+//    never waits for memory;
+//  * after the barrier, each row's lane partials are summed in step order
+//    and across the wavefront: the digit row kernel's slices, expressions and
+//    order, so the two forms agree bit for bit.
+// Partials are double-buffered by tile parity: the barrier of tile i+1 sits
+// between the reads of tile i and the writes of tile i+2.
+constexpr int kXsMaxWaves = 16;
+constexpr int kXsThreads = 64 * kXsMaxWaves;
+constexpr int kXsMaxRows = 4096;   // rows per workgroup (one LDS float each)
+constexpr int kXsStagePasses = 3;
+constexpr int kXsMinThreads = 64 * 10;  // S * G >= 10 for every S = 1..8  // 8-value runs per thread: 32 * 60 <= 3 * 64 * S * G for S * G >= 10
+
+// Digits of one 8-value run r (0..31) of a staged superblock; the four runs
+// of a 32-value block sit in one lane quad, which shares the block maximum.
+// Same digits, exponent and run sums as stage_digits (the two 4-value sums
+// converted and added the same way).
+__device__ __forceinline__ void stage_run8(const float (&v)[8], uint8_t *xb, int r, bool store) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __builtin_bit_cast(float, dpp_i<0xB1>(__builtin_bit_cast(int, m))));
+    m = fmaxf(m, __builtin_bit_cast(float, dpp_i<0x4E>(__builtin_bit_cast(int, m))));
+    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
+    const int se = min(275 - E, 254);
+    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
+    uint32_t pl[3][2];
+    float zs = 0.f;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        uint32_t b0 = 0, b1 = 0, b2 = 0;
+        int zsum = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int Z = __builtin_bit_cast(int, fmaf(v[4 * w + t], sc, 12582912.0f)) - 0x4B400000;
+            const int z0 = (Z << 24) >> 24;
+            const int Z1 = (Z - z0) >> 8;
+            const int z1 = (Z1 << 24) >> 24;
+            const int z2 = (Z1 - z1) >> 8;
+            b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
+            b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
+            b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
+            zsum += Z;
+        }
+        pl[0][w] = b0;
+        pl[1][w] = b1;
+        pl[2][w] = b2;
+        zs += static_cast<float>(zsum);
+    }
+    if (store) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+            *reinterpret_cast<uint2 *>(xb + kDgPlane * p + 8 * r) = make_uint2(pl[p][0], pl[p][1]);
+        if ((r & 3) == 0) reinterpret_cast<int *>(xb + kDgExp)[r >> 2] = 127 - se;
+        reinterpret_cast<float *>(xb + kDgZsum)[r] = zs;
+    }
+}
+
+template <int TYPE, int RB>
+__global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G, int rows_per_wg) {
+    using K = Kq<TYPE>;
+    using KD = KqDg<TYPE>;
+    extern __shared__ float4 lds_xs[];
+    const int S = (a.nb + kBlocksPerStep - 1) / kBlocksPerStep;
+    const int W = S * G;
+    const int nthr = 64 * W;
+    const int tile = G * RB;
+    uint8_t *lds = reinterpret_cast<uint8_t *>(lds_xs);
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride);
+    float *part = reinterpret_cast<float *>(grid + K::kGrid);  // 2 x tile x S x 64
+    float *ybuf = part + 2 * tile * S * 64;                     // rows_per_wg results
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int g = wave / S, t = wave % S;
+    const int s = lane / kBlocksPerStep;
+    const int bloc = kBlocksPerStep * t + lane % kBlocksPerStep;
+    const bool valid = bloc < a.nb;
+    const uint32_t babs = static_cast<uint32_t>(a.b0 + (valid ? bloc : a.nb - 1));
+    const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
+    const int64_t row_end = row_begin + rows_per_wg < a.N ? row_begin + rows_per_wg : a.N;
+    const int n_tiles = row_end > row_begin ? static_cast<int>((row_end - row_begin + tile - 1) / tile) : 0;
+
+    // 1. activation loads: 8-value runs threadIdx.x + nthr * j (clamped)
+    const int n8 = a.nb * 32;
+    float xv[kXsStagePasses][8];
+#pragma unroll
+    for (int j = 0; j < kXsStagePasses; ++j) {
+        const int r = static_cast<int>(threadIdx.x) + nthr * j;
+        const int rc = r < n8 ? r : n8 - 1;
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(a.b0) * 256 + 8 * rc);
+        const float4 f0 = src[0], f1 = src[1];
+        xv[j][0] = f0.x;
+        xv[j][1] = f0.y;
+        xv[j][2] = f0.z;
+        xv[j][3] = f0.w;
+        xv[j][4] = f1.x;
+        xv[j][5] = f1.y;
+        xv[j][6] = f1.z;
+        xv[j][7] = f1.w;
+    }
+    GridRegs<TYPE, kXsMinThreads> gr;
+    gr.fetch(a, threadIdx.x, nthr);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. weight loads of the first two tiles (rows past the range read nothing)
+    typename K::Regs regs[2][RB];
+    auto load_tile = [&](int buf, int ti) {
+        const int64_t r0 = row_begin + static_cast<int64_t>(ti) * tile + g * RB;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) regs[buf][j] = K::load(make_row_pl<TYPE>(a, r0 + j, row_end), babs, s);
+    };
+    load_tile(0, 0);
+    load_tile(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. digits into LDS (waits for the activation loads only); codebook
+#pragma unroll
+    for (int j = 0; j < kXsStagePasses; ++j) {
+        const int r = static_cast<int>(threadIdx.x) + nthr * j;
+        if (nthr * j < n8)  // uniform: every lane of the pass takes part in the quad maxima
+            stage_run8(xv[j], lds + kDgStride * (r >> 5), r & 31, r < n8);
+    }
+    gr.put(grid, threadIdx.x, nthr);
+    __syncthreads();
+
+    // 4. this lane's slice of step t, kept in registers
+    XDig xr;
+    KD::x_slice(s, lds + kDgStride * (valid ? bloc : a.nb - 1), xr);
+
+    // 5. tiles: decode, next loads, barrier, per-row sums into LDS.  The
+    // loop issues the same loads on every pass (the tiles past the range
+    // read nothing) and stores nothing to memory, so each wait for a row's
+    // loads counts exactly the loads issued after them and never waits for
+    // the next tile's.
+    const int n_rows = static_cast<int>(row_end - row_begin);
+    auto do_tile = [&](int buf, int ti) {
+        float *pb = part + buf * (tile * S * 64);
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const float p = KD::compute(regs[buf][j], s, xr, grid);
+            pb[((g * RB + j) * S + t) * 64 + lane] = valid ? p : 0.f;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile(buf, ti + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        for (int r = wave; r < tile; r += W) {
+            const int lr = ti * tile + r;
+            if (lr >= n_rows) break;
+            float acc = 0.f;
+            for (int u = 0; u < S; ++u) acc += pb[(r * S + u) * 64 + lane];
+            const float tot = wave_sum(acc);
+            if (lane == 0) ybuf[lr] = tot;
+        }
+    };
+    // tiles in pairs, the last pair possibly half empty (its rows read
+    // nothing and are not kept): both halves on every pass, so the waits
+    // of the first half also count the second half's loads
+    for (int ti = 0; ti < n_tiles; ti += 2) {
+        do_tile(0, ti);
+        do_tile(1, ti + 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_rows; i += nthr) {
+        const int64_t row = row_begin + i;
+        a.y[row] = a.accumulate ? a.y[row] + ybuf[i] : ybuf[i];
+    }
+}
+
+typedef void (*kq_xs_fn)(KqArgs, int, int);
+
+template <int RB>
+kq_xs_fn pick_xs_kernel(int type) {
+    switch (type) {
+    case MI355X_TYPE_Q4_K: return gemv_kq_xs_kernel<MI355X_TYPE_Q4_K, RB>;
+    case MI355X_TYPE_Q5_K: return gemv_kq_xs_kernel<MI355X_TYPE_Q5_K, RB>;
+    case MI355X_TYPE_Q3_K: return gemv_kq_xs_kernel<MI355X_TYPE_Q3_K, RB>;
+    case MI355X_TYPE_Q6_K: return gemv_kq_xs_kernel<MI355X_TYPE_Q6_K, RB>;
+    case MI355X_TYPE_IQ4_XS: return gemv_kq_xs_kernel<MI355X_TYPE_IQ4_XS, RB>;
+    case MI355X_TYPE_IQ3_S: return gemv_kq_xs_kernel<MI355X_TYPE_IQ3_S, RB>;
+    case MI355X_TYPE_IQ3_XXS: return gemv_kq_xs_kernel<MI355X_TYPE_IQ3_XXS, RB>;
+    case MI355X_TYPE_IQ2_S: return gemv_kq_xs_kernel<MI355X_TYPE_IQ2_S, RB>;
+    default: return nullptr;
+    }
+}
+
+kq_xs_fn pick_xs(int type, int rb) { return rb == 2 ? pick_xs_kernel<2>(type) : pick_xs_kernel<4>(type); }
+
+// Rows per group and tile: 4 where two register sets of 4 rows' loads fit
+// in 128 VGPRs without spilling, else 2 (Q3_K, Q5_K, Q6_K).
+int xs_default_rows(int type) {
+    return type == MI355X_TYPE_Q3_K || type == MI355X_TYPE_Q5_K || type == MI355X_TYPE_Q6_K ? 2 : 4;
 }
 
 typedef void (*kq_kernel_fn)(KqArgs);
@@ -1260,11 +1556,7 @@ constexpr int kQ8kMaxBatch = 16;      // rows per batch
 // a step (lanes of one slice) read 8 different bank groups
 constexpr int kQ8kStride = 272;
 
-// integer max / min / sum across the wavefront (all lanes active)
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
+// integer max / min / sum across the wavefront (all lanes active): dpp_i above
 
 __device__ __forceinline__ float max_swap32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
@@ -1432,7 +1724,7 @@ __device__ __forceinline__ void k6_partial(const Kq<MI355X_TYPE_Q6_K>::Regs &g, 
     for (int t = 0; t < 8; ++t) part[t] = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int sc = sext8(g.sw[j >> 1], 2 * (j & 1) + (k >> 1));
+        const int sc = sext8(g.sw4, j);
         const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 128 * hh + 32 * j + 8 * k);
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
@@ -1492,9 +1784,13 @@ __device__ __forceinline__ int iq3s_bsum(const Kq<MI355X_TYPE_IQ3_S>::Regs &g, i
     const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 32 * s);
     int sumi = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t idx = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
-        sumi = sdot4(apply_signs(grid[idx], sign_mask4(g.sg >> (4 * k))), qv[k], sumi);
+    for (int k = 0; k < 8; k += 2) {
+        const uint32_t i0 = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
+        const uint32_t i1 = byte_u(g.qs[k >> 2], (k & 3) + 1) | (((g.qh >> (k + 1)) & 1u) << 8);
+        uint32_t v0, v1;
+        signed8(grid[i0], grid[i1], byte_u(g.sg, k >> 1), v0, v1);
+        sumi = sdot4(v0, qv[k], sumi);
+        sumi = sdot4(v1, qv[k + 1], sumi);
     }
     return sumi * (1 + 2 * static_cast<int>((g.scb >> (4 * (s & 1))) & 15u));
 }
@@ -1505,12 +1801,11 @@ __device__ __forceinline__ int iq3xxs_bsum(const Kq<MI355X_TYPE_IQ3_XXS>::Regs &
     int sumi = 0;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const uint32_t sg = ksigns((g.aux >> (7 * l)) & 127u);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t gv = grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + h)];
-            sumi = sdot4(apply_signs(gv, sign_mask4(sg >> (4 * h))), qv[2 * l + h], sumi);
-        }
+        uint32_t v0, v1;
+        signed8(grid[byte_u(g.qs[l >> 1], 2 * (l & 1))], grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + 1)],
+                ksigns((g.aux >> (7 * l)) & 127u), v0, v1);
+        sumi = sdot4(v0, qv[2 * l], sumi);
+        sumi = sdot4(v1, qv[2 * l + 1], sumi);
     }
     return sumi * (1 + 2 * static_cast<int>(g.aux >> 28));
 }
@@ -1522,9 +1817,10 @@ __device__ __forceinline__ int iq2s_bsum(const Kq<MI355X_TYPE_IQ2_S>::Regs &g, i
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
         const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
-        const uint32_t sb8 = byte_u(g.sg, l);
-        int t = sdot4(apply_signs(grid[2 * idx], sign_mask4(sb8)), qv[2 * l], 0);
-        t = sdot4(apply_signs(grid[2 * idx + 1], sign_mask4(sb8 >> 4)), qv[2 * l + 1], t);
+        uint32_t v0, v1;
+        signed8(grid[2 * idx], grid[2 * idx + 1], byte_u(g.sg, l), v0, v1);
+        int t = sdot4(v0, qv[2 * l], 0);
+        t = sdot4(v1, qv[2 * l + 1], t);
         if (l < 2) s1 += t;
         else s2 += t;
     }
@@ -1592,13 +1888,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_q8k_kernel(KqArgs a, int rb)
 
     // first row's weights in flight while the activations are quantized
     typename K::Regs regs[1][NIT];
+    GridRegs<TYPE, kThreads> gr;
+    gr.fetch(a, threadIdx.x, kThreads);
     load_group<TYPE, 1, NIT>(a, row < a.N ? row : a.N - 1, s, bl, regs);
     __builtin_amdgcn_sched_barrier(0);
     q8k_stage(a.x, S, qs, bs, dq, wave, lane);
-    if constexpr (K::kGrid > 0) {
-        const uint32_t *src = TYPE == MI355X_TYPE_IQ3_S ? kIq3sGrid : a.grid;
-        for (int i = threadIdx.x; i < K::kGrid; i += kThreads) grid[i] = src[i];
-    }
+    gr.put(grid, threadIdx.x, kThreads);
     __syncthreads();
 
     while (row < a.N) {
@@ -1824,6 +2119,36 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
                         (ctx->form_override == MI355X_FORM_PIPE ||
                          (ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO &&
                           pl_types && nit <= 2));
+        const bool xs = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && ctx->form_override == MI355X_FORM_KSPLIT;
+        if (xs) {
+            const int rb = ctx->rows_override == 2 || ctx->rows_override == 4 ? ctx->rows_override
+                                                                                : xs_default_rows(a.type);
+            const kq_xs_fn k = pick_xs(a.type, rb);
+            const int S = nit;
+            const int G = std::max(1, kXsMaxWaves / S);
+            if (kXsStagePasses * 64 * S * G < 32 * nb || 64 * S * G < kXsMinThreads)
+                return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds the staging passes");
+            // LDS: digits, codebook, two tiles of lane partials, then one
+            // float per row of the workgroup (at most kXsMaxRows)
+            const size_t lds0 = static_cast<size_t>(nb) * kDgStride + grid_words(a.type) * 4u +
+                                2u * static_cast<size_t>(G) * rb * S * 64 * sizeof(float);
+            const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * S * G, lds0 + kXsMaxRows * sizeof(float));
+            const int64_t tile = static_cast<int64_t>(G) * rb;
+            int64_t wgs = std::min<int64_t>((a.N + tile - 1) / tile, static_cast<int64_t>(ctx->num_cus) * std::max(occ, 1));
+            if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);
+            wgs = std::max<int64_t>({wgs, 1, (a.N + kXsMaxRows - 1) / kXsMaxRows});
+            const int64_t rows_per_wg = (a.N + wgs - 1) / wgs;
+            wgs = (a.N + rows_per_wg - 1) / rows_per_wg;
+            if (wgs >= (int64_t(1) << 31)) return set_error(MI355X_EUNSUPPORTED, "too many rows");
+            const size_t lds = lds0 + static_cast<size_t>(rows_per_wg) * sizeof(float);
+            if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
+            KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, x, a.y, b0 > 0 ? 1 : 0,
+                        grid};
+            hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(wgs)), dim3(64 * S * G), lds, ctx->stream, args, G,
+                               static_cast<int>(rows_per_wg));
+            MI355X_HIP(hipGetLastError());
+            continue;
+        }
         if (pl) {
             const kq_pl_fn k = pick_pl_kernel(a.type, nit);
             const size_t lds = static_cast<size_t>(nb) * kDgStride + grid_words(a.type) * 4u;

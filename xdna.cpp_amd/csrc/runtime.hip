@@ -497,14 +497,17 @@ int mi355x_set_iq_grid(int type, const void *table, size_t bytes) {
     if (type == MI355X_TYPE_IQ3_XXS) {
         if (bytes != kIq3xxsGridBytes)
             return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: IQ3_XXS grid is 1024 bytes");
-        g_iq3xxs_grid.assign(p, p + bytes);
     } else if (type == MI355X_TYPE_IQ2_S) {
         if (bytes != kIq2sGridBytes)
             return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: IQ2_S grid is 8192 bytes");
-        g_iq2s_grid.assign(p, p + bytes);
     } else {
         return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: only IQ3_XXS and IQ2_S take a grid");
     }
+    // the kernels negate magnitudes bytewise (carry-free for 1..127)
+    for (size_t i = 0; i < bytes; ++i)
+        if (p[i] == 0 || p[i] > 127)
+            return set_error(MI355X_EINVAL, "mi355x_set_iq_grid: grid magnitudes must be 1..127");
+    (type == MI355X_TYPE_IQ3_XXS ? g_iq3xxs_grid : g_iq2s_grid).assign(p, p + bytes);
     g_grid_version.fetch_add(1);
     return MI355X_OK;
 }
