@@ -586,9 +586,9 @@ __device__ __forceinline__ void dot3(uint32_t c, const XDig &x, int i, int (&s)[
 // with 0x03020100 makes a v_perm selector taking byte j of g (selector j) or
 // of -g (j + 4); -g is 0x01010100 - g, exact per byte while no byte of g is
 // zero.
+__device__ __forceinline__ uint32_t sign_sel(uint32_t n) { return ((n * 0x810204u) & 0x04040404u) | 0x03020100u; }
 __device__ __forceinline__ uint32_t signed4(uint32_t g, uint32_t n) {
-    const uint32_t sel = ((n * 0x810204u) & 0x04040404u) | 0x03020100u;
-    return __builtin_amdgcn_perm(0x01010100u - g, g, sel);
+    return __builtin_amdgcn_perm(0x01010100u - g, g, sign_sel(n));
 }
 // Two grid words with the low and high nibble of sign byte b.
 __device__ __forceinline__ void signed8(uint32_t g_lo, uint32_t g_hi, uint32_t b, uint32_t &lo, uint32_t &hi) {
@@ -781,15 +781,16 @@ struct KqDg<MI355X_TYPE_IQ3_S> {
     __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ3_S>::Regs &g, int s, const XDig &x,
                                     const uint32_t *grid) {
+        const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
+        const uint2 *st = gt + kIq3sGridSize;
         int sm[3] = {0, 0, 0};
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
             const uint32_t i0 = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
             const uint32_t i1 = byte_u(g.qs[k >> 2], (k & 3) + 1) | (((g.qh >> (k + 1)) & 1u) << 8);
-            uint32_t v0, v1;
-            signed8(grid[i0], grid[i1], byte_u(g.sg, k >> 1), v0, v1);
-            dot3(v0, x, k, sm);
-            dot3(v1, x, k + 1, sm);
+            const uint2 e0 = gt[i0], e1 = gt[i1], sl = st[byte_u(g.sg, k >> 1)];
+            dot3(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, k, sm);
+            dot3(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, k + 1, sm);
         }
         const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
         return db * ldexpf(combine(sm), x.e[0]);
@@ -801,14 +802,15 @@ struct KqDg<MI355X_TYPE_IQ3_XXS> {
     __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ3_XXS>::Regs &g, int, const XDig &x,
                                     const uint32_t *grid) {
+        const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
+        const uint2 *st = gt + 256;
         int sm[3] = {0, 0, 0};
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            uint32_t v0, v1;
-            signed8(grid[byte_u(g.qs[l >> 1], 2 * (l & 1))], grid[byte_u(g.qs[l >> 1], 2 * (l & 1) + 1)],
-                    ksigns((g.aux >> (7 * l)) & 127u), v0, v1);
-            dot3(v0, x, 2 * l, sm);
-            dot3(v1, x, 2 * l + 1, sm);
+            const uint2 e0 = gt[byte_u(g.qs[l >> 1], 2 * (l & 1))], e1 = gt[byte_u(g.qs[l >> 1], 2 * (l & 1) + 1)];
+            const uint2 sl = st[(g.aux >> (7 * l)) & 127u];
+            dot3(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, 2 * l, sm);
+            dot3(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, 2 * l + 1, sm);
         }
         const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
         return db * ldexpf(combine(sm), x.e[0]);
@@ -824,8 +826,9 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
-            uint32_t g0, g1;
-            signed8(grid[2 * idx], grid[2 * idx + 1], byte_u(g.sg, l), g0, g1);
+            const uint4 e = reinterpret_cast<const uint4 *>(grid)[idx];
+            const uint2 sl = reinterpret_cast<const uint2 *>(grid + 4096)[byte_u(g.sg, l)];
+            const uint32_t g0 = __builtin_amdgcn_perm(e.y, e.x, sl.x), g1 = __builtin_amdgcn_perm(e.w, e.z, sl.y);
             if (l < 2) {
                 dot3(g0, x, 2 * l, s0);
                 dot3(g1, x, 2 * l + 1, s0);
@@ -884,6 +887,14 @@ __device__ __forceinline__ void stage_digits(const float (&v)[32], uint8_t *xb, 
     *reinterpret_cast<float4 *>(xb + kDgZsum + 16 * j) = make_float4(zs[0], zs[1], zs[2], zs[3]);
 }
 
+// LDS words of the digit kernels' codebook tables (GridRegs::put_dg).
+constexpr int dg_table_words(int type) {
+    return type == MI355X_TYPE_IQ3_S     ? 2 * kIq3sGridSize + 2 * 256
+           : type == MI355X_TYPE_IQ3_XXS ? 2 * 256 + 2 * 128
+           : type == MI355X_TYPE_IQ2_S   ? 2 * 2048 + 2 * 256
+                                         : 0;
+}
+
 // ---- codebook staging ----------------------------------------------------------
 // A thread's share of the codebook (words tid + nthr * k) is read into
 // registers before the weight loads and written to LDS after them: vector
@@ -910,6 +921,28 @@ struct GridRegs {
             for (int k = 0; k < kN; ++k) {
                 const int i = tid + nthr * k;
                 if (i < Kq<TYPE>::kGrid) grid[i] = w[k];
+            }
+        }
+    }
+    // The digit kernels' tables (dg_table_words): each codebook word beside
+    // its bytewise negation, then the v_perm selector pairs of every sign
+    // byte (IQ3_XXS: of every 7-bit sign index, through ksigns).
+    __device__ void put_dg(uint32_t *tab, int tid, int nthr) const {
+        if constexpr (Kq<TYPE>::kGrid > 0) {
+            constexpr int G = Kq<TYPE>::kGrid;
+#pragma unroll
+            for (int k = 0; k < kN; ++k) {
+                const int i = tid + nthr * k;
+                if (i < G) {
+                    tab[2 * i] = w[k];
+                    tab[2 * i + 1] = 0x01010100u - w[k];
+                }
+            }
+            constexpr int nsel = TYPE == MI355X_TYPE_IQ3_XXS ? 128 : 256;
+            for (int b = tid; b < nsel; b += nthr) {
+                const uint32_t bits = TYPE == MI355X_TYPE_IQ3_XXS ? ksigns(static_cast<uint32_t>(b)) : b;
+                tab[2 * G + 2 * b] = sign_sel(bits & 15u);
+                tab[2 * G + 2 * b + 1] = sign_sel(bits >> 4);
             }
         }
     }
@@ -1036,7 +1069,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             }
         }
     }
-    gr.put(grid, threadIdx.x, kThreads);
+    if constexpr (DG) gr.put_dg(grid, threadIdx.x, kThreads);
+    else gr.put(grid, threadIdx.x, kThreads);
     __syncthreads();
 
     // 4. row groups
@@ -1183,7 +1217,7 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
         const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
         if (t < n32) stage_digits(xv[j], lds + kDgStride * (t >> 3), t & 7);
     }
-    gr.put(grid, threadIdx.x, kPlqThreads);
+    gr.put_dg(grid, threadIdx.x, kPlqThreads);
     __builtin_amdgcn_sched_barrier(0);
     load_row(2, row0 + 2);
     __syncthreads();
@@ -1347,7 +1381,7 @@ __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G,
     const int tile = G * RB;
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_xs);
     uint32_t *grid = reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride);
-    float *part = reinterpret_cast<float *>(grid + K::kGrid);  // 2 x tile x S x 64
+    float *part = reinterpret_cast<float *>(grid + dg_table_words(TYPE));  // 2 x tile x S x 64
     float *ybuf = part + 2 * tile * S * 64;                     // rows_per_wg results
 
     const int lane = threadIdx.x & 63;
@@ -1401,7 +1435,7 @@ __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G,
         if (nthr * j < n8)  // uniform: every lane of the pass takes part in the quad maxima
             stage_run8(xv[j], lds + kDgStride * (r >> 5), r & 31, r < n8);
     }
-    gr.put(grid, threadIdx.x, nthr);
+    gr.put_dg(grid, threadIdx.x, nthr);
     __syncthreads();
 
     // 4. this lane's slice of step t, kept in registers
@@ -1478,10 +1512,23 @@ typedef void (*kq_kernel_fn)(KqArgs);
 // R = 2 rows per wavefront only for short rows (NIT <= 2), where both rows'
 // loads and decode stay within ~128 VGPRs.
 constexpr int kMaxNitR2 = 2;
+// Types whose loads of one step fit in at most 8 VGPRs take R = 2 up to
+// four steps per row.
+constexpr bool small_regs(int type) {
+    return type == MI355X_TYPE_Q3_K || type == MI355X_TYPE_IQ3_S || type == MI355X_TYPE_IQ3_XXS ||
+           type == MI355X_TYPE_IQ2_S || type == MI355X_TYPE_IQ4_XS || type == MI355X_TYPE_Q4_K;
+}
+constexpr int max_nit_r2(int type) { return small_regs(type) ? 4 : kMaxNitR2; }
 
 template <int TYPE, bool DG>
 kq_kernel_fn pick_dg(int R, int nit) {
-    if (R == 2 && nit <= kMaxNitR2) return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG> : gemv_kq_kernel<TYPE, 2, 2, DG>;
+    if (R == 2 && nit <= max_nit_r2(TYPE)) {
+        if constexpr (small_regs(TYPE)) {
+            if (nit == 3) return gemv_kq_kernel<TYPE, 2, 3, DG>;
+            if (nit == 4) return gemv_kq_kernel<TYPE, 2, 4, DG>;
+        }
+        return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG> : gemv_kq_kernel<TYPE, 2, 2, DG>;
+    }
     switch (nit) {
     case 1: return gemv_kq_kernel<TYPE, 1, 1, DG>;
     case 2: return gemv_kq_kernel<TYPE, 1, 2, DG>;
@@ -2098,10 +2145,14 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         return MI355X_OK;
     }
 
-    // f32 activations unless the caller asks for the digit path: with the
-    // activations re-staged by every workgroup, the digit path's cheaper
-    // dot products do not yet pay for its costlier staging
-    const bool dg = ctx->kernel_variant == MI355X_VARIANT_DIGITS;
+    // f32 activations unless the caller asks for the digit path, or (AUTO)
+    // for the grid types at up to four steps per row, where the digit row
+    // kernel with two rows per wavefront step is measured as fast or faster
+    // (8192x8192 on MI355X: IQ3_XXS 12.7 vs 13.2 us, IQ3_S 13.9 vs 14.5,
+    // IQ2_S 12.9 vs 12.9): its table-driven sign application and dot4
+    // products cost fewer VALU instructions than the f32 decode
+    const bool grid_type = a.type == MI355X_TYPE_IQ3_S || a.type == MI355X_TYPE_IQ3_XXS || a.type == MI355X_TYPE_IQ2_S;
+    const bool dg_forced = ctx->kernel_variant == MI355X_VARIANT_DIGITS;
 
     // equal chunks of at most kChunkBlocks superblocks
     const int64_t n_chunks = (B + kChunkBlocks - 1) / kChunkBlocks;
@@ -2130,7 +2181,7 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
                 return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds the staging passes");
             // LDS: digits, codebook, two tiles of lane partials, then one
             // float per row of the workgroup (at most kXsMaxRows)
-            const size_t lds0 = static_cast<size_t>(nb) * kDgStride + grid_words(a.type) * 4u +
+            const size_t lds0 = static_cast<size_t>(nb) * kDgStride + dg_table_words(a.type) * 4u +
                                 2u * static_cast<size_t>(G) * rb * S * 64 * sizeof(float);
             const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * S * G, lds0 + kXsMaxRows * sizeof(float));
             const int64_t tile = static_cast<int64_t>(G) * rb;
@@ -2151,7 +2202,7 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         }
         if (pl) {
             const kq_pl_fn k = pick_pl_kernel(a.type, nit);
-            const size_t lds = static_cast<size_t>(nb) * kDgStride + grid_words(a.type) * 4u;
+            const size_t lds = static_cast<size_t>(nb) * kDgStride + dg_table_words(a.type) * 4u;
             if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
             const int64_t slots = static_cast<int64_t>(ctx->num_cus) * kPlqWaves;
             const int64_t rows = (a.N + slots - 1) / slots;
@@ -2163,12 +2214,15 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
             MI355X_HIP(hipGetLastError());
             continue;
         }
-        int R = a.N >= 8192 && nit <= kMaxNitR2 ? 2 : 1;
-        if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= kMaxNitR2)) R = ctx->rows_override;
+        const bool dg_auto = ctx->kernel_variant == MI355X_VARIANT_AUTO && grid_type && nit <= max_nit_r2(a.type) &&
+                             a.N >= 4096;
+        const bool dg = dg_forced || dg_auto;
+        int R = (a.N >= 8192 && nit <= kMaxNitR2) || dg_auto ? 2 : 1;
+        if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
         const int64_t n_groups = (a.N + R - 1) / R;
         const size_t per_block = dg ? kDgStride : (kXStride + kSumStride) * sizeof(float);
-        const size_t lds = static_cast<size_t>(nb) * per_block + grid_words(a.type) * 4u;
+        const size_t lds = static_cast<size_t>(nb) * per_block + (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u;
         if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
         const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
         int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
