@@ -204,6 +204,25 @@ MI355X_API int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64
  * K must be a multiple of the block, N*row_bytes must not overflow. */
 MI355X_API int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                            const float *x, float *y);
+/* Several GEMVs that share the activation row: y_j = W_j x for j < njobs
+ * (1..MI355X_MULTI_MAX_JOBS), every W_j a resident tensor of `type` with
+ * N_j rows of K values.  Q4_0 matrices whose rows are whole 64-block columns
+ * (K a multiple of 2048, up to 16384), 16-byte aligned, with a 16-byte
+ * aligned x, run as one launch of the pipelined form (AUTO and DIGITS
+ * variants; the same per-row arithmetic as mi355x_gemv, the 64 lane partials
+ * of a row added in the order of the rows-per-wavefront the combined row
+ * count picks); otherwise one launch per matrix, as mi355x_gemv.  No
+ * counterpart in the reference: it serves graph_compute, which groups the
+ * consecutive MUL_MAT nodes that read one activation (src/ggml-xdna.cpp:
+ * 783-823 runs them one at a time). */
+#define MI355X_MULTI_MAX_JOBS 8
+typedef struct mi355x_gemv_job {
+    const void *W; /* resident tensor of N rows */
+    int64_t N;
+    float *y;      /* N outputs (device memory) */
+} mi355x_gemv_job;
+MI355X_API int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int njobs,
+                                 const mi355x_gemv_job *jobs);
 /* Same with BF16 activations (raw bits), widened exactly to f32. */
 MI355X_API int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                                 const uint16_t *x_bf16, float *y);

@@ -138,6 +138,37 @@ def test_graph_compute_matches_oracle(plugin, oracle, N, K):
         buf.free()
 
 
+def test_graph_compute_groups_mul_mats_sharing_an_activation(plugin, oracle):
+    """Consecutive MUL_MAT nodes that read one activation row (a q|k|v and a
+    gate|up group, as a decoder layer's graph has them) go to one
+    mi355x_gemv_multi call; a node reading another activation ends a group.
+    Every output matches the oracle."""
+    K = 2048
+    Ns = [2048, 256, 256, 512, 1024]
+    raws = [synth.random_q4_0(n, K, seed=40 + i) for i, n in enumerate(Ns)]
+    x = synth.activations(K, seed=41)
+    x2 = synth.activations(K, seed=42)
+    buf = plugin.buft.alloc(sum(n * RB(K) for n in Ns) + 8 * 4 * K + 4 * 8192 + 16 * 256)
+    try:
+        ws = [weight_tensor(buf, raw, n, K, b"w%d" % i) for i, (raw, n) in enumerate(zip(raws, Ns))]
+        xt = f32_tensor(buf, x, [K, 1])
+        x2t = f32_tensor(buf, x2, [K, 1], b"x2")
+        plan = [(0, xt, x), (1, xt, x), (2, xt, x), (3, x2t, x2), (4, x2t, x2), (0, x2t, x2)]
+        nodes = []
+        for wi, at, _ in plan:
+            d = gh.mul_mat(ws[wi], at, [Ns[wi], 1])
+            buf.place(d, 4 * Ns[wi])
+            nodes.append(d)
+        assert plugin.backend.compute(nodes) == gh.STATUS_SUCCESS
+        plugin.backend.call("synchronize")
+        for (wi, _, a), d in zip(plan, nodes):
+            n = Ns[wi]
+            check_gemv(read_f32(buf, d, n), oracle.gemv(Q4_0, raws[wi], n, K, a),
+                       oracle.row_norms(Q4_0, raws[wi], n, K), a, f"node w{wi}")
+    finally:
+        buf.free()
+
+
 def test_supports_op_through_device(plugin):
     N, K = 64, 512
     raw = synth.random_q4_0(N, K, seed=3)

@@ -1063,10 +1063,11 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
 // nothing).
 constexpr int kPlWaves = 8;
 
+// The body of one workgroup: `blk` is the workgroup's index among those of
+// its matrix (W, y, N).
 template <int NBL, int RW>
-__global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
-    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int, int64_t, int,
-    int rw) {
+__device__ __forceinline__ void pl_body(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                        float *__restrict__ y, int N, int rw, int blk) {
     // rows are NBL full 64-block columns: B and the row length are constants
     constexpr int B = 64 * NBL;
     constexpr int64_t row_bytes = 18 * B;
@@ -1077,7 +1078,7 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int rows = RW > 0 ? RW : rw;
-    const int row0 = (blockIdx.x * kPlWaves + wave) * rows;
+    const int row0 = (blk * kPlWaves + wave) * rows;
     // rows of this wavefront that exist; loads past them read nothing
     const int lim = min(N, row0 + rows);
     const int nrows = max(0, lim - row0);
@@ -1151,6 +1152,34 @@ __global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
             }
         }
     }
+}
+
+template <int NBL, int RW>
+__global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_pl_kernel(
+    const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N, int, int64_t, int,
+    int rw) {
+    pl_body<NBL, RW>(W, x, y, N, rw, static_cast<int>(blockIdx.x));
+}
+
+// Several matrices that share the activation row in one launch: job j owns
+// workgroups [first[j], first[j + 1]), each running the pipelined body on
+// its matrix with the same rows per wavefront.
+constexpr int kPlMaxJobs = 8;
+struct PlJobs {
+    const uint8_t *W[kPlMaxJobs];
+    float *y[kPlMaxJobs];
+    int N[kPlMaxJobs];
+    int first[kPlMaxJobs + 1];
+    int n;
+};
+
+template <int NBL, int RW>
+__global__ __launch_bounds__(64 * kPlWaves) void gemv_q4_0_plj_kernel(PlJobs jobs, const float *__restrict__ x,
+                                                                      int rw) {
+    const int b = static_cast<int>(blockIdx.x);
+    int j = 0;
+    while (j + 1 < jobs.n && b >= jobs.first[j + 1]) ++j;
+    pl_body<NBL, RW>(jobs.W[j], x, jobs.y[j], jobs.N[j], rw, b - jobs.first[j]);
 }
 
 // Pipelined batched variant for NBL x MB <= 8 (rows of full 64-block
@@ -1269,6 +1298,40 @@ pl_kernel_t pick_pl_rw(int rw) {
         }
     }
     return nullptr;
+}
+
+typedef void (*plj_kernel_t)(PlJobs, const float *, int);
+
+template <int NBL>
+plj_kernel_t pick_plj_rw(int rw) {
+    switch (rw) {
+    case 1: return gemv_q4_0_plj_kernel<NBL, 1>;
+    case 2: return gemv_q4_0_plj_kernel<NBL, 2>;
+    case 3: return gemv_q4_0_plj_kernel<NBL, 3>;
+    case 4: return gemv_q4_0_plj_kernel<NBL, 4>;
+    default: break;
+    }
+    if constexpr (NBL <= 6) {
+        switch (rw) {
+        case 6: return gemv_q4_0_plj_kernel<NBL, 6>;
+        case 8: return gemv_q4_0_plj_kernel<NBL, 8>;
+        default: return gemv_q4_0_plj_kernel<NBL, 0>;
+        }
+    }
+    return nullptr;
+}
+
+plj_kernel_t pick_plj(int nbl, int rw) {
+    switch (nbl) {
+    case 1: return pick_plj_rw<1>(rw);
+    case 2: return pick_plj_rw<2>(rw);
+    case 3: return pick_plj_rw<3>(rw);
+    case 4: return pick_plj_rw<4>(rw);
+    case 5: return pick_plj_rw<5>(rw);
+    case 6: return pick_plj_rw<6>(rw);
+    case 7: return pick_plj_rw<7>(rw);
+    default: return pick_plj_rw<8>(rw);
+    }
 }
 
 pl_kernel_t pick_pl(int nbl, int rw) {
@@ -1501,6 +1564,51 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
                        static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B),
                        row_bytes, x_al16 ? 1 : 0);
     MI355X_HIP(hipGetLastError());
+    return MI355X_OK;
+}
+
+int launch_gemv_q4_0_multi(mi355x_ctx *ctx, int64_t K, const float *x, const MultiJob *jobs, int n, bool *launched) {
+    *launched = false;
+    const int64_t B = K / 32;
+    const int64_t row_bytes = 18 * B;
+    const int nbl = static_cast<int>((B + 63) / 64);
+    // the pipelined form's conditions, for every matrix
+    if (n < 1 || n > kPlMaxJobs || ctx->kernel_variant == MI355X_VARIANT_EXACT_F32 ||
+        ctx->kernel_variant == MI355X_VARIANT_GGML_Q8 ||
+        (ctx->form_override != MI355X_FORM_AUTO && ctx->form_override != MI355X_FORM_PIPE) || B % 64 != 0 ||
+        nbl > 8 || row_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+        return MI355X_OK;
+    int64_t total = 0;
+    for (int j = 0; j < n; ++j) {
+        if (reinterpret_cast<uintptr_t>(jobs[j].W) % 16 != 0 || jobs[j].N <= 0 || jobs[j].N > INT32_MAX) return MI355X_OK;
+        total += jobs[j].N;
+    }
+    const int64_t slots = static_cast<int64_t>(ctx->num_cus) * kPlWaves;
+    const int64_t need = (total + slots - 1) / slots;
+    if (ctx->form_override == MI355X_FORM_AUTO && need > kPlRows[5]) return MI355X_OK;
+    int rw = 0;
+    for (int c : kPlRows)
+        if (c >= need) {
+            rw = c;
+            break;
+        }
+    const int rows = rw > 0 ? rw : static_cast<int>(need);
+    const plj_kernel_t k = pick_plj(nbl, rw);
+    if (!k) return MI355X_OK;
+    PlJobs pj{};
+    pj.n = n;
+    int64_t grid = 0;
+    for (int j = 0; j < n; ++j) {
+        pj.W[j] = jobs[j].W;
+        pj.y[j] = jobs[j].y;
+        pj.N[j] = static_cast<int>(jobs[j].N);
+        pj.first[j] = static_cast<int>(grid);
+        grid += (jobs[j].N + static_cast<int64_t>(rows) * kPlWaves - 1) / (static_cast<int64_t>(rows) * kPlWaves);
+    }
+    pj.first[n] = static_cast<int>(grid);
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * kPlWaves), 0, ctx->stream, pj, x, rows);
+    MI355X_HIP(hipGetLastError());
+    *launched = true;
     return MI355X_OK;
 }
 

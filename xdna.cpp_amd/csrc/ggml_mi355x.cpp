@@ -710,6 +710,42 @@ bool process_mul_mat(BackendCtx *bc, T *node, bool host) {
     return true;
 }
 
+// A MUL_MAT node that is one GEMV of a single activation row (M = 1, no
+// weight or activation batches, dense f32 rows, all data in place): the
+// nodes graph_compute may group.  Anything else goes through
+// process_mul_mat, which also reports what is wrong.
+bool single_row_gemv(const ggml_tensor *node) {
+    const ggml_tensor *src0 = node->src[0], *src1 = node->src[1];
+    if (!src0 || !src1 || !node->data || !src0->data || !src1->data || src1->type != GGML_TYPE_F32) return false;
+    const int bv = block_values(src0->type);
+    const int64_t K = src0->ne[0], N = src0->ne[1];
+    if (bv == 0 || K <= 0 || N <= 0 || K % bv != 0 || src1->ne[0] != K) return false;
+    if (src1->ne[1] != 1 || src1->ne[2] != 1 || src1->ne[3] != 1 || src0->ne[2] != 1 || src0->ne[3] != 1)
+        return false;
+    if (node->ne[0] != N || node->ne[1] != 1 || node->ne[2] != 1 || node->ne[3] != 1) return false;
+    const size_t row_bytes = static_cast<size_t>(mi355x_row_bytes(src0->type, K));
+    if (src0->nb[1] != 0 && src0->nb[1] != row_bytes) return false;
+    if ((src1->nb[0] != 0 && src1->nb[0] != sizeof(float)) || (node->nb[0] != 0 && node->nb[0] != sizeof(float)))
+        return false;
+    return true;
+}
+
+// Consecutive nodes i.. that read the same activation row with weights of
+// one type and length: the number that can go to one mi355x_gemv_multi.
+int gemv_group(ggml_cgraph *g, int i, int mm) {
+    const ggml_tensor *a = g->nodes[i];
+    if (!single_row_gemv(a)) return 1;
+    int n = 1;
+    while (i + n < g->n_nodes && n < MI355X_MULTI_MAX_JOBS) {
+        const ggml_tensor *b = g->nodes[i + n];
+        if (!b || b->op != mm || !single_row_gemv(b) || b->src[1]->data != a->src[1]->data ||
+            b->src[0]->type != a->src[0]->type || b->src[0]->ne[0] != a->src[0]->ne[0])
+            break;
+        ++n;
+    }
+    return n;
+}
+
 enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
     if (!backend || !cgraph) return GGML_STATUS_FAILED;
     if (cgraph->n_nodes > 0 && !cgraph->nodes) return GGML_STATUS_FAILED;
@@ -723,6 +759,24 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
     for (int i = 0; i < cgraph->n_nodes; ++i) {
         ggml_tensor *node = cgraph->nodes[i];
         if (!node || mm < 0 || node->op != mm) continue;  // other nodes carry no work here
+        // consecutive MUL_MATs that share their activation row: one launch
+        // (the per-node trace keeps one call per node)
+        const int n = trace ? 1 : gemv_group(cgraph, i, mm);
+        if (n > 1) {
+            mi355x_gemv_job jobs[MI355X_MULTI_MAX_JOBS];
+            for (int j = 0; j < n; ++j) {
+                const ggml_tensor *t = cgraph->nodes[i + j];
+                jobs[j] = {t->src[0]->data, t->src[0]->ne[1], static_cast<float *>(t->data)};
+            }
+            if (mi355x_gemv_multi(bc->ctx, node->src[0]->type, node->src[0]->ne[0],
+                                  static_cast<const float *>(node->src[1]->data), n, jobs) != MI355X_OK) {
+                std::fprintf(stderr, "[mi355x error] nodes '%s'.. (%d sharing one activation) GEMV dispatch: %s\n",
+                             node->name, n, mi355x_last_error());
+                return GGML_STATUS_FAILED;
+            }
+            i += n - 1;
+            continue;
+        }
         auto t0 = std::chrono::steady_clock::now();
         if (!process_mul_mat(bc, node, false)) return GGML_STATUS_FAILED;
         if (trace) {

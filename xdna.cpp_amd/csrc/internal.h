@@ -95,6 +95,15 @@ int launch_gemv_q4_0_mb(mi355x_ctx *ctx, const GemvArgs &a, int64_t x_stride, in
 // current); resolved once per device with hipGetSymbolAddress.
 int resolve_scratch(int device, void **out);
 size_t scratch_bytes();
+// Several Q4_0 matrices that share the activation row x as one launch of
+// the pipelined form (*launched = false where that form does not apply: the
+// caller launches each matrix on its own).
+struct MultiJob {
+    const uint8_t *W;
+    int64_t N;
+    float *y;
+};
+int launch_gemv_q4_0_multi(mi355x_ctx *ctx, int64_t K, const float *x, const MultiJob *jobs, int n, bool *launched);
 bool q4_0_st_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a);
 int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a);

@@ -604,6 +604,40 @@ int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
     return gemv_common(ctx, type, W, N, K, x, false, y, "mi355x_gemv");
 }
 
+int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int njobs, const mi355x_gemv_job *jobs) {
+    clear_error();
+    static const char *who = "mi355x_gemv_multi";
+    if (!ctx || !x || !jobs) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
+    if (njobs < 1 || njobs > MI355X_MULTI_MAX_JOBS)
+        return set_error(MI355X_EINVAL, std::string(who) + ": 1 to " + std::to_string(MI355X_MULTI_MAX_JOBS) +
+                                            " jobs per call");
+    MultiJob mj[MI355X_MULTI_MAX_JOBS];
+    for (int j = 0; j < njobs; ++j) {
+        uint64_t total = 0;
+        const int rc = check_tensor(type, jobs[j].N, K, &total, who);
+        if (rc) return rc;
+        if (!jobs[j].W || !jobs[j].y)
+            return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
+        mj[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].N, jobs[j].y};
+    }
+    if (type == MI355X_TYPE_Q4_0 && K > 0) {
+        bool all = true;
+        for (int j = 0; j < njobs; ++j) all = all && jobs[j].N > 0 && (reinterpret_cast<uintptr_t>(jobs[j].W) & 1) == 0;
+        if (all) {
+            DeviceGuard dg(ctx->device);
+            bool launched = false;
+            const int rc = launch_gemv_q4_0_multi(ctx, K, x, mj, njobs, &launched);
+            if (rc || launched) return rc;
+        }
+    }
+    // one launch per matrix where the shared form does not apply
+    for (int j = 0; j < njobs; ++j) {
+        const int rc = gemv_common(ctx, type, jobs[j].W, jobs[j].N, K, x, false, jobs[j].y, who);
+        if (rc) return rc;
+    }
+    return MI355X_OK;
+}
+
 int mi355x_gemv_bf16(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const uint16_t *x_bf16,
                      float *y) {
     return gemv_common(ctx, type, W, N, K, x_bf16, true, y, "mi355x_gemv_bf16");

@@ -74,6 +74,7 @@ _SIGNATURES = {
     "mi355x_unpack_to_host": (_c.c_int, [_vp, _c.c_int, _c.c_int64, _c.c_int64, _vp, _vp, _c.c_size_t,
                                          _c.c_size_t]),
     "mi355x_gemv": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _vp]),
+    "mi355x_gemv_multi": (_c.c_int, [_vp, _c.c_int, _c.c_int64, _vp, _c.c_int, _vp]),
     "mi355x_gemv_bf16": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _vp]),
     "mi355x_gemv_batched": (_c.c_int, [_vp, _c.c_int, _vp, _c.c_int64, _c.c_int64, _vp, _c.c_int64, _vp,
                                        _c.c_int64, _c.c_int64]),
@@ -82,6 +83,13 @@ _SIGNATURES = {
     "mi355x_time_gemv": (_c.c_int, [_vp, _c.c_int, _c.POINTER(_vp), _c.c_int, _c.c_int64, _c.c_int64, _vp,
                                     _vp, _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
 }
+
+class GemvJob(_c.Structure):
+    """mi355x_gemv_job: {const void *W; int64_t N; float *y;}"""
+    _fields_ = [("W", _c.c_void_p), ("N", _c.c_int64), ("y", _c.c_void_p)]
+
+
+MULTI_MAX_JOBS = 8
 
 _lib = None
 
@@ -295,6 +303,11 @@ class Context:
     def gemv_ptr(self, t: int, w_ptr: int, N: int, K: int, x_ptr: int, y_ptr: int, bf16: bool = False) -> int:
         fn = self.lib.mi355x_gemv_bf16 if bf16 else self.lib.mi355x_gemv
         return fn(self.h, t, w_ptr, N, K, x_ptr, y_ptr)
+
+    def gemv_multi_ptr(self, t: int, K: int, x_ptr: int, jobs) -> int:
+        """mi355x_gemv_multi over (w_ptr, N, y_ptr) jobs sharing x."""
+        arr = (GemvJob * len(jobs))(*[GemvJob(w, n, y) for w, n, y in jobs])
+        return self.lib.mi355x_gemv_multi(self.h, t, K, x_ptr, len(jobs), arr)
 
     def gemv_batched_ptr(self, t: int, w_ptr: int, N: int, K: int, x_ptr: int, x_stride: int, y_ptr: int,
                          y_stride: int, M: int) -> int:
