@@ -237,23 +237,25 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         model.set_wait(model.WAIT_STREAM)
         sync_toks, tw, _ = run()
         # launch + fence with activations and outputs copied through HBM
-        # (staged I/O), then also one launch per weight matrix: the traffic
-        # of a ggml graph with one MUL_MAT node per weight
+        # (staged I/O)
         model.set_wait(model.WAIT_FENCE)
         model.set_io(model.IO_STAGED)
         staged_toks, ts, _ = run()
-        model.set_fuse(False)
-        node_toks, tn, _ = run()
-        node_launches = model.last_launches() / passes
-        model.set_fuse(True)
         model.set_io(model.IO_MAPPED)
+        # through the ggml plugin, the drop-in boundary: weights set_tensor'd
+        # into its buffer, per group activation in, graph_compute over the
+        # group's MUL_MAT nodes, outputs out, synchronize
+        model.set_wait(model.WAIT_PLUGIN)
+        model.generate(prompt[:8], 4)  # places the weights in the plugin's buffer
+        plugin_toks, tp, _ = run()
+        plugin_nodes = model.last_launches() / passes
         model.set_wait(model.WAIT_SERVER)
         # the digit-plane f32-activation arithmetic (library default)
         model.set_variant(mi355x.VARIANT_AUTO)
         dg_toks, td, dg_tok_s = run()
         log(f"bench: decode (ggml Q8_0 numerics): launch + fence {passes / tf['gen_s']:.1f} tok/s; "
             f"hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s; staged I/O {passes / ts['gen_s']:.1f} "
-            f"tok/s; per-matrix launches with staged I/O {passes / tn['gen_s']:.1f} tok/s")
+            f"tok/s; through the ggml plugin's graph_compute {passes / tp['gen_s']:.1f} tok/s")
         log(f"bench: decode: GPU {tok_s:.1f} tok/s in ggml Q8_0 numerics ({t['gen_s'] / passes * 1e3:.3f} "
             f"ms/token, GEMV calls {t['gen_gemv_s'] / passes * 1e3:.3f} ms, host ops "
             f"{t['gen_host_s'] / passes * 1e3:.3f} ms); digit-plane mode {dg_tok_s:.1f} tok/s; prompt "
@@ -288,11 +290,15 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                           "tokens_match": bool(np.array_equal(staged_toks, gq_toks)),
                           "note": "launch + fence with the activation copied host->HBM and outputs HBM->host "
                                   "around every GEMV group"},
-            "per_node": {"tok_s": round(passes / tn["gen_s"], 2), "gemv_launches_per_token": node_launches,
-                         "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
-                         "tokens_match_fused": bool(np.array_equal(node_toks, gq_toks)),
-                         "note": "one GEMV launch per weight matrix (q, k, v, gate, up separately) with staged I/O: "
-                                 "the pattern of a ggml graph with one MUL_MAT node per weight on this backend"},
+            "plugin": {"tok_s": round(passes / tp["gen_s"], 2), "mul_mat_nodes_per_token": plugin_nodes,
+                       "gemv_ms_per_token": round(tp["gen_gemv_s"] / passes * 1e3, 4),
+                       "host_ms_per_token": round(tp["gen_host_s"] / passes * 1e3, 4),
+                       "tokens_match": bool(np.array_equal(plugin_toks, gq_toks)),
+                       "note": "every GEMV group through the ggml plugin as ggml-backend drives a backend split: "
+                               "weights are ggml tensors in the plugin's device buffer (set_tensor prepacks them), "
+                               "per group the activation is copied in (set_tensor_async), one graph_compute runs "
+                               "the group's MUL_MAT nodes (q|k|v and gate|up as one mi355x_gemv_multi launch "
+                               "each), the outputs are copied out (get_tensor_async), then synchronize"},
             "digit_mode": {"tok_s": round(dg_tok_s, 2),
                            "gemv_ms_per_token": round(td["gen_gemv_s"] / passes * 1e3, 4),
                            "host_ms_per_token": round(td["gen_host_s"] / passes * 1e3, 4),
@@ -304,7 +310,8 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                      "job each); norms, RoPE, attention, SwiGLU, argmax on the host; mode 'server': each GEMV "
                      "group is a command to a resident server kernel (mi355x_server_*) that reads the activation "
                      "and the command from pinned host memory and writes outputs there; the 'fence', "
-                     "'stream_wait', 'staged_io' and 'per_node' runs launch one kernel per group instead",
+                     "'stream_wait' and 'staged_io' runs launch one kernel per group instead, the 'plugin' run "
+                     "goes through the ggml backend interface",
         }
         if cpu:
             sys.path.insert(0, os.path.join(ROOT, "oracle"))

@@ -29,6 +29,12 @@
  *                                            no counterpart: the reference reaches
  *                                            IQ3_XXS / IQ2_S only through ggml-cpu
  *                                            (src/xdna-gemv-engine.cpp:1388-1396)
+ *   ggml_backend_mi355x_set_kernel_variant   no counterpart: selects the arithmetic
+ *                                            (MI355X_OPT_VARIANT), e.g. ggml-cpu's
+ *                                            Q8 activation numerics, which the
+ *                                            reference takes from ggml-cpu when it
+ *                                            is loaded (src/xdna-gemv-engine.cpp:
+ *                                            1382-1399)
  *
  * The compatibility API takes host pointers in `data` (like the reference's
  * harness); ggml graphs handed to graph_compute hold device pointers of
@@ -101,6 +107,10 @@ GGML_MI355X_API bool ggml_backend_mi355x_set_op_mul_mat(int op);
  * cross-checks random blocks against them, and installs the grids.  Returns
  * the number of types enabled (0, 1 or 2). */
 GGML_MI355X_API int ggml_backend_mi355x_load_iq_grids_from_ggml(void);
+/* The kernel variant (MI355X_VARIANT_* of mi355x-gemv.h) of this backend's
+ * GEMVs; also reachable through the registry's get_proc_address.  False for a
+ * backend of another type or an unknown variant. */
+GGML_MI355X_API bool ggml_backend_mi355x_set_kernel_variant(struct ggml_backend *backend, int variant);
 
 #ifdef __cplusplus
 }

@@ -153,6 +153,12 @@ MI355X_API int mi355x_host_free(void *hptr);
 MI355X_API int mi355x_memcpy_h2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2h(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Enqueue-only copies on the context's stream: with host memory from
+ * mi355x_host_malloc they return at once (wait with mi355x_ctx_sync or
+ * mi355x_ctx_fence before touching the host side); pageable host memory
+ * works but the runtime may stage it synchronously. */
+MI355X_API int mi355x_memcpy_h2d_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
+MI355X_API int mi355x_memcpy_d2h_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Fill with a byte value using a kernel (safe under graph capture). */
 MI355X_API int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes);
 
@@ -206,12 +212,13 @@ MI355X_API int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, 
                            const float *x, float *y);
 /* Several GEMVs that share the activation row: y_j = W_j x for j < njobs
  * (1..MI355X_MULTI_MAX_JOBS), every W_j a resident tensor of `type` with
- * N_j rows of K values.  Q4_0 matrices whose rows are whole 64-block columns
- * (K a multiple of 2048, up to 16384), 16-byte aligned, with a 16-byte
- * aligned x, run as one launch of the pipelined form (AUTO and DIGITS
- * variants; the same per-row arithmetic as mi355x_gemv, the 64 lane partials
- * of a row added in the order of the rows-per-wavefront the combined row
- * count picks); otherwise one launch per matrix, as mi355x_gemv.  No
+ * N_j rows of K values.  Q4_0 runs as one launch: in the AUTO and DIGITS
+ * variants for rows of whole 64-block columns (K a multiple of 2048, up to
+ * 16384), 16-byte aligned, with a 16-byte aligned x (the pipelined form; the
+ * same per-row arithmetic as mi355x_gemv, the 64 lane partials of a row
+ * added in the order of the rows-per-wavefront the combined row count
+ * picks), in the GGML_Q8 variant for K up to 16384 (bit-identical to one
+ * call per matrix); otherwise one launch per matrix, as mi355x_gemv.  No
  * counterpart in the reference: it serves graph_compute, which groups the
  * consecutive MUL_MAT nodes that read one activation (src/ggml-xdna.cpp:
  * 783-823 runs them one at a time). */

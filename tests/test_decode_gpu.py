@@ -159,6 +159,37 @@ def test_server_decode_token_identical(cfg, n_prompt, n_gen):
     assert t["gen_passes"] == n_gen - 1
 
 
+@pytest.mark.parametrize("cfg", [TINY, SHAPE_3B_2L], ids=["tiny", "3b_2layers"])
+def test_decode_through_the_plugin(cfg):
+    """Every GEMV group through the ggml plugin (set_tensor'd weights,
+    activation in, graph_compute over the group's MUL_MAT nodes -- one
+    multi-job launch for q|k|v and gate|up -- outputs out, synchronize):
+    the CPU engine's tokens; in the GGML_Q8 variant the restated ggml path's
+    tokens and logits bit for bit."""
+    import mi355x
+    with decode.Model(threads=8, **cfg) as m:
+        p = decode.prompt_tokens(9, cfg["vocab"], 6)
+        f, _ = orc.decode_gemv("oracle")
+        cpu_toks, _ = m.generate(p, 7, f)
+        cpu_logits = m.last_logits()
+        fq, _ = orc.decode_gemv("ggml_q8")
+        q8_toks, _ = m.generate(p, 7, fq)
+        q8_logits = m.last_logits()
+        m.attach_gpu(0)
+        m.set_wait(m.WAIT_PLUGIN)
+        toks, t = m.generate(p, 7)
+        logits = m.last_logits()
+        assert m.last_wait() == m.WAIT_PLUGIN
+        assert m.last_launches() == 6 * (7 * cfg["n_layers"] + 1)  # MUL_MAT nodes
+        m.set_variant(mi355x.VARIANT_GGML_Q8)
+        gq_toks, _ = m.generate(p, 7)
+        gq_logits = m.last_logits()
+        m.set_variant(mi355x.VARIANT_AUTO)
+        m.set_wait(m.WAIT_SERVER)
+    check(cpu_toks, cpu_logits, toks, logits)
+    assert np.array_equal(gq_toks, q8_toks) and np.array_equal(gq_logits, q8_logits)
+
+
 @pytest.mark.timeout(900)
 def test_config5_full_decode_token_identical():
     """BASELINE config 5 at full size: the Qwen2.5-3B shape (36 layers), a

@@ -53,15 +53,31 @@ def test_q4_0_one_launch_matches_single_calls_and_oracle(ctx, oracle, K, Ns):
         assert np.abs(ym - ys).max() <= 1e-6 * np.abs(ys).max() + 1e-30
 
 
-@pytest.mark.parametrize("case", ["row_length", "unaligned_x", "q4_k", "ggml_q8"])
+@pytest.mark.parametrize("K,Ns", [(2048, [2048, 256, 256]), (2048, [11008, 11008]), (11008, [2048, 5]),
+                                  (4096, [1, 2, 3, 4, 5, 6, 7, 8])])
+def test_ggml_q8_one_launch_is_bit_identical_to_single_calls(ctx, K, Ns):
+    """The ggml-cpu numerics variant's multi-job launch: every row summed by
+    one lane in block order, so bit-identical to one call per matrix."""
+    raws = [synth.random_q4_0(n, K, seed=3 * n + i) for i, n in enumerate(Ns)]
+    x = synth.activations(K, seed=K + 1)
+    ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_GGML_Q8)
+    try:
+        multi, single = run_multi(ctx, mi355x.Q4_0, K, raws, Ns, x)
+    finally:
+        ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
+    for ym, ys in zip(multi, single):
+        assert np.array_equal(ym.view(np.uint32), ys.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["row_length", "unaligned_x", "q4_k", "ggml_q8_unaligned"])
 def test_fallback_equals_single_calls(ctx, case):
     t, K, Ns, off = mi355x.Q4_0, 11008, [512, 512], 0
     if case == "unaligned_x":
         K, off = 2048, 1
     if case == "q4_k":
         t, K, Ns = mi355x.Q4_K, 2048, [300, 64, 64]
-    if case == "ggml_q8":
-        K = 2048
+    if case == "ggml_q8_unaligned":
+        K, off = 2048, 1
         ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_GGML_Q8)
     try:
         raws = [synth.random_blocks(t, n, K, seed=n) if t != mi355x.Q4_0 else synth.random_q4_0(n, K, seed=n)

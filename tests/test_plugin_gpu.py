@@ -311,7 +311,11 @@ def test_memset_clear_and_copy(plugin):
 
 def test_async_uploads_are_ordered_after_compute(plugin, oracle):
     """Per-token pattern: set x (async), compute, next x, compute, ... with a
-    single synchronize at the end; each token's output must use its own x."""
+    single synchronize at the end; each token's output must use its own x.
+    The caller's activation buffers are overwritten right after each
+    set_tensor_async (the backend must have taken its own copy), and the
+    get_tensor_async destinations are read after synchronize, as ggml's
+    contract has it."""
     N, K, T = 4096, 4096, 6
     raw = synth.random_q4_0(N, K, seed=8)
     xs = [synth.activations(K, seed=100 + t) for t in range(T)]
@@ -321,19 +325,22 @@ def test_async_uploads_are_ordered_after_compute(plugin, oracle):
         w = weight_tensor(buf, raw, N, K)
         xt = f32_tensor(buf, None, [K, 1])
         outs = []
+        src = (C.c_float * K)()
         for t in range(T):
-            src = (C.c_float * K).from_buffer_copy(xs[t].tobytes())
+            C.memmove(src, xs[t].ctypes.data, 4 * K)
             be.call("set_tensor_async", C.addressof(xt), C.addressof(src), 0, 4 * K)
+            C.memset(src, 0xFF, 4 * K)  # the backend holds its own copy
             d = gh.mul_mat(w, xt, [N, 1])
             buf.place(d, 4 * N)
             assert be.compute([d]) == gh.STATUS_SUCCESS
             outs.append(d)
-        got = []
+        dsts = []
         for d in outs:
             dst = (C.c_float * N)()
             be.call("get_tensor_async", C.addressof(d), C.addressof(dst), 0, 4 * N)
-            got.append(np.ctypeslib.as_array(dst).copy())
+            dsts.append(dst)
         be.call("synchronize")
+        got = [np.ctypeslib.as_array(dst).copy() for dst in dsts]
         norms = oracle.row_norms(Q4_0, raw, N, K)
         for t in range(T):
             check_gemv(got[t], oracle.gemv(Q4_0, raw, N, K, xs[t]), norms, xs[t], f"token {t}")

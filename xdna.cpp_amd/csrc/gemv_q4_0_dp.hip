@@ -1408,10 +1408,35 @@ dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail, bool pf) {
 // contributions of every wavefront's rows (WAVES * R * B floats).  Each row
 // is summed by one lane in block order, ggml's sequential f32 sum, so the
 // result is bit-identical to ggml's generic path for the same activations.
-template <int NBL, int R, bool A16, bool TAIL>
-__global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                                           float *__restrict__ y, int N, int B, int64_t row_bytes,
-                                                           int x_al16) {
+// Job lookup of the single-matrix kernel: group g of W.
+struct Q8OneJob {
+    const uint8_t *W;
+    float *y;
+    int N;
+    __device__ void at(int g, const uint8_t *&w, float *&yy, int &n, int &gl) const {
+        w = W;
+        yy = y;
+        n = N;
+        gl = g;
+    }
+};
+// Job lookup of the multi-matrix kernel: job j owns the row groups
+// [first[j], first[j + 1]); groups past the last read nothing.
+struct Q8JobTable {
+    PlJobs t;
+    __device__ void at(int g, const uint8_t *&w, float *&yy, int &n, int &gl) const {
+        int j = 0;
+        while (j + 1 < t.n && g >= t.first[j + 1]) ++j;
+        w = t.W[j];
+        yy = t.y[j];
+        n = t.N[j];
+        gl = g - t.first[j];
+    }
+};
+
+template <int NBL, int R, bool A16, bool TAIL, class J>
+__device__ __forceinline__ void q8_body(const J &jobs, int n_groups, const float *__restrict__ x, int B,
+                                        int64_t row_bytes, int x_al16) {
 #pragma clang fp contract(off)
     constexpr int WAVES = 8;
     extern __shared__ uint4 lds_q8[];
@@ -1422,7 +1447,6 @@ __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__rest
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     constexpr int ROWS = WAVES * R;
-    const int n_groups = (N + ROWS - 1) / ROWS;
     int bc[NBL];
 #pragma unroll
     for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
@@ -1435,31 +1459,73 @@ __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__rest
     xt.load(x, B, x_al16 != 0);
     __builtin_amdgcn_sched_barrier(0);
     int g = blockIdx.x;
+    const uint8_t *W;
+    float *y;
+    int N, gl;
+    jobs.at(g, W, y, N, gl);
     RowGroup<NBL, R, A16, TAIL> grp;
-    grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+    grp.load(W, gl * ROWS + wave * R, N, B, row_bytes, lane);
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dx, sx);
     __syncthreads();
 
     float *cs = cs_all + wave * R * B;
     while (g < n_groups) {
-        const int row0 = g * ROWS + wave * R;
+        const int row0 = gl * ROWS + wave * R;
+        float *yr = y;
+        const int nr = N;
         q8_blocks<NBL, R, A16, TAIL>(grp, cs, B, Q, dx, sx, B, lane, bc, tail_mask);
         g += gridDim.x;
-        grp.load(W, g * ROWS + wave * R, N, B, row_bytes, lane);
+        jobs.at(g, W, y, N, gl);
+        grp.load(W, gl * ROWS + wave * R, N, B, row_bytes, lane);
         __syncthreads();
         if (lane < R) {
             float sumf = 0.0f;
             for (int b = 0; b < B; ++b) sumf = (sumf + cs[lane * B + b]);
-            if (row0 + lane < N) y[row0 + lane] = sumf;
+            if (row0 + lane < nr) yr[row0 + lane] = sumf;
         }
         __syncthreads();
     }
+}
+
+template <int NBL, int R, bool A16, bool TAIL>
+__global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                           float *__restrict__ y, int N, int B, int64_t row_bytes,
+                                                           int x_al16) {
+    constexpr int ROWS = 8 * R;
+    q8_body<NBL, R, A16, TAIL>(Q8OneJob{W, y, N}, (N + ROWS - 1) / ROWS, x, B, row_bytes, x_al16);
+}
+
+template <int NBL, int R, bool A16, bool TAIL>
+__global__ __launch_bounds__(512) void gemv_q4_0_q8j_kernel(PlJobs jobs, const float *__restrict__ x, int B,
+                                                            int64_t row_bytes, int x_al16) {
+    q8_body<NBL, R, A16, TAIL>(Q8JobTable{jobs}, jobs.first[jobs.n], x, B, row_bytes, x_al16);
 }
 
 template <int NBL, int R>
 dp_kernel_t pick_q8_at(bool a16, bool tail) {
     if (a16) return tail ? gemv_q4_0_q8_kernel<NBL, R, true, true> : gemv_q4_0_q8_kernel<NBL, R, true, false>;
     return tail ? gemv_q4_0_q8_kernel<NBL, R, false, true> : gemv_q4_0_q8_kernel<NBL, R, false, false>;
+}
+
+typedef void (*q8j_kernel_t)(PlJobs, const float *, int, int64_t, int);
+
+template <int NBL, int R>
+q8j_kernel_t pick_q8j_at(bool a16, bool tail) {
+    if (a16) return tail ? gemv_q4_0_q8j_kernel<NBL, R, true, true> : gemv_q4_0_q8j_kernel<NBL, R, true, false>;
+    return tail ? gemv_q4_0_q8j_kernel<NBL, R, false, true> : gemv_q4_0_q8j_kernel<NBL, R, false, false>;
+}
+
+q8j_kernel_t pick_q8j(int nbl, bool a16, bool tail) {
+    switch (nbl) {
+    case 1: return pick_q8j_at<1, 4>(a16, tail);
+    case 2: return pick_q8j_at<2, 2>(a16, tail);
+    case 3: return pick_q8j_at<3, 1>(a16, tail);
+    case 4: return pick_q8j_at<4, 1>(a16, tail);
+    case 5: return pick_q8j_at<5, 1>(a16, tail);
+    case 6: return pick_q8j_at<6, 1>(a16, tail);
+    case 7: return pick_q8j_at<7, 1>(a16, tail);
+    default: return pick_q8j_at<8, 1>(a16, tail);
+    }
 }
 
 // rows per wavefront as the digit kernel's defaults: 4 for one block
@@ -1567,8 +1633,47 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     return MI355X_OK;
 }
 
+size_t q8_lds_bytes(int64_t B);
+
+// ggml-cpu numerics: the Q8_0 kernel's row groups of every matrix in one
+// launch (row sums in block order by one lane, so bit-identical to one
+// launch per matrix)
+static int launch_q8_multi(mi355x_ctx *ctx, int64_t K, const float *x, const MultiJob *jobs, int n, bool *launched) {
+    const int64_t B = K / 32;
+    const int64_t row_bytes = 18 * B;
+    const int nbl = static_cast<int>((B + 63) / 64);
+    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
+    const size_t lds = q8_lds_bytes(B);
+    if (n < 1 || n > kPlMaxJobs || B <= 0 || B > kDpMaxBlocks || lds > ctx->max_lds_per_block) return MI355X_OK;
+    bool a16 = row_bytes % 16 == 0;
+    PlJobs pj{};
+    pj.n = n;
+    int64_t groups = 0;
+    for (int j = 0; j < n; ++j) {
+        if (jobs[j].N <= 0 || jobs[j].N > INT32_MAX) return MI355X_OK;
+        a16 = a16 && reinterpret_cast<uintptr_t>(jobs[j].W) % 16 == 0;
+        pj.W[j] = jobs[j].W;
+        pj.y[j] = jobs[j].y;
+        pj.N[j] = static_cast<int>(jobs[j].N);
+        pj.first[j] = static_cast<int>(groups);
+        groups += (jobs[j].N + 8 * R - 1) / (8 * R);
+    }
+    if (groups > INT32_MAX) return MI355X_OK;
+    pj.first[n] = static_cast<int>(groups);
+    const q8j_kernel_t k = pick_q8j(nbl, a16, B % 64 != 0);
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, lds);
+    int64_t grid = std::min<int64_t>(groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
+    if (ctx->grid_override > 0) grid = std::min<int64_t>(groups, ctx->grid_override);
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(grid, 1))), dim3(512), lds, ctx->stream, pj, x,
+                       static_cast<int>(B), row_bytes, reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0);
+    MI355X_HIP(hipGetLastError());
+    *launched = true;
+    return MI355X_OK;
+}
+
 int launch_gemv_q4_0_multi(mi355x_ctx *ctx, int64_t K, const float *x, const MultiJob *jobs, int n, bool *launched) {
     *launched = false;
+    if (ctx->kernel_variant == MI355X_VARIANT_GGML_Q8) return launch_q8_multi(ctx, K, x, jobs, n, launched);
     const int64_t B = K / 32;
     const int64_t row_bytes = 18 * B;
     const int nbl = static_cast<int>((B + 63) / 64);

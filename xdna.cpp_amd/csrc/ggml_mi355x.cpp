@@ -498,13 +498,52 @@ struct BackendCtx {
     // device scratch for the compatibility path (host-pointer graphs)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Pinned bounce memory of the async tensor copies: set_tensor_async
+    // copies the caller's bytes into it and enqueues the upload;
+    // get_tensor_async enqueues the download into it and synchronize copies
+    // the bytes out to the caller (ggml's contract: the destination is read
+    // after synchronize).  Slices are handed out in order and released
+    // together at synchronize.
+    static constexpr size_t kPinBytes = size_t(32) << 20;
+    uint8_t *pin = nullptr;
+    size_t pin_used = 0;
+    struct Pending {
+        void *dst;
+        const void *src;
+        size_t n;
+    };
+    std::vector<Pending> pending;
 
     ~BackendCtx() {
         if (ctx) {
+            flush();
             if (scratch) mi355x_free(ctx, scratch);
             mi355x_ctx_destroy(ctx);
         }
+        if (pin) mi355x_host_free(pin);
         magic = 0;
+    }
+
+    // A 256-byte aligned slice of the bounce memory, or null (too large, or
+    // no pinned memory): the caller takes the synchronous path.
+    uint8_t *take(size_t n) {
+        if (!pin && mi355x_host_malloc(kPinBytes, reinterpret_cast<void **>(&pin)) != MI355X_OK) pin = nullptr;
+        if (!pin || n > kPinBytes) return nullptr;
+        if (pin_used + n > kPinBytes && flush() != 0) return nullptr;
+        uint8_t *p = pin + pin_used;
+        pin_used = (pin_used + n + 255) & ~size_t(255);
+        return p;
+    }
+
+    // Waits for everything queued, hands the downloads to their callers and
+    // frees the bounce memory.
+    int flush() {
+        if (!ctx) return -1;
+        const int rc = mi355x_ctx_fence(ctx);
+        for (const Pending &p : pending) std::memcpy(p.dst, p.src, p.n);
+        pending.clear();
+        pin_used = 0;
+        return rc == MI355X_OK ? 0 : -1;
     }
 
     void *ensure_scratch(size_t bytes) {
@@ -557,6 +596,14 @@ void backend_set_tensor_async(ggml_backend_t backend, ggml_tensor *tensor, const
     if (!bc || !tensor || !tensor->buffer || !tensor->data || !data || size == 0) return;
     if (!on_backend_device(bc, tensor)) return buf_set_tensor(tensor->buffer, tensor, data, offset, size);
     std::lock_guard<std::mutex> lk(bc->mu);
+    if (!prepacked(tensor)) {
+        if (uint8_t *b = bc->take(size)) {
+            std::memcpy(b, data, size);
+            if (mi355x_memcpy_h2d_async(bc->ctx, static_cast<uint8_t *>(tensor->data) + offset, b, size))
+                log_error("set_tensor_async");
+            return;
+        }
+    }
     upload(bc->ctx, tensor, data, offset, size);
 }
 
@@ -569,12 +616,22 @@ void backend_get_tensor_async(ggml_backend_t backend, const ggml_tensor *tensor,
         return buf_get_tensor(tensor->buffer, tensor, data, offset, size);
     }
     std::lock_guard<std::mutex> lk(bc->mu);
+    if (!prepacked(tensor)) {
+        if (uint8_t *b = bc->take(size)) {
+            if (mi355x_memcpy_d2h_async(bc->ctx, b, static_cast<const uint8_t *>(tensor->data) + offset, size))
+                return log_error("get_tensor_async");
+            bc->pending.push_back({data, b, size});
+            return;
+        }
+    }
     download(bc->ctx, tensor, data, offset, size);
 }
 
 void backend_synchronize(ggml_backend_t backend) {
     BackendCtx *bc = backend_ctx(backend);
-    if (bc && mi355x_ctx_sync(bc->ctx)) log_error("synchronize");
+    if (!bc) return;
+    std::lock_guard<std::mutex> lk(bc->mu);
+    if (bc->flush()) log_error("synchronize");
 }
 
 // One MUL_MAT node: validation and batch/row iteration of the reference's
@@ -933,6 +990,8 @@ void *reg_get_proc_address(ggml_backend_reg_t, const char *name) {
     if (!std::strcmp(name, "ggml_backend_mi355x_free")) return reinterpret_cast<void *>(ggml_backend_mi355x_free);
     if (!std::strcmp(name, "ggml_backend_mi355x_load_iq_grids_from_ggml"))
         return reinterpret_cast<void *>(ggml_backend_mi355x_load_iq_grids_from_ggml);
+    if (!std::strcmp(name, "ggml_backend_mi355x_set_kernel_variant"))
+        return reinterpret_cast<void *>(ggml_backend_mi355x_set_kernel_variant);
     return nullptr;
 }
 
@@ -1039,5 +1098,12 @@ bool ggml_backend_mi355x_set_op_mul_mat(int op) {
 }
 
 int ggml_backend_mi355x_load_iq_grids_from_ggml(void) { return mi355x_iq_grids_from_ggml_impl(); }
+
+bool ggml_backend_mi355x_set_kernel_variant(ggml_backend *backend, int variant) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc) return false;
+    std::lock_guard<std::mutex> lk(bc->mu);
+    return mi355x_ctx_set_option(bc->ctx, MI355X_OPT_VARIANT, variant) == MI355X_OK;
+}
 
 }  // extern "C"

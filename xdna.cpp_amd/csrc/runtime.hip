@@ -458,6 +458,23 @@ int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes)
     return copy_sync(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, "mi355x_memcpy_d2d");
 }
 
+static int copy_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind,
+                      const char *who) {
+    clear_error();
+    if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
+    if (bytes == 0) return MI355X_OK;
+    if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
+    DeviceGuard dg(ctx->device);
+    MI355X_HIP(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    return MI355X_OK;
+}
+int mi355x_memcpy_h2d_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_async(ctx, dst, src, bytes, hipMemcpyHostToDevice, "mi355x_memcpy_h2d_async");
+}
+int mi355x_memcpy_d2h_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_async(ctx, dst, src, bytes, hipMemcpyDeviceToHost, "mi355x_memcpy_d2h_async");
+}
+
 int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_fill: null context");

@@ -146,13 +146,15 @@ class Model:
         if self.lib.qd_set_io(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 
-    WAIT_STREAM, WAIT_FENCE, WAIT_SERVER = 0, 1, 2
+    WAIT_STREAM, WAIT_FENCE, WAIT_SERVER, WAIT_PLUGIN = 0, 1, 2, 3
 
     def set_wait(self, mode: int) -> None:
         """WAIT_SERVER (default): GEMV groups as commands to a persistent
         server kernel (where it applies, else WAIT_FENCE); WAIT_FENCE: one
         launch per GEMV group, then a spin on a completion word; WAIT_STREAM:
-        hipStreamSynchronize instead."""
+        hipStreamSynchronize instead; WAIT_PLUGIN: every group through the
+        ggml plugin (weights as tensors in its buffer, activation in, one
+        graph_compute per group, outputs out, synchronize)."""
         if self.lib.qd_set_wait(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 

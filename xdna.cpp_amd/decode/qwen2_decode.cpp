@@ -5,6 +5,8 @@
 // embeddings); only the matrix-vector products leave the host.
 #include "qwen2_decode.h"
 
+#include "ggml-mi355x.h"
+#include "ggml_abi.h"
 #include "mi355x-gemv.h"
 
 #include <hip/hip_runtime_api.h>
@@ -161,6 +163,28 @@ struct Matrix {
     void *dev = nullptr;     // resident copy in HBM (inside qd_model::weights)
 };
 
+// The decode's GEMVs through the ggml plugin, the drop-in boundary: the
+// weights are ggml tensors in the plugin's device buffer (set_tensor
+// prepacks them), and each GEMV group is a graph of MUL_MAT nodes reading one
+// activation tensor, run as ggml-backend runs a backend's split of a graph:
+// the activation copied in (set_tensor_async), graph_compute (which sends
+// consecutive nodes that share the activation to one multi-job launch), the
+// outputs copied out (get_tensor_async), synchronize.  No ggml is linked
+// here, so the harness names the MUL_MAT op id itself.
+constexpr int kPluginOpMulMat = 29;
+
+struct PluginDecode {
+    ggml_backend *be = nullptr;
+    ggml_backend_buffer *buf = nullptr;
+    std::vector<ggml_tensor> w, out;  // per matrix id: weight, MUL_MAT node
+    ggml_tensor x{};                  // the activation row (ne[0] set per group)
+
+    ~PluginDecode() {
+        if (buf && buf->iface.free_buffer) buf->iface.free_buffer(buf);
+        if (be) ggml_backend_mi355x_free(be);
+    }
+};
+
 }  // namespace
 
 struct qd_model {
@@ -188,8 +212,10 @@ struct qd_model {
     int last_wait = QD_WAIT_FENCE;  // the mode the last GPU decode used
 
     mi355x_server *server = nullptr;
+    std::unique_ptr<PluginDecode> plugin;
 
     ~qd_model() {
+        plugin.reset();
         if (server) mi355x_server_destroy(server);
         if (ctx) {
             if (weights) mi355x_free(ctx, weights);
@@ -511,7 +537,7 @@ int qd_set_io(qd_model *m, int mode) {
 
 int qd_set_wait(qd_model *m, int mode) {
     if (!m) return fail("qd_set_wait: null model");
-    if (mode != QD_WAIT_STREAM && mode != QD_WAIT_FENCE && mode != QD_WAIT_SERVER)
+    if (mode != QD_WAIT_STREAM && mode != QD_WAIT_FENCE && mode != QD_WAIT_SERVER && mode != QD_WAIT_PLUGIN)
         return fail("qd_set_wait: unknown mode");
     m->wait_mode = mode;
     return 0;
@@ -577,6 +603,85 @@ int qd_attach_gpu(qd_model *m, int device) {
     return 0;
 }
 
+namespace {
+
+// Puts every matrix into the plugin's buffer on the context's device and
+// builds the MUL_MAT nodes (weights, then node outputs, then the activation
+// row, each at the buffer type's alignment).
+int attach_plugin(qd_model *m) {
+    if (m->plugin) return 0;
+    if (!m->ctx) return fail("plugin decode: qd_attach_gpu first");
+    const int device = mi355x_ctx_device(m->ctx);
+    if (!ggml_backend_mi355x_set_op_mul_mat(kPluginOpMulMat)) return fail("plugin decode: op id");
+    auto P = std::make_unique<PluginDecode>();
+    P->be = ggml_backend_mi355x_init(static_cast<size_t>(device));
+    if (!P->be) return fail("plugin decode: ggml_backend_mi355x_init failed");
+    ggml_backend_buffer_type *buft = ggml_backend_mi355x_buffer_type(static_cast<size_t>(device));
+    if (!buft) return fail("plugin decode: no buffer type");
+    const size_t al = buft->iface.get_alignment(buft);
+    auto up = [al](size_t v) { return (v + al - 1) / al * al; };
+    const size_t n = m->mats.size();
+    std::vector<size_t> woff(n), ooff(n);
+    size_t total = 0;
+    int64_t max_k = 0;
+    for (size_t i = 0; i < n; ++i) {
+        woff[i] = total;
+        total = up(total + m->mats[i].q.size());
+        max_k = std::max(max_k, m->mats[i].K);
+    }
+    for (size_t i = 0; i < n; ++i) {
+        ooff[i] = total;
+        total = up(total + static_cast<size_t>(m->mats[i].N) * 4);
+    }
+    const size_t xoff = total;
+    total = up(total + static_cast<size_t>(max_k) * 4);
+    P->buf = buft->iface.alloc_buffer(buft, total);
+    if (!P->buf) return fail("plugin decode: buffer allocation failed");
+    P->buf->usage = GGML_BACKEND_BUFFER_USAGE_WEIGHTS;
+    auto *base = static_cast<uint8_t *>(P->buf->iface.get_base(P->buf));
+    P->w.resize(n);
+    P->out.resize(n);
+    P->x.type = GGML_TYPE_F32;
+    P->x.buffer = P->buf;
+    P->x.data = base + xoff;
+    std::snprintf(P->x.name, sizeof(P->x.name), "x");
+    for (size_t i = 0; i < n; ++i) {
+        const Matrix &mat = m->mats[i];
+        const size_t rb = static_cast<size_t>(mat.K / 32 * 18);
+        ggml_tensor &w = P->w[i];
+        w.type = GGML_TYPE_Q4_0;
+        w.ne[0] = mat.K;
+        w.ne[1] = mat.N;
+        w.ne[2] = w.ne[3] = 1;
+        w.nb[0] = 18;
+        w.nb[1] = rb;
+        w.nb[2] = w.nb[3] = rb * static_cast<size_t>(mat.N);
+        w.buffer = P->buf;
+        w.data = base + woff[i];
+        std::snprintf(w.name, sizeof(w.name), "w%zu", i);
+        if (P->buf->iface.init_tensor && P->buf->iface.init_tensor(P->buf, &w) != GGML_STATUS_SUCCESS)
+            return fail("plugin decode: init_tensor failed");
+        P->buf->iface.set_tensor(P->buf, &w, mat.q.data(), 0, mat.q.size());
+        ggml_tensor &o = P->out[i];
+        o.type = GGML_TYPE_F32;
+        o.ne[0] = mat.N;
+        o.ne[1] = o.ne[2] = o.ne[3] = 1;
+        o.nb[0] = 4;
+        o.nb[1] = o.nb[2] = o.nb[3] = static_cast<size_t>(mat.N) * 4;
+        o.op = kPluginOpMulMat;
+        o.src[0] = &P->w[i];
+        o.src[1] = &P->x;
+        o.buffer = P->buf;
+        o.data = base + ooff[i];
+        std::snprintf(o.name, sizeof(o.name), "mm%zu", i);
+    }
+    P->be->iface.synchronize(P->be);
+    m->plugin = std::move(P);
+    return 0;
+}
+
+}  // namespace
+
 int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const int32_t *prompt, int n_prompt,
                 int n_gen, int32_t *out_tokens, double *timings) {
     if (!m || !prompt || n_prompt <= 0 || n_gen < 0 || (n_gen > 0 && !out_tokens))
@@ -590,6 +695,12 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     // the server computes the digit-plane arithmetic or ggml-cpu's Q8_0
     // numerics on rows of multiples of 256 values; the exact-f32 variant and
     // other shapes take launch + fence
+    const bool use_plugin = backend == 0 && m->wait_mode == QD_WAIT_PLUGIN;
+    if (use_plugin) {
+        if (attach_plugin(m)) return -1;
+        if (!ggml_backend_mi355x_set_kernel_variant(m->plugin->be, m->variant))
+            return fail("qd_generate: plugin kernel variant");
+    }
     bool use_server = backend == 0 && m->wait_mode == QD_WAIT_SERVER && m->variant != MI355X_VARIANT_EXACT_F32;
     int64_t max_k = 0;
     for (const Matrix &mat : m->mats) {
@@ -620,7 +731,26 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     constexpr int64_t kMappedOutMax = 65536;
     auto gemvs = [&](const float *x, int64_t K, std::initializer_list<int> ids, std::initializer_list<float *> outs) {
         const double t0 = now();
-        if (backend == 0 && use_server) {
+        if (use_plugin) {
+            PluginDecode &P = *m->plugin;
+            P.x.ne[0] = K;
+            P.x.ne[1] = P.x.ne[2] = P.x.ne[3] = 1;
+            P.x.nb[0] = 4;
+            P.x.nb[1] = P.x.nb[2] = P.x.nb[3] = static_cast<size_t>(K) * 4;
+            P.be->iface.set_tensor_async(P.be, &P.x, x, 0, static_cast<size_t>(K) * 4);
+            ggml_tensor *nodes[8];
+            int nn = 0;
+            for (int id : ids) nodes[nn++] = &P.out[id];
+            ggml_cgraph g{};
+            g.size = g.n_nodes = nn;
+            g.nodes = nodes;
+            if (P.be->iface.graph_compute(P.be, &g) != GGML_STATUS_SUCCESS) return -1;
+            auto oi = outs.begin();
+            for (int id : ids)
+                P.be->iface.get_tensor_async(P.be, &P.out[id], *oi++, 0, static_cast<size_t>(m->mats[id].N) * 4);
+            P.be->iface.synchronize(P.be);
+            launches += nn;  // nodes
+        } else if (backend == 0 && use_server) {
             // one server command per group: runs of matrices adjacent in HBM
             // with the same K are one job, outputs land in pinned memory
             mi355x_server_job jobs[4];
@@ -779,7 +909,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     if (rc) return fail(std::string("qd_generate: GEMV failed: ") + (backend == 0 ? mi355x_last_error() : "callback"));
     if (n_gen > 0) m->last_logits = logits;
     m->last_launches = backend == 0 ? launches : 0;
-    if (backend == 0) m->last_wait = use_server ? QD_WAIT_SERVER : wait;
+    if (backend == 0) m->last_wait = use_plugin ? QD_WAIT_PLUGIN : use_server ? QD_WAIT_SERVER : wait;
     if (timings) {
         timings[0] = t_gen0 - t_start;
         timings[1] = t_end - t_gen0;

@@ -97,6 +97,13 @@ QD_API int qd_set_io(qd_model *m, int mode);
 #define QD_WAIT_STREAM 0
 #define QD_WAIT_FENCE 1
 #define QD_WAIT_SERVER 2
+/* QD_WAIT_PLUGIN: every group through the ggml plugin (the drop-in
+ * boundary): weights placed as ggml tensors in the plugin's device buffer
+ * (a second resident copy, made on first use), and per group the activation
+ * copied in, one graph_compute over the group's MUL_MAT nodes, the outputs
+ * copied out and a synchronize -- the calls ggml-backend makes for a
+ * backend's split of a graph.  qd_last_launches counts MUL_MAT nodes. */
+#define QD_WAIT_PLUGIN 3
 QD_API int qd_set_wait(qd_model *m, int mode);
 QD_API int qd_last_wait(const qd_model *m);
 /* Kernel variant of the GPU GEMVs (MI355X_OPT_VARIANT of mi355x-gemv.h):
