@@ -42,17 +42,9 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSlices = 8;  // lanes per superblock
 constexpr int kBlocksPerStep = 64 / kSlices;
-// LDS strides (floats) of one staged superblock and of its 32 sums.  Lane
-// l works on superblock l % 8 and slice l / 8, so the 8 lanes served by one
-// LDS cycle read 8 different superblocks at the same offset; the 4-float
-// pad puts those 8 reads on 8 different bank groups for every slice shape.
-constexpr int kXStride = 256 + 4;
-constexpr int kSumStride = 32 + 1;
-// Superblocks of x staged per pass: 60 (15360 values) keeps the LDS of a
-// workgroup under 80 KB with the largest codebook, so two fit on a CU.
+// Superblocks of x staged per pass: 60 (15360 values) keeps the LDS of an
+// f32 workgroup within 80 KB with the largest codebook, so two fit on a CU.
 constexpr int kChunkBlocks = 60;
-// Staging items (8 values each) per thread: 60 * 32 / 512 rounded up.
-constexpr int kStageItems = (kChunkBlocks * 32 + kThreads - 1) / kThreads;
 
 struct KqArgs {
     const uint8_t *W;
@@ -141,6 +133,102 @@ struct XSlice {
     float s[4];
 };
 
+// ---- lane-major activation staging ---------------------------------------------
+// At step t of a row, lane l = 8 s + bl works on slice s of superblock
+// 8 t + bl.  Staging stores each (superblock, slice) record at index l of
+// its superblock's 8-superblock group, in 16-byte slots laid out
+// [slot][lane]: every slot read of the row loops is one contiguous 1 KB per
+// wavefront, which the LDS serves at its full rate whatever the slice shape.
+// (A superblock-major layout, even padded, leaves the Q4_K and Q6_K slice
+// shapes and the digit slices with 2- and 3-way bank conflicts, measured
+// with SQ_LDS_BANK_CONFLICT on MI355X.)
+// A slice is four 8-value runs; the shapes differ in which runs of the
+// superblock they take, at positions p = 0..3 in the order the computes use:
+//  * S32 (the IQ types): runs 4s + p, the 32-value block s;
+//  * K4 (Q4_K, Q5_K; s = 2c + h): runs 8c + 2h + (p & 1) + 4 (p >> 1), i.e.
+//    values [64c + 16h, +16) then [64c + 32 + 16h, +16) (the low and high
+//    nibbles of code bytes [32c + 16h, +16); include/xdna/kquants.h:290-348);
+//  * K6 (Q3_K, Q6_K; s = 4hh + k): runs 16hh + 4p + k, i.e. positions
+//    [8k, 8k + 8) of the four 32-value groups of half hh
+//    (include/xdna/kquants.h:350-419).
+enum SliceShape { kS32 = 0, kK4 = 1, kK6 = 2 };
+constexpr int slice_shape(int type) {
+    return type == MI355X_TYPE_Q4_K || type == MI355X_TYPE_Q5_K   ? kK4
+           : type == MI355X_TYPE_Q3_K || type == MI355X_TYPE_Q6_K ? kK6
+                                                                  : kS32;
+}
+// run at position p of slice s
+template <int SH>
+__device__ __forceinline__ int run_of(int s, int p) {
+    return SH == kS32 ? 4 * s + p
+           : SH == kK4 ? 8 * (s >> 1) + 2 * (s & 1) + (p & 1) + 4 * (p >> 1)
+                       : 16 * (s >> 2) + 4 * p + (s & 3);
+}
+constexpr int kLmSlot = 16 * 64;                // bytes of one slot row (64 records)
+constexpr int kXGroupBytes = 9 * kLmSlot;       // f32: 8 value slots, the run sums
+constexpr int kDgGroupBytes = 8 * kLmSlot;      // digits: 3 planes x 2, exponents, Z sums
+// byte offset of the record of slice s of chunk superblock bc
+__device__ __forceinline__ int lm_record(int group_bytes, int bc, int s) {
+    return group_bytes * (bc >> 3) + 16 * (8 * s + (bc & 7));
+}
+constexpr size_t x_lds_bytes(int nb) { return static_cast<size_t>((nb + 7) / 8) * kXGroupBytes; }
+constexpr size_t dg_lds_bytes(int nb) { return static_cast<size_t>((nb + 7) / 8) * kDgGroupBytes; }
+
+// Staging is one record per thread: thread r stages record r & 63 of group
+// r >> 6, i.e. slice s = (r & 63) >> 3 of chunk superblock 8 (r >> 6) +
+// (r & 7), so each slot store of a wavefront is again one contiguous 1 KB.
+// The record's four runs, from the chunk's activations xc (bc clamped into
+// the chunk by the caller):
+template <int SH>
+__device__ __forceinline__ void load_record(const float *xc, int bc, int s, float4 (&v)[8]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const float4 *src = reinterpret_cast<const float4 *>(xc + 256 * bc + 8 * run_of<SH>(s, p));
+        v[2 * p] = src[0];
+        v[2 * p + 1] = src[1];
+    }
+}
+
+// f32 record: slots 2p and 2p + 1 hold run p's 8 values, slot 8 the four
+// run sums.
+__device__ __forceinline__ void put_record_f32(uint8_t *rec, const float4 (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<float4 *>(rec + kLmSlot * i) = v[i];
+    float S[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const float4 a = v[2 * p], b = v[2 * p + 1];
+        S[p] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    }
+    *reinterpret_cast<float4 *>(rec + kLmSlot * 8) = make_float4(S[0], S[1], S[2], S[3]);
+}
+
+// The slice of a record: its 32 values and the sums the computes subtract
+// (K6: each run's; K4: each 16-value half's; S32: the block's).
+template <int SH>
+__device__ __forceinline__ void x_slice_lm(const uint8_t *rec, XSlice &x) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 a = *reinterpret_cast<const float4 *>(rec + kLmSlot * i);
+        x.v[4 * i + 0] = a.x;
+        x.v[4 * i + 1] = a.y;
+        x.v[4 * i + 2] = a.z;
+        x.v[4 * i + 3] = a.w;
+    }
+    const float4 S = *reinterpret_cast<const float4 *>(rec + kLmSlot * 8);
+    if constexpr (SH == kS32) {
+        x.s[0] = (S.x + S.y) + (S.z + S.w);
+    } else if constexpr (SH == kK4) {
+        x.s[0] = S.x + S.y;
+        x.s[1] = S.z + S.w;
+    } else {
+        x.s[0] = S.x;
+        x.s[1] = S.y;
+        x.s[2] = S.z;
+        x.s[3] = S.w;
+    }
+}
+
 template <int TYPE>
 struct Kq;
 
@@ -148,26 +236,6 @@ struct Kq;
 // Slice s = (chunk c = s/2, half h = s%2): code bytes [32c+16h, +16) of the
 // chunk's 32; low nibbles are values 64c+16h+l (sub-block 2c), high nibbles
 // 64c+32+16h+l (sub-block 2c+1) (include/xdna/kquants.h:290-348).
-__device__ __forceinline__ void x_slice_k4(int s, const float *xb, const float *sb, XSlice &x) {
-    const int c = s >> 1, h = s & 1;
-    const float4 *p0 = reinterpret_cast<const float4 *>(xb + 64 * c + 16 * h);
-    const float4 *p1 = reinterpret_cast<const float4 *>(xb + 64 * c + 32 + 16 * h);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 a = p0[i], b = p1[i];
-        x.v[4 * i + 0] = a.x;
-        x.v[4 * i + 1] = a.y;
-        x.v[4 * i + 2] = a.z;
-        x.v[4 * i + 3] = a.w;
-        x.v[16 + 4 * i + 0] = b.x;
-        x.v[16 + 4 * i + 1] = b.y;
-        x.v[16 + 4 * i + 2] = b.z;
-        x.v[16 + 4 * i + 3] = b.w;
-    }
-    const int g0 = (64 * c + 16 * h) >> 3;
-    x.s[0] = sb[g0] + sb[g0 + 1];
-    x.s[1] = sb[g0 + 4] + sb[g0 + 5];
-}
 
 // 6-bit (scale, min) pair j of a Q4_K/Q5_K block from its 12 scale bytes
 // (words w0 = bytes 0-3, w1 = 4-7, w2 = 8-11); include/xdna/kquants.h:204-212.
@@ -195,7 +263,6 @@ struct Kq<MI355X_TYPE_Q4_K> {
     struct Regs {
         u32x4 q, hd;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k4(s, xb, sb, x); }
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int c = s >> 1, h = s & 1;
         return {ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h), ld128(r, r.P[1] + 16 * b)};
@@ -217,7 +284,6 @@ struct Kq<MI355X_TYPE_Q5_K> {
     struct Regs {
         u32x4 q, qh, hd;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k4(s, xb, sb, x); }
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const int c = s >> 1, h = s & 1;
         return {ld128(r, r.P[0] + 128 * b + 32 * c + 16 * h), ld128(r, r.P[1] + 32 * b + 16 * h),
@@ -241,23 +307,6 @@ struct Kq<MI355X_TYPE_Q5_K> {
 // Slice s = (half hh = s/4, k = s%4): positions l in [8k, 8k+8) of each of the
 // four 32-value groups j of the half, values 128hh + 32j + l; every 8-value
 // run lies inside one 16-value scale group (8hh + 2j + k/2).
-__device__ __forceinline__ void x_slice_k6(int s, const float *xb, const float *sb, XSlice &x) {
-    const int hh = s >> 2, k = s & 3;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float4 *p = reinterpret_cast<const float4 *>(xb + 128 * hh + 32 * j + 8 * k);
-        const float4 a = p[0], b = p[1];
-        x.v[8 * j + 0] = a.x;
-        x.v[8 * j + 1] = a.y;
-        x.v[8 * j + 2] = a.z;
-        x.v[8 * j + 3] = a.w;
-        x.v[8 * j + 4] = b.x;
-        x.v[8 * j + 5] = b.y;
-        x.v[8 * j + 6] = b.z;
-        x.v[8 * j + 7] = b.w;
-        x.s[j] = sb[16 * hh + 4 * j + k];
-    }
-}
 
 // Q6_K: ql[128] (low nibbles), qh[64] (2 high bits), int8 scales[16], fp16 d;
 // value = d * sc * (code6 - 32) (include/xdna/kquants.h:391-419).
@@ -269,7 +318,6 @@ struct Kq<MI355X_TYPE_Q6_K> {
         u32x2 qa, qb, qh;
         uint32_t sw4, d;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
     // lane record (ql, ql, qh runs), the slice pair's scale word, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 210, b, s);
@@ -308,7 +356,6 @@ struct Kq<MI355X_TYPE_Q3_K> {
         u32x2 q, hm, sw01;
         uint32_t sw2, d;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_k6(s, xb, sb, x); }
     // lane record (8 code bytes, this slice's half of the 8 hmask bytes it
     // shares with slice s ^ 4, whose lane is lane ^ 32: one permlane32 swap
     // brings the other half), the 12 scale bytes, d.  The swap of the
@@ -353,18 +400,6 @@ struct Kq<MI355X_TYPE_Q3_K> {
 };
 
 // ---- 32-value slices: IQ4_XS, IQ3_S, IQ3_XXS, IQ2_S ---------------------------
-__device__ __forceinline__ void x_slice_32(int s, const float *xb, const float *sb, XSlice &x) {
-    const float4 *p = reinterpret_cast<const float4 *>(xb + 32 * s);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 a = p[i];
-        x.v[4 * i + 0] = a.x;
-        x.v[4 * i + 1] = a.y;
-        x.v[4 * i + 2] = a.z;
-        x.v[4 * i + 3] = a.w;
-    }
-    x.s[0] = (sb[4 * s] + sb[4 * s + 1]) + (sb[4 * s + 2] + sb[4 * s + 3]);
-}
 
 // IQ4_XS: d, scales_h, scales_l[4], qs[128]; sub-block ib has the 6-bit
 // scale ls and 32 codebook indices (low nibbles first); value =
@@ -388,7 +423,6 @@ struct Kq<MI355X_TYPE_IQ4_XS> {
         const uint32_t mask = (m1 << 8) - m1;
         return (hi & mask) | (lo & ~mask);
     }
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         return {ld128(r, r.P[0] + 128 * b + 16 * s), ld64(r, r.P[1] + 8 * b)};
     }
@@ -422,7 +456,6 @@ struct Kq<MI355X_TYPE_IQ3_S> {
         u32x2 qs;
         uint32_t sg, qh, scb, d;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
     // lane record (qs, signs), qh byte, scale byte, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 110, b, s);
@@ -456,7 +489,6 @@ struct Kq<MI355X_TYPE_IQ3_XXS> {
         u32x2 qs;
         uint32_t aux, d;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
     // lane record (qs, scales_and_signs word), d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 98, b, s);
@@ -489,7 +521,6 @@ struct Kq<MI355X_TYPE_IQ2_S> {
     struct Regs {
         uint32_t qs, sg, qh, scb, d;
     };
-    __device__ static void x_slice(int s, const float *xb, const float *sb, XSlice &x) { x_slice_32(s, xb, sb, x); }
     // lane record (qs, signs), the (qh, scale) byte pair, d
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 82, b, s);
@@ -519,19 +550,15 @@ struct Kq<MI355X_TYPE_IQ2_S> {
 // Activations as fixed point: each 32-value block b of x has a power-of-two
 // scale with x = Z * 2^e(b), |Z| < 2^22 (the block's largest |x| maps into
 // [2^21, 2^22)), and Z = z0 + 2^8 z1 + 2^16 z2 in balanced signed bytes.  A
-// staged superblock in LDS (kDgStride bytes) holds three digit planes of 256
-// bytes in value order, e(b) of its 8 blocks, and sum(Z) over every 8 values.
+// staged slice record (lane-major, as the f32 records above) holds, per
+// digit plane, the 4 runs' 8 bytes in position order (slots 2p, 2p + 1),
+// then e(b) of the block each run lies in (slot 6) and each run's sum of Z
+// (slot 7).
 // Weight codes (small unsigned integers, or signed bytes for the signed
 // codebooks) meet the digits in v_dot4_i32_i8: sum_i code_i * Z_i over a run
 // is s0 + 2^8 s1 + 2^16 s2 with s_p = sum_i code_i * z_p,i, exact in int32.
 // Rounding x to Z changes each product by at most 2^-22 of its block's
 // largest |x|, well inside the GEMV tolerance of 1e-4 * |w_r| * |x|.
-constexpr int kDgPlane = 256;                       // bytes per digit plane
-constexpr int kDgExp = 3 * kDgPlane;                // 8 x int32 exponents
-constexpr int kDgZsum = kDgExp + 32;                // 32 x f32 sums of Z per 8 values
-constexpr int kDgStride = 260 * 4;                  // bytes per superblock (4-word pad mod 32 banks)
-static_assert(kDgZsum + 128 <= kDgStride, "digit superblock layout");
-
 struct XDig {
     uint32_t z[3][8];  // digit planes: 8 dwords (32 values) per plane
     int e[4];          // exponents of the 32-blocks the slice's runs lie in
@@ -596,62 +623,44 @@ __device__ __forceinline__ void signed8(uint32_t g_lo, uint32_t g_hi, uint32_t b
     hi = signed4(g_hi, (b >> 4) & 15u);
 }
 
-__device__ __forceinline__ void dg_load_run16(const uint8_t *xb, int off, XDig &x, int slot) {
+// The slice of a digit record (K4: e and Z sums per 16-value half; K6: per
+// run; S32: the block's exponent).
+template <int SH>
+__device__ __forceinline__ void dg_slice_lm(const uint8_t *rec, XDig &x) {
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(xb + kDgPlane * p + off);
-        x.z[p][slot + 0] = v.x;
-        x.z[p][slot + 1] = v.y;
-        x.z[p][slot + 2] = v.z;
-        x.z[p][slot + 3] = v.w;
+        const uint4 a = *reinterpret_cast<const uint4 *>(rec + kLmSlot * (2 * p));
+        const uint4 b = *reinterpret_cast<const uint4 *>(rec + kLmSlot * (2 * p + 1));
+        x.z[p][0] = a.x;
+        x.z[p][1] = a.y;
+        x.z[p][2] = a.z;
+        x.z[p][3] = a.w;
+        x.z[p][4] = b.x;
+        x.z[p][5] = b.y;
+        x.z[p][6] = b.z;
+        x.z[p][7] = b.w;
     }
-}
-
-__device__ __forceinline__ void dg_load_run8(const uint8_t *xb, int off, XDig &x, int slot) {
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(xb + kDgPlane * p + off);
-        x.z[p][slot + 0] = v.x;
-        x.z[p][slot + 1] = v.y;
+    const int4 E = *reinterpret_cast<const int4 *>(rec + kLmSlot * 6);
+    if constexpr (SH == kS32) {
+        x.e[0] = E.x;
+    } else {
+        const float4 Z = *reinterpret_cast<const float4 *>(rec + kLmSlot * 7);
+        if constexpr (SH == kK4) {
+            x.e[0] = E.x;
+            x.e[1] = E.z;
+            x.zs[0] = Z.x + Z.y;
+            x.zs[1] = Z.z + Z.w;
+        } else {
+            x.e[0] = E.x;
+            x.e[1] = E.y;
+            x.e[2] = E.z;
+            x.e[3] = E.w;
+            x.zs[0] = Z.x;
+            x.zs[1] = Z.y;
+            x.zs[2] = Z.z;
+            x.zs[3] = Z.w;
+        }
     }
-}
-
-__device__ __forceinline__ int dg_exp(const uint8_t *xb, int blk32) {
-    return reinterpret_cast<const int *>(xb + kDgExp)[blk32];
-}
-__device__ __forceinline__ float dg_zsum(const uint8_t *xb, int run8) {
-    return reinterpret_cast<const float *>(xb + kDgZsum)[run8];
-}
-
-// Q4_K / Q5_K slice: runs [64c+16h, +16) and [64c+32+16h, +16).
-__device__ __forceinline__ void dg_slice_k4(int s, const uint8_t *xb, XDig &x) {
-    const int c = s >> 1, h = s & 1;
-    const int a = 64 * c + 16 * h, b = a + 32;
-    dg_load_run16(xb, a, x, 0);
-    dg_load_run16(xb, b, x, 4);
-    x.e[0] = dg_exp(xb, 2 * c);
-    x.e[1] = dg_exp(xb, 2 * c + 1);
-    x.zs[0] = dg_zsum(xb, a >> 3) + dg_zsum(xb, (a >> 3) + 1);
-    x.zs[1] = dg_zsum(xb, b >> 3) + dg_zsum(xb, (b >> 3) + 1);
-}
-
-// Q3_K / Q6_K slice: runs [128hh + 32j + 8k, +8), j = 0..3.
-__device__ __forceinline__ void dg_slice_k6(int s, const uint8_t *xb, XDig &x) {
-    const int hh = s >> 2, k = s & 3;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int off = 128 * hh + 32 * j + 8 * k;
-        dg_load_run8(xb, off, x, 2 * j);
-        x.e[j] = dg_exp(xb, 4 * hh + j);
-        x.zs[j] = dg_zsum(xb, off >> 3);
-    }
-}
-
-// 32-value slice [32s, +32).
-__device__ __forceinline__ void dg_slice_32(int s, const uint8_t *xb, XDig &x) {
-    dg_load_run16(xb, 32 * s, x, 0);
-    dg_load_run16(xb, 32 * s + 16, x, 4);
-    x.e[0] = dg_exp(xb, s);
 }
 
 template <int TYPE>
@@ -659,7 +668,6 @@ struct KqDg;
 
 template <>
 struct KqDg<MI355X_TYPE_Q4_K> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k4(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_Q4_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
 #pragma unroll
@@ -678,7 +686,6 @@ struct KqDg<MI355X_TYPE_Q4_K> {
 
 template <>
 struct KqDg<MI355X_TYPE_Q5_K> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k4(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_Q5_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int c = s >> 1;
         int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
@@ -697,7 +704,6 @@ struct KqDg<MI355X_TYPE_Q5_K> {
 
 template <>
 struct KqDg<MI355X_TYPE_Q6_K> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k6(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_Q6_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         int sg[4][3] = {};
 #pragma unroll
@@ -720,7 +726,6 @@ struct KqDg<MI355X_TYPE_Q6_K> {
 
 template <>
 struct KqDg<MI355X_TYPE_Q3_K> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_k6(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
         int sg[4][3] = {};
@@ -761,7 +766,6 @@ struct KqDg<MI355X_TYPE_IQ4_XS> {
         const uint32_t mask = (m1 << 8) - m1;
         return (hi & mask) | (lo & ~mask);
     }
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ4_XS>::Regs &g, int s, const XDig &x, const uint32_t *) {
         int sm[3] = {0, 0, 0};
 #pragma unroll
@@ -778,7 +782,6 @@ struct KqDg<MI355X_TYPE_IQ4_XS> {
 
 template <>
 struct KqDg<MI355X_TYPE_IQ3_S> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ3_S>::Regs &g, int s, const XDig &x,
                                     const uint32_t *grid) {
         const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
@@ -799,7 +802,6 @@ struct KqDg<MI355X_TYPE_IQ3_S> {
 
 template <>
 struct KqDg<MI355X_TYPE_IQ3_XXS> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ3_XXS>::Regs &g, int, const XDig &x,
                                     const uint32_t *grid) {
         const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
@@ -819,7 +821,6 @@ struct KqDg<MI355X_TYPE_IQ3_XXS> {
 
 template <>
 struct KqDg<MI355X_TYPE_IQ2_S> {
-    __device__ static void x_slice(int s, const uint8_t *xb, XDig &x) { dg_slice_32(s, xb, x); }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ2_S>::Regs &g, int, const XDig &x,
                                     const uint32_t *grid) {
         int s0[3] = {0, 0, 0}, s1[3] = {0, 0, 0};
@@ -844,47 +845,95 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
     }
 };
 
-// Digits of one 32-value block (values v[0..31]) into a staged superblock.
-__device__ __forceinline__ void stage_digits(const float (&v)[32], uint8_t *xb, int j) {
-    float m = 0.f;
+// One DPP move of a float: row_ror:8 (the lane 8 apart within its row of 16)
+__device__ __forceinline__ float ror8_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<0x128>(__builtin_bit_cast(int, v)));
+}
+// lane ^ 16 within each half wavefront (ds_swizzle, bit mode: xor 0x10)
+__device__ __forceinline__ float swz16_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// Digit record of the values v (load_record).  Each run takes the exponent
+// of its 32-value block, whose largest |x| is the maximum over the runs of
+// that block: all in this record (S32); two here and two in the record of
+// slice s ^ 1, lane ^ 8 (K4); one here and one in each record of slices
+// 4hh + k', lanes ^ 8, ^ 16, ^ 24 (K6).  Every lane of the wavefront must
+// take part (the exchanges read other lanes); `store` masks the stores.
+// The digits, exponent fields and Z sums equal those of staging each
+// 32-value block at once: the maximum is exact in any order and each Z and
+// dword sum is formed from the same values.
+template <int SH>
+__device__ __forceinline__ void put_record_dg(uint8_t *rec, const float4 (&v)[8], bool store) {
+    float m[4];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
-    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
-    const int se = min(275 - E, 254);  // biased exponent of s = 2^-e: m * s in [2^21, 2^22)
-    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
-    uint32_t pl[3][8];
-    float zs[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < 4; ++p) {
+        const float4 a = v[2 * p], b = v[2 * p + 1];
+        m[p] = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    }
+    if constexpr (SH == kS32) {
+        const float M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+        m[0] = m[1] = m[2] = m[3] = M;
+    } else if constexpr (SH == kK4) {
+        float A = fmaxf(m[0], m[1]), B = fmaxf(m[2], m[3]);
+        A = fmaxf(A, ror8_f(A));
+        B = fmaxf(B, ror8_f(B));
+        m[0] = m[1] = A;
+        m[2] = m[3] = B;
+    } else {
 #pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        uint32_t b0 = 0, b1 = 0, b2 = 0;
-        int zsum = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            // round to nearest integer: |v * s| < 2^22, so 1.5 * 2^23 + v * s
-            // lies in [2^23, 2^24) where f32 spacing is 1
-            const int Z = __builtin_bit_cast(int, fmaf(v[4 * w + t], sc, 12582912.0f)) - 0x4B400000;
-            const int z0 = (Z << 24) >> 24;
-            const int Z1 = (Z - z0) >> 8;
-            const int z1 = (Z1 << 24) >> 24;
-            const int z2 = (Z1 - z1) >> 8;
-            b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
-            b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
-            b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
-            zsum += Z;
+        for (int p = 0; p < 4; ++p) {
+            m[p] = fmaxf(m[p], ror8_f(m[p]));
+            m[p] = fmaxf(m[p], swz16_f(m[p]));
         }
-        pl[0][w] = b0;
-        pl[1][w] = b1;
-        pl[2][w] = b2;
-        zs[w >> 1] += static_cast<float>(zsum);
     }
+    uint32_t pl[3][8];
+    int ef[4];
+    float zs[4];
 #pragma unroll
-    for (int p = 0; p < 3; ++p) {
-        uint4 *dst = reinterpret_cast<uint4 *>(xb + kDgPlane * p + 32 * j);
-        dst[0] = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
-        dst[1] = make_uint4(pl[p][4], pl[p][5], pl[p][6], pl[p][7]);
+    for (int p = 0; p < 4; ++p) {
+        const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m[p]) >> 23) & 0xFFu);
+        const int se = min(275 - E, 254);  // biased exponent of s = 2^-e: m * s in [2^21, 2^22)
+        const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
+        ef[p] = 127 - se;
+        zs[p] = 0.f;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const float4 f = v[2 * p + w];
+            const float q[4] = {f.x, f.y, f.z, f.w};
+            uint32_t b0 = 0, b1 = 0, b2 = 0;
+            int zsum = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                // round to nearest integer: |v * s| < 2^22, so 1.5 * 2^23 + v * s
+                // lies in [2^23, 2^24) where f32 spacing is 1
+                const int Z = __builtin_bit_cast(int, fmaf(q[t], sc, 12582912.0f)) - 0x4B400000;
+                const int z0 = (Z << 24) >> 24;
+                const int Z1 = (Z - z0) >> 8;
+                const int z1 = (Z1 << 24) >> 24;
+                const int z2 = (Z1 - z1) >> 8;
+                b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
+                b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
+                b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
+                zsum += Z;
+            }
+            pl[0][2 * p + w] = b0;
+            pl[1][2 * p + w] = b1;
+            pl[2][2 * p + w] = b2;
+            zs[p] += static_cast<float>(zsum);
+        }
     }
-    reinterpret_cast<int *>(xb + kDgExp)[j] = 127 - se;
-    *reinterpret_cast<float4 *>(xb + kDgZsum + 16 * j) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+    if (store) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+            *reinterpret_cast<uint4 *>(rec + kLmSlot * (2 * p)) = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
+            *reinterpret_cast<uint4 *>(rec + kLmSlot * (2 * p + 1)) =
+                make_uint4(pl[p][4], pl[p][5], pl[p][6], pl[p][7]);
+        }
+        *reinterpret_cast<int4 *>(rec + kLmSlot * 6) = make_int4(ef[0], ef[1], ef[2], ef[3]);
+        *reinterpret_cast<float4 *>(rec + kLmSlot * 7) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+    }
 }
 
 // LDS words of the digit kernels' codebook tables (GridRegs::put_dg).
@@ -987,19 +1036,16 @@ __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, in
     }
 }
 
-static_assert(kChunkBlocks * 8 <= kThreads, "one 32-value block per thread when staging digits");
+static_assert(kChunkBlocks <= kBlocksPerStep * kWaves, "one staged record per thread");
 
 template <int TYPE, int R, int NIT, bool DG>
 __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     using K = Kq<TYPE>;
     extern __shared__ float4 lds_kq[];
-    // f32 path: nb * kXStride values, then nb * kSumStride sums of 8;
-    // digit path: nb * kDgStride bytes; then the codebook
+    // lane-major records (f32 or digit), then the codebook
+    constexpr int SH = slice_shape(TYPE);
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_kq);
-    float *xs = reinterpret_cast<float *>(lds_kq);
-    float *sums = xs + a.nb * kXStride;
-    uint32_t *grid = DG ? reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride)
-                        : reinterpret_cast<uint32_t *>(sums + a.nb * kSumStride);
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + (DG ? dg_lds_bytes(a.nb) : x_lds_bytes(a.nb)));
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1009,27 +1055,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
     int64_t g = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
 
-    // 1. activation loads for staging (clamped index): the f32 path takes
-    // kStageItems runs of 8 values per thread, the digit path one 32-value
-    // block per thread
-    const int n8 = a.nb * 32;
-    const int n32 = a.nb * 8;
-    constexpr int kXv = DG ? 4 : kStageItems;
-    float4 xv[kXv][2];
-#pragma unroll
-    for (int j = 0; j < kXv; ++j) {
-        const float *src;
-        if constexpr (DG) {
-            const int t = threadIdx.x < n32 ? static_cast<int>(threadIdx.x) : n32 - 1;
-            src = a.x + static_cast<int64_t>(a.b0) * 256 + 32 * t + 8 * j;
-        } else {
-            const int i = threadIdx.x + kThreads * j;
-            const int ic = i < n8 ? i : n8 - 1;
-            src = a.x + static_cast<int64_t>(a.b0) * 256 + 8 * ic;
-        }
-        xv[j][0] = reinterpret_cast<const float4 *>(src)[0];
-        xv[j][1] = reinterpret_cast<const float4 *>(src)[1];
-    }
+    // 1. activation loads for staging: thread r's record (superblock
+    // clamped into the chunk)
+    const int rec_t = wave, rec_l = lane;
+    const int rec_bc = kBlocksPerStep * rec_t + (rec_l & 7);
+    const bool rec_ok = rec_bc < a.nb;
+    float4 xv[8];
+    load_record<SH>(a.x + static_cast<int64_t>(a.b0) * 256, rec_ok ? rec_bc : a.nb - 1, rec_l >> 3, xv);
     GridRegs<TYPE, kThreads> gr;
     gr.fetch(a, threadIdx.x, kThreads);
     __builtin_amdgcn_sched_barrier(0);
@@ -1039,35 +1071,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     load_group<TYPE, R, NIT>(a, g < n_groups ? g : n_groups - 1, s, bl, regs);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. activations into LDS (f32 with 8-value sums, or digit planes); codebook
-    if constexpr (DG) {
-        if (static_cast<int>(threadIdx.x) < n32) {
-            float v[32];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[8 * j + 0] = xv[j][0].x;
-                v[8 * j + 1] = xv[j][0].y;
-                v[8 * j + 2] = xv[j][0].z;
-                v[8 * j + 3] = xv[j][0].w;
-                v[8 * j + 4] = xv[j][1].x;
-                v[8 * j + 5] = xv[j][1].y;
-                v[8 * j + 6] = xv[j][1].z;
-                v[8 * j + 7] = xv[j][1].w;
-            }
-            stage_digits(v, lds + kDgStride * (threadIdx.x >> 3), threadIdx.x & 7);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < kStageItems; ++j) {
-            const int i = threadIdx.x + kThreads * j;
-            if (i < n8) {
-                float4 *dst = reinterpret_cast<float4 *>(xs + kXStride * (i >> 5) + 8 * (i & 31));
-                dst[0] = xv[j][0];
-                dst[1] = xv[j][1];
-                const float4 p = xv[j][0], q = xv[j][1];
-                sums[kSumStride * (i >> 5) + (i & 31)] = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
-            }
-        }
+    // 3. activation records into LDS (waves past the chunk's groups store
+    // nothing); codebook
+    if (kBlocksPerStep * rec_t < a.nb) {
+        if constexpr (DG) put_record_dg<SH>(lds + kDgGroupBytes * rec_t + 16 * rec_l, xv, rec_ok);
+        else if (rec_ok) put_record_f32(lds + kXGroupBytes * rec_t + 16 * rec_l, xv);
     }
     if constexpr (DG) gr.put_dg(grid, threadIdx.x, kThreads);
     else gr.put(grid, threadIdx.x, kThreads);
@@ -1085,7 +1093,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             const int bc = valid ? bloc : a.nb - 1;
             if constexpr (DG) {
                 XDig x;
-                KqDg<TYPE>::x_slice(s, lds + kDgStride * bc, x);
+                dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), x);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float p = KqDg<TYPE>::compute(regs[r][t], s, x, grid);
@@ -1093,7 +1101,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
                 }
             } else {
                 XSlice x;
-                K::x_slice(s, xs + kXStride * bc, sums + kSumStride * bc, x);
+                x_slice_lm<SH>(lds + lm_record(kXGroupBytes, bc, s), x);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float p = K::compute(regs[r][t], s, x, grid);
@@ -1136,8 +1144,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
 constexpr int kPlqWaves = 4;
 constexpr int kPlqThreads = 64 * kPlqWaves;
 constexpr int kPlqDepth = 3;
-constexpr int kPlqStageBlocks = 2;  // 32-value blocks staged per thread (<= 512 per chunk)
-static_assert(kChunkBlocks * 8 <= kPlqThreads * kPlqStageBlocks, "staging covers a chunk");
+constexpr int kPlqStageBlocks = 2;  // records staged per thread
+static_assert(kChunkBlocks <= kBlocksPerStep * kPlqWaves * kPlqStageBlocks, "staging covers a chunk");
 
 // Buffer view of one row; rows at or past `lim` get an empty range.
 template <int TYPE>
@@ -1163,10 +1171,11 @@ template <int TYPE, int NIT, bool XREG>
 __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int rows) {
     using K = Kq<TYPE>;
     using KD = KqDg<TYPE>;
+    constexpr int SH = slice_shape(TYPE);
     constexpr int D = kPlqDepth;
     extern __shared__ float4 lds_plq[];
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_plq);
-    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride);
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + dg_lds_bytes(a.nb));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int s = lane / kBlocksPerStep;
@@ -1175,22 +1184,13 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
     const int64_t lim = row0 + rows < a.N ? row0 + rows : a.N;
     const int nrows = lim > row0 ? static_cast<int>(lim - row0) : 0;
 
-    // 1. activation loads: 32-value blocks threadIdx.x + 256 j (clamped)
-    const int n32 = a.nb * 8;
-    float xv[kPlqStageBlocks][32];
+    // 1. activation loads: the records of groups wave + 4 j (superblocks
+    // clamped into the chunk)
+    float4 xv[kPlqStageBlocks][8];
 #pragma unroll
     for (int j = 0; j < kPlqStageBlocks; ++j) {
-        const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
-        const int tc = t < n32 ? t : n32 - 1;
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(a.b0) * 256 + 32 * tc);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 f = src[i];
-            xv[j][4 * i] = f.x;
-            xv[j][4 * i + 1] = f.y;
-            xv[j][4 * i + 2] = f.z;
-            xv[j][4 * i + 3] = f.w;
-        }
+        const int bc = kBlocksPerStep * (wave + kPlqWaves * j) + bl;
+        load_record<SH>(a.x + static_cast<int64_t>(a.b0) * 256, bc < a.nb ? bc : a.nb - 1, s, xv[j]);
     }
     GridRegs<TYPE, kPlqThreads> gr;
     gr.fetch(a, threadIdx.x, kPlqThreads);
@@ -1214,8 +1214,9 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
     // 3. digits into LDS (waits for the activation loads only); codebook
 #pragma unroll
     for (int j = 0; j < kPlqStageBlocks; ++j) {
-        const int t = static_cast<int>(threadIdx.x) + kPlqThreads * j;
-        if (t < n32) stage_digits(xv[j], lds + kDgStride * (t >> 3), t & 7);
+        const int rt = wave + kPlqWaves * j;
+        if (kBlocksPerStep * rt < a.nb)
+            put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lane, xv[j], kBlocksPerStep * rt + bl < a.nb);
     }
     gr.put_dg(grid, threadIdx.x, kPlqThreads);
     __builtin_amdgcn_sched_barrier(0);
@@ -1234,7 +1235,7 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
     XDig xr[XREG ? NIT : 1];
     if constexpr (XREG) {
 #pragma unroll
-        for (int t = 0; t < NIT; ++t) KD::x_slice(s, lds + kDgStride * bcs[t], xr[t]);
+        for (int t = 0; t < NIT; ++t) dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bcs[t], s), xr[t]);
     }
 
     // 5. rows, D loads ahead
@@ -1250,7 +1251,7 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
                     p = KD::compute(regs[slot][t], s, xr[t], grid);
                 } else {
                     XDig x;
-                    KD::x_slice(s, lds + kDgStride * bcs[t], x);
+                    dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bcs[t], s), x);
                     p = KD::compute(regs[slot][t], s, x, grid);
                     // one step's activations live at a time
                     __builtin_amdgcn_sched_barrier(0);
@@ -1322,65 +1323,20 @@ kq_pl_fn pick_pl_kernel(int type, int nit) {
 constexpr int kXsMaxWaves = 16;
 constexpr int kXsThreads = 64 * kXsMaxWaves;
 constexpr int kXsMaxRows = 4096;   // rows per workgroup (one LDS float each)
-constexpr int kXsStagePasses = 3;
-constexpr int kXsMinThreads = 64 * 10;  // S * G >= 10 for every S = 1..8  // 8-value runs per thread: 32 * 60 <= 3 * 64 * S * G for S * G >= 10
-
-// Digits of one 8-value run r (0..31) of a staged superblock; the four runs
-// of a 32-value block sit in one lane quad, which shares the block maximum.
-// Same digits, exponent and run sums as stage_digits (the two 4-value sums
-// converted and added the same way).
-__device__ __forceinline__ void stage_run8(const float (&v)[8], uint8_t *xb, int r, bool store) {
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, __builtin_bit_cast(float, dpp_i<0xB1>(__builtin_bit_cast(int, m))));
-    m = fmaxf(m, __builtin_bit_cast(float, dpp_i<0x4E>(__builtin_bit_cast(int, m))));
-    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
-    const int se = min(275 - E, 254);
-    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
-    uint32_t pl[3][2];
-    float zs = 0.f;
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-        uint32_t b0 = 0, b1 = 0, b2 = 0;
-        int zsum = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int Z = __builtin_bit_cast(int, fmaf(v[4 * w + t], sc, 12582912.0f)) - 0x4B400000;
-            const int z0 = (Z << 24) >> 24;
-            const int Z1 = (Z - z0) >> 8;
-            const int z1 = (Z1 << 24) >> 24;
-            const int z2 = (Z1 - z1) >> 8;
-            b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
-            b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
-            b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
-            zsum += Z;
-        }
-        pl[0][w] = b0;
-        pl[1][w] = b1;
-        pl[2][w] = b2;
-        zs += static_cast<float>(zsum);
-    }
-    if (store) {
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-            *reinterpret_cast<uint2 *>(xb + kDgPlane * p + 8 * r) = make_uint2(pl[p][0], pl[p][1]);
-        if ((r & 3) == 0) reinterpret_cast<int *>(xb + kDgExp)[r >> 2] = 127 - se;
-        reinterpret_cast<float *>(xb + kDgZsum)[r] = zs;
-    }
-}
+constexpr int kXsMinThreads = 64 * 10;  // S * G >= 10 for every S = 1..8
 
 template <int TYPE, int RB>
 __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G, int rows_per_wg) {
     using K = Kq<TYPE>;
     using KD = KqDg<TYPE>;
+    constexpr int SH = slice_shape(TYPE);
     extern __shared__ float4 lds_xs[];
     const int S = (a.nb + kBlocksPerStep - 1) / kBlocksPerStep;
     const int W = S * G;
     const int nthr = 64 * W;
     const int tile = G * RB;
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_xs);
-    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + a.nb * kDgStride);
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + dg_lds_bytes(a.nb));
     float *part = reinterpret_cast<float *>(grid + dg_table_words(TYPE));  // 2 x tile x S x 64
     float *ybuf = part + 2 * tile * S * 64;                     // rows_per_wg results
 
@@ -1395,24 +1351,13 @@ __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G,
     const int64_t row_end = row_begin + rows_per_wg < a.N ? row_begin + rows_per_wg : a.N;
     const int n_tiles = row_end > row_begin ? static_cast<int>((row_end - row_begin + tile - 1) / tile) : 0;
 
-    // 1. activation loads: 8-value runs threadIdx.x + nthr * j (clamped)
-    const int n8 = a.nb * 32;
-    float xv[kXsStagePasses][8];
-#pragma unroll
-    for (int j = 0; j < kXsStagePasses; ++j) {
-        const int r = static_cast<int>(threadIdx.x) + nthr * j;
-        const int rc = r < n8 ? r : n8 - 1;
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + static_cast<int64_t>(a.b0) * 256 + 8 * rc);
-        const float4 f0 = src[0], f1 = src[1];
-        xv[j][0] = f0.x;
-        xv[j][1] = f0.y;
-        xv[j][2] = f0.z;
-        xv[j][3] = f0.w;
-        xv[j][4] = f1.x;
-        xv[j][5] = f1.y;
-        xv[j][6] = f1.z;
-        xv[j][7] = f1.w;
-    }
+    // 1. activation loads: wavefront w < S stages the records of group w
+    // (the others load group S - 1 again and store nothing; superblocks
+    // clamped into the chunk)
+    const int rt = wave < S ? wave : S - 1;
+    const int rbc = kBlocksPerStep * rt + lane % kBlocksPerStep;
+    float4 xv[8];
+    load_record<SH>(a.x + static_cast<int64_t>(a.b0) * 256, rbc < a.nb ? rbc : a.nb - 1, s, xv);
     GridRegs<TYPE, kXsMinThreads> gr;
     gr.fetch(a, threadIdx.x, nthr);
     __builtin_amdgcn_sched_barrier(0);
@@ -1428,19 +1373,14 @@ __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G,
     load_tile(1, 1);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. digits into LDS (waits for the activation loads only); codebook
-#pragma unroll
-    for (int j = 0; j < kXsStagePasses; ++j) {
-        const int r = static_cast<int>(threadIdx.x) + nthr * j;
-        if (nthr * j < n8)  // uniform: every lane of the pass takes part in the quad maxima
-            stage_run8(xv[j], lds + kDgStride * (r >> 5), r & 31, r < n8);
-    }
+    // 3. digit records into LDS (waits for the activation loads only); codebook
+    if (wave < S) put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lane, xv, rbc < a.nb);
     gr.put_dg(grid, threadIdx.x, nthr);
     __syncthreads();
 
     // 4. this lane's slice of step t, kept in registers
     XDig xr;
-    KD::x_slice(s, lds + kDgStride * (valid ? bloc : a.nb - 1), xr);
+    dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, valid ? bloc : a.nb - 1, s), xr);
 
     // 5. tiles: decode, next loads, barrier, per-row sums into LDS.  The
     // loop issues the same loads on every pass (the tiles past the range
@@ -2177,11 +2117,11 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
             const kq_xs_fn k = pick_xs(a.type, rb);
             const int S = nit;
             const int G = std::max(1, kXsMaxWaves / S);
-            if (kXsStagePasses * 64 * S * G < 32 * nb || 64 * S * G < kXsMinThreads)
-                return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds the staging passes");
+            if (64 * S * G < kXsMinThreads)
+                return set_error(MI355X_EUNSUPPORTED, "too few wavefronts for the codebook staging");
             // LDS: digits, codebook, two tiles of lane partials, then one
             // float per row of the workgroup (at most kXsMaxRows)
-            const size_t lds0 = static_cast<size_t>(nb) * kDgStride + dg_table_words(a.type) * 4u +
+            const size_t lds0 = dg_lds_bytes(nb) + dg_table_words(a.type) * 4u +
                                 2u * static_cast<size_t>(G) * rb * S * 64 * sizeof(float);
             const int occ = occupancy(reinterpret_cast<const void *>(k), 64 * S * G, lds0 + kXsMaxRows * sizeof(float));
             const int64_t tile = static_cast<int64_t>(G) * rb;
@@ -2202,7 +2142,7 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         }
         if (pl) {
             const kq_pl_fn k = pick_pl_kernel(a.type, nit);
-            const size_t lds = static_cast<size_t>(nb) * kDgStride + dg_table_words(a.type) * 4u;
+            const size_t lds = dg_lds_bytes(nb) + dg_table_words(a.type) * 4u;
             if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
             const int64_t slots = static_cast<int64_t>(ctx->num_cus) * kPlqWaves;
             const int64_t rows = (a.N + slots - 1) / slots;
@@ -2221,8 +2161,8 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
         const int64_t n_groups = (a.N + R - 1) / R;
-        const size_t per_block = dg ? kDgStride : (kXStride + kSumStride) * sizeof(float);
-        const size_t lds = static_cast<size_t>(nb) * per_block + (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u;
+        const size_t lds = (dg ? dg_lds_bytes(nb) : x_lds_bytes(nb)) +
+                           (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u;
         if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
         const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
         int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
