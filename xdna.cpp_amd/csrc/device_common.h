@@ -76,4 +76,42 @@ __device__ __forceinline__ u32x4 load_16_a2(const uint8_t *p) {
     return v;
 }
 
+// s = 0, then s = s + c[i] for i = 0 .. n-1 in index order (ggml's
+// sequential sum): exactly the rounding of the plain loop.  With c 16-byte
+// aligned and n a multiple of 8, the reads of 8-value chunk k + 2 are issued
+// before the additions of chunk k, so the chain waits on the additions
+// rather than on each chunk's LDS latency; otherwise the plain loop.
+__device__ __forceinline__ float ordered_sum(const float *c, int n) {
+#pragma clang fp contract(off)
+    float s = 0.0f;
+    if ((reinterpret_cast<uintptr_t>(c) & 15u) != 0 || (n & 7) != 0) {
+        for (int i = 0; i < n; ++i) s = s + c[i];
+        return s;
+    }
+    // every read is in bounds (indices clamped to the last chunk) and
+    // unconditional, so the reads stay LDS reads and their waits counted
+    const float4 *p = reinterpret_cast<const float4 *>(c);
+    const int nc = n >> 3, last = 2 * nc - 2;
+    float4 a0 = p[0], a1 = p[1];
+    float4 b0 = p[min(2, last)], b1 = p[min(2, last) + 1];
+    for (int k = 0; k < nc; ++k) {
+        const int q = min(2 * k + 4, last);
+        const float4 n0 = p[q], n1 = p[q + 1];
+        __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the additions
+        s = s + a0.x;
+        s = s + a0.y;
+        s = s + a0.z;
+        s = s + a0.w;
+        s = s + a1.x;
+        s = s + a1.y;
+        s = s + a1.z;
+        s = s + a1.w;
+        a0 = b0;
+        a1 = b1;
+        b0 = n0;
+        b1 = n1;
+    }
+    return s;
+}
+
 }  // namespace mi355x

@@ -1952,7 +1952,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_q8k_kernel(KqArgs a, int rb)
                 const float *src = tw + r * per_row + c * S;
                 float acc = 0.0f;
                 if (c < 8) {
-                    for (int i = 0; i < S; ++i) acc = (acc + src[i]);
+                    acc = ordered_sum(src, S);
                 } else {
                     for (int i = 0; i < S; ++i) acc = (acc - src[i]);
                 }
@@ -1970,9 +1970,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_q8k_kernel(KqArgs a, int rb)
             }
         } else {
             if (lane < nrow) {
-                const float *src = tw + lane * per_row;
-                float sumf = 0.0f;
-                for (int i = 0; i < per_row; ++i) sumf = (sumf + src[i]);
+                float sumf = ordered_sum(tw + lane * per_row, per_row);
                 if constexpr (TYPE == MI355X_TYPE_IQ3_XXS) sumf = (0.25f * sumf);
                 if constexpr (TYPE == MI355X_TYPE_IQ2_S) sumf = (0.125f * sumf);
                 a.y[first + lane * stride] = sumf;

@@ -824,7 +824,9 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 // beyond) v*R, v*R + 8R, ... (lane = block, the next run's loads in flight)
 // and stores (float(sumi) * d_w) * d_x per block; then one thread per row adds
 // its row's contributions in block order (ggml's sequential sum).  Rows of a
-// chunk sit B + 1 floats apart, so those threads read distinct banks.
+// chunk sit B + 4 floats apart: 16-byte aligned for the sum's vector reads,
+// and (B a multiple of 8) an odd number of 16-byte slots, so 16 consecutive
+// rows start on 16 different bank groups.
 constexpr int kSrvCsFloats = 8192;
 
 template <int NBL, bool TAIL>
@@ -840,7 +842,7 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int64_t row_bytes = 18 * static_cast<int64_t>(B);
-    const int stride = B + 1;
+    const int stride = B + 4;
     // rows per chunk: a multiple of ROWS, so a wavefront's runs continue from
     // one chunk into the next, and at most one per thread (>= ROWS: B <= 64
     // for R = 4, B <= 128 for R = 2, B <= 512 for R = 1)
@@ -878,13 +880,7 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
             }
             __syncthreads();
             const int t = static_cast<int>(threadIdx.x);
-            if (t < c1 - c0) {
-                const float *cr = csb + t * stride;
-                float sumf = 0.0f;
-#pragma unroll 8
-                for (int b = 0; b < B; ++b) sumf = (sumf + cr[b]);
-                out[c0 - lo + t] = sumf;
-            }
+            if (t < c1 - c0) out[c0 - lo + t] = ordered_sum(csb + t * stride, B);
             __syncthreads();  // csb is rewritten by the next chunk
         }
         for (int i = threadIdx.x; i < hi - lo; i += blockDim.x)
@@ -903,6 +899,8 @@ __device__ __forceinline__ void srv_job(const SrvCmd &c, int B, uint4 *lds, cons
 // Command-record fields as 32-bit words (the record is copied word by word).
 constexpr int kSrvCmdWords = static_cast<int>(sizeof(SrvCmd) / 4);
 static_assert(sizeof(SrvCmd) % 4 == 0, "command record in words");
+static_assert(kSrvCmdWords <= 64 * kSrvWaves, "one record word per thread");
+static_assert(kSrvCopyDepth * 64 * kSrvWaves * 4 >= 16384, "x of K <= 16384 in one batch");
 
 __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd *cmd, const float *hx,
                                                                             SrvDev *dev, float *dx,
@@ -913,7 +911,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
     __shared__ int32_t shk;       // K of this command (workgroup 0)
     __shared__ SrvCmd cs;         // this command
     __shared__ float outb[kSrvOutMax];
-    __shared__ float csb[kSrvCsFloats];  // block contributions (Q8_0 jobs)
+    __shared__ __align__(16) float csb[kSrvCsFloats];  // block contributions (Q8_0 jobs)
     const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
     uint32_t *csw = reinterpret_cast<uint32_t *>(&cs);
     for (uint32_t expect = first;; ++expect) {
@@ -944,30 +942,32 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                 return;
             }
             // the record and x in one round trip: K came with the command
-            // number; x in 16-byte pieces, kSrvCopyDepth loads in flight per
-            // thread (K is a multiple of 256, so K / 4 pieces)
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(cmd);
-            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
-                csw[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            const int K4 = shk / 4;
+            // number; x in 16-byte pieces, kSrvCopyDepth per thread (one batch,
+            // K <= 16384), issued before the record's words so that one wait
+            // covers both; stores past the K / 4 pieces fall outside the
+            // descriptor's range and are dropped
+            const int K4 = __builtin_amdgcn_readfirstlane(shk / 4);  // uniform: descriptors in SGPRs
             const __amdgpu_buffer_rsrc_t hs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(hx), 0, static_cast<uint32_t>(16 * K4), kBufferWord3);
             const __amdgpu_buffer_rsrc_t ds =
                 __builtin_amdgcn_make_buffer_rsrc(dx, 0, static_cast<uint32_t>(16 * K4), kBufferWord3);
-            for (int base = 0; base < K4; base += kSrvCopyDepth * 64 * kSrvWaves) {
-                u32x4 v[kSrvCopyDepth];
+            u32x4 v[kSrvCopyDepth];
 #pragma unroll
-                for (int k = 0; k < kSrvCopyDepth; ++k)
-                    v[k] = __builtin_amdgcn_raw_buffer_load_b128(
-                        hs, 16 * (base + k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)), 0, kSysCoherent);
+            for (int k = 0; k < kSrvCopyDepth; ++k)
+                v[k] = __builtin_amdgcn_raw_buffer_load_b128(hs, 16 * (k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)),
+                                                             0, kSysCoherent);
+            const bool rec = static_cast<int>(threadIdx.x) < kSrvCmdWords;
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(cmd);
+            const uint32_t w = __hip_atomic_load(&src[rec ? threadIdx.x : 0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 #pragma unroll
-                for (int k = 0; k < kSrvCopyDepth; ++k)
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        v[k], ds, 16 * (base + k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)), 0, kSysCoherent);
-            }
+            for (int k = 0; k < kSrvCopyDepth; ++k)
+                __builtin_amdgcn_raw_buffer_store_b128(v[k], ds, 16 * (k * 64 * kSrvWaves + static_cast<int>(threadIdx.x)),
+                                                       0, kSysCoherent);
             uint32_t *dcw = reinterpret_cast<uint32_t *>(&dev->cmd);
-            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
-                __hip_atomic_store(&dcw[i], csw[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (rec) {
+                csw[threadIdx.x] = w;
+                __hip_atomic_store(&dcw[threadIdx.x], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
             __builtin_amdgcn_s_waitcnt(0);  // every copy store has completed
             __syncthreads();  // and the record is in LDS
             if (threadIdx.x == 0) __hip_atomic_store(&dev->seq[0], expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1479,8 +1479,7 @@ __device__ __forceinline__ void q8_body(const J &jobs, int n_groups, const float
         grp.load(W, gl * ROWS + wave * R, N, B, row_bytes, lane);
         __syncthreads();
         if (lane < R) {
-            float sumf = 0.0f;
-            for (int b = 0; b < B; ++b) sumf = (sumf + cs[lane * B + b]);
+            const float sumf = ordered_sum(cs + lane * B, B);
             if (row0 + lane < nr) yr[row0 + lane] = sumf;
         }
         __syncthreads();
