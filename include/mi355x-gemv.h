@@ -88,11 +88,12 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 
 /* Per-context options.
  *   MI355X_OPT_VARIANT: which kernel family computes GEMVs --
- *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply,
- *       for the K/IQ types f32 activations, except Q4_K/Q5_K/Q6_K rows of at
- *       most 4096 values, which take the pipelined form's 22-bit digits, and
- *       IQ3_S/IQ3_XXS/IQ2_S rows of at most 8192 values with N >= 4096,
- *       which take the digit row form at two rows per wavefront),
+ *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply;
+ *       for the K/IQ types 22-bit activation digits for Q4_K (the pipelined
+ *       form up to 4096 values per row, the row form beyond), Q5_K, Q6_K
+ *       rows of at most 4096 values, and IQ3_S/IQ3_XXS/IQ2_S rows of at
+ *       most 8192 values with N >= 4096 (row form, two rows per wavefront),
+ *       f32 activations for the rest: Q3_K, IQ4_XS, longer Q6_K rows),
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit

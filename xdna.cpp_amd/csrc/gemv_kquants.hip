@@ -2083,31 +2083,40 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         return MI355X_OK;
     }
 
-    // f32 activations unless the caller asks for the digit path, or (AUTO)
-    // for the grid types at up to four steps per row, where the digit row
-    // kernel with two rows per wavefront step is measured as fast or faster
-    // (8192x8192 on MI355X: IQ3_XXS 12.7 vs 13.2 us, IQ3_S 13.9 vs 14.5,
-    // IQ2_S 12.9 vs 12.9): its table-driven sign application and dot4
-    // products cost fewer VALU instructions than the f32 decode
     const bool grid_type = a.type == MI355X_TYPE_IQ3_S || a.type == MI355X_TYPE_IQ3_XXS || a.type == MI355X_TYPE_IQ2_S;
     const bool dg_forced = ctx->kernel_variant == MI355X_VARIANT_DIGITS;
 
     // equal chunks of at most kChunkBlocks superblocks
     const int64_t n_chunks = (B + kChunkBlocks - 1) / kChunkBlocks;
     const int64_t per_chunk = (B + n_chunks - 1) / n_chunks;
-    // Pipelined form (digit numerics).  By default (sweeps on MI355X) for
-    // Q4_K, Q5_K and Q6_K with at most two steps per row (K <= 4096):
-    // 14336x4096 Q4_K 10.2 vs 11.7 us, Q5_K 12.2 vs 12.9, Q6_K 13.6 vs 15.8.
-    // Longer rows, Q3_K and the IQ types stay on the kernel above, whose
-    // several workgroups per CU hide more of their heavier decode.
-    const bool pl_types = a.type == MI355X_TYPE_Q4_K || a.type == MI355X_TYPE_Q5_K || a.type == MI355X_TYPE_Q6_K;
+    // Default forms (variant and form AUTO), from sweeps of the BASELINE
+    // shapes on MI355X (us, 14336x4096 / 4096x14336; 8192x8192 for IQ):
+    //  * Q4_K: pipelined form up to two steps per row (10.5 vs 10.8 digit
+    //    rows, 11.1 f32 rows), digit rows beyond (11.5 vs 12.9 f32);
+    //  * Q5_K: digit rows (11.7 / 13.1 vs pipelined 12.6, f32 12.2 / 13.6);
+    //  * Q6_K: digit rows up to two steps (12.4 vs pipelined 13.0, f32 12.6),
+    //    f32 rows beyond (14.3 vs 14.8 digits);
+    //  * IQ3_S, IQ3_XXS, IQ2_S up to four steps (N >= 4096): digit rows, two
+    //    rows per wavefront step (13.2 / 11.9 / 12.2 vs f32 15.4 / 14.0 /
+    //    13.4): table-driven sign application and dot4 products cost fewer
+    //    VALU instructions than the f32 decode;
+    //  * Q3_K, IQ4_XS and the rest: f32 rows, one row per step (Q3_K 11.7
+    //    vs 13.0 with two rows, 13.6 digits).
+    const bool auto_form = ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO;
+    auto pl_auto = [&](int nit) { return a.type == MI355X_TYPE_Q4_K && nit <= 2; };
+    auto dg_rows_auto = [&](int nit) {
+        switch (a.type) {
+        case MI355X_TYPE_Q4_K:
+        case MI355X_TYPE_Q5_K: return true;
+        case MI355X_TYPE_Q6_K: return nit <= 2;
+        default: return grid_type && nit <= max_nit_r2(a.type) && a.N >= 4096;
+        }
+    };
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
         const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
         const bool pl = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 &&
-                        (ctx->form_override == MI355X_FORM_PIPE ||
-                         (ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO &&
-                          pl_types && nit <= 2));
+                        (ctx->form_override == MI355X_FORM_PIPE || (auto_form && pl_auto(nit)));
         const bool xs = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && ctx->form_override == MI355X_FORM_KSPLIT;
         if (xs) {
             const int rb = ctx->rows_override == 2 || ctx->rows_override == 4 ? ctx->rows_override
@@ -2152,10 +2161,9 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
             MI355X_HIP(hipGetLastError());
             continue;
         }
-        const bool dg_auto = ctx->kernel_variant == MI355X_VARIANT_AUTO && grid_type && nit <= max_nit_r2(a.type) &&
-                             a.N >= 4096;
+        const bool dg_auto = ctx->kernel_variant == MI355X_VARIANT_AUTO && dg_rows_auto(nit);
         const bool dg = dg_forced || dg_auto;
-        int R = (a.N >= 8192 && nit <= kMaxNitR2) || dg_auto ? 2 : 1;
+        int R = dg_auto && grid_type ? 2 : 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
         const int64_t n_groups = (a.N + R - 1) / R;
