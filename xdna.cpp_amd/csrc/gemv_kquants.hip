@@ -553,7 +553,8 @@ struct Kq<MI355X_TYPE_IQ2_S> {
 // staged slice record (lane-major, as the f32 records above) holds, per
 // digit plane, the 4 runs' 8 bytes in position order (slots 2p, 2p + 1),
 // then e(b) of the block each run lies in (slot 6) and each run's sum of Z
-// (slot 7).
+// (slot 7); K4 records, whose computes take an exponent and a Z sum per
+// 16-value half, hold those four words in slot 6 (one full-width read).
 // Weight codes (small unsigned integers, or signed bytes for the signed
 // codebooks) meet the digits in v_dot4_i32_i8: sum_i code_i * Z_i over a run
 // is s0 + 2^8 s1 + 2^16 s2 with s_p = sum_i code_i * z_p,i, exact in int32.
@@ -643,23 +644,22 @@ __device__ __forceinline__ void dg_slice_lm(const uint8_t *rec, XDig &x) {
     const int4 E = *reinterpret_cast<const int4 *>(rec + kLmSlot * 6);
     if constexpr (SH == kS32) {
         x.e[0] = E.x;
+    } else if constexpr (SH == kK4) {
+        // slot 6 holds both halves' exponents and Z sums (put_record_dg)
+        x.e[0] = E.x;
+        x.e[1] = E.y;
+        x.zs[0] = __builtin_bit_cast(float, E.z);
+        x.zs[1] = __builtin_bit_cast(float, E.w);
     } else {
         const float4 Z = *reinterpret_cast<const float4 *>(rec + kLmSlot * 7);
-        if constexpr (SH == kK4) {
-            x.e[0] = E.x;
-            x.e[1] = E.z;
-            x.zs[0] = Z.x + Z.y;
-            x.zs[1] = Z.z + Z.w;
-        } else {
-            x.e[0] = E.x;
-            x.e[1] = E.y;
-            x.e[2] = E.z;
-            x.e[3] = E.w;
-            x.zs[0] = Z.x;
-            x.zs[1] = Z.y;
-            x.zs[2] = Z.z;
-            x.zs[3] = Z.w;
-        }
+        x.e[0] = E.x;
+        x.e[1] = E.y;
+        x.e[2] = E.z;
+        x.e[3] = E.w;
+        x.zs[0] = Z.x;
+        x.zs[1] = Z.y;
+        x.zs[2] = Z.z;
+        x.zs[3] = Z.w;
     }
 }
 
@@ -931,8 +931,14 @@ __device__ __forceinline__ void put_record_dg(uint8_t *rec, const float4 (&v)[8]
             *reinterpret_cast<uint4 *>(rec + kLmSlot * (2 * p + 1)) =
                 make_uint4(pl[p][4], pl[p][5], pl[p][6], pl[p][7]);
         }
-        *reinterpret_cast<int4 *>(rec + kLmSlot * 6) = make_int4(ef[0], ef[1], ef[2], ef[3]);
-        *reinterpret_cast<float4 *>(rec + kLmSlot * 7) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+        if constexpr (SH == kK4) {
+            // the reader needs each 16-value half's exponent and Z sum: one slot
+            *reinterpret_cast<int4 *>(rec + kLmSlot * 6) =
+                make_int4(ef[0], ef[2], __builtin_bit_cast(int, zs[0] + zs[1]), __builtin_bit_cast(int, zs[2] + zs[3]));
+        } else {
+            *reinterpret_cast<int4 *>(rec + kLmSlot * 6) = make_int4(ef[0], ef[1], ef[2], ef[3]);
+            *reinterpret_cast<float4 *>(rec + kLmSlot * 7) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+        }
     }
 }
 
