@@ -160,15 +160,20 @@ KQ_TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 IQ_TYPES = {"IQ2_S": 22, "IQ3_S": 21, "IQ3_XXS": 18, "IQ4_XS": 23}
 
 
+def synthetic_grids():
+    """IQ3_XXS / IQ2_S codebooks of odd bytes 1..63 (seeded), installed once."""
+    rng = np.random.default_rng(0)
+    for t, (n, w) in ((18, (256, 4)), (22, (1024, 8))):
+        g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
+        mi355x.set_iq_grid(t, g.view(np.uint32 if w == 4 else np.uint64).reshape(n))
+
+
 def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
     """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
     (rotated) weights.  Inputs are random valid blocks (any encoding is a
     valid input for a dequant-dot kernel); IQ3_XXS / IQ2_S run with a
     synthetic grid, as ggml's grids are not part of this build."""
-    rng = np.random.default_rng(0)
-    for t, (n, w) in ((18, (256, 4)), (22, (1024, 8))):
-        g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
-        mi355x.set_iq_grid(t, g.view(np.uint32 if w == 4 else np.uint64).reshape(n))
+    synthetic_grids()
     res = {}
     shapes = [(name, t, N, K) for name, t in KQ_TYPES.items() for (N, K) in ((14336, 4096), (4096, 14336))]
     shapes += [(name, t, 8192, 8192) for name, t in IQ_TYPES.items()]
@@ -180,6 +185,32 @@ def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
         res[f"{name} {N}x{K}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
         log(f"bench: {name} {N}x{K}: {ms * 1e3:.2f} us, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+    return res
+
+
+def rows_sweep(ctx, steps, warmup, settle_s=0.0):
+    """Duration against row count for two K/IQ types at a fixed K (rotated
+    weights): t(N) = fixed + N * per_row by least squares over N >= 1024.
+    The fixed part is what a launch costs before and after its rows
+    (dispatch, activation and codebook staging, the last reduction); the
+    per-row slope gives the marginal rate once many rows share that cost."""
+    synthetic_grids()
+    res = {}
+    for name, t, K in (("IQ2_S", IQ_TYPES["IQ2_S"], 8192), ("Q4_K", KQ_TYPES["Q4_K"], 4096)):
+        pts = []
+        for N in (256, 1024, 4096, 8192, 16384, 32768):
+            raw = synth.random_blocks(t, N, K, seed=7)
+            x = synth.activations(K, seed=43)
+            ms, _, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
+            pts.append((N, ms * 1e3))
+        fit = np.polyfit([n for n, _ in pts if n >= 1024], [u for n, u in pts if n >= 1024], 1)
+        per_row_ns, fixed_us = fit[0] * 1e3, fit[1]
+        row_b = algorithmic_bytes(t, 1, K) - 4 * K
+        res[f"{name} K={K}"] = {"us": {str(n): round(u, 3) for n, u in pts}, "fixed_us": round(fixed_us, 3),
+                                "per_row_ns": round(per_row_ns, 4),
+                                "marginal_GB/s": round(row_b / per_row_ns, 1)}
+        log(f"bench: rows sweep {name} K={K}: " + ", ".join(f"{n}: {u:.2f} us" for n, u in pts) +
+            f"; fit {fixed_us:.2f} us + {per_row_ns:.3f} ns/row ({row_b / per_row_ns:.0f} GB/s marginal)")
     return res
 
 
@@ -373,6 +404,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
     ap.add_argument("--kquants", action="store_true",
                     help="also time the K-quant (14336x4096, 4096x14336) and IQ (8192x8192) BASELINE configs")
+    ap.add_argument("--rows-sweep", action="store_true",
+                    help="also time IQ2_S (K=8192) and Q4_K (K=4096) at N = 256..32768 rows: fixed cost + per row")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one device-to-device copy of 256 MiB (a plain copy kernel of known size, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -437,6 +470,7 @@ def main() -> int:
         kq = {}
         if args.kquants:
             kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle)
+        rs = rows_sweep(ctx, args.steps, args.warmup, args.settle) if args.rows_sweep else {}
 
     # the timed output must still be the right answer (checked, not measured)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -492,6 +526,8 @@ def main() -> int:
         out["sweep"] = sweep
     if kq:
         out["kquants"] = kq
+    if rs:
+        out["rows_sweep"] = rs
     if not args.no_cpu:
         log(f"bench: CPU baseline for ~{args.cpu_seconds:.0f} s")
         out["cpu_baseline"] = cpu_baseline(raw, N, K, x, args.cpu_seconds)
