@@ -161,24 +161,36 @@ IQ_TYPES = {"IQ2_S": 22, "IQ3_S": 21, "IQ3_XXS": 18, "IQ4_XS": 23}
 
 
 def synthetic_grids():
-    """IQ3_XXS / IQ2_S codebooks of odd bytes 1..63 (seeded), installed once."""
+    """IQ3_XXS / IQ2_S codebooks of odd bytes 1..63 (seeded), installed; with
+    IQ3_S's own codebook, the grids the quantizer encodes against."""
     rng = np.random.default_rng(0)
+    grids = {21: synth.iq3s_grid()}
     for t, (n, w) in ((18, (256, 4)), (22, (1024, 8))):
         g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
-        mi355x.set_iq_grid(t, g.view(np.uint32 if w == 4 else np.uint64).reshape(n))
+        grids[t] = g.view(np.uint32 if w == 4 else np.uint64).reshape(n)
+        mi355x.set_iq_grid(t, grids[t])
+    return grids
+
+
+def kq_weights(t, N, K, grids, seed=7):
+    """BASELINE configs 3 and 4: f32 N(0, 0.02) weights (IQ types: 1% of them
+    x8) quantized to type t."""
+    heavy = t in IQ_TYPES.values()
+    w = synth.heavy_tail_weights(N, K, seed) if heavy else synth.normal_weights(N, K, seed)
+    return synth.quantize_kq(t, w, grids.get(t))
 
 
 def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
     """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
-    (rotated) weights.  Inputs are random valid blocks (any encoding is a
-    valid input for a dequant-dot kernel); IQ3_XXS / IQ2_S run with a
-    synthetic grid, as ggml's grids are not part of this build."""
-    synthetic_grids()
+    (rotated) weights, built by the configs' recipe (kq_weights); IQ3_XXS /
+    IQ2_S run with a synthetic grid, as ggml's grids are not part of this
+    build."""
+    grids = synthetic_grids()
     res = {}
     shapes = [(name, t, N, K) for name, t in KQ_TYPES.items() for (N, K) in ((14336, 4096), (4096, 14336))]
     shapes += [(name, t, 8192, 8192) for name, t in IQ_TYPES.items()]
     for name, t, N, K in shapes:
-        raw = synth.random_blocks(t, N, K, seed=7)
+        raw = kq_weights(t, N, K, grids)
         x = synth.activations(K, seed=43)
         ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
         gbs = algorithmic_bytes(t, N, K) / (ms * 1e-3) / 1e9
@@ -194,12 +206,14 @@ def rows_sweep(ctx, steps, warmup, settle_s=0.0):
     The fixed part is what a launch costs before and after its rows
     (dispatch, activation and codebook staging, the last reduction); the
     per-row slope gives the marginal rate once many rows share that cost."""
-    synthetic_grids()
+    grids = synthetic_grids()
     res = {}
     for name, t, K in (("IQ2_S", IQ_TYPES["IQ2_S"], 8192), ("Q4_K", KQ_TYPES["Q4_K"], 4096)):
         pts = []
-        for N in (256, 1024, 4096, 8192, 16384, 32768):
-            raw = synth.random_blocks(t, N, K, seed=7)
+        rows = (256, 1024, 4096, 8192, 16384, 32768)
+        full = kq_weights(t, max(rows), K, grids)
+        for N in rows:
+            raw = np.ascontiguousarray(full[:N])
             x = synth.activations(K, seed=43)
             ms, _, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
             pts.append((N, ms * 1e3))
@@ -526,6 +540,8 @@ def main() -> int:
         out["sweep"] = sweep
     if kq:
         out["kquants"] = kq
+        out["kquants_data"] = ("f32 N(0,0.02) weights (seed 7; IQ types with 1% of them x8) quantized per type by "
+                               "synth.quantize_kq, x ~ N(0,1) (seed 43); IQ3_XXS/IQ2_S on synthetic grids")
     if rs:
         out["rows_sweep"] = rs
     if not args.no_cpu:

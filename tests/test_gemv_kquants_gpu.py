@@ -8,6 +8,8 @@ the prepack round trip.  IQ3_XXS / IQ2_S run with a synthetic grid installed
 through mi355x_set_iq_grid (their ggml grids are not available here), so
 their parity is against the oracle's restatement only.
 """
+import functools
+
 import numpy as np
 import pytest
 
@@ -75,8 +77,21 @@ def run(ctx, t, raw, N, K, x):
         w.free()
 
 
-def parity(ctx, oracle, t, N, K, seed, x=None, what=""):
-    raw = blocks(t, N, K, seed)
+@functools.lru_cache(maxsize=16)
+def quantized(t, N, K, seed):
+    """The BASELINE recipe: f32 N(0, 0.02) weights quantized to type t (IQ
+    types: with 1% of the weights scaled by 8), on the installed grids."""
+    if t in (18, 21, 22, 23):
+        w = synth.heavy_tail_weights(N, K, seed)
+    else:
+        w = synth.normal_weights(N, K, seed)
+    grid = synth.iq3s_grid() if t == 21 else GRIDS.get(t)
+    return synth.quantize_kq(t, w, grid)
+
+
+def parity(ctx, oracle, t, N, K, seed, x=None, what="", raw=None):
+    if raw is None:
+        raw = blocks(t, N, K, seed)
     if x is None:
         x = np.random.default_rng(seed + 1).uniform(-0.5, 0.5, K).astype(np.float32)
     y = run(ctx, t, raw, N, K, x)
@@ -103,14 +118,22 @@ def test_parity_two_lds_chunks(ctx, oracle, name):
 @pytest.mark.parametrize("name", ["Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_parity_baseline_kquant_shapes(ctx, oracle, name, N, K):
-    # BASELINE config 3 at full size
-    parity(ctx, oracle, REF_TYPES[name], N, K, seed=3)
+    # BASELINE config 3 at full size: random blocks, then the config's own
+    # recipe (quantized N(0, 0.02) weights, N(0, 1) activations)
+    t = REF_TYPES[name]
+    parity(ctx, oracle, t, N, K, seed=3)
+    parity(ctx, oracle, t, N, K, seed=3, x=synth.activations(K, seed=43), raw=quantized(t, N, K, 3),
+           what=f"{name} {N}x{K} quantized")
 
 
 @pytest.mark.parametrize("name", ["IQ2_S", "IQ3_S", "IQ3_XXS", "IQ4_XS"])
 def test_parity_baseline_iq_shape(ctx, oracle, name):
-    # BASELINE config 4 at full size (8192 x 8192)
-    parity(ctx, oracle, ALL[name], 8192, 8192, seed=4)
+    # BASELINE config 4 at full size (8192 x 8192), random blocks and the
+    # config's recipe (N(0, 0.02) weights with 1% x8 outliers, quantized)
+    t = ALL[name]
+    parity(ctx, oracle, t, 8192, 8192, seed=4)
+    parity(ctx, oracle, t, 8192, 8192, seed=4, x=synth.activations(8192, seed=43), raw=quantized(t, 8192, 8192, 4),
+           what=f"{name} 8192x8192 quantized")
 
 
 @pytest.mark.parametrize("name", list(ALL))

@@ -670,6 +670,79 @@ def test_quantize_q4_0_invariants(oracle):
     assert np.array_equal(at, -8 * d)
 
 
+# ---- the K/IQ quantizers used to build the BASELINE configs ------------------
+# synth.quantize_kq encodes f32 weights per type; decoding its blocks through
+# the (pinned) oracle must give back the weights up to each format's
+# quantization error.  A wrong nibble order, shift or sign in the encoder gives
+# errors of the order of the weights themselves (relative RMS ~1), far above
+# these bounds (about 1.25 x what the encoder reaches on these inputs).
+
+KQ_RMS_BOUND = {  # (N(0, 0.02), N(0, 0.02) with 1% x8 outliers)
+    "Q3_K": (0.19, 0.24), "Q4_K": (0.10, 0.12), "Q5_K": (0.048, 0.059), "Q6_K": (0.024, 0.033),
+    "IQ4_XS": (0.10, 0.133), "IQ3_S": (0.172, 0.218),
+    # synthetic grids (random odd magnitudes) fit the weights far worse than ggml's
+    "IQ3_XXS": (0.32, 0.61), "IQ2_S": (0.39, 0.68)}
+KQ_TYPE_IDS = {"Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "IQ4_XS": IQ4_XS, "IQ3_S": IQ3_S,
+               "IQ3_XXS": IQ3_XXS, "IQ2_S": IQ2_S}
+
+
+def quant_grid(t):
+    if t == IQ3_S:
+        return synth.iq3s_grid()
+    rng = np.random.default_rng(t)
+    n, w = (256, 4) if t == IQ3_XXS else (1024, 8)
+    g = (2 * rng.integers(0, 32, (n, w)) + 1).astype(np.uint8)
+    return g.view(np.uint32 if w == 4 else np.uint64).reshape(n)
+
+
+def test_iq3s_grid_table_matches_oracle(oracle):
+    # the quantizer reads the kernels' compiled-in table; the oracle's is
+    # pinned against the reference build by hash
+    assert np.array_equal(synth.iq3s_grid(), extract_iq3s_grid(oracle))
+
+
+def test_heavy_tail_weights_recipe():
+    base = synth.normal_weights(256, 1024, seed=5)
+    w = synth.heavy_tail_weights(256, 1024, seed=5)
+    changed = w != base
+    assert 0.008 < changed.mean() < 0.012
+    assert np.array_equal(w[changed], base[changed] * np.float32(8))
+
+
+@pytest.mark.parametrize("recipe", ["normal", "heavy_tail"])
+@pytest.mark.parametrize("name", list(KQ_RMS_BOUND))
+def test_kq_quantizer_round_trip(oracle, name, recipe):
+    t = KQ_TYPE_IDS[name]
+    N, K = 16, 2048
+    w = synth.normal_weights(N, K, 3) if recipe == "normal" else synth.heavy_tail_weights(N, K, 3)
+    grid = quant_grid(t) if t in (IQ3_S, IQ3_XXS, IQ2_S) else None
+    raw = synth.quantize_kq(t, w, grid)
+    assert raw.shape == (N, K // 256 * oracle.block_bytes(t))
+    deq = np.stack([oracle.dequant_row(t, raw[r], K, grid=grid if t != IQ3_S else None) for r in range(N)])
+    assert np.all(np.isfinite(deq))
+    rel = np.sqrt(np.mean((deq - w) ** 2) / np.mean(w ** 2))
+    assert rel < KQ_RMS_BOUND[name][recipe != "normal"], (name, recipe, rel)
+    # row by row the same (rows are quantized independently, on threads)
+    one = synth.quantize_kq(t, w[5:6], grid)
+    assert np.array_equal(one[0], raw[5])
+
+
+def test_kq_quantizer_zero_and_constant_blocks(oracle):
+    # an all-zero superblock encodes to zero for every type; a constant block
+    # is reproduced to within the format's step (grid types: to within the
+    # spacing of the grid's entries, which holds no constant entry at the
+    # top of its range, and with every sign right)
+    for name, t in KQ_TYPE_IDS.items():
+        grid = quant_grid(t) if t in (IQ3_S, IQ3_XXS, IQ2_S) else None
+        g = grid if t in (IQ3_XXS, IQ2_S) else None
+        z = synth.quantize_kq(t, np.zeros((1, 256), np.float32), grid)
+        assert np.all(oracle.dequant_row(t, z[0], 256, grid=g) == 0), name
+        c = synth.quantize_kq(t, np.full((1, 256), -0.03, np.float32), grid)
+        v = oracle.dequant_row(t, c[0], 256, grid=g)
+        tol = 0.6 if grid is not None else 0.15
+        assert np.all(v < 0) and np.all(np.abs(v + 0.03) <= 0.03 * tol), (name, v[:4])
+
+
 # ---- ggml-cpu Q4_0 x Q8_0 numerics (external restatement) -------------------
 # ggml is not vendored in the reference, so this path cannot be compared with
 # ggml itself here ("parity unpinned"); what the mathematics fixes is pinned.
