@@ -89,11 +89,12 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 /* Per-context options.
  *   MI355X_OPT_VARIANT: which kernel family computes GEMVs --
  *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply;
- *       for the K/IQ types 22-bit activation digits for Q4_K (the pipelined
- *       form up to 4096 values per row, the row form beyond), Q5_K, Q6_K
- *       rows of at most 4096 values, and IQ3_S/IQ3_XXS/IQ2_S rows of at
- *       most 8192 values with N >= 4096 (row form, two rows per wavefront),
- *       f32 activations for the rest: Q3_K, IQ4_XS, longer Q6_K rows),
+ *       for the K/IQ types 22-bit activation digits (row form) for Q4_K,
+ *       Q5_K, Q6_K rows of at most 4096 values, IQ4_XS rows of at most 8192
+ *       values, and IQ3_S/IQ3_XXS/IQ2_S rows of at most 8192 values with
+ *       N >= 4096 (two rows per wavefront), f32 activations for the rest:
+ *       Q3_K, longer IQ4_XS and Q6_K rows; Q3_K and Q5_K rows of at most
+ *       4096 values with prefetch),
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
@@ -112,7 +113,8 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     (digit-plane Q4_0 kernel).
  *   MI355X_OPT_GRID: 0 (auto) or a cap on the number of workgroups.
  *   MI355X_OPT_PREFETCH: 0 (auto), 1 (each wavefront requests its next row
- *     group before reducing the current one), 2 (off).
+ *     group before reducing the current one -- for the K/IQ row form before
+ *     decoding it, one row per wavefront step), 2 (off).
  *   MI355X_OPT_FORM: work split of the digit-plane kernels (Q4_0; the
  *     pipelined form also for the K/IQ types) --
  *     MI355X_FORM_AUTO (default), MI355X_FORM_ROWS (a wavefront owns whole

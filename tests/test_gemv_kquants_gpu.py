@@ -42,19 +42,28 @@ def install_grids():
     yield
 
 
-@pytest.fixture(params=["digits", "exact_f32", "pipelined"], autouse=True)
+@pytest.fixture(params=["digits", "exact_f32", "pipelined", "digits_prefetch", "f32_prefetch", "auto"], autouse=True)
 def variant(request, ctx):
-    """Every test runs on the three kernel families: activations as 22-bit
-    digit planes with integer dot products (several workgroups per CU), f32
-    activations as given, and the pipelined form (digit arithmetic, one
-    workgroup per CU, each lane's digit slices kept in registers)."""
-    v = mi355x.VARIANT_EXACT_F32 if request.param == "exact_f32" else mi355x.VARIANT_DIGITS
-    ctx.set_option(mi355x.OPT_VARIANT, v)
-    if request.param == "pipelined":
+    """Every test runs on each kernel family: activations as 22-bit digit
+    planes with integer dot products (several workgroups per CU), f32
+    activations as given, the pipelined form (digit arithmetic, one
+    workgroup per CU, each lane's digit slices kept in registers), the row
+    form with prefetch (each wavefront's next row group requested before
+    the current one's decode) in both arithmetics, and the defaults."""
+    p = request.param
+    if p != "auto":
+        v = mi355x.VARIANT_EXACT_F32 if p.startswith(("exact", "f32")) else mi355x.VARIANT_DIGITS
+        ctx.set_option(mi355x.OPT_VARIANT, v)
+    if p == "pipelined":
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_PIPE)
-    yield request.param
+    if p.endswith("prefetch"):
+        ctx.set_option(mi355x.OPT_PREFETCH, 1)
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 1)
+    yield p
     ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
     ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
+    ctx.set_option(mi355x.OPT_PREFETCH, 0)
+    ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
 
 
 def blocks(t, N, K, seed):

@@ -845,6 +845,15 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
     }
 };
 
+// Byte J of each of four words, gathered into one word (byte t from w_t):
+// two v_perm (selector 0x0C gives a zero byte) and an or.
+template <int J>
+__device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    constexpr uint32_t lo = 0x0C0C0000u | ((4u + J) << 8) | J;
+    constexpr uint32_t hi = ((4u + J) << 24) | (static_cast<uint32_t>(J) << 16) | 0x0C0Cu;
+    return __builtin_amdgcn_perm(w1, w0, lo) | __builtin_amdgcn_perm(w3, w2, hi);
+}
+
 // One DPP move of a float: row_ror:8 (the lane 8 apart within its row of 16)
 __device__ __forceinline__ float ror8_f(float v) {
     return __builtin_bit_cast(float, dpp_i<0x128>(__builtin_bit_cast(int, v)));
@@ -897,32 +906,36 @@ __device__ __forceinline__ void put_record_dg(uint8_t *rec, const float4 (&v)[8]
         const int se = min(275 - E, 254);  // biased exponent of s = 2^-e: m * s in [2^21, 2^22)
         const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
         ef[p] = 127 - se;
-        zs[p] = 0.f;
+        // F = bits of 1.5 * 2^23 + v * s: |v * s| < 2^22, so the sum lies in
+        // [2^23, 2^24) where f32 spacing is 1 and F = 0x4B400000 + Z, Z the
+        // rounded integer.  The signed digits z0 + 2^8 z1 + 2^16 z2 = Z
+        // (z0, z1 in [-128, 127]) have z0 = sext(byte 0 of Z), z1 = sext(byte
+        // 1 of Z + 128) and z2 = (Z + 32896) >> 16, whose byte is byte 2 of
+        // Z + 32896; 0x4B400000 adds nothing below bit 16 and 0x40 to byte
+        // 2, so the three digit bytes are bytes 0, 1, 2 of F, F + 128 and
+        // F + 32896 - 0x400000.
+        uint32_t F[8], G1[8], G2[8];
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const float4 f = v[2 * p + w];
             const float q[4] = {f.x, f.y, f.z, f.w};
-            uint32_t b0 = 0, b1 = 0, b2 = 0;
-            int zsum = 0;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                // round to nearest integer: |v * s| < 2^22, so 1.5 * 2^23 + v * s
-                // lies in [2^23, 2^24) where f32 spacing is 1
-                const int Z = __builtin_bit_cast(int, fmaf(q[t], sc, 12582912.0f)) - 0x4B400000;
-                const int z0 = (Z << 24) >> 24;
-                const int Z1 = (Z - z0) >> 8;
-                const int z1 = (Z1 << 24) >> 24;
-                const int z2 = (Z1 - z1) >> 8;
-                b0 |= (static_cast<uint32_t>(z0) & 0xFFu) << (8 * t);
-                b1 |= (static_cast<uint32_t>(z1) & 0xFFu) << (8 * t);
-                b2 |= (static_cast<uint32_t>(z2) & 0xFFu) << (8 * t);
-                zsum += Z;
+                F[4 * w + t] = __builtin_bit_cast(uint32_t, fmaf(q[t], sc, 12582912.0f));
+                G1[4 * w + t] = F[4 * w + t] + 128u;
+                G2[4 * w + t] = F[4 * w + t] + (32896u - 0x400000u);
             }
-            pl[0][2 * p + w] = b0;
-            pl[1][2 * p + w] = b1;
-            pl[2][2 * p + w] = b2;
-            zs[p] += static_cast<float>(zsum);
         }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            pl[0][2 * p + w] = gather_byte<0>(F[4 * w], F[4 * w + 1], F[4 * w + 2], F[4 * w + 3]);
+            pl[1][2 * p + w] = gather_byte<1>(G1[4 * w], G1[4 * w + 1], G1[4 * w + 2], G1[4 * w + 3]);
+            pl[2][2 * p + w] = gather_byte<2>(G2[4 * w], G2[4 * w + 1], G2[4 * w + 2], G2[4 * w + 3]);
+        }
+        // sum of the eight Z: the F sum less 8 * 0x4B400000 (mod 2^32; the
+        // true sum is below 2^25 in magnitude)
+        const uint32_t fs = (F[0] + F[1] + F[2]) + (F[3] + F[4] + F[5]) + (F[6] + F[7]);
+        zs[p] = static_cast<float>(static_cast<int>(fs - 8u * 0x4B400000u));
     }
     if (store) {
 #pragma unroll
@@ -1004,10 +1017,12 @@ struct GridRegs {
 };
 
 // ---- kernel ------------------------------------------------------------------
+// Buffer views of the R rows of group g; with live == false an empty range
+// (loads through it return zeros and read nothing).
 template <int TYPE, int R>
-__device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows)[R]) {
+__device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows)[R], bool live = true) {
     constexpr KqLayout L = kq_layout(TYPE);
-    const uint32_t records = static_cast<uint32_t>(a.row_bytes);
+    const uint32_t records = live ? static_cast<uint32_t>(a.row_bytes) : 0u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t row = g * R + r < a.N ? g * R + r : a.N - 1;
@@ -1029,9 +1044,9 @@ __device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows
 // clamped into the chunk; lanes past the chunk's end are masked at use).
 template <int TYPE, int R, int NIT>
 __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, int bl,
-                                           typename Kq<TYPE>::Regs (&regs)[R][NIT]) {
+                                           typename Kq<TYPE>::Regs (&regs)[R][NIT], bool live = true) {
     Row rows[R];
-    make_rows<TYPE, R>(a, g, rows);
+    make_rows<TYPE, R>(a, g, rows, live);
 #pragma unroll
     for (int t = 0; t < NIT; ++t) {
         const int bloc = kBlocksPerStep * t + bl;
@@ -1044,7 +1059,54 @@ __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, in
 
 static_assert(kChunkBlocks <= kBlocksPerStep * kWaves, "one staged record per thread");
 
+// One row group: its NIT steps against the staged activations, then the
+// wavefront sums and the stores of its R outputs.
 template <int TYPE, int R, int NIT, bool DG>
+__device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, const typename Kq<TYPE>::Regs (&regs)[R][NIT],
+                                             const uint8_t *lds, const uint32_t *grid, int s, int bl, int lane) {
+    using K = Kq<TYPE>;
+    constexpr int SH = slice_shape(TYPE);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NIT; ++t) {
+        const int bloc = kBlocksPerStep * t + bl;
+        const bool valid = bloc < a.nb;
+        const int bc = valid ? bloc : a.nb - 1;
+        if constexpr (DG) {
+            XDig x;
+            dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), x);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float p = KqDg<TYPE>::compute(regs[r][t], s, x, grid);
+                acc[r] += valid ? p : 0.f;
+            }
+        } else {
+            XSlice x;
+            x_slice_lm<SH>(lds + lm_record(kXGroupBytes, bc, s), x);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float p = K::compute(regs[r][t], s, x, grid);
+                acc[r] += valid ? p : 0.f;
+            }
+        }
+        // one step's activations live at a time (no hoisting of the
+        // next step's LDS reads into this one)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float tot = wave_sum(acc[r]);
+        const int64_t row = g * R + r;
+        if (lane == 0 && row < a.N) a.y[row] = a.accumulate ? a.y[row] + tot : tot;
+    }
+}
+
+// PF: a wavefront's next row group is requested before the current one's
+// decode (two register sets, alternating), so its loads travel while the
+// current group computes; requests past the last group read nothing.
+template <int TYPE, int R, int NIT, bool DG, bool PF>
 __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     using K = Kq<TYPE>;
     extern __shared__ float4 lds_kq[];
@@ -1072,9 +1134,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     gr.fetch(a, threadIdx.x, kThreads);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. weight loads of the first row group (clamped; results unused past N)
+    // 2. weight loads of the first row group (waves without one read nothing)
     typename K::Regs regs[R][NIT];
-    load_group<TYPE, R, NIT>(a, g < n_groups ? g : n_groups - 1, s, bl, regs);
+    load_group<TYPE, R, NIT>(a, g < n_groups ? g : n_groups - 1, s, bl, regs, g < n_groups);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. activation records into LDS (waves past the chunk's groups store
@@ -1088,44 +1150,27 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     __syncthreads();
 
     // 4. row groups
-    for (; g < n_groups; g += stride) {
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.f;
-#pragma unroll
-        for (int t = 0; t < NIT; ++t) {
-            const int bloc = kBlocksPerStep * t + bl;
-            const bool valid = bloc < a.nb;
-            const int bc = valid ? bloc : a.nb - 1;
-            if constexpr (DG) {
-                XDig x;
-                dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), x);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float p = KqDg<TYPE>::compute(regs[r][t], s, x, grid);
-                    acc[r] += valid ? p : 0.f;
-                }
-            } else {
-                XSlice x;
-                x_slice_lm<SH>(lds + lm_record(kXGroupBytes, bc, s), x);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float p = K::compute(regs[r][t], s, x, grid);
-                    acc[r] += valid ? p : 0.f;
-                }
+    if constexpr (PF) {
+        typename K::Regs nxt[R][NIT];
+        if (g < n_groups) {
+            for (;;) {
+                const int64_t g1 = g + stride;
+                load_group<TYPE, R, NIT>(a, g1 < n_groups ? g1 : n_groups - 1, s, bl, nxt, g1 < n_groups);
+                kq_row_group<TYPE, R, NIT, DG>(a, g, regs, lds, grid, s, bl, lane);
+                if (g1 >= n_groups) break;
+                const int64_t g2 = g1 + stride;
+                load_group<TYPE, R, NIT>(a, g2 < n_groups ? g2 : n_groups - 1, s, bl, regs, g2 < n_groups);
+                kq_row_group<TYPE, R, NIT, DG>(a, g1, nxt, lds, grid, s, bl, lane);
+                if (g2 >= n_groups) break;
+                g = g2;
             }
-            // one step's activations live at a time (no hoisting of the
-            // next step's LDS reads into this one)
-            __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float tot = wave_sum(acc[r]);
-            const int64_t row = g * R + r;
-            if (lane == 0 && row < a.N) a.y[row] = a.accumulate ? a.y[row] + tot : tot;
+    } else {
+        for (; g < n_groups; g += stride) {
+            kq_row_group<TYPE, R, NIT, DG>(a, g, regs, lds, grid, s, bl, lane);
+            const int64_t gn = g + stride;
+            if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
         }
-        const int64_t gn = g + stride;
-        if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
     }
 }
 
@@ -1466,42 +1511,47 @@ constexpr bool small_regs(int type) {
 }
 constexpr int max_nit_r2(int type) { return small_regs(type) ? 4 : kMaxNitR2; }
 
-template <int TYPE, bool DG>
+// R = 2 only without prefetch (two rows' loads and decode already fill the
+// registers); prefetch doubles the weight registers of R = 1.
+template <int TYPE, bool DG, bool PF>
 kq_kernel_fn pick_dg(int R, int nit) {
-    if (R == 2 && nit <= max_nit_r2(TYPE)) {
-        if constexpr (small_regs(TYPE)) {
-            if (nit == 3) return gemv_kq_kernel<TYPE, 2, 3, DG>;
-            if (nit == 4) return gemv_kq_kernel<TYPE, 2, 4, DG>;
+    if constexpr (!PF) {
+        if (R == 2 && nit <= max_nit_r2(TYPE)) {
+            if constexpr (small_regs(TYPE)) {
+                if (nit == 3) return gemv_kq_kernel<TYPE, 2, 3, DG, false>;
+                if (nit == 4) return gemv_kq_kernel<TYPE, 2, 4, DG, false>;
+            }
+            return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG, false> : gemv_kq_kernel<TYPE, 2, 2, DG, false>;
         }
-        return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG> : gemv_kq_kernel<TYPE, 2, 2, DG>;
     }
     switch (nit) {
-    case 1: return gemv_kq_kernel<TYPE, 1, 1, DG>;
-    case 2: return gemv_kq_kernel<TYPE, 1, 2, DG>;
-    case 3: return gemv_kq_kernel<TYPE, 1, 3, DG>;
-    case 4: return gemv_kq_kernel<TYPE, 1, 4, DG>;
-    case 5: return gemv_kq_kernel<TYPE, 1, 5, DG>;
-    case 6: return gemv_kq_kernel<TYPE, 1, 6, DG>;
-    case 7: return gemv_kq_kernel<TYPE, 1, 7, DG>;
-    default: return gemv_kq_kernel<TYPE, 1, 8, DG>;
+    case 1: return gemv_kq_kernel<TYPE, 1, 1, DG, PF>;
+    case 2: return gemv_kq_kernel<TYPE, 1, 2, DG, PF>;
+    case 3: return gemv_kq_kernel<TYPE, 1, 3, DG, PF>;
+    case 4: return gemv_kq_kernel<TYPE, 1, 4, DG, PF>;
+    case 5: return gemv_kq_kernel<TYPE, 1, 5, DG, PF>;
+    case 6: return gemv_kq_kernel<TYPE, 1, 6, DG, PF>;
+    case 7: return gemv_kq_kernel<TYPE, 1, 7, DG, PF>;
+    default: return gemv_kq_kernel<TYPE, 1, 8, DG, PF>;
     }
 }
 
 template <int TYPE>
-kq_kernel_fn pick(int R, int nit, bool dg) {
-    return dg ? pick_dg<TYPE, true>(R, nit) : pick_dg<TYPE, false>(R, nit);
+kq_kernel_fn pick(int R, int nit, bool dg, bool pf) {
+    if (pf) return dg ? pick_dg<TYPE, true, true>(R, nit) : pick_dg<TYPE, false, true>(R, nit);
+    return dg ? pick_dg<TYPE, true, false>(R, nit) : pick_dg<TYPE, false, false>(R, nit);
 }
 
-kq_kernel_fn pick_kernel(int type, int R, int nit, bool dg) {
+kq_kernel_fn pick_kernel(int type, int R, int nit, bool dg, bool pf) {
     switch (type) {
-    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, nit, dg);
-    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, nit, dg);
-    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, nit, dg);
-    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, nit, dg);
-    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, nit, dg);
-    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, nit, dg);
-    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, nit, dg);
-    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, nit, dg);
+    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, nit, dg, pf);
+    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, nit, dg, pf);
+    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, nit, dg, pf);
+    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, nit, dg, pf);
+    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, nit, dg, pf);
+    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, nit, dg, pf);
+    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, nit, dg, pf);
+    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, nit, dg, pf);
     default: return nullptr;
     }
 }
@@ -2097,32 +2147,43 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
     const int64_t per_chunk = (B + n_chunks - 1) / n_chunks;
     // Default forms (variant and form AUTO), from sweeps of the BASELINE
     // shapes on MI355X (us, 14336x4096 / 4096x14336; 8192x8192 for IQ):
-    //  * Q4_K: pipelined form up to two steps per row (10.5 vs 10.8 digit
-    //    rows, 11.1 f32 rows), digit rows beyond (11.5 vs 12.9 f32);
-    //  * Q5_K: digit rows (11.7 / 13.1 vs pipelined 12.6, f32 12.2 / 13.6);
-    //  * Q6_K: digit rows up to two steps (12.4 vs pipelined 13.0, f32 12.6),
-    //    f32 rows beyond (14.3 vs 14.8 digits);
+    //  * Q4_K: digit rows (9.8 vs pipelined 10.0, f32 rows 10.4 at two
+    //    steps; 10.5 vs 11.6 f32 at seven);
+    //  * Q5_K: digit rows, with prefetch up to two steps (10.3 vs 10.9
+    //    without, pipelined 11.1; 11.8 vs f32 12.9 at seven steps, where
+    //    prefetch costs 0.9);
+    //  * Q6_K: digit rows up to two steps (11.8-12.0 vs pipelined 12.6, f32
+    //    11.9 with prefetch), f32 rows beyond (13.7 vs 13.9 digits);
     //  * IQ3_S, IQ3_XXS, IQ2_S up to four steps (N >= 4096): digit rows, two
-    //    rows per wavefront step (13.2 / 11.9 / 12.2 vs f32 15.4 / 14.0 /
-    //    13.4): table-driven sign application and dot4 products cost fewer
-    //    VALU instructions than the f32 decode;
-    //  * Q3_K, IQ4_XS and the rest: f32 rows, one row per step (Q3_K 11.7
-    //    vs 13.0 with two rows, 13.6 digits).
+    //    rows per wavefront step (12.4 / 11.1 / 11.2 vs one row 12.5 / 10.9
+    //    / 11.4, f32 14.0 / 12.7 / 12.2): table-driven sign application and
+    //    dot4 products cost fewer VALU instructions than the f32 decode;
+    //  * IQ4_XS up to four steps: digit rows (11.4 vs f32 11.6-11.8);
+    //  * Q3_K and the rest: f32 rows, one row per step, with prefetch up to
+    //    two steps (Q3_K 10.5 vs 10.8 without, 12.0-12.3 digits; 12.0 vs
+    //    13.1 with prefetch at seven steps).
+    // Prefetch (the next row group requested before the current one's
+    // decode) pays where a wavefront has several short groups; with long
+    // rows it lets every wavefront's second group compete with the first
+    // groups' loads and costs more than it hides.
     const bool auto_form = ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO;
-    auto pl_auto = [&](int nit) { return a.type == MI355X_TYPE_Q4_K && nit <= 2; };
     auto dg_rows_auto = [&](int nit) {
         switch (a.type) {
         case MI355X_TYPE_Q4_K:
         case MI355X_TYPE_Q5_K: return true;
         case MI355X_TYPE_Q6_K: return nit <= 2;
+        case MI355X_TYPE_IQ4_XS: return nit <= 4;
         default: return grid_type && nit <= max_nit_r2(a.type) && a.N >= 4096;
         }
+    };
+    auto pf_auto = [&](int nit) {
+        return auto_form && nit <= 2 && (a.type == MI355X_TYPE_Q5_K || a.type == MI355X_TYPE_Q3_K);
     };
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
         const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
         const bool pl = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 &&
-                        (ctx->form_override == MI355X_FORM_PIPE || (auto_form && pl_auto(nit)));
+                        ctx->form_override == MI355X_FORM_PIPE;
         const bool xs = ctx->kernel_variant != MI355X_VARIANT_EXACT_F32 && ctx->form_override == MI355X_FORM_KSPLIT;
         if (xs) {
             const int rb = ctx->rows_override == 2 || ctx->rows_override == 4 ? ctx->rows_override
@@ -2171,7 +2232,8 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         const bool dg = dg_forced || dg_auto;
         int R = dg_auto && grid_type ? 2 : 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
-        const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg);
+        const bool pf = R == 1 && (ctx->prefetch_override == 1 || (ctx->prefetch_override == 0 && pf_auto(nit)));
+        const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf);
         const int64_t n_groups = (a.N + R - 1) / R;
         const size_t lds = (dg ? dg_lds_bytes(nb) : x_lds_bytes(nb)) +
                            (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u;
