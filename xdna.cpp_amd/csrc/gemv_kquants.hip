@@ -406,6 +406,17 @@ struct Kq<MI355X_TYPE_Q3_K> {
 // d * (ls - 32) * kvalues_iq4nl[idx] (include/xdna/kquants.h:421-441).
 // The codebook (biased by +128 into unsigned bytes) is looked up four
 // indices at a time with byte permutes.
+// Four 16-entry table lookups at once: nibble bytes n (each < 16) index the
+// 16 bytes t0..t3.  Two v_perm read entry n & 7 of each 8-byte half; a third
+// takes, per byte b, byte b of the first (selector b) or of the second half's
+// result (selector b + 4, when bit 3 of the nibble is set).
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+    return __builtin_amdgcn_perm(hi, lo, ((n >> 1) & 0x04040404u) | 0x03020100u);
+}
+
 template <>
 struct Kq<MI355X_TYPE_IQ4_XS> {
     static constexpr int kGrid = 0;
@@ -416,12 +427,7 @@ struct Kq<MI355X_TYPE_IQ4_XS> {
         u32x2 hd;
     };
     __device__ static uint32_t lookup(uint32_t n) {
-        const uint32_t sel = n & 0x07070707u;
-        const uint32_t lo = __builtin_amdgcn_perm(kT1, kT0, sel);
-        const uint32_t hi = __builtin_amdgcn_perm(kT3, kT2, sel);
-        const uint32_t m1 = (n >> 3) & 0x01010101u;
-        const uint32_t mask = (m1 << 8) - m1;
-        return (hi & mask) | (lo & ~mask);
+        return iq4_lookup(n, kT0, kT1, kT2, kT3);
     }
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         return {ld128(r, r.P[0] + 128 * b + 16 * s), ld64(r, r.P[1] + 8 * b)};
@@ -759,12 +765,7 @@ struct KqDg<MI355X_TYPE_IQ4_XS> {
     // kvalues_iq4nl: {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}
     static constexpr uint32_t kT0 = 0xBFAD9881u, kT1 = 0xF6EADDCFu, kT2 = 0x26190D01u, kT3 = 0x71594535u;
     __device__ static uint32_t lookup(uint32_t n) {
-        const uint32_t sel = n & 0x07070707u;
-        const uint32_t lo = __builtin_amdgcn_perm(kT1, kT0, sel);
-        const uint32_t hi = __builtin_amdgcn_perm(kT3, kT2, sel);
-        const uint32_t m1 = (n >> 3) & 0x01010101u;
-        const uint32_t mask = (m1 << 8) - m1;
-        return (hi & mask) | (lo & ~mask);
+        return iq4_lookup(n, kT0, kT1, kT2, kT3);
     }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ4_XS>::Regs &g, int s, const XDig &x, const uint32_t *) {
         int sm[3] = {0, 0, 0};

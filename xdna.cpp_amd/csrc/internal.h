@@ -42,6 +42,16 @@ struct mi355x_ctx {
     int prefetch_override = 0;
     int64_t grid_override = 0;
     int form_override = MI355X_FORM_AUTO;
+    // MI355X_OPT_OVERLAP: a second stream of the same flags and priority;
+    // consecutive eligible mi355x_gemv calls alternate between the two
+    // (ov_next: the stream of the next one) after a fork event on the first
+    // stream; any other call joins the second stream back first.
+    bool overlap = false;
+    bool ov_open = false;
+    int ov_next = 0;
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ov_fork = nullptr;
+    hipEvent_t ov_join_ev = nullptr;
     std::mutex mu;  // serialises calls that share the staging buffer
     // completion word for mi355x_ctx_fence: pinned host memory the signal
     // kernel writes, and the last value handed out
@@ -51,6 +61,10 @@ struct mi355x_ctx {
 };
 
 namespace mi355x {
+
+// Ends an open run of overlapped GEMVs: the context's stream waits for the
+// second stream's work (no-op when none is open).
+int ov_join(mi355x_ctx *ctx);
 
 // Thread-local error message plumbing.
 int set_error(int code, const std::string &msg);

@@ -115,7 +115,7 @@ struct DeviceGuard {
 };
 
 int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *x, bool xbf16,
-                float *y, const char *who) {
+                float *y, const char *who, bool overlap_ok = false) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
     uint64_t total = 0;
@@ -129,13 +129,37 @@ int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
         return set_error(MI355X_EUNSUPPORTED, std::string(who) + ": " + type_name(type) +
                                                   " needs its grid table (mi355x_set_iq_grid)");
     DeviceGuard dg(ctx->device);
-    if (type == MI355X_TYPE_IQ3_XXS || type == MI355X_TYPE_IQ2_S) {
+    // Overlapped GEMVs use nothing of the context's but its streams and its
+    // grid copies: f32 activations, 16-byte aligned (no conversion buffer),
+    // and for IQ3_XXS / IQ2_S grids already on the context (no upload into
+    // a buffer that a GEMV on the other stream may be reading).
+    const bool grid_type = type == MI355X_TYPE_IQ3_XXS || type == MI355X_TYPE_IQ2_S;
+    const bool ov = overlap_ok && ctx->overlap && !xbf16 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                    (!grid_type || ctx->grids_version == g_grid_version.load());
+    if (!ov) {
+        rc = ov_join(ctx);
+        if (rc) return rc;
+    }
+    if (grid_type && !ov) {
         rc = sync_iq_grids(ctx);
         if (rc) return rc;
     }
     GemvArgs a{type, static_cast<const uint8_t *>(W), N, K, x, xbf16, y};
-    if (type == MI355X_TYPE_Q4_0) return launch_gemv_q4_0(ctx, a);
-    return launch_gemv_kquant(ctx, a);
+    if (!ov) return type == MI355X_TYPE_Q4_0 ? launch_gemv_q4_0(ctx, a) : launch_gemv_kquant(ctx, a);
+    if (!ctx->ov_open) {
+        // the second stream starts after everything queued so far
+        MI355X_HIP(hipEventRecord(ctx->ov_fork, ctx->stream));
+        MI355X_HIP(hipStreamWaitEvent(ctx->stream2, ctx->ov_fork, 0));
+        ctx->ov_open = true;
+        ctx->ov_next = 0;
+    }
+    // the launchers queue on ctx->stream: point it at this call's stream
+    hipStream_t primary = ctx->stream;
+    if (ctx->ov_next) ctx->stream = ctx->stream2;
+    rc = type == MI355X_TYPE_Q4_0 ? launch_gemv_q4_0(ctx, a) : launch_gemv_kquant(ctx, a);
+    ctx->stream = primary;
+    ctx->ov_next ^= 1;
+    return rc;
 }
 
 }  // namespace
@@ -152,9 +176,19 @@ int hip_error(hipError_t e, const char *what) {
 
 void clear_error() { g_last_error.clear(); }
 
+int ov_join(mi355x_ctx *ctx) {
+    if (!ctx || !ctx->ov_open) return MI355X_OK;
+    ctx->ov_open = false;
+    MI355X_HIP(hipEventRecord(ctx->ov_join_ev, ctx->stream2));
+    MI355X_HIP(hipStreamWaitEvent(ctx->stream, ctx->ov_join_ev, 0));
+    return MI355X_OK;
+}
+
 int free_device(mi355x_ctx *ctx, void *p) {
     if (!p) return MI355X_OK;
-    int rc = stop_servers(ctx);
+    int rc = ov_join(ctx);
+    if (rc) return rc;
+    rc = stop_servers(ctx);
     if (rc) return rc;
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
     MI355X_HIP(hipFree(p));
@@ -278,11 +312,18 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
 void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     if (!ctx) return;
     DeviceGuard dg(ctx->device);
+    (void)ov_join(ctx);
     for (void *p : {ctx->staging, ctx->xconv, ctx->mbtiles, ctx->iq3xxs_grid, ctx->iq2s_grid})
         (void)free_device(ctx, p);
     (void)stop_servers(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->fence_host) (void)hipHostFree(ctx->fence_host);
+    if (ctx->stream2) {
+        (void)hipStreamSynchronize(ctx->stream2);
+        (void)hipStreamDestroy(ctx->stream2);
+    }
+    if (ctx->ov_fork) (void)hipEventDestroy(ctx->ov_fork);
+    if (ctx->ov_join_ev) (void)hipEventDestroy(ctx->ov_join_ev);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -290,6 +331,8 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
 int mi355x_ctx_sync(mi355x_ctx *ctx) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_sync: null context");
+    const int rc = ov_join(ctx);
+    if (rc) return rc;
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
     return MI355X_OK;
 }
@@ -312,6 +355,8 @@ int mi355x_ctx_fence(mi355x_ctx *ctx) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_fence: null context");
     DeviceGuard dg(ctx->device);
+    const int jrc = ov_join(ctx);
+    if (jrc) return jrc;
     const uint32_t v = ctx->fence_seq.fetch_add(1) + 1;
     fence_signal_kernel<<<1, 64, 0, ctx->stream>>>(ctx->fence_dev, v);
     MI355X_HIP(hipGetLastError());
@@ -333,7 +378,24 @@ int mi355x_ctx_fence(mi355x_ctx *ctx) {
 int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: null context");
+    {
+        DeviceGuard dg(ctx->device);
+        const int rc = ov_join(ctx);
+        if (rc) return rc;
+    }
     switch (option) {
+    case MI355X_OPT_OVERLAP: {
+        if (value != 0 && value != 1)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap must be 0 or 1");
+        if (value == 1 && !ctx->stream2) {
+            DeviceGuard dg(ctx->device);
+            MI355X_HIP(hipStreamCreateWithFlags(&ctx->stream2, hipStreamNonBlocking));
+            if (!ctx->ov_fork) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_fork, hipEventDisableTiming));
+            if (!ctx->ov_join_ev) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_join_ev, hipEventDisableTiming));
+        }
+        ctx->overlap = value == 1;
+        return MI355X_OK;
+    }
     case MI355X_OPT_VARIANT:
         if (value != MI355X_VARIANT_AUTO && value != MI355X_VARIANT_EXACT_F32 && value != MI355X_VARIANT_DIGITS &&
             value != MI355X_VARIANT_GGML_Q8)
@@ -371,7 +433,12 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
     }
 }
 
-void *mi355x_ctx_stream(mi355x_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+void *mi355x_ctx_stream(mi355x_ctx *ctx) {
+    if (!ctx) return nullptr;
+    // work the caller queues on the stream comes after every overlapped GEMV
+    (void)ov_join(ctx);
+    return static_cast<void *>(ctx->stream);
+}
 
 int mi355x_ctx_device(mi355x_ctx *ctx) { return ctx ? ctx->device : -1; }
 
@@ -443,6 +510,8 @@ static int copy_sync(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes, 
     if (bytes == 0) return MI355X_OK;
     if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
     DeviceGuard dg(ctx->device);
+    const int jrc = ov_join(ctx);
+    if (jrc) return jrc;
     MI355X_HIP(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
     return MI355X_OK;
@@ -465,6 +534,8 @@ static int copy_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes,
     if (bytes == 0) return MI355X_OK;
     if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
     DeviceGuard dg(ctx->device);
+    const int jrc = ov_join(ctx);
+    if (jrc) return jrc;
     MI355X_HIP(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
     return MI355X_OK;
 }
@@ -480,6 +551,8 @@ int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes) {
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_fill: null context");
     if (bytes && !dst) return set_error(MI355X_EINVAL, "mi355x_fill: null pointer");
     DeviceGuard dg(ctx->device);
+    const int rc = ov_join(ctx);
+    if (rc) return rc;
     return launch_fill(ctx, dst, value, bytes);
 }
 
@@ -559,6 +632,8 @@ int mi355x_prepack_from_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, vo
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
+    rc = ov_join(ctx);
+    if (rc) return rc;
     rc = ensure_staging(ctx, size);
     if (rc) return rc;
     const uint8_t *src = static_cast<const uint8_t *>(raw_host);
@@ -584,6 +659,8 @@ int mi355x_prepack_from_device(mi355x_ctx *ctx, int type, int64_t N, int64_t K, 
     rc = check_resident_base(type, packed_dev, "mi355x_prepack_from_device");
     if (rc) return rc;
     DeviceGuard dg(ctx->device);
+    rc = ov_join(ctx);
+    if (rc) return rc;
     rc = launch_prepack_scatter(ctx, type, N, K, static_cast<uint8_t *>(packed_dev),
                                 static_cast<const uint8_t *>(raw_dev), offset, size);
     if (rc) return rc;
@@ -602,6 +679,8 @@ int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, const
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
+    rc = ov_join(ctx);
+    if (rc) return rc;
     rc = ensure_staging(ctx, size);
     if (rc) return rc;
     uint8_t *dst = static_cast<uint8_t *>(raw_host);
@@ -618,7 +697,7 @@ int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, const
 }
 
 int mi355x_gemv(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *x, float *y) {
-    return gemv_common(ctx, type, W, N, K, x, false, y, "mi355x_gemv");
+    return gemv_common(ctx, type, W, N, K, x, false, y, "mi355x_gemv", true);
 }
 
 int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int njobs, const mi355x_gemv_job *jobs) {
@@ -636,6 +715,11 @@ int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int 
         if (!jobs[j].W || !jobs[j].y)
             return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
         mj[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].N, jobs[j].y};
+    }
+    {
+        DeviceGuard dg(ctx->device);
+        const int rc = ov_join(ctx);
+        if (rc) return rc;
     }
     if (type == MI355X_TYPE_Q4_0 && K > 0) {
         bool all = true;
@@ -668,6 +752,11 @@ int gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                  float *y, int64_t y_stride, int64_t M, bool noalloc, const char *who) {
     clear_error();
     if (M < 0) return set_error(MI355X_EINVAL, std::string(who) + ": negative M");
+    if (ctx) {
+        DeviceGuard dg(ctx->device);
+        const int rc = ov_join(ctx);
+        if (rc) return rc;
+    }
     if (M > 1 && (x_stride < K || y_stride < N))
         return set_error(MI355X_EINVAL, std::string(who) + ": strides smaller than a row");
     if (noalloc && ctx && M > 0 && N > 0) {
@@ -732,8 +821,15 @@ int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int 
     if (!ctx || !weights || n_weights < 1 || iters < 1 || warmup < 0 || !ms_total)
         return set_error(MI355X_EINVAL, "mi355x_time_gemv: bad arguments");
     DeviceGuard dg(ctx->device);
+    // with MI355X_OPT_OVERLAP consecutive launches may run at once: they
+    // write y and y + N alternately
+    auto out = [&](int i) { return ctx->overlap ? y + (i & 1) * N : y; };
     for (int i = 0; i < warmup; ++i) {
-        int rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, y);
+        int rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, out(i));
+        if (rc) return rc;
+    }
+    {
+        const int rc = ov_join(ctx);
         if (rc) return rc;
     }
     hipEvent_t e0, e1;
@@ -745,7 +841,9 @@ int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int 
     }
     int rc = MI355X_OK;
     if (hipEventRecord(e0, ctx->stream) != hipSuccess) rc = set_error(MI355X_EHIP, "hipEventRecord");
-    for (int i = 0; i < iters && rc == MI355X_OK; ++i) rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, y);
+    for (int i = 0; i < iters && rc == MI355X_OK; ++i)
+        rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, out(i));
+    if (rc == MI355X_OK) rc = ov_join(ctx);
     if (rc == MI355X_OK && hipEventRecord(e1, ctx->stream) != hipSuccess) rc = set_error(MI355X_EHIP, "hipEventRecord");
     if (rc == MI355X_OK) {
         e = hipEventSynchronize(e1);

@@ -26,7 +26,7 @@ BLOCK_BYTES = {Q4_0: 18, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98
                IQ2_S: 82, IQ4_XS: 136}
 
 
-OPT_VARIANT, OPT_ROWS_PER_WAVE, OPT_WAVES_PER_GROUP, OPT_GRID, OPT_PREFETCH, OPT_FORM = 1, 2, 3, 4, 5, 6
+OPT_VARIANT, OPT_ROWS_PER_WAVE, OPT_WAVES_PER_GROUP, OPT_GRID, OPT_PREFETCH, OPT_FORM, OPT_OVERLAP = 1, 2, 3, 4, 5, 6, 7
 FORM_AUTO, FORM_ROWS, FORM_KSPLIT, FORM_STREAM, FORM_PIPE = 0, 1, 2, 3, 4
 VARIANT_AUTO, VARIANT_EXACT_F32, VARIANT_DIGITS, VARIANT_GGML_Q8 = 0, 1, 2, 3
 
