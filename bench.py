@@ -188,7 +188,7 @@ def kq_weights(t, N, K, grids, seed=7):
     return synth.quantize_kq(t, w, grids.get(t))
 
 
-def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
+def kquant_sweep(ctx, steps, warmup, settle_s=0.0, overlap=True):
     """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
     (rotated) weights, built by the configs' recipe (kq_weights); IQ3_XXS /
     IQ2_S run with a synthetic grid, as ggml's grids are not part of this
@@ -202,7 +202,7 @@ def kquant_sweep(ctx, steps, warmup, settle_s=0.0):
         x = synth.activations(K, seed=43)
         ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
         gbs = algorithmic_bytes(t, N, K) / (ms * 1e-3) / 1e9
-        mso = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s, overlap=True)[0]
+        mso = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s, overlap=True)[0] if overlap else ms
         gbo = algorithmic_bytes(t, N, K) / (mso * 1e-3) / 1e9
         res[f"{name} {N}x{K}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies,
@@ -430,6 +430,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
     ap.add_argument("--kquants", action="store_true",
                     help="also time the K-quant (14336x4096, 4096x14336) and IQ (8192x8192) BASELINE configs")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="time in-order launches only (one stream): a kernel trace then shows each kernel alone")
     ap.add_argument("--rows-sweep", action="store_true",
                     help="also time IQ2_S (K=8192) and Q4_K (K=4096) at N = 256..32768 rows: fixed cost + per row")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -466,13 +468,16 @@ def main() -> int:
             log(f"bench: copy calibration: one {nbytes} B device-to-device copy done")
         name, pci = ctx.describe()
         log(f"bench: device {name} at {pci}; timing {args.steps} launches after {args.warmup} warmup")
-        ms, copies, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle,
-                                  overlap=True)
-        log(f"bench: {ms * 1e3:.2f} us/launch over {copies} resident copies (consecutive launches overlap)")
-        ms_seq, _, y_seq = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle)
-        log(f"bench: in order (one stream) {ms_seq * 1e3:.2f} us/launch")
-        if not np.array_equal(y, y_seq):
-            raise RuntimeError("overlapped and in-order launches disagree")
+        overlap = not args.no_overlap
+        ms_seq, copies, y_seq = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle)
+        log(f"bench: in order (one stream) {ms_seq * 1e3:.2f} us/launch over {copies} resident copies")
+        ms, y = ms_seq, y_seq
+        if overlap:
+            ms, _, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle,
+                                 overlap=True)
+            log(f"bench: {ms * 1e3:.2f} us/launch with consecutive launches overlapping")
+            if not np.array_equal(y, y_seq):
+                raise RuntimeError("overlapped and in-order launches disagree")
         ms_hot, _, _ = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, 0, args.settle)
         log(f"bench: cache-hot (one copy) {ms_hot * 1e3:.2f} us/launch")
         # the other arithmetic variants on the same workload
@@ -495,7 +500,7 @@ def main() -> int:
                 ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle)
                 gbs2 = algorithmic_bytes(t, n2, k2) / (ms2 * 1e-3) / 1e9
                 mso = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle,
-                                overlap=True)[0]
+                                overlap=True)[0] if overlap else ms2
                 gbo = algorithmic_bytes(t, n2, k2) / (mso * 1e-3) / 1e9
                 sweep[f"{n2}x{k2}"] = {"us": round(ms2 * 1e3, 3), "GB/s": round(gbs2, 1),
                                        "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2,
@@ -505,7 +510,7 @@ def main() -> int:
 
         kq = {}
         if args.kquants:
-            kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle)
+            kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle, overlap)
         rs = rows_sweep(ctx, args.steps, args.warmup, args.settle) if args.rows_sweep else {}
 
     # the timed output must still be the right answer (checked, not measured)
@@ -541,15 +546,19 @@ def main() -> int:
         "config": {"workload": f"Q4_0 GEMV {N}x{K} (N rows x K), 1 f32 activation row, "
                                f"weights rotated over {copies} resident copies "
                                f"({copies * (alg - 4 * K - 4 * N) / 2**30:.2f} GiB) so HBM, not cache, serves them; "
-                               "back-to-back independent launches that may overlap (two streams)",
+                               + ("back-to-back independent launches that may overlap (two streams)" if overlap
+                                  else "back-to-back launches on one stream"),
                    "N": N, "K": K, "weight_type": "Q4_0", "rotate_copies": copies,
-                   "launch_overlap": True, "parallelism": "single GPU"},
+                   "launch_overlap": overlap, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "note": "achieved = algorithmic bytes / mean time per launch of the timed back-to-back "
-                             "launches (HIP events on the library's stream, after it has joined the second "
-                             "stream): consecutive launches overlap (MI355X_OPT_OVERLAP), so a kernel trace "
-                             "shows each kernel running longer than the launch interval"},
+                             "launches (HIP events on the library's stream" +
+                             (", after it has joined the second stream): consecutive launches overlap "
+                              "(MI355X_OPT_OVERLAP), so a kernel trace shows each kernel running longer than the "
+                              "launch interval" if overlap else
+                              "): each launch starts after the previous one ends, so the figure includes the "
+                              "gap between kernels")},
         "in_order": {"us_per_launch": round(ms_seq * 1e3, 3), "GB/s": round(alg / (ms_seq * 1e-3) / 1e9, 2),
                      "frac": round(alg / (ms_seq * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "note": "the same launches on one stream, each starting after the previous one ends "
