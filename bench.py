@@ -49,14 +49,14 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes, settle_s=0.0, overlap=False):
+def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes, settle_s=0.0, overlap=0):
     """Returns (ms_per_launch, copies, y) for `steps` launches over resident
     copies.  With settle_s > 0 the same launches first run untimed for about
     that long, so the GPU's clocks have left their idle state before the
     warm-up and the timed launches (a cold GPU adds ~0.3 us per launch).
-    With overlap the context's MI355X_OPT_OVERLAP is on: consecutive
-    launches (independent: other weight copies, alternate outputs) may run
-    at once, one starting while the previous one drains."""
+    With overlap = S (2-4) the context's MI355X_OPT_OVERLAP is S: up to S
+    consecutive launches (independent: other weight copies, S outputs in
+    turn) may run at once, each starting while the previous ones drain."""
     wbytes = N * mi355x.row_bytes(t, K)
     copies = max(1, -(-rotate_bytes // wbytes)) if rotate_bytes else 1
     first = ctx.resident(t, raw, N, K)
@@ -66,16 +66,17 @@ def gemv_rate(ctx, t, raw, N, K, x, steps, warmup, rotate_bytes, settle_s=0.0, o
         mi355x.check(ctx.lib.mi355x_memcpy_d2d(ctx.h, b.ptr, first.ptr, wbytes))
         bufs.append(b)
     xb = ctx.to_device(x)
-    yb = ctx.alloc(8 * N)
+    yb = ctx.alloc(4 * N * max(1, overlap))
     try:
-        ctx.set_option(mi355x.OPT_OVERLAP, 1 if overlap else 0)
+        ctx.set_option(mi355x.OPT_OVERLAP, overlap)
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < settle_s:
             ctx.time_gemv(t, [b.ptr for b in bufs], N, K, xb.ptr, yb.ptr, 0, 1000)
         ms = ctx.time_gemv(t, [b.ptr for b in bufs], N, K, xb.ptr, yb.ptr, warmup, steps)
         ctx.set_option(mi355x.OPT_OVERLAP, 0)
         y = yb.download(np.float32, N)
-        if overlap and not np.array_equal(y, yb.download(np.float32, 2 * N)[N:]):
+        if overlap and any(not np.array_equal(y, o)
+                           for o in yb.download(np.float32, overlap * N).reshape(overlap, N)):
             raise RuntimeError("overlapped launches wrote different outputs")
     finally:
         ctx.set_option(mi355x.OPT_OVERLAP, 0)
@@ -188,7 +189,7 @@ def kq_weights(t, N, K, grids, seed=7):
     return synth.quantize_kq(t, w, grids.get(t))
 
 
-def kquant_sweep(ctx, steps, warmup, settle_s=0.0, overlap=True):
+def kquant_sweep(ctx, steps, warmup, settle_s=0.0, overlap=0):
     """BASELINE configs 3 and 4: each K/IQ type at its shapes, HBM-resident
     (rotated) weights, built by the configs' recipe (kq_weights); IQ3_XXS /
     IQ2_S run with a synthetic grid, as ggml's grids are not part of this
@@ -202,7 +203,7 @@ def kquant_sweep(ctx, steps, warmup, settle_s=0.0, overlap=True):
         x = synth.activations(K, seed=43)
         ms, copies, _ = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s)
         gbs = algorithmic_bytes(t, N, K) / (ms * 1e-3) / 1e9
-        mso = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s, overlap=True)[0] if overlap else ms
+        mso = gemv_rate(ctx, t, raw, N, K, x, steps, warmup, ROTATE_BYTES, settle_s, overlap=overlap)[0] if overlap else ms
         gbo = algorithmic_bytes(t, N, K) / (mso * 1e-3) / 1e9
         res[f"{name} {N}x{K}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies,
@@ -430,6 +431,10 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the other BASELINE Q4_0 shapes")
     ap.add_argument("--kquants", action="store_true",
                     help="also time the K-quant (14336x4096, 4096x14336) and IQ (8192x8192) BASELINE configs")
+    ap.add_argument("--overlap", type=int, default=4, choices=(2, 3, 4),
+                    help="streams over which consecutive launches of the headline GEMV may overlap "
+                         "(MI355X_OPT_OVERLAP); the --sweep and --kquants shapes use 2, which serves them "
+                         "as well as more")
     ap.add_argument("--no-overlap", action="store_true",
                     help="time in-order launches only (one stream): a kernel trace then shows each kernel alone")
     ap.add_argument("--rows-sweep", action="store_true",
@@ -468,13 +473,13 @@ def main() -> int:
             log(f"bench: copy calibration: one {nbytes} B device-to-device copy done")
         name, pci = ctx.describe()
         log(f"bench: device {name} at {pci}; timing {args.steps} launches after {args.warmup} warmup")
-        overlap = not args.no_overlap
+        overlap = 0 if args.no_overlap else args.overlap
         ms_seq, copies, y_seq = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle)
         log(f"bench: in order (one stream) {ms_seq * 1e3:.2f} us/launch over {copies} resident copies")
         ms, y = ms_seq, y_seq
         if overlap:
             ms, _, y = gemv_rate(ctx, t, raw, N, K, x, args.steps, args.warmup, ROTATE_BYTES, args.settle,
-                                 overlap=True)
+                                 overlap=overlap)
             log(f"bench: {ms * 1e3:.2f} us/launch with consecutive launches overlapping")
             if not np.array_equal(y, y_seq):
                 raise RuntimeError("overlapped and in-order launches disagree")
@@ -500,7 +505,7 @@ def main() -> int:
                 ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle)
                 gbs2 = algorithmic_bytes(t, n2, k2) / (ms2 * 1e-3) / 1e9
                 mso = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle,
-                                overlap=True)[0] if overlap else ms2
+                                overlap=min(overlap, 2))[0] if overlap else ms2
                 gbo = algorithmic_bytes(t, n2, k2) / (mso * 1e-3) / 1e9
                 sweep[f"{n2}x{k2}"] = {"us": round(ms2 * 1e3, 3), "GB/s": round(gbs2, 1),
                                        "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2,
@@ -510,7 +515,7 @@ def main() -> int:
 
         kq = {}
         if args.kquants:
-            kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle, overlap)
+            kq = kquant_sweep(ctx, args.steps, args.warmup, args.settle, min(overlap, 2))
         rs = rows_sweep(ctx, args.steps, args.warmup, args.settle) if args.rows_sweep else {}
 
     # the timed output must still be the right answer (checked, not measured)
@@ -546,7 +551,7 @@ def main() -> int:
         "config": {"workload": f"Q4_0 GEMV {N}x{K} (N rows x K), 1 f32 activation row, "
                                f"weights rotated over {copies} resident copies "
                                f"({copies * (alg - 4 * K - 4 * N) / 2**30:.2f} GiB) so HBM, not cache, serves them; "
-                               + ("back-to-back independent launches that may overlap (two streams)" if overlap
+                               + (f"back-to-back independent launches, up to {overlap} in flight ({overlap} streams)" if overlap
                                   else "back-to-back launches on one stream"),
                    "N": N, "K": K, "weight_type": "Q4_0", "rotate_copies": copies,
                    "launch_overlap": overlap, "parallelism": "single GPU"},
@@ -554,7 +559,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "note": "achieved = algorithmic bytes / mean time per launch of the timed back-to-back "
                              "launches (HIP events on the library's stream" +
-                             (", after it has joined the second stream): consecutive launches overlap "
+                             (", after it has joined the other streams): consecutive launches overlap "
                               "(MI355X_OPT_OVERLAP), so a kernel trace shows each kernel running longer than the "
                               "launch interval" if overlap else
                               "): each launch starts after the previous one ends, so the figure includes the "

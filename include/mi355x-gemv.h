@@ -128,12 +128,13 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     their dot products; Q4_0: K a multiple of 2048 up to 16384, 16-byte
  *     aligned weights and activation row; K/IQ types: 22-bit digit
  *     arithmetic, any K).
- *   MI355X_OPT_OVERLAP: 0 (default) or 1.  With 1, consecutive mi355x_gemv
- *     calls may run at the same time: the context gets a second stream of
- *     the same kind, and GEMVs with f32 activations on a 16-byte boundary
- *     (IQ3_XXS and IQ2_S once the context holds the current grid, after
- *     one such GEMV) alternate between the two, so that one launch's start
- *     overlaps the previous one's end.  The caller promises
+ *   MI355X_OPT_OVERLAP: 0 (default: off) or S = 2, 3, 4.  With S,
+ *     consecutive mi355x_gemv calls may run at the same time: the context
+ *     gets S - 1 more streams of the same kind, and GEMVs with f32
+ *     activations on a 16-byte boundary (IQ3_XXS and IQ2_S once the context
+ *     holds the current grid, after one such GEMV) take the S streams in
+ *     turn, so that up to S launches are in flight and each one's start
+ *     overlaps the previous ones' ends.  The caller promises
  *     that such a run of calls is independent: none reads an output that
  *     another in the run writes, and no two write the same output.  Every
  *     other call on the context (copies, fills, prepack, the other GEMV
@@ -321,9 +322,9 @@ MI355X_API void mi355x_server_destroy(mi355x_server *s);
  * Times `iters` back-to-back launches of mi355x_gemv on the context's stream
  * with HIP events, rotating through `n_weights` resident copies of W
  * (weights[i]), after `warmup` untimed launches.  *ms_total receives the
- * elapsed milliseconds of the timed launches.  With MI355X_OPT_OVERLAP on,
- * launch i writes y + (i % 2) * N (y holds 2N floats) and the timed span
- * ends after both streams' launches. */
+ * elapsed milliseconds of the timed launches.  With MI355X_OPT_OVERLAP = S,
+ * launch i writes y + (i % S) * N (y holds S * N floats) and the timed span
+ * ends after every stream's launches. */
 MI355X_API int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights,
                                 int n_weights, int64_t N, int64_t K, const float *x, float *y,
                                 int warmup, int iters, double *ms_total);

@@ -25,11 +25,11 @@ def synthetic_grid(t, seed):
 
 
 class overlap:
-    def __init__(self, ctx):
-        self.ctx = ctx
+    def __init__(self, ctx, streams=2):
+        self.ctx, self.streams = ctx, streams
 
     def __enter__(self):
-        self.ctx.set_option(mi355x.OPT_OVERLAP, 1)
+        self.ctx.set_option(mi355x.OPT_OVERLAP, self.streams)
 
     def __exit__(self, *exc):
         self.ctx.set_option(mi355x.OPT_OVERLAP, 0)
@@ -54,7 +54,8 @@ def mats(ctx):
         b.free()
 
 
-def test_overlapped_gemvs_match_in_order(ctx, mats):
+@pytest.mark.parametrize("streams", [2, 3, 4])
+def test_overlapped_gemvs_match_in_order(ctx, mats, streams):
     ws, xs = mats
     runs = [ws[i % len(ws)] for i in range(40)]
     ys = [ctx.alloc(4 * N) for _, N, _, _ in runs]
@@ -65,7 +66,7 @@ def test_overlapped_gemvs_match_in_order(ctx, mats):
         refs = [y.download(np.float32, N) for (_, N, _, _), y in zip(runs, ys)]
         for y in ys:
             mi355x.check(ctx.lib.mi355x_fill(ctx.h, y.ptr, 0xFF, y.nbytes))
-        with overlap(ctx):
+        with overlap(ctx, streams):
             for (t, N, K, w), y in zip(runs, ys):
                 mi355x.check(ctx.gemv_ptr(t, w.ptr, N, K, xs[K].ptr, y.ptr))
             ctx.sync()
@@ -77,7 +78,8 @@ def test_overlapped_gemvs_match_in_order(ctx, mats):
         assert np.array_equal(a, b), i
 
 
-def test_join_orders_later_work(ctx, mats):
+@pytest.mark.parametrize("streams", [2, 4])
+def test_join_orders_later_work(ctx, mats, streams):
     """An overlapped run, then a multi-GEMV that reads the run's outputs as its
     activation, then another overlapped run reading the multi's output: each
     step sees the previous one's results (the multi joins the second stream
@@ -101,7 +103,7 @@ def test_join_orders_later_work(ctx, mats):
         ref = chain()
         for b in (ya, yb, yc, yd):
             mi355x.check(ctx.lib.mi355x_fill(ctx.h, b.ptr, 0, b.nbytes))
-        with overlap(ctx):
+        with overlap(ctx, streams):
             got = chain()
     finally:
         for b in (ya, yb, yc, yd):
@@ -119,7 +121,7 @@ def test_ctx_stream_and_copies_after_overlap(ctx, mats):
     try:
         mi355x.check(ctx.gemv_ptr(t, w.ptr, N, K, xs[K].ptr, ys[0].ptr))
         ref = ys[0].download(np.float32, N)
-        with overlap(ctx):
+        with overlap(ctx, 3):
             for y in ys:
                 mi355x.check(ctx.gemv_ptr(t, w.ptr, N, K, xs[K].ptr, y.ptr))
             # a copy the caller queues on the context's stream comes after the run
@@ -139,25 +141,28 @@ def test_ctx_stream_and_copies_after_overlap(ctx, mats):
         assert np.array_equal(o, ref)
 
 
-def test_time_gemv_overlap_alternates_outputs(ctx, mats):
+@pytest.mark.parametrize("streams", [2, 4])
+def test_time_gemv_overlap_rotates_outputs(ctx, mats, streams):
     ws, xs = mats
     t, N, K, w = ws[1]
-    y = ctx.alloc(8 * N)
+    y = ctx.alloc(4 * streams * N)
     ref_b = ctx.alloc(4 * N)
     try:
         mi355x.check(ctx.gemv_ptr(t, w.ptr, N, K, xs[K].ptr, ref_b.ptr))
         ref = ref_b.download(np.float32, N)
-        with overlap(ctx):
+        with overlap(ctx, streams):
             ms = ctx.time_gemv(t, [w.ptr], N, K, xs[K].ptr, y.ptr, 3, 20)
-            both = y.download(np.float32, 2 * N)
+            outs = y.download(np.float32, streams * N).reshape(streams, N)
     finally:
         y.free()
         ref_b.free()
     assert ms > 0
-    assert np.array_equal(both[:N], ref) and np.array_equal(both[N:], ref)
+    for o in outs:
+        assert np.array_equal(o, ref)
 
 
 def test_overlap_option_values(ctx):
-    assert ctx.lib.mi355x_ctx_set_option(ctx.h, mi355x.OPT_OVERLAP, 2) == mi355x.EINVAL
-    ctx.set_option(mi355x.OPT_OVERLAP, 1)
-    ctx.set_option(mi355x.OPT_OVERLAP, 0)
+    for bad in (1, 5, -1):
+        assert ctx.lib.mi355x_ctx_set_option(ctx.h, mi355x.OPT_OVERLAP, bad) == mi355x.EINVAL
+    for v in (2, 4, 3, 0):
+        ctx.set_option(mi355x.OPT_OVERLAP, v)

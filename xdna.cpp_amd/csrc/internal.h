@@ -42,16 +42,17 @@ struct mi355x_ctx {
     int prefetch_override = 0;
     int64_t grid_override = 0;
     int form_override = MI355X_FORM_AUTO;
-    // MI355X_OPT_OVERLAP: a second stream of the same flags and priority;
-    // consecutive eligible mi355x_gemv calls alternate between the two
-    // (ov_next: the stream of the next one) after a fork event on the first
-    // stream; any other call joins the second stream back first.
-    bool overlap = false;
+    // MI355X_OPT_OVERLAP: `overlap` streams in rotation (0: off) -- the
+    // context's stream and up to three more of the same flags and priority;
+    // consecutive eligible mi355x_gemv calls take them in turn (ov_next: the
+    // stream of the next one) after a fork event on the context's stream;
+    // any other call joins the others back first.
+    int overlap = 0;
     bool ov_open = false;
     int ov_next = 0;
-    hipStream_t stream2 = nullptr;
+    hipStream_t ov_streams[3] = {nullptr, nullptr, nullptr};
     hipEvent_t ov_fork = nullptr;
-    hipEvent_t ov_join_ev = nullptr;
+    hipEvent_t ov_join_ev[3] = {nullptr, nullptr, nullptr};
     std::mutex mu;  // serialises calls that share the staging buffer
     // completion word for mi355x_ctx_fence: pinned host memory the signal
     // kernel writes, and the last value handed out

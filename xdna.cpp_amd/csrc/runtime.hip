@@ -147,18 +147,18 @@ int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
     GemvArgs a{type, static_cast<const uint8_t *>(W), N, K, x, xbf16, y};
     if (!ov) return type == MI355X_TYPE_Q4_0 ? launch_gemv_q4_0(ctx, a) : launch_gemv_kquant(ctx, a);
     if (!ctx->ov_open) {
-        // the second stream starts after everything queued so far
+        // the other streams start after everything queued so far
         MI355X_HIP(hipEventRecord(ctx->ov_fork, ctx->stream));
-        MI355X_HIP(hipStreamWaitEvent(ctx->stream2, ctx->ov_fork, 0));
+        for (int i = 0; i + 1 < ctx->overlap; ++i) MI355X_HIP(hipStreamWaitEvent(ctx->ov_streams[i], ctx->ov_fork, 0));
         ctx->ov_open = true;
         ctx->ov_next = 0;
     }
     // the launchers queue on ctx->stream: point it at this call's stream
     hipStream_t primary = ctx->stream;
-    if (ctx->ov_next) ctx->stream = ctx->stream2;
+    if (ctx->ov_next) ctx->stream = ctx->ov_streams[ctx->ov_next - 1];
     rc = type == MI355X_TYPE_Q4_0 ? launch_gemv_q4_0(ctx, a) : launch_gemv_kquant(ctx, a);
     ctx->stream = primary;
-    ctx->ov_next ^= 1;
+    ctx->ov_next = (ctx->ov_next + 1) % ctx->overlap;
     return rc;
 }
 
@@ -179,8 +179,10 @@ void clear_error() { g_last_error.clear(); }
 int ov_join(mi355x_ctx *ctx) {
     if (!ctx || !ctx->ov_open) return MI355X_OK;
     ctx->ov_open = false;
-    MI355X_HIP(hipEventRecord(ctx->ov_join_ev, ctx->stream2));
-    MI355X_HIP(hipStreamWaitEvent(ctx->stream, ctx->ov_join_ev, 0));
+    for (int i = 0; i + 1 < ctx->overlap; ++i) {
+        MI355X_HIP(hipEventRecord(ctx->ov_join_ev[i], ctx->ov_streams[i]));
+        MI355X_HIP(hipStreamWaitEvent(ctx->stream, ctx->ov_join_ev[i], 0));
+    }
     return MI355X_OK;
 }
 
@@ -318,12 +320,14 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     (void)stop_servers(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->fence_host) (void)hipHostFree(ctx->fence_host);
-    if (ctx->stream2) {
-        (void)hipStreamSynchronize(ctx->stream2);
-        (void)hipStreamDestroy(ctx->stream2);
+    for (int i = 0; i < 3; ++i) {
+        if (ctx->ov_streams[i]) {
+            (void)hipStreamSynchronize(ctx->ov_streams[i]);
+            (void)hipStreamDestroy(ctx->ov_streams[i]);
+        }
+        if (ctx->ov_join_ev[i]) (void)hipEventDestroy(ctx->ov_join_ev[i]);
     }
     if (ctx->ov_fork) (void)hipEventDestroy(ctx->ov_fork);
-    if (ctx->ov_join_ev) (void)hipEventDestroy(ctx->ov_join_ev);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -385,15 +389,17 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
     }
     switch (option) {
     case MI355X_OPT_OVERLAP: {
-        if (value != 0 && value != 1)
-            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap must be 0 or 1");
-        if (value == 1 && !ctx->stream2) {
-            DeviceGuard dg(ctx->device);
-            MI355X_HIP(hipStreamCreateWithFlags(&ctx->stream2, hipStreamNonBlocking));
-            if (!ctx->ov_fork) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_fork, hipEventDisableTiming));
-            if (!ctx->ov_join_ev) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_join_ev, hipEventDisableTiming));
+        if (value < 0 || value > 4)
+            return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap must be 0 (off) or 2 to 4 streams");
+        if (value == 1) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap needs 2 to 4 streams");
+        DeviceGuard dg(ctx->device);
+        if (value >= 2 && !ctx->ov_fork) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_fork, hipEventDisableTiming));
+        for (int i = 0; i + 1 < value; ++i) {
+            if (!ctx->ov_streams[i]) MI355X_HIP(hipStreamCreateWithFlags(&ctx->ov_streams[i], hipStreamNonBlocking));
+            if (!ctx->ov_join_ev[i])
+                MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_join_ev[i], hipEventDisableTiming));
         }
-        ctx->overlap = value == 1;
+        ctx->overlap = static_cast<int>(value);
         return MI355X_OK;
     }
     case MI355X_OPT_VARIANT:
@@ -821,9 +827,9 @@ int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int 
     if (!ctx || !weights || n_weights < 1 || iters < 1 || warmup < 0 || !ms_total)
         return set_error(MI355X_EINVAL, "mi355x_time_gemv: bad arguments");
     DeviceGuard dg(ctx->device);
-    // with MI355X_OPT_OVERLAP consecutive launches may run at once: they
-    // write y and y + N alternately
-    auto out = [&](int i) { return ctx->overlap ? y + (i & 1) * N : y; };
+    // with MI355X_OPT_OVERLAP (S streams) consecutive launches may run at
+    // once: launch i writes y + (i % S) * N
+    auto out = [&](int i) { return ctx->overlap ? y + (i % ctx->overlap) * N : y; };
     for (int i = 0; i < warmup; ++i) {
         int rc = mi355x_gemv(ctx, type, weights[i % n_weights], N, K, x, out(i));
         if (rc) return rc;
