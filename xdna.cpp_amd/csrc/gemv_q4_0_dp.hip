@@ -1404,10 +1404,11 @@ dp_kernel_t pick_dp_n(int nbl, int r, bool a16, bool tail, bool pf) {
     }
 }
 
-// LDS: Q planes (2 * B uint4), d_x (B floats), S (B ints), then the block
-// contributions of every wavefront's rows (WAVES * R * B floats).  Each row
-// is summed by one lane in block order, ggml's sequential f32 sum, so the
-// result is bit-identical to ggml's generic path for the same activations.
+// LDS: Q planes (2 * B uint4), d_x (B floats), S (B ints), then a chunk of
+// block contributions, `cg` row groups of WAVES * R rows (q8_cs_stride(B)
+// floats per row).  Each row is summed by one thread in block order, ggml's
+// sequential f32 sum, so the result is bit-identical to ggml's generic path
+// for the same activations.
 // Job lookup of the single-matrix kernel: group g of W.
 struct Q8OneJob {
     const uint8_t *W;
@@ -1434,16 +1435,27 @@ struct Q8JobTable {
     }
 };
 
+// Row stride (floats) of the block-contribution chunk: 16-byte rows whose
+// dword stride is an odd multiple of 4, so the summing lanes' b128 reads of
+// a row each (one row per lane) fall in distinct banks.
+__host__ __device__ constexpr int q8_cs_stride(int B) { return 4 * (((B + 3) / 4) % 2 == 0 ? (B + 3) / 4 + 1 : (B + 3) / 4 + 2); }
+
+// A workgroup computes the block contributions of `cg` row groups (its
+// groups g, g + G, ...) into one chunk, then sums every row of the chunk at
+// once, one row per thread, each in block order (ordered_sum): the sums of
+// many rows share each instruction instead of one lane per row.
 template <int NBL, int R, bool A16, bool TAIL, class J>
 __device__ __forceinline__ void q8_body(const J &jobs, int n_groups, const float *__restrict__ x, int B,
-                                        int64_t row_bytes, int x_al16) {
+                                        int64_t row_bytes, int x_al16, int cg) {
 #pragma clang fp contract(off)
     constexpr int WAVES = 8;
     extern __shared__ uint4 lds_q8[];
     uint4 *Q = lds_q8;
     float *dx = reinterpret_cast<float *>(lds_q8 + 2 * B);
     int *sx = reinterpret_cast<int *>(dx + B);
-    float *cs_all = reinterpret_cast<float *>(sx + B);
+    // 16-byte aligned start of the chunk
+    float *cs_all = reinterpret_cast<float *>(lds_q8 + 2 * B + (2 * B + 3) / 4);
+    const int stride = q8_cs_stride(B);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     constexpr int ROWS = WAVES * R;
@@ -1458,6 +1470,7 @@ __device__ __forceinline__ void q8_body(const J &jobs, int n_groups, const float
     XTile<XI> xt;
     xt.load(x, B, x_al16 != 0);
     __builtin_amdgcn_sched_barrier(0);
+    const int G = static_cast<int>(gridDim.x);
     int g = blockIdx.x;
     const uint8_t *W;
     float *y;
@@ -1468,45 +1481,53 @@ __device__ __forceinline__ void q8_body(const J &jobs, int n_groups, const float
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dx, sx);
     __syncthreads();
 
-    float *cs = cs_all + wave * R * B;
     while (g < n_groups) {
-        const int row0 = gl * ROWS + wave * R;
-        float *yr = y;
-        const int nr = N;
-        q8_blocks<NBL, R, A16, TAIL>(grp, cs, B, Q, dx, sx, B, lane, bc, tail_mask);
-        g += gridDim.x;
-        jobs.at(g, W, y, N, gl);
-        grp.load(W, gl * ROWS + wave * R, N, B, row_bytes, lane);
-        __syncthreads();
-        if (lane < R) {
-            const float sumf = ordered_sum(cs + lane * B, B);
-            if (row0 + lane < nr) yr[row0 + lane] = sumf;
+        const int g0 = g;
+        int used = 0;
+        for (; used < cg && g < n_groups; ++used) {
+            q8_blocks<NBL, R, A16, TAIL>(grp, cs_all + (used * ROWS + wave * R) * stride, stride, Q, dx, sx, B, lane,
+                                         bc, tail_mask);
+            g += G;
+            jobs.at(g, W, y, N, gl);
+            grp.load(W, gl * ROWS + wave * R, N, B, row_bytes, lane);
         }
         __syncthreads();
+        const int t = static_cast<int>(threadIdx.x);
+        if (t < used * ROWS) {
+            const uint8_t *Wt;
+            float *yt;
+            int Nt, glt;
+            jobs.at(g0 + (t / ROWS) * G, Wt, yt, Nt, glt);
+            const int row = glt * ROWS + t % ROWS;
+            if (row < Nt) yt[row] = ordered_sum(cs_all + t * stride, B);
+        }
+        __syncthreads();  // the chunk is rewritten next
     }
 }
 
 template <int NBL, int R, bool A16, bool TAIL>
 __global__ __launch_bounds__(512) void gemv_q4_0_q8_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
                                                            float *__restrict__ y, int N, int B, int64_t row_bytes,
-                                                           int x_al16) {
+                                                           int x_al16, int cg) {
     constexpr int ROWS = 8 * R;
-    q8_body<NBL, R, A16, TAIL>(Q8OneJob{W, y, N}, (N + ROWS - 1) / ROWS, x, B, row_bytes, x_al16);
+    q8_body<NBL, R, A16, TAIL>(Q8OneJob{W, y, N}, (N + ROWS - 1) / ROWS, x, B, row_bytes, x_al16, cg);
 }
 
 template <int NBL, int R, bool A16, bool TAIL>
 __global__ __launch_bounds__(512) void gemv_q4_0_q8j_kernel(PlJobs jobs, const float *__restrict__ x, int B,
-                                                            int64_t row_bytes, int x_al16) {
-    q8_body<NBL, R, A16, TAIL>(Q8JobTable{jobs}, jobs.first[jobs.n], x, B, row_bytes, x_al16);
+                                                            int64_t row_bytes, int x_al16, int cg) {
+    q8_body<NBL, R, A16, TAIL>(Q8JobTable{jobs}, jobs.first[jobs.n], x, B, row_bytes, x_al16, cg);
 }
 
+typedef void (*q8_kernel_t)(const uint8_t *, const float *, float *, int, int, int64_t, int, int);
+
 template <int NBL, int R>
-dp_kernel_t pick_q8_at(bool a16, bool tail) {
+q8_kernel_t pick_q8_at(bool a16, bool tail) {
     if (a16) return tail ? gemv_q4_0_q8_kernel<NBL, R, true, true> : gemv_q4_0_q8_kernel<NBL, R, true, false>;
     return tail ? gemv_q4_0_q8_kernel<NBL, R, false, true> : gemv_q4_0_q8_kernel<NBL, R, false, false>;
 }
 
-typedef void (*q8j_kernel_t)(PlJobs, const float *, int, int64_t, int);
+typedef void (*q8j_kernel_t)(PlJobs, const float *, int, int64_t, int, int);
 
 template <int NBL, int R>
 q8j_kernel_t pick_q8j_at(bool a16, bool tail) {
@@ -1529,7 +1550,7 @@ q8j_kernel_t pick_q8j(int nbl, bool a16, bool tail) {
 
 // rows per wavefront as the digit kernel's defaults: 4 for one block
 // column, 2 for two, 1 beyond
-dp_kernel_t pick_q8(int nbl, bool a16, bool tail) {
+q8_kernel_t pick_q8(int nbl, bool a16, bool tail) {
     switch (nbl) {
     case 1: return pick_q8_at<1, 4>(a16, tail);
     case 2: return pick_q8_at<2, 2>(a16, tail);
@@ -1632,7 +1653,8 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
     return MI355X_OK;
 }
 
-size_t q8_lds_bytes(int64_t B);
+size_t q8_lds_bytes(int64_t B, int cg);
+int q8_chunk_groups(int64_t B, int64_t n_groups, int64_t grid);
 
 // ggml-cpu numerics: the Q8_0 kernel's row groups of every matrix in one
 // launch (row sums in block order by one lane, so bit-identical to one
@@ -1642,8 +1664,8 @@ static int launch_q8_multi(mi355x_ctx *ctx, int64_t K, const float *x, const Mul
     const int64_t row_bytes = 18 * B;
     const int nbl = static_cast<int>((B + 63) / 64);
     const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
-    const size_t lds = q8_lds_bytes(B);
-    if (n < 1 || n > kPlMaxJobs || B <= 0 || B > kDpMaxBlocks || lds > ctx->max_lds_per_block) return MI355X_OK;
+    if (n < 1 || n > kPlMaxJobs || B <= 0 || B > kDpMaxBlocks || q8_lds_bytes(B, 1) > ctx->max_lds_per_block)
+        return MI355X_OK;
     bool a16 = row_bytes % 16 == 0;
     PlJobs pj{};
     pj.n = n;
@@ -1660,11 +1682,15 @@ static int launch_q8_multi(mi355x_ctx *ctx, int64_t K, const float *x, const Mul
     if (groups > INT32_MAX) return MI355X_OK;
     pj.first[n] = static_cast<int>(groups);
     const q8j_kernel_t k = pick_q8j(nbl, a16, B % 64 != 0);
-    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, lds);
+    // occupancy with the largest chunk, then the chunk this grid needs
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, q8_lds_bytes(B, q8_chunk_groups(B, groups, 1)));
     int64_t grid = std::min<int64_t>(groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
     if (ctx->grid_override > 0) grid = std::min<int64_t>(groups, ctx->grid_override);
+    const int cg = q8_chunk_groups(B, groups, grid);
+    const size_t lds = q8_lds_bytes(B, cg);
+    if (lds > ctx->max_lds_per_block) return MI355X_OK;
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(grid, 1))), dim3(512), lds, ctx->stream, pj, x,
-                       static_cast<int>(B), row_bytes, reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0);
+                       static_cast<int>(B), row_bytes, reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0, cg);
     MI355X_HIP(hipGetLastError());
     *launched = true;
     return MI355X_OK;
@@ -1720,15 +1746,30 @@ int launch_gemv_q4_0_multi(mi355x_ctx *ctx, int64_t K, const float *x, const Mul
 
 namespace mi355x {
 
-size_t q8_lds_bytes(int64_t B) {
+// LDS of the Q8_0 kernels for B blocks per row and cg row groups per chunk.
+size_t q8_lds_bytes(int64_t B, int cg) {
     const int nbl = static_cast<int>((B + 63) / 64);
     const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
-    return static_cast<size_t>(B) * (2 * sizeof(uint4) + sizeof(float) + sizeof(int) + 8 * R * sizeof(float));
+    const size_t base = sizeof(uint4) * static_cast<size_t>(2 * B + (2 * B + 3) / 4);
+    return base + static_cast<size_t>(cg) * 8 * R * q8_cs_stride(static_cast<int>(B)) * sizeof(float);
+}
+
+// Row groups per chunk: what one workgroup gets of n_groups (as the grid
+// spreads them), at most 512 rows (one per thread) and a chunk that keeps
+// the workgroup within 64 KiB of LDS (two per CU).
+int q8_chunk_groups(int64_t B, int64_t n_groups, int64_t grid) {
+    const int nbl = static_cast<int>((B + 63) / 64);
+    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
+    const size_t per = static_cast<size_t>(8 * R) * q8_cs_stride(static_cast<int>(B)) * sizeof(float);
+    const size_t base = q8_lds_bytes(B, 0);
+    const int64_t by_lds = base + per < (64u << 10) ? static_cast<int64_t>(((64u << 10) - base) / per) : 1;
+    const int64_t per_wg = (n_groups + std::max<int64_t>(grid, 1) - 1) / std::max<int64_t>(grid, 1);
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({by_lds, per_wg, 512 / (8 * R)})));
 }
 
 bool q4_0_q8_supports(const mi355x_ctx *ctx, const GemvArgs &a) {
     const int64_t B = a.K / 32;
-    const size_t lds = q8_lds_bytes(B);
+    const size_t lds = q8_lds_bytes(B, 1);
     return !a.x_bf16 && B > 0 && B <= kDpMaxBlocks && lds <= ctx->max_lds_per_block && a.N <= INT32_MAX &&
            static_cast<int64_t>(a.N) * 18 * B < (int64_t(1) << 40);
 }
@@ -1740,15 +1781,18 @@ int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a) {
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
     const int nbl = static_cast<int>((B + 63) / 64);
     const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
-    const dp_kernel_t k = pick_q8(nbl, a16, B % 64 != 0);
-    const size_t lds = q8_lds_bytes(B);
-    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, lds);
+    const q8_kernel_t k = pick_q8(nbl, a16, B % 64 != 0);
     const int64_t n_groups = (a.N + 8 * R - 1) / (8 * R);
+    // occupancy with the largest chunk, then the chunk this grid needs
+    const int occ = occupancy(reinterpret_cast<const void *>(k), 512, q8_lds_bytes(B, q8_chunk_groups(B, n_groups, 1)));
     int64_t grid = std::min<int64_t>(n_groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
     if (ctx->grid_override > 0) grid = std::min<int64_t>(n_groups, ctx->grid_override);
+    const int cg = q8_chunk_groups(B, n_groups, grid);
+    const size_t lds = q8_lds_bytes(B, cg);
+    if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "Q8_0 chunk exceeds LDS");
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(grid, 1))), dim3(512), lds, ctx->stream, a.W,
                        static_cast<const float *>(a.x), a.y, static_cast<int>(a.N), static_cast<int>(B), row_bytes,
-                       x_al16 ? 1 : 0);
+                       x_al16 ? 1 : 0, cg);
     MI355X_HIP(hipGetLastError());
     return MI355X_OK;
 }
