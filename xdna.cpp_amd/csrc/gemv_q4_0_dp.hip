@@ -760,7 +760,81 @@ __device__ __forceinline__ void srv_load_x(XTile<XI> &xt, const float *x, int B)
 // workgroup's rows are contiguous, so the stores of a wavefront cover 256
 // contiguous bytes (written through to memory one 4-byte row at a time they
 // would cost a PCIe transaction each when y is host memory).
-constexpr int kSrvOutMax = 4096;  // rows of one job per workgroup
+constexpr int kSrvOutMax = 4096;  // rows of a command's jobs per workgroup (padded)
+
+// A workgroup's rows of a command's jobs as one local row space: job j's
+// share [lo_j, hi_j) of its N_j rows takes local rows [start_j, start_j +
+// hi_j - lo_j), each job's segment padded to a multiple of ROWS so that a
+// wavefront's group of R rows never spans two jobs.  A wavefront walks its
+// groups wave * R + k * ROWS through every job in one sequence, so the next
+// group's loads are in flight across job boundaries too, and the outputs of
+// all jobs are stored once at the end.  Indices are uniform; the per-job
+// values sit in registers behind constant-index selects.
+template <int ROWS>
+struct SrvSpan {
+    static_assert(kSrvMaxJobs == 4, "four jobs per command");
+    // separate scalars, not arrays: a select over an array becomes an
+    // indexed load from scratch memory
+    int lo0, lo1, lo2, lo3, hi0, hi1, hi2, hi3, st1, st2, st3, tot;
+    __device__ __forceinline__ SrvSpan(const SrvCmd &c, int g, int G) {
+        const int n = c.njobs;
+        // A workgroup's share of a job is a run of whole 64-byte lines of
+        // y (16 outputs; the first unit ends at y's first line boundary):
+        // workgroups that stored parts of one line of pinned host memory
+        // would serialise on it (~6 us per job of small shares).
+        auto share = [&](int j, int &lo, int &hi) {
+            lo = hi = 0;
+            if (j >= n) return;
+            const int64_t N = c.jobs[j].N;
+            const int64_t b0 = static_cast<int64_t>((16u - (reinterpret_cast<uintptr_t>(c.jobs[j].y) >> 2)) & 15u);
+            const int64_t U = 1 + (max(N - b0, int64_t(0)) + 15) / 16;
+            auto at = [&](int64_t u) { return u == 0 ? int64_t(0) : min(N, b0 + 16 * (u - 1)); };
+            lo = static_cast<int>(at(U * g / G));
+            hi = static_cast<int>(at(U * (g + 1) / G));
+        };
+        share(0, lo0, hi0);
+        share(1, lo1, hi1);
+        share(2, lo2, hi2);
+        share(3, lo3, hi3);
+        auto pad = [](int a) { return (a + ROWS - 1) / ROWS * ROWS; };
+        st1 = pad(hi0 - lo0);
+        st2 = st1 + pad(hi1 - lo1);
+        st3 = st2 + pad(hi2 - lo2);
+        tot = st3 + pad(hi3 - lo3);
+    }
+    __device__ __forceinline__ int total() const { return tot; }
+    // job of local row L < total()
+    __device__ __forceinline__ int job_of(int L) const {
+        return (L >= st1 ? 1 : 0) + (L >= st2 ? 1 : 0) + (L >= st3 ? 1 : 0);
+    }
+    __device__ __forceinline__ int lo_of(int j) const { return j == 0 ? lo0 : j == 1 ? lo1 : j == 2 ? lo2 : lo3; }
+    __device__ __forceinline__ int hi_of(int j) const { return j == 0 ? hi0 : j == 1 ? hi1 : j == 2 ? hi2 : hi3; }
+    __device__ __forceinline__ int start_of(int j) const { return j == 0 ? 0 : j == 1 ? st1 : j == 2 ? st2 : st3; }
+    // loads of the group at local row L (past the end: an empty range)
+    template <class Grp>
+    __device__ __forceinline__ void load(Grp &grp, const SrvCmd &c, int L, int B, int64_t row_bytes,
+                                         int lane) const {
+        const bool live = L < tot;
+        const int j = live ? job_of(L) : 0;
+        const int row = live ? lo_of(j) + (L - start_of(j)) : 0;
+        grp.load(c.jobs[j].W, row, live ? hi_of(j) : 0, B, row_bytes, lane);
+    }
+    // every job's outputs from out[start_j + i], system-scope stores
+    // (written through to memory, so the command completes without an L2
+    // write-back)
+    __device__ __forceinline__ void store(const SrvCmd &c, const float *out) const {
+        auto one = [&](int j, int lo, int hi, int st) {
+            float *y = c.jobs[j].y;
+            const int n = j < c.njobs ? hi - lo : 0;
+            for (int i = threadIdx.x; i < n; i += blockDim.x)
+                __hip_atomic_store(&y[lo + i], out[st + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        };
+        one(0, lo0, hi0, 0);
+        one(1, lo1, hi1, st1);
+        one(2, lo2, hi2, st2);
+        one(3, lo3, hi3, st3);
+    }
+};
 
 template <int NBL, bool TAIL>
 __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
@@ -777,43 +851,34 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 #pragma unroll
     for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
     const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
-    const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
+    const SrvSpan<ROWS> sp(c, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+    const int T = sp.total();
 
-    // the first job's first rows are requested before the staging math
-    const int lo0 = static_cast<int>(c.jobs[0].N * g / G), hi0 = static_cast<int>(c.jobs[0].N * (g + 1) / G);
+    // the first group's rows are requested before the staging math
     XTile<XI> xt;
     srv_load_x(xt, x, B);
     __builtin_amdgcn_sched_barrier(0);
     RowGroup<NBL, R, true, TAIL> grp;
-    grp.load(c.jobs[0].W, lo0 + wave * R, hi0, B, row_bytes, lane);
+    sp.load(grp, c, wave * R, B, row_bytes, lane);
     xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
     __syncthreads();
 
-    for (int j = 0; j < c.njobs; ++j) {
-        const SrvJob &job = c.jobs[j];
-        const int lo = static_cast<int>(job.N * g / G), hi = static_cast<int>(job.N * (g + 1) / G);
-        if (j > 0) grp.load(job.W, lo + wave * R, hi, B, row_bytes, lane);
-        for (int row0 = lo + wave * R; row0 < hi; row0 += ROWS) {
-            RowGroup<NBL, R, true, TAIL> nxt;
-            nxt.load(job.W, row0 + ROWS, hi, B, row_bytes, lane);  // empty range past hi
-            float acc[R];
+    for (int L = wave * R; L < T; L += ROWS) {
+        RowGroup<NBL, R, true, TAIL> nxt;
+        sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
+        float acc[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-            grp.accumulate(acc, planes, ub, B, bc, tail_mask);
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        grp.accumulate(acc, planes, ub, B, bc, tail_mask);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float s = wave_sum(acc[r]);
-                if (lane == 0 && row0 + r < hi) out[row0 + r - lo] = s;
-            }
-            grp = nxt;
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == 0) out[L + r] = s;  // padding rows (zero loads) are never stored
         }
-        __syncthreads();
-        // system-scope stores: written through to memory, so the command
-        // completes without an L2 write-back
-        for (int i = threadIdx.x; i < hi - lo; i += blockDim.x)
-            __hip_atomic_store(&job.y[lo + i], out[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __syncthreads();  // `out` is reused by the next job
+        grp = nxt;
     }
+    __syncthreads();
+    sp.store(c, out);
 }
 
 // ggml-cpu numerics job form (MI355X_VARIANT_GGML_Q8): the arithmetic of
@@ -843,50 +908,44 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int64_t row_bytes = 18 * static_cast<int64_t>(B);
     const int stride = B + 4;
-    // rows per chunk: a multiple of ROWS, so a wavefront's runs continue from
-    // one chunk into the next, and at most one per thread (>= ROWS: B <= 64
-    // for R = 4, B <= 128 for R = 2, B <= 512 for R = 1)
+    // rows per chunk: a multiple of ROWS, so a wavefront's groups continue
+    // from one chunk into the next, and at most one per thread (>= ROWS:
+    // B <= 64 for R = 4, B <= 128 for R = 2, B <= 512 for R = 1)
     const int chunk = min((kSrvCsFloats / stride) / ROWS * ROWS, 64 * kSrvWaves);
     int bc[NBL];
 #pragma unroll
     for (int j = 0; j < NBL; ++j) bc[j] = min(lane + 64 * j, B - 1);
     const uint32_t tail_mask = lane + 64 * (NBL - 1) < B ? 0xFFFFu : 0u;
-    const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
+    const SrvSpan<ROWS> sp(c, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+    const int T = sp.total();
 
-    const int lo0 = static_cast<int>(c.jobs[0].N * g / G), hi0 = static_cast<int>(c.jobs[0].N * (g + 1) / G);
     XTile<XI> xt;
     srv_load_x(xt, x, B);
     __builtin_amdgcn_sched_barrier(0);
     using Grp = RowGroup<NBL, R, true, TAIL>;
     Grp grp;
-    grp.load(c.jobs[0].W, lo0 + wave * R, hi0, B, row_bytes, lane);
+    sp.load(grp, c, wave * R, B, row_bytes, lane);
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dxs, sxs);
     __syncthreads();
 
-    for (int j = 0; j < c.njobs; ++j) {
-        const SrvJob &job = c.jobs[j];
-        const int lo = static_cast<int>(job.N * g / G), hi = static_cast<int>(job.N * (g + 1) / G);
-        if (j > 0) grp.load(job.W, lo + wave * R, hi, B, row_bytes, lane);
-        for (int c0 = lo; c0 < hi; c0 += chunk) {
-            const int c1 = min(hi, c0 + chunk);
-            for (int row0 = c0 + wave * R; row0 < c1; row0 += ROWS) {
-                Grp nxt;
-                nxt.load(job.W, row0 + ROWS, hi, B, row_bytes, lane);  // empty range past hi
-                // rows past c1 (at most R - 1) land inside the chunk's
-                // buffer and are never summed
-                q8_blocks<NBL, R, true, TAIL>(grp, csb + (row0 - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
-                                              tail_mask);
-                grp = nxt;
-            }
-            __syncthreads();
-            const int t = static_cast<int>(threadIdx.x);
-            if (t < c1 - c0) out[c0 - lo + t] = ordered_sum(csb + t * stride, B);
-            __syncthreads();  // csb is rewritten by the next chunk
+    for (int c0 = 0; c0 < T; c0 += chunk) {
+        const int c1 = min(T, c0 + chunk);
+        for (int L = c0 + wave * R; L < c1; L += ROWS) {
+            Grp nxt;
+            sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
+            q8_blocks<NBL, R, true, TAIL>(grp, csb + (L - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
+                                          tail_mask);
+            grp = nxt;
         }
-        for (int i = threadIdx.x; i < hi - lo; i += blockDim.x)
-            __hip_atomic_store(&job.y[lo + i], out[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __syncthreads();  // `out` is reused by the next job
+        __syncthreads();
+        const int t = static_cast<int>(threadIdx.x);
+        if (t < c1 - c0) {
+            const int Lt = c0 + t, j = sp.job_of(Lt);
+            if (sp.lo_of(j) + (Lt - sp.start_of(j)) < sp.hi_of(j)) out[Lt] = ordered_sum(csb + t * stride, B);
+        }
+        __syncthreads();  // csb is rewritten by the next chunk
     }
+    sp.store(c, out);
 }
 
 template <int NBL, bool TAIL>
@@ -2135,10 +2194,18 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
     for (int j = 0; j < njobs; ++j) {
         if (!jobs[j].W || !jobs[j].y || jobs[j].N <= 0)
             return set_error(MI355X_EINVAL, "mi355x_server_gemv: bad job");
-        if (jobs[j].N > static_cast<int64_t>(mi355x::kSrvOutMax) * s.grid - s.grid)
-            return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: job of more rows than the server holds");
+
         if (reinterpret_cast<uintptr_t>(jobs[j].W) % 16 != 0)
             return set_error(MI355X_EINVAL, "mi355x_server_gemv: weights must be 16-byte aligned");
+    }
+    {
+        // a workgroup keeps its rows of every job in LDS: a share of whole
+        // 16-row units (one more, partial, at the start) padded to a multiple
+        // of its row group (at most 32 rows)
+        int64_t rows = 0;
+        for (int j = 0; j < njobs; ++j) rows += 16 * ((jobs[j].N / 16 + 2 + s.grid - 1) / s.grid + 1) + 31;
+        if (rows > mi355x::kSrvOutMax)
+            return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: jobs of more rows than the server holds");
     }
     std::lock_guard<std::mutex> sl(s.mu);
     mi355x::DeviceScope dg(s.ctx->device);
