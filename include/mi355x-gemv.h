@@ -312,6 +312,27 @@ typedef struct mi355x_server_job {
 MI355X_API int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out);
 MI355X_API int mi355x_server_gemv(mi355x_server *s, const float *x, int64_t K, int njobs,
                                   const mi355x_server_job *jobs);
+/* A SwiGLU feed-forward block as one server command (no counterpart in the
+ * reference, where ggml-cpu runs the GLU between two MUL_MATs):
+ *   g = W_gate x, u = W_up x   (F rows each, K columns),
+ *   h_i = silu(g_i) * u_i      (h stays in the server's device memory),
+ *   y = W_down h               (N rows, F columns),
+ * with a grid barrier between the stages instead of a return to the host.
+ * Each GEMV has the arithmetic mi355x_server_gemv gives it in the context's
+ * variant.  silu(g) * u is computed in f32, one IEEE operation per step, with
+ * no other contraction than the fmas named:
+ *   t = -g; c = min(max(t, -87.3), 88);
+ *   n = fma(c, 1.44269504088896341, 12582912) - 12582912;
+ *   r = fma(-n, 0.693145751953125, c); r = fma(-n, 1.42860682030941723e-6, r);
+ *   p = 1/5040; p = fma(p, r, k) for k = 1/720, 1/120, 1/24, 1/6, 0.5, 1, 1
+ *     (each constant the f32 quotient);
+ *   e = t < -87.3 ? 0 : p * 2^n;  h = g / (1 + e) * u  (division correctly
+ *   rounded),
+ * so a host that evaluates the same steps gets the same h, and then the same
+ * y.  K and F: multiples of 256 up to max_k; weights 16-byte aligned; y
+ * device-visible as for mi355x_server_gemv. */
+MI355X_API int mi355x_server_swiglu(mi355x_server *s, const float *x, int64_t K, const void *W_gate,
+                                    const void *W_up, int64_t F, const void *W_down, int64_t N, float *y);
 MI355X_API int mi355x_server_stop(mi355x_server *s);
 /* 1 while the server's resident kernel is running, 0 once it has left (after
  * its idle time, a stop, or before the first command); < 0 on error. */

@@ -1,6 +1,8 @@
 """The end-to-end decode harness on the CPU (callback backend): its weight
 quantizer against the Q4_0 recipe pinned elsewhere, its forward pass against
 an independent float64 numpy Qwen2 decoder, and its error paths."""
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
@@ -113,3 +115,77 @@ def test_errors():
             raise ValueError("boom")
         with pytest.raises(RuntimeError, match="GEMV failed"):
             m.generate(np.array([1, 2], dtype=np.int32), 2, bad)
+
+
+# ---- the SwiGLU step shared by the host and mi355x_server_swiglu ------------
+def _round_f32(q: Fraction) -> np.float32:
+    """q rounded to the nearest f32, ties to even (exact, no double rounding)."""
+    f = np.float32(float(q))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        d = abs(Fraction(float(c)) - q)
+        if best is None or d < best[0] or (d == best[0] and (int(c.view(np.uint32)) & 1) == 0):
+            best = (d, c)
+    return best[1]
+
+
+def _q(v) -> Fraction:
+    return Fraction(float(v))
+
+
+def _silu_mul_steps(g: np.float32, u: np.float32) -> np.float32:
+    """The stated f32 steps (mi355x-gemv.h, mi355x_server_swiglu), each
+    rounded exactly once."""
+    fma = lambda a, b, c: _round_f32(_q(a) * _q(b) + _q(c))  # noqa: E731
+    lit = lambda s: _round_f32(Fraction(s))  # noqa: E731  an f32 literal
+    t = -g
+    c = min(max(t, lit("-87.3")), lit("88"))
+    n = _round_f32(_q(fma(c, lit("1.44269504088896341"), lit("12582912"))) - 12582912)
+    r = fma(-n, lit("0.693145751953125"), c)
+    r = fma(-n, lit("1.42860682030941723e-6"), r)
+    p = _round_f32(Fraction(1, 5040))
+    for k in (Fraction(1, 720), Fraction(1, 120), Fraction(1, 24), Fraction(1, 6), Fraction(1, 2), 1, 1):
+        p = fma(p, r, _round_f32(Fraction(k)))
+    e = np.float32(0) if t < lit("-87.3") else _round_f32(_q(p) * Fraction(2) ** int(n))
+    d = _round_f32(1 + _q(e))
+    if g == 0 or u == 0:
+        return np.float32(g / d * u)  # an exact zero: IEEE's sign rules
+    return _round_f32(_q(_round_f32(_q(g) / _q(d))) * _q(u))
+
+
+def _silu_inputs():
+    rng = np.random.default_rng(31)
+    g = np.concatenate([rng.normal(0, 2, 1200), rng.uniform(-95, 95, 200),
+                        [0.0, -0.0, 1e-30, -1e-30, 87.29, 87.3, 87.31, -88.0, -88.5, 100.0, -100.0, 0.5, -0.5,
+                         np.log(2) / 2, -np.log(2) / 2]]).astype(np.float32)
+    u = rng.normal(0, 1, g.size).astype(np.float32)
+    return g, u
+
+
+def test_host_silu_mul_is_the_stated_steps():
+    """qd_silu_mul (the decoder's host SwiGLU step) equals an exact-rational
+    evaluation of the f32 steps mi355x_server_swiglu states, bit for bit:
+    a contraction the steps do not name, or a step left out, changes bits."""
+    g, u = _silu_inputs()
+    h = decode.silu_mul(g, u)
+    want = np.array([_silu_mul_steps(a, b) for a, b in zip(g, u)], dtype=np.float32)
+    bad = np.flatnonzero(h.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, (g[bad[:5]], h[bad[:5]], want[bad[:5]])
+
+
+def test_host_silu_mul_accuracy():
+    """Against silu in float64 (the steps approximate e^t with relative error
+    below 5e-9, then add a few f32 roundings): within 4 ulp of the result
+    where e^-g is in range; below g = -88 (e^-g clamped to e^88) the result
+    stays below 1e-35 in magnitude."""
+    g, u = _silu_inputs()
+    h = decode.silu_mul(g, u).astype(np.float64)
+    low = g < -88
+    assert low.sum() >= 5 and np.abs(h[low]).max() < 1e-35
+    g, u, h = g[~low], u[~low], h[~low]
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    with np.errstate(over="ignore"):
+        ref = g64 / (1.0 + np.exp(-g64)) * u64
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    ok = np.abs(h - ref) <= 4 * ulp + 1e-37
+    assert ok.all(), (g[~ok][:5], h[~ok][:5], ref[~ok][:5])

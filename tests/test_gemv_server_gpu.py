@@ -14,6 +14,7 @@ import time
 import numpy as np
 import pytest
 
+import decode
 import mi355x
 import synth
 from tolerance import check_gemv
@@ -214,6 +215,104 @@ def test_free_on_another_context_stops_the_server(ctx, server):
     finally:
         y.free()
         w.free()
+
+
+# (K, F, N): the decode FFN, tiny, ragged N, F = max_k, N above the grid
+SWIGLU_SHAPES = [(2048, 11008, 2048), (256, 256, 3), (4096, 1024, 777), (512, 16384, 100), (1024, 768, 4099)]
+
+
+def swiglu_weights(ctx, K, F, N, seed):
+    raws = [synth.random_q4_0(F, K, seed=seed), synth.random_q4_0(F, K, seed=seed + 1),
+            synth.random_q4_0(N, F, seed=seed + 2)]
+    ws = [ctx.resident(Q4_0, raws[0], F, K), ctx.resident(Q4_0, raws[1], F, K), ctx.resident(Q4_0, raws[2], N, F)]
+    return raws, ws
+
+
+def swiglu_separate(ctx, server, ws, x):
+    """gate and up as one command, the host's SwiGLU step, down as another."""
+    g, u = run_server(ctx, server, ws[:2], x)
+    (y,) = run_server(ctx, server, ws[2:], decode.silu_mul(g, u))
+    return y, g, u
+
+
+def swiglu_fused(ctx, server, ws, x):
+    F, N = ws[0].N, ws[2].N
+    y = ctx.alloc(4 * N)
+    try:
+        server.swiglu(x, ws[0].ptr, ws[1].ptr, F, ws[2].ptr, N, y.ptr)
+        return y.download(np.float32, N)
+    finally:
+        y.free()
+
+
+@pytest.mark.parametrize("v", [mi355x.VARIANT_AUTO, mi355x.VARIANT_GGML_Q8])
+@pytest.mark.parametrize("K,F,N", SWIGLU_SHAPES)
+def test_server_swiglu_matches_separate_commands(ctx, server, oracle, K, F, N, v):
+    """mi355x_server_swiglu (gate|up, SiLU on the device, grid barrier, down)
+    equals three separate steps -- server GEMVs around the host's SwiGLU
+    step -- bit for bit, in the digit and the ggml Q8_0 arithmetic; in the
+    latter also the oracle's ggml-cpu chain."""
+    raws, ws = swiglu_weights(ctx, K, F, N, seed=K ^ F ^ N)
+    x = synth.activations(K, seed=F + 3)
+    try:
+        with variant(ctx, v):
+            want, g, u = swiglu_separate(ctx, server, ws, x)
+            got = swiglu_fused(ctx, server, ws, x)
+    finally:
+        for w in ws:
+            w.free()
+    assert np.array_equal(got, want), (K, F, N, np.abs(got - want).max())
+    if v == mi355x.VARIANT_GGML_Q8 and F * K <= 30_000_000:
+        go = oracle.gemv_q4_0_q8_0(raws[0], F, K, x)
+        uo = oracle.gemv_q4_0_q8_0(raws[1], F, K, x)
+        assert np.array_equal(g, go) and np.array_equal(u, uo)
+        assert np.array_equal(got, oracle.gemv_q4_0_q8_0(raws[2], N, F, decode.silu_mul(go, uo)))
+
+
+def test_server_swiglu_between_plain_commands(ctx, server):
+    """SwiGLU and plain commands alternating on one resident kernel (the grid
+    barrier's count carries across commands): every output equals its
+    reference and the kernel stays resident."""
+    K, F, N = 2048, 2816, 2048
+    _, ws = swiglu_weights(ctx, K, F, N, seed=40)
+    xs = [synth.activations(K, seed=600 + it) for it in range(12)]
+    want = [swiglu_separate(ctx, server, ws, x)[0] for x in xs]
+    plain = [rows_form(ctx, ws[0], x) for x in xs]
+    y = ctx.alloc(4 * N)
+    yp = ctx.alloc(4 * F)
+    try:
+        server.stop()
+        for it, x in enumerate(xs):
+            server.swiglu(x, ws[0].ptr, ws[1].ptr, F, ws[2].ptr, N, y.ptr)
+            assert server.running(), it
+            assert np.array_equal(y.download(np.float32, N), want[it]), it
+            server.gemv(x, [(ws[0].ptr, F, yp.ptr)])
+            assert np.array_equal(yp.download(np.float32, F), plain[it]), it
+    finally:
+        for b in [y, yp] + ws:
+            b.free()
+
+
+def test_server_swiglu_rejects_bad_arguments(ctx, server):
+    K, F, N = 512, 512, 64
+    _, ws = swiglu_weights(ctx, K, F, N, seed=50)
+    y = ctx.alloc(4 * N)
+    try:
+        x = np.ones(K, np.float32)
+        g, u, d = ws[0].ptr, ws[1].ptr, ws[2].ptr
+        assert server.swiglu_ptr(x[:500], g, u, F, d, N, y.ptr) == mi355x.EINVAL  # K % 256
+        assert server.swiglu_ptr(x, g, u, 500, d, N, y.ptr) == mi355x.EINVAL  # F % 256
+        assert server.swiglu_ptr(x, g, u, 16640, d, N, y.ptr) == mi355x.EINVAL  # F > max_k
+        assert server.swiglu_ptr(x, g, u, F, d, 0, y.ptr) == mi355x.EINVAL
+        assert server.swiglu_ptr(x, g + 2, u, F, d, N, y.ptr) == mi355x.EINVAL  # alignment
+        assert server.swiglu_ptr(x, g, u, F, d + 8, N, y.ptr) == mi355x.EINVAL
+        assert server.swiglu_ptr(x, g, u, F, d, N, 0) == mi355x.EINVAL
+        with variant(ctx, mi355x.VARIANT_EXACT_F32):
+            assert server.swiglu_ptr(x, g, u, F, d, N, y.ptr) == mi355x.EUNSUPPORTED
+        server.swiglu(x, g, u, F, d, N, y.ptr)  # still serves
+    finally:
+        for b in [y] + ws:
+            b.free()
 
 
 def test_server_rejects_bad_arguments(ctx, server):

@@ -711,6 +711,15 @@ struct SrvCmd {
     int32_t njobs;
     int32_t mode;  // kSrvDigits or kSrvGgmlQ8
     SrvJob jobs[kSrvMaxJobs];
+    // SwiGLU command (K2 > 0): jobs 0 and 1 are the gate and up matrices,
+    // both of K2 rows and both with y = h; the first stage writes
+    // h = silu(gate x) * (up x) instead of their outputs, every workgroup
+    // waits at a grid barrier, and the second stage computes down h (K2
+    // columns).  K2 == 0: one stage.
+    int32_t K2;
+    int32_t pad_;
+    float *h;
+    SrvJob down;
 };
 // job arithmetic: the row form's digit planes, or ggml-cpu's Q8_0 numerics
 constexpr int32_t kSrvDigits = 0;
@@ -722,6 +731,11 @@ struct SrvDev {
     uint32_t quit[32];
     uint64_t group[8][16];
     uint64_t top[16];
+    // grid barrier of SwiGLU commands: arrivals per group, then on the top
+    // counter; the last arrival raises every group's flag
+    uint64_t bar_group[8][16];
+    uint64_t bar_top[16];
+    uint32_t bar_flag[8][32];
     SrvCmd cmd;  // copy of the current command record
 };
 
@@ -836,6 +850,45 @@ struct SrvSpan {
     }
 };
 
+// silu(g) * u = g / (1 + e^-g) * u, each step one IEEE f32 operation as
+// written (contraction off, fmas explicit), so a host that performs the same
+// steps gets the same bits.  e^t: t clamped to [-87.3, 88]; n = t / ln2
+// rounded to an integer (one fma against 1.5 * 2^23); r = t - n ln2 in two
+// fmas (ln2 split into a part exact in f32 and a remainder); e^r by its
+// degree-7 Taylor polynomial in Horner fmas (|r| <= ln2 / 2: relative error
+// < 5e-9); times 2^n from the exponent bits; 0 for t < -87.3.
+__device__ __forceinline__ float srv_silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float t = -g;
+    const float tc = fminf(fmaxf(t, -87.3f), 88.0f);
+    const float n = __builtin_fmaf(tc, 1.44269504088896341f, 12582912.0f) - 12582912.0f;
+    float r = __builtin_fmaf(-n, 0.693145751953125f, tc);
+    r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+    float p = 1.0f / 5040.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float e = p * __builtin_bit_cast(float, (static_cast<int32_t>(n) + 127) << 23);
+    const float ex = t < -87.3f ? 0.0f : e;
+    return g / (1.0f + ex) * u;
+}
+
+// The store pass of a SwiGLU command's first stage: jobs 0 and 1 (gate and
+// up) have the same rows and the same y, so a workgroup holds the same share
+// [lo0, hi0) of both, at out[0 ..] and out[st1 ..]; it writes
+// h[i] = silu(gate_i) * up_i for its share (system-scope stores).
+template <int ROWS>
+__device__ __forceinline__ void srv_store_glu(const SrvSpan<ROWS> &sp, const SrvCmd &c, const float *out) {
+    const int n = sp.hi0 - sp.lo0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        __hip_atomic_store(&c.h[sp.lo0 + i], srv_silu_mul(out[i], out[sp.st1 + i]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <int NBL, bool TAIL>
 __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                          float *out) {
@@ -878,7 +931,8 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
         grp = nxt;
     }
     __syncthreads();
-    sp.store(c, out);
+    if (c.K2) srv_store_glu(sp, c, out);
+    else sp.store(c, out);
 }
 
 // ggml-cpu numerics job form (MI355X_VARIANT_GGML_Q8): the arithmetic of
@@ -945,7 +999,8 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
         }
         __syncthreads();  // csb is rewritten by the next chunk
     }
-    sp.store(c, out);
+    if (c.K2) srv_store_glu(sp, c, out);
+    else sp.store(c, out);
 }
 
 template <int NBL, bool TAIL>
@@ -953,6 +1008,28 @@ __device__ __forceinline__ void srv_job(const SrvCmd &c, int B, uint4 *lds, cons
                                         float *out, float *csb) {
     if (c.mode == kSrvGgmlQ8) srv_rows_q8<NBL, TAIL>(c, B, lds, x, out, csb);
     else srv_rows<NBL, TAIL>(c, B, lds, x, out);
+}
+
+// One stage of a command: its jobs over the activation x of c.K columns.
+__device__ __forceinline__ void srv_stage(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb) {
+    const int B = c.K / 32;
+    switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
+    case 2: srv_job<1, false>(c, B, lds, x, outb, csb); break;
+    case 3: srv_job<1, true>(c, B, lds, x, outb, csb); break;
+    case 4: srv_job<2, false>(c, B, lds, x, outb, csb); break;
+    case 5: srv_job<2, true>(c, B, lds, x, outb, csb); break;
+    case 6: srv_job<3, false>(c, B, lds, x, outb, csb); break;
+    case 7: srv_job<3, true>(c, B, lds, x, outb, csb); break;
+    case 8: srv_job<4, false>(c, B, lds, x, outb, csb); break;
+    case 9: srv_job<4, true>(c, B, lds, x, outb, csb); break;
+    case 10: srv_job<5, false>(c, B, lds, x, outb, csb); break;
+    case 11: srv_job<5, true>(c, B, lds, x, outb, csb); break;
+    case 12: srv_job<6, false>(c, B, lds, x, outb, csb); break;
+    case 13: srv_job<6, true>(c, B, lds, x, outb, csb); break;
+    case 14: srv_job<7, false>(c, B, lds, x, outb, csb); break;
+    case 15: srv_job<7, true>(c, B, lds, x, outb, csb); break;
+    default: srv_job<8, false>(c, B, lds, x, outb, csb); break;  // B = 512 (the host checks K)
+    }
 }
 
 // Command-record fields as 32-bit words (the record is copied word by word).
@@ -969,10 +1046,12 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
     __shared__ uint32_t verdict;  // 0 run, 1 leave
     __shared__ int32_t shk;       // K of this command (workgroup 0)
     __shared__ SrvCmd cs;         // this command
+    __shared__ SrvCmd cs2;        // the second stage of a SwiGLU command
     __shared__ float outb[kSrvOutMax];
     __shared__ __align__(16) float csb[kSrvCsFloats];  // block contributions (Q8_0 jobs)
     const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
     uint32_t *csw = reinterpret_cast<uint32_t *>(&cs);
+    uint64_t nbar = 0;  // grid barriers passed in this launch
     for (uint32_t expect = first;; ++expect) {
         if (g == 0) {
             // workgroup 0: wait for the host, then copy the command record
@@ -1055,24 +1134,56 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             __syncthreads();
             if (cs.exit) return;
         }
-        const SrvCmd &c = cs;
-        const int B = c.K / 32;
-        switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
-        case 2: srv_job<1, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 3: srv_job<1, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 4: srv_job<2, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 5: srv_job<2, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 6: srv_job<3, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 7: srv_job<3, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 8: srv_job<4, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 9: srv_job<4, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 10: srv_job<5, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 11: srv_job<5, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 12: srv_job<6, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 13: srv_job<6, true>(c, B, lds_dp, dx, outb, csb); break;
-        case 14: srv_job<7, false>(c, B, lds_dp, dx, outb, csb); break;
-        case 15: srv_job<7, true>(c, B, lds_dp, dx, outb, csb); break;
-        default: srv_job<8, false>(c, B, lds_dp, dx, outb, csb); break;  // B = 512 (the host checks K)
+        srv_stage(cs, lds_dp, dx, outb, csb);
+        if (cs.K2) {
+            // SwiGLU: every workgroup's h stores have completed before its
+            // arrival at the grid barrier (all workgroups are resident: the
+            // launch is cooperative); the wait is bounded like the others
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            ++nbar;
+            if (threadIdx.x == 0) {
+                // 256 arrivals on one counter serialise (~25 ns each, measured);
+                // in two levels, as the completion count below, each counter
+                // takes at most 32, and the pollers read their group's flag
+                // line, not a counter line that takes atomics
+                const int gi = g & 7;
+                const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
+                const uint64_t a =
+                    __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+                if (a == nbar * members) {
+                    const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
+                    const uint64_t t =
+                        __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+                    if (t == nbar * groups)
+                        for (int i = 0; i < static_cast<int>(groups); ++i)
+                            __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(nbar), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
+                const uint64_t t0 = srv_clock();
+                uint32_t leave = 0;
+                while (static_cast<int32_t>(
+                           __hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
+                           static_cast<uint32_t>(nbar)) < 0) {
+                    if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                        srv_clock() - t0 > 2 * idle_ticks) {
+                        leave = 1;
+                        __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                verdict = leave;
+                // the second stage: the down job over h
+                cs2.K = cs.K2;
+                cs2.njobs = 1;
+                cs2.mode = cs.mode;
+                cs2.K2 = 0;
+                cs2.jobs[0] = cs.down;
+            }
+            __syncthreads();
+            if (verdict) return;
+            srv_stage(cs2, lds_dp, cs.h, outb, csb);
         }
         // every wave's output stores have completed (they write through) before
         // the barrier, and so before thread 0 counts the arrival; no fence:
@@ -2040,6 +2151,7 @@ struct ServerImpl {
     uint32_t *done_h = nullptr, *done_d = nullptr;
     SrvDev *dev = nullptr;
     float *dx = nullptr;   // device copy of x (written by workgroup 0)
+    float *dh = nullptr;   // h of SwiGLU commands (max_k floats)
     uint32_t seq = 0;      // last command number handed out
     bool running = false;
     std::chrono::steady_clock::time_point last{};
@@ -2111,6 +2223,60 @@ int stop_servers(mi355x_ctx *ctx) {
 
 }  // namespace mi355x
 
+namespace mi355x {
+namespace {
+// A workgroup keeps its rows of every job of a stage in LDS: a share of
+// whole 16-row units (one more, partial, at the start) padded to a multiple
+// of its row group (at most 32 rows).
+bool server_rows_fit(const ServerImpl &s, const mi355x_server_job *jobs, int njobs) {
+    int64_t rows = 0;
+    for (int j = 0; j < njobs; ++j) rows += 16 * ((jobs[j].N / 16 + 2 + s.grid - 1) / s.grid + 1) + 31;
+    return rows <= kSrvOutMax;
+}
+
+// Hands command c (its jobs and stages filled in) with x of K columns to the
+// resident kernel, launching it first when needed, and waits for completion.
+int server_submit(ServerImpl &s, const float *x, int64_t K, const SrvCmd &c, const char *who) {
+    std::lock_guard<std::mutex> sl(s.mu);
+    DeviceScope dg(s.ctx->device);
+    const auto now = std::chrono::steady_clock::now();
+    if (s.running && std::chrono::duration<double>(now - s.last).count() > kSrvIdleSeconds / 2) {
+        int rc = server_stop(&s);
+        if (rc) return rc;
+    }
+    if (!s.running) {
+        int rc = server_launch(&s);
+        if (rc) return rc;
+    }
+    std::memcpy(s.hx_h, x, static_cast<size_t>(K) * sizeof(float));
+    s.cmd_h->K = static_cast<int32_t>(K);
+    s.cmd_h->njobs = c.njobs;
+    s.cmd_h->mode = c.mode;
+    for (int j = 0; j < kSrvMaxJobs; ++j) s.cmd_h->jobs[j] = c.jobs[j];
+    s.cmd_h->K2 = c.K2;
+    s.cmd_h->h = c.h;
+    s.cmd_h->down = c.down;
+    const uint32_t v = ++s.seq;
+    __hip_atomic_store(&s.cmd_h->seqk, static_cast<uint64_t>(v) | (static_cast<uint64_t>(K) << 32), __ATOMIC_RELEASE,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0;; ++i) {
+        if (static_cast<int32_t>(__hip_atomic_load(s.done_h, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) - v) >= 0)
+            break;
+        if ((i & 1023) == 1023 &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kSrvWaitSeconds) {
+            // the kernel leaves by its idle rule; collect it and report
+            s.running = false;
+            (void)hipStreamSynchronize(s.stream);
+            return set_error(MI355X_EHIP, std::string(who) + ": no completion within 5 s");
+        }
+    }
+    s.last = std::chrono::steady_clock::now();
+    return MI355X_OK;
+}
+}  // namespace
+}  // namespace mi355x
+
 using mi355x::set_error;
 using mi355x::hip_error;
 using mi355x::clear_error;
@@ -2160,6 +2326,8 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
     if (e == hipSuccess) s.dev = static_cast<mi355x::SrvDev *>(p);
     if (e == hipSuccess) e = hipMalloc(&p, static_cast<size_t>(max_k) * sizeof(float));
     if (e == hipSuccess) s.dx = static_cast<float *>(p);
+    if (e == hipSuccess) e = hipMalloc(&p, static_cast<size_t>(max_k) * sizeof(float));
+    if (e == hipSuccess) s.dh = static_cast<float *>(p);
     int per_cu = 0;
     if (e == hipSuccess)
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -2198,49 +2366,43 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
         if (reinterpret_cast<uintptr_t>(jobs[j].W) % 16 != 0)
             return set_error(MI355X_EINVAL, "mi355x_server_gemv: weights must be 16-byte aligned");
     }
-    {
-        // a workgroup keeps its rows of every job in LDS: a share of whole
-        // 16-row units (one more, partial, at the start) padded to a multiple
-        // of its row group (at most 32 rows)
-        int64_t rows = 0;
-        for (int j = 0; j < njobs; ++j) rows += 16 * ((jobs[j].N / 16 + 2 + s.grid - 1) / s.grid + 1) + 31;
-        if (rows > mi355x::kSrvOutMax)
-            return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: jobs of more rows than the server holds");
-    }
-    std::lock_guard<std::mutex> sl(s.mu);
-    mi355x::DeviceScope dg(s.ctx->device);
-    const auto now = std::chrono::steady_clock::now();
-    if (s.running && std::chrono::duration<double>(now - s.last).count() > mi355x::kSrvIdleSeconds / 2) {
-        int rc = mi355x::server_stop(&s);
-        if (rc) return rc;
-    }
-    if (!s.running) {
-        int rc = mi355x::server_launch(&s);
-        if (rc) return rc;
-    }
-    std::memcpy(s.hx_h, x, static_cast<size_t>(K) * sizeof(float));
-    s.cmd_h->K = static_cast<int32_t>(K);
-    s.cmd_h->njobs = njobs;
-    s.cmd_h->mode = mode;
-    for (int j = 0; j < njobs; ++j)
-        s.cmd_h->jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
-    const uint32_t v = ++s.seq;
-    __hip_atomic_store(&s.cmd_h->seqk, static_cast<uint64_t>(v) | (static_cast<uint64_t>(K) << 32), __ATOMIC_RELEASE,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
-    const auto t0 = std::chrono::steady_clock::now();
-    for (int i = 0;; ++i) {
-        if (static_cast<int32_t>(__hip_atomic_load(s.done_h, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) - v) >= 0)
-            break;
-        if ((i & 1023) == 1023 &&
-            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > mi355x::kSrvWaitSeconds) {
-            // the kernel leaves by its idle rule; collect it and report
-            s.running = false;
-            (void)hipStreamSynchronize(s.stream);
-            return set_error(MI355X_EHIP, "mi355x_server_gemv: no completion within 5 s");
-        }
-    }
-    s.last = std::chrono::steady_clock::now();
-    return MI355X_OK;
+    if (!mi355x::server_rows_fit(s, jobs, njobs))
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: jobs of more rows than the server holds");
+    mi355x::SrvCmd c{};
+    c.njobs = njobs;
+    c.mode = mode;
+    for (int j = 0; j < njobs; ++j) c.jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
+    return mi355x::server_submit(s, x, K, c, "mi355x_server_gemv");
+}
+
+int mi355x_server_swiglu(mi355x_server *srv, const float *x, int64_t K, const void *W_gate, const void *W_up,
+                         int64_t F, const void *W_down, int64_t N, float *y) {
+    clear_error();
+    if (!srv || !x || !W_gate || !W_up || !W_down || !y)
+        return set_error(MI355X_EINVAL, "mi355x_server_swiglu: null pointer");
+    mi355x::ServerImpl &s = srv->impl;
+    if (K <= 0 || K % 256 != 0 || K > s.max_k || F <= 0 || F % 256 != 0 || F > s.max_k)
+        return set_error(MI355X_EINVAL, "mi355x_server_swiglu: K and F must be multiples of 256 up to max_k");
+    if (N <= 0) return set_error(MI355X_EINVAL, "mi355x_server_swiglu: N must be positive");
+    for (const void *w : {W_gate, W_up, W_down})
+        if (reinterpret_cast<uintptr_t>(w) % 16 != 0)
+            return set_error(MI355X_EINVAL, "mi355x_server_swiglu: weights must be 16-byte aligned");
+    const int variant = s.ctx->kernel_variant;
+    if (variant == MI355X_VARIANT_EXACT_F32)
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_swiglu: no exact-f32 form in the server");
+    const mi355x_server_job up_stage[2] = {{W_gate, F, s.dh}, {W_up, F, s.dh}};
+    const mi355x_server_job down_stage[1] = {{W_down, N, y}};
+    if (!mi355x::server_rows_fit(s, up_stage, 2) || !mi355x::server_rows_fit(s, down_stage, 1))
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_swiglu: jobs of more rows than the server holds");
+    mi355x::SrvCmd c{};
+    c.njobs = 2;
+    c.mode = variant == MI355X_VARIANT_GGML_Q8 ? mi355x::kSrvGgmlQ8 : mi355x::kSrvDigits;
+    c.jobs[0] = {static_cast<const uint8_t *>(W_gate), s.dh, F};
+    c.jobs[1] = {static_cast<const uint8_t *>(W_up), s.dh, F};
+    c.K2 = static_cast<int32_t>(F);
+    c.h = s.dh;
+    c.down = {static_cast<const uint8_t *>(W_down), y, N};
+    return mi355x::server_submit(s, x, K, c, "mi355x_server_swiglu");
 }
 
 int mi355x_server_stop(mi355x_server *srv) {
@@ -2278,6 +2440,7 @@ void mi355x_server_destroy(mi355x_server *srv) {
         if (s.stream) (void)hipStreamDestroy(s.stream);
         if (s.dev) (void)hipFree(s.dev);
         if (s.dx) (void)hipFree(s.dx);
+        if (s.dh) (void)hipFree(s.dh);
     }
     if (s.cmd_h) (void)hipHostFree(s.cmd_h);
     if (s.hx_h) (void)hipHostFree(s.hx_h);

@@ -51,6 +51,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_last_logits.restype = C.c_int
     lib.qd_last_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_quantize_q4_0.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
+    lib.qd_silu_mul.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_set_fuse.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_variant.restype = C.c_int
     lib.qd_set_variant.argtypes = [C.c_void_p, C.c_int]
@@ -77,6 +78,16 @@ def quantize_q4_0(w: np.ndarray) -> np.ndarray:
     out = np.empty(N * (K // 32) * 18, dtype=np.uint8)
     load().qd_quantize_q4_0(w.ctypes.data, N, K, out.ctypes.data)
     return out.reshape(N, -1)
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """The decoder's host SwiGLU step: silu(g) * u in the f32 steps that
+    mi355x_server_swiglu states."""
+    g = np.array(g, dtype=np.float32, copy=True)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    assert g.shape == u.shape and g.ndim == 1
+    load().qd_silu_mul(g.ctypes.data, u.ctypes.data, g.size)
+    return g
 
 
 def prompt_tokens(n: int, vocab: int, seed: int) -> np.ndarray:

@@ -295,25 +295,35 @@ void rope(float *v, int hd, const float *cs) {
 // in float and a remainder), e^r by its degree-7 Taylor polynomial (relative
 // error < 5e-9 on that range), times 2^n built in the exponent bits.  Inputs
 // below -87.3 give 0, above 88 are clamped to 88 (the callers never get there:
-// softmax arguments are <= 0, SiLU's are -g).
+// softmax arguments are <= 0, SiLU's are -g).  Every multiply-add is an
+// explicit fma, so the result does not depend on the compiler's contraction
+// choices: these are the steps of mi355x_server_swiglu's SiLU, which gives the
+// same bits on the GPU (the one product left, p * 2^n, is exact unless it is
+// subnormal, where 1 + e^x rounds to 1 either way).
 inline float fast_exp(float x) {
     const float xc = std::min(std::max(x, -87.3f), 88.0f);
     // round to nearest by adding and subtracting 1.5 * 2^23 (|x / ln2| < 2^22)
-    const float n = (xc * 1.44269504088896341f + 12582912.0f) - 12582912.0f;
-    const float r = (xc - n * 0.693145751953125f) - n * 1.42860682030941723e-6f;
+    const float n = std::fma(xc, 1.44269504088896341f, 12582912.0f) - 12582912.0f;
+    const float r = std::fma(-n, 1.42860682030941723e-6f, std::fma(-n, 0.693145751953125f, xc));
     float p = 1.0f / 5040.0f;
-    p = p * r + 1.0f / 720.0f;
-    p = p * r + 1.0f / 120.0f;
-    p = p * r + 1.0f / 24.0f;
-    p = p * r + 1.0f / 6.0f;
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
+    p = std::fma(p, r, 1.0f / 720.0f);
+    p = std::fma(p, r, 1.0f / 120.0f);
+    p = std::fma(p, r, 1.0f / 24.0f);
+    p = std::fma(p, r, 1.0f / 6.0f);
+    p = std::fma(p, r, 0.5f);
+    p = std::fma(p, r, 1.0f);
+    p = std::fma(p, r, 1.0f);
     const int32_t bits = (static_cast<int32_t>(n) + 127) << 23;
     float scale;
     std::memcpy(&scale, &bits, 4);
     const float e = p * scale;  // computed unconditionally so the select vectorizes
     return x < -87.3f ? 0.0f : e;
+}
+
+// g[i] = silu(g[i]) * u[i] = g / (1 + e^-g) * u
+void silu_mul(float *g, const float *u, int n) {
+#pragma omp simd
+    for (int i = 0; i < n; ++i) g[i] = g[i] / (1.0f + fast_exp(-g[i])) * u[i];
 }
 
 // Grouped-query attention of one position over n_t cached positions:
@@ -710,6 +720,8 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     if (use_server && !m->server && mi355x_server_create(m->ctx, max_k, &m->server) != MI355X_OK)
         use_server = false;  // e.g. no cooperative launch: one launch per group
     const int wait = !use_server && m->wait_mode == QD_WAIT_SERVER ? QD_WAIT_FENCE : m->wait_mode;
+    // the feed-forward block as one SwiGLU server command (fused groups only)
+    const bool swiglu = backend == 0 && use_server && m->fuse && c.ffn % 256 == 0;
 
     // per layer: keys [g][t / 8][i][t % 8], values [g][t][i] (see attention())
     const int tcap = (T + 7) / 8 * 8;
@@ -883,13 +895,28 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             for (int i = 0; i < H; ++i) h[i] += o[i];
             rmsnorm(h.data(), m->ffn_norm[l].data(), xn.data(), H, c.norm_eps);
             t_host += now() - th;
-            if ((rc = gemvs(xn.data(), H, {7 * l + QD_GATE, 7 * l + QD_UP}, {g.data(), u.data()}))) break;
-            th = now();
-#pragma omp simd
-            for (int i = 0; i < c.ffn; ++i) g[i] = g[i] / (1.0f + fast_exp(-g[i])) * u[i];
-            t_host += now() - th;
-            if ((rc = gemvs(g.data(), c.ffn, {7 * l + QD_DOWN}, {dn.data()}))) break;
-            th = now();
+            if (swiglu) {
+                // gate|up, SiLU and down as one server command
+                const double t0 = now();
+                const Matrix &wg = m->mats[7 * l + QD_GATE], &wu = m->mats[7 * l + QD_UP],
+                             &wd = m->mats[7 * l + QD_DOWN];
+                if (mi355x_server_swiglu(m->server, xn.data(), H, wg.dev, wu.dev, c.ffn, wd.dev, H, m->hy_dev) !=
+                    MI355X_OK) {
+                    rc = -1;
+                    break;
+                }
+                std::memcpy(dn.data(), m->hy, static_cast<size_t>(H) * 4);
+                launches += 2;
+                t_gemv += now() - t0;
+                th = now();
+            } else {
+                if ((rc = gemvs(xn.data(), H, {7 * l + QD_GATE, 7 * l + QD_UP}, {g.data(), u.data()}))) break;
+                th = now();
+                silu_mul(g.data(), u.data(), c.ffn);
+                t_host += now() - th;
+                if ((rc = gemvs(g.data(), c.ffn, {7 * l + QD_DOWN}, {dn.data()}))) break;
+                th = now();
+            }
             for (int i = 0; i < H; ++i) h[i] += dn[i];
         }
         if (rc) break;
@@ -918,5 +945,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     }
     return 0;
 }
+
+void qd_silu_mul(float *g, const float *u, int n) { silu_mul(g, u, n); }
 
 }  // extern "C"

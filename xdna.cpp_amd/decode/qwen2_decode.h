@@ -66,6 +66,9 @@ QD_API const char *qd_last_error(void);
 QD_API int qd_last_logits(const qd_model *m, float *out, int n);
 /* The weight quantizer (ggml's Q4_0 rule), exposed for tests. */
 QD_API void qd_quantize_q4_0(const float *x, int64_t N, int64_t K, uint8_t *out);
+/* The host's SwiGLU step, g[i] = silu(g[i]) * u[i], in the f32 steps that
+ * mi355x_server_swiglu states (exposed for tests). */
+QD_API void qd_silu_mul(float *g, const float *u, int n);
 
 /* Moves every matrix into HBM (prepacked) on `device`; later runs with
  * backend 0 use it. */

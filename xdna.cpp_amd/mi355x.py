@@ -48,6 +48,7 @@ _SIGNATURES = {
     "mi355x_ctx_fence": (_c.c_int, [_vp]),
     "mi355x_server_create": (_c.c_int, [_vp, _c.c_int64, _c.POINTER(_vp)]),
     "mi355x_server_gemv": (_c.c_int, [_vp, _vp, _c.c_int64, _c.c_int, _vp]),
+    "mi355x_server_swiglu": (_c.c_int, [_vp, _vp, _c.c_int64, _vp, _vp, _c.c_int64, _vp, _c.c_int64, _vp]),
     "mi355x_server_stop": (_c.c_int, [_vp]),
     "mi355x_server_running": (_c.c_int, [_vp]),
     "mi355x_server_destroy": (None, [_vp]),
@@ -222,6 +223,14 @@ class Server:
 
     def gemv(self, x: np.ndarray, jobs) -> None:
         check(self.gemv_ptr(x, jobs))
+
+    def swiglu_ptr(self, x: np.ndarray, w_gate: int, w_up: int, F: int, w_down: int, N: int, y: int) -> int:
+        """y = W_down (silu(W_gate x) * (W_up x)) as one command (device pointers)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        return self.lib.mi355x_server_swiglu(self.h, x.ctypes.data, x.size, w_gate, w_up, F, w_down, N, y)
+
+    def swiglu(self, x: np.ndarray, w_gate: int, w_up: int, F: int, w_down: int, N: int, y: int) -> None:
+        check(self.swiglu_ptr(x, w_gate, w_up, F, w_down, N, y))
 
     def stop(self) -> None:
         check(self.lib.mi355x_server_stop(self.h))
