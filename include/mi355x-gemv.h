@@ -333,6 +333,24 @@ MI355X_API int mi355x_server_gemv(mi355x_server *s, const float *x, int64_t K, i
  * device-visible as for mi355x_server_gemv. */
 MI355X_API int mi355x_server_swiglu(mi355x_server *s, const float *x, int64_t K, const void *W_gate,
                                     const void *W_up, int64_t F, const void *W_down, int64_t N, float *y);
+/* The rest of a pre-norm transformer layer after attention as one server
+ * command (no counterpart in the reference):
+ *   r  = resid + W_o x           (W_o: H rows, K columns; resid: H floats),
+ *   xn = rmsnorm(r) * norm_w     (norm_w: H floats in device memory),
+ *   y  = r + W_down (silu(W_gate xn) * (W_up xn))   (gate/up: F rows, H
+ *        columns; down: H rows, F columns; SiLU as mi355x_server_swiglu),
+ * with grid barriers between the stages.  The GEMVs have mi355x_server_gemv's
+ * arithmetic in the context's variant, the additions are single f32 adds,
+ * and rmsnorm takes these steps: ss = the sum of r_i^2 in double as 16
+ * partial sums p_k = sum over i0 = 0, 16, 32, ... of r[i0 + k]^2 in that order,
+ * l_k = (p_k + p_{4+k}) + (p_{8+k} + p_{12+k}) for k < 4,
+ * ss = (l_0 + l_1) + (l_2 + l_3);  s = 1 / sqrt(float(ss / H) + eps) in f32
+ * (correctly rounded);  xn_i = (r_i * s) * norm_w_i.  K, H, F: multiples of
+ * 256, H <= 4096, F <= max_k and K + H <= max_k; y device-visible. */
+MI355X_API int mi355x_server_block(mi355x_server *s, const float *x, int64_t K, const void *W_o,
+                                   const float *resid, int64_t H, const float *norm_w, float eps,
+                                   const void *W_gate, const void *W_up, int64_t F, const void *W_down,
+                                   float *y);
 MI355X_API int mi355x_server_stop(mi355x_server *s);
 /* 1 while the server's resident kernel is running, 0 once it has left (after
  * its idle time, a stop, or before the first command); < 0 on error. */

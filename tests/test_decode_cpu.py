@@ -189,3 +189,53 @@ def test_host_silu_mul_accuracy():
     ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
     ok = np.abs(h - ref) <= 4 * ulp + 1e-37
     assert ok.all(), (g[~ok][:5], h[~ok][:5], ref[~ok][:5])
+
+
+def _rmsnorm_steps(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """The stated RMSNorm steps (mi355x-gemv.h, mi355x_server_block) with
+    Python floats (IEEE double, each add rounded once, squares exact)."""
+    H = x.size
+    xd = [float(v) for v in x]
+    p = []
+    for k in range(16):
+        acc = 0.0
+        for i0 in range(0, H, 16):
+            acc = acc + xd[i0 + k] * xd[i0 + k]
+        p.append(acc)
+    lanes = [(p[k] + p[4 + k]) + (p[8 + k] + p[12 + k]) for k in range(4)]
+    ss = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3])
+    s = np.float32(1.0) / np.sqrt(np.float32(ss / H) + np.float32(eps))
+    return (x * s) * w
+
+
+@pytest.mark.parametrize("H", [256, 2048, 4096])
+def test_host_rmsnorm_is_the_stated_steps(H):
+    """qd_rmsnorm equals the stated steps bit for bit and is within 2 ulp of
+    the float64 formula."""
+    rng = np.random.default_rng(H)
+    x = (rng.standard_normal(H) * np.exp(rng.uniform(-3, 3, H))).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    got = decode.rmsnorm(x, w, 1e-6)
+    assert np.array_equal(got.view(np.uint32), _rmsnorm_steps(x, w, 1e-6).view(np.uint32))
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * w.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2 * np.spacing(np.abs(ref).astype(np.float32)))
+
+
+def test_host_rmsnorm_order_is_pinned():
+    """Over 300 short vectors the stated steps hold every time, while a
+    float32 sum of squares (a plausible slip) changes the output of some: the
+    bit-exact check above can tell the two apart."""
+    rng = np.random.default_rng(5)
+    differ = 0
+    for _ in range(300):
+        x = (rng.standard_normal(256) * np.exp(rng.uniform(-4, 4, 256))).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+        want = _rmsnorm_steps(x, w, 1e-6)
+        assert np.array_equal(decode.rmsnorm(x, w, 1e-6).view(np.uint32), want.view(np.uint32))
+        ss32 = np.float32(0)
+        for v in x:
+            ss32 = np.float32(ss32 + np.float32(v * v))
+        alt = (x * (np.float32(1) / np.sqrt(np.float32(ss32 / np.float32(256)) + np.float32(1e-6)))) * w
+        differ += not np.array_equal(alt, want)
+    assert differ > 0

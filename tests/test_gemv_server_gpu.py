@@ -70,9 +70,10 @@ def run_server(ctx, server, ws, x):
 
 
 # decode shapes (q|k|v, o, gate|up, down, vocabulary) and others: 1-8 block
-# columns per lane, with and without a partial last column, tiny N
+# columns per lane, with and without a partial last column (8 with one:
+# 448 < K / 32 < 512), tiny N
 SHAPES = [(2560, 2048), (2048, 2048), (22016, 2048), (2048, 11008), (151936, 2048), (300, 4096), (777, 5120),
-          (513, 8192), (64, 14336), (200, 16384), (3, 2048), (255, 256)]
+          (513, 8192), (64, 14336), (129, 15616), (200, 16384), (3, 2048), (255, 256)]
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
@@ -312,6 +313,119 @@ def test_server_swiglu_rejects_bad_arguments(ctx, server):
         server.swiglu(x, g, u, F, d, N, y.ptr)  # still serves
     finally:
         for b in [y] + ws:
+            b.free()
+
+
+# (K, H, F): the 3B decode layer, tiny, H at its 4096 limit, F = max_k, K != H
+BLOCK_SHAPES = [(2048, 2048, 11008), (256, 256, 512), (4096, 4096, 1024), (512, 1024, 16384 - 1024),
+                (1024, 2048, 768)]
+EPS = 1e-6
+
+
+def block_weights(ctx, K, H, F, seed):
+    shapes = [(H, K), (F, H), (F, H), (H, F)]
+    raws = [synth.random_q4_0(n, k, seed=seed + i) for i, (n, k) in enumerate(shapes)]
+    return raws, [ctx.resident(Q4_0, r, n, k) for r, (n, k) in zip(raws, shapes)]
+
+
+def block_separate(ctx, server, ws, x, resid, norm_w):
+    """o, the residual add, the host's RMSNorm, gate|up, the host's SwiGLU
+    step, down and the second residual add as separate steps."""
+    (o,) = run_server(ctx, server, ws[:1], x)
+    r = resid + o
+    g, u = run_server(ctx, server, ws[1:3], decode.rmsnorm(r, norm_w, EPS))
+    (dn,) = run_server(ctx, server, ws[3:], decode.silu_mul(g, u))
+    return r + dn
+
+
+def block_fused(ctx, server, ws, x, resid, nw):
+    H, F = ws[0].N, ws[1].N
+    y = ctx.alloc(4 * H)
+    try:
+        server.block(x, ws[0].ptr, resid, nw.ptr, EPS, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, y.ptr)
+        return y.download(np.float32, H)
+    finally:
+        y.free()
+
+
+@pytest.mark.parametrize("v", [mi355x.VARIANT_AUTO, mi355x.VARIANT_GGML_Q8])
+@pytest.mark.parametrize("K,H,F", BLOCK_SHAPES)
+def test_server_block_matches_separate_steps(ctx, server, K, H, F, v):
+    """mi355x_server_block (o, residual, RMSNorm on the device, gate|up, SiLU,
+    down, residual, with grid barriers) equals the separate steps around the
+    host's RMSNorm and SwiGLU step, bit for bit, in both arithmetics."""
+    _, ws = block_weights(ctx, K, H, F, seed=K ^ H ^ F)
+    rng = np.random.default_rng(H + F)
+    x = synth.activations(K, seed=K + 9)
+    resid = (rng.standard_normal(H) * 0.5).astype(np.float32)
+    norm_w = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    nw = ctx.to_device(norm_w)
+    try:
+        with variant(ctx, v):
+            want = block_separate(ctx, server, ws, x, resid, norm_w)
+            got = block_fused(ctx, server, ws, x, resid, nw)
+            again = block_fused(ctx, server, ws, x, resid, nw)
+    finally:
+        for b in ws + [nw]:
+            b.free()
+    assert np.array_equal(got, want), (K, H, F, np.abs(got - want).max())
+    assert np.array_equal(again, got)
+
+
+def test_server_block_between_other_commands(ctx, server):
+    """Block, SwiGLU and plain commands in turn on one resident kernel (the
+    barrier count carries across commands of both kinds)."""
+    K, H, F = 2048, 2048, 2816
+    _, ws = block_weights(ctx, K, H, F, seed=70)
+    rng = np.random.default_rng(71)
+    norm_w = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    nw = ctx.to_device(norm_w)
+    xs = [synth.activations(K, seed=700 + it) for it in range(8)]
+    rs = [(rng.standard_normal(H) * 0.5).astype(np.float32) for _ in xs]
+    want = [block_separate(ctx, server, ws, x, r, norm_w) for x, r in zip(xs, rs)]
+    want_sw = [swiglu_separate(ctx, server, ws[1:], x)[0] for x in xs]
+    plain = [rows_form(ctx, ws[0], x) for x in xs]
+    y = ctx.alloc(4 * H)
+    try:
+        server.stop()
+        for it, (x, r) in enumerate(zip(xs, rs)):
+            server.block(x, ws[0].ptr, r, nw.ptr, EPS, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, y.ptr)
+            assert np.array_equal(y.download(np.float32, H), want[it]), it
+            server.swiglu(x, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, H, y.ptr)
+            assert np.array_equal(y.download(np.float32, H), want_sw[it]), it
+            server.gemv(x, [(ws[0].ptr, H, y.ptr)])
+            assert np.array_equal(y.download(np.float32, H), plain[it]), it
+            assert server.running(), it
+    finally:
+        for b in [y, nw] + ws:
+            b.free()
+
+
+def test_server_block_rejects_bad_arguments(ctx, server):
+    K, H, F = 512, 512, 512
+    _, ws = block_weights(ctx, K, H, F, seed=80)
+    nw = ctx.to_device(np.ones(H, np.float32))
+    y = ctx.alloc(4 * H)
+    try:
+        x, r = np.ones(K, np.float32), np.ones(H, np.float32)
+        o, g, u, d = (w.ptr for w in ws)
+        args = lambda **kw: dict(dict(x=x, w_o=o, resid=r, norm_w=nw.ptr, eps=EPS, w_gate=g, w_up=u, F=F,  # noqa: E731
+                                      w_down=d, y=y.ptr), **kw)
+        call = lambda **kw: server.block_ptr(**args(**kw))  # noqa: E731
+        assert call(x=x[:500]) == mi355x.EINVAL  # K % 256
+        assert call(resid=r[:500]) == mi355x.EINVAL  # H % 256
+        assert call(F=500) == mi355x.EINVAL
+        assert call(resid=np.ones(4352, np.float32)) == mi355x.EINVAL  # H > 4096
+        assert call(x=np.ones(16384, np.float32)) == mi355x.EINVAL  # K + H > max_k
+        assert call(w_o=o + 2) == mi355x.EINVAL
+        assert call(w_down=d + 8) == mi355x.EINVAL
+        assert call(norm_w=0) == mi355x.EINVAL
+        assert call(y=0) == mi355x.EINVAL
+        with variant(ctx, mi355x.VARIANT_EXACT_F32):
+            assert call() == mi355x.EUNSUPPORTED
+        assert call() == mi355x.OK  # still serves
+    finally:
+        for b in [y, nw] + ws:
             b.free()
 
 

@@ -711,16 +711,35 @@ struct SrvCmd {
     int32_t njobs;
     int32_t mode;  // kSrvDigits or kSrvGgmlQ8
     SrvJob jobs[kSrvMaxJobs];
+    // how the store pass writes job 0's rows (kSrvStore*) and, for the
+    // residual kinds, the vector added to them
+    int32_t kind;
+    int32_t pad_;
+    const float *add;
     // SwiGLU command (K2 > 0): jobs 0 and 1 are the gate and up matrices,
     // both of K2 rows and both with y = h; the first stage writes
-    // h = silu(gate x) * (up x) instead of their outputs, every workgroup
-    // waits at a grid barrier, and the second stage computes down h (K2
-    // columns).  K2 == 0: one stage.
+    // h = silu(gate x) * (up x) instead of their outputs (kind
+    // kSrvStoreGlu), every workgroup waits at a grid barrier, and the second
+    // stage computes down h (K2 columns).  K2 == 0: one stage.
     int32_t K2;
-    int32_t pad_;
+    int32_t H;  // block command: rows of pre and columns of gate / up
     float *h;
     SrvJob down;
+    // block command (pre.N > 0): before the SwiGLU stages, r = resid +
+    // pre x (pre: H rows, K columns; resid: the H floats after x in the
+    // payload) into r_dev, a grid barrier, then xn = rmsnorm(r) * norm_w
+    // (eps) as the gate / up activation; the down stage writes y = r + down h.
+    SrvJob pre;
+    float *r_dev;
+    const float *norm_w;
+    float eps;
+    int32_t pad2_;
 };
+// store-pass kinds
+constexpr int32_t kSrvStoreY = 0;     // y[row] = out
+constexpr int32_t kSrvStoreGlu = 1;   // h[row] = silu(out of job 0) * out of job 1
+constexpr int32_t kSrvStoreAddG = 2;  // y[row] = out + add[row], add in device memory written this command
+constexpr int32_t kSrvStoreAddL = 3;  // y[row] = out + add[row], add in this workgroup's LDS
 // job arithmetic: the row form's digit planes, or ggml-cpu's Q8_0 numerics
 constexpr int32_t kSrvDigits = 0;
 constexpr int32_t kSrvGgmlQ8 = 1;
@@ -889,7 +908,38 @@ __device__ __forceinline__ void srv_store_glu(const SrvSpan<ROWS> &sp, const Srv
                            __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <int NBL, bool TAIL>
+// Residual store pass (one job): y[lo0 + i] = out[i] + add[lo0 + i]; the
+// add vector is read through the system-coherent path when another
+// workgroup wrote it in this command (kSrvStoreAddG), else from LDS.
+template <int ROWS>
+__device__ __forceinline__ void srv_store_add(const SrvSpan<ROWS> &sp, const SrvCmd &c, const float *out) {
+#pragma clang fp contract(off)
+    const int n = sp.hi0 - sp.lo0;
+    float *y = c.jobs[0].y;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int r = sp.lo0 + i;
+        const float a = c.kind == kSrvStoreAddG ? __hip_atomic_load(&c.add[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                                                : c.add[r];
+        __hip_atomic_store(&y[r], out[i] + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void srv_store(const SrvSpan<ROWS> &sp, const SrvCmd &c, const float *out) {
+    if (c.kind == kSrvStoreGlu) srv_store_glu(sp, c, out);
+    else if (c.kind == kSrvStoreY) sp.store(c, out);
+    else srv_store_add(sp, c, out);
+}
+
+// The activation of a stage: from device memory written in this command
+// (the system-coherent path), or (XL) from this workgroup's LDS.
+template <bool XL, int XI>
+__device__ __forceinline__ void srv_activation(XTile<XI> &xt, const float *x, int B) {
+    if constexpr (XL) xt.load(x, B, true);
+    else srv_load_x(xt, x, B);
+}
+
+template <int NBL, bool TAIL, bool XL>
 __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                          float *out) {
     constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
@@ -909,7 +959,7 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 
     // the first group's rows are requested before the staging math
     XTile<XI> xt;
-    srv_load_x(xt, x, B);
+    srv_activation<XL>(xt, x, B);
     __builtin_amdgcn_sched_barrier(0);
     RowGroup<NBL, R, true, TAIL> grp;
     sp.load(grp, c, wave * R, B, row_bytes, lane);
@@ -931,8 +981,7 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
         grp = nxt;
     }
     __syncthreads();
-    if (c.K2) srv_store_glu(sp, c, out);
-    else sp.store(c, out);
+    srv_store(sp, c, out);
 }
 
 // ggml-cpu numerics job form (MI355X_VARIANT_GGML_Q8): the arithmetic of
@@ -948,7 +997,7 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 // rows start on 16 different bank groups.
 constexpr int kSrvCsFloats = 8192;
 
-template <int NBL, bool TAIL>
+template <int NBL, bool TAIL, bool XL>
 __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                             float *out, float *csb) {
 #pragma clang fp contract(off)
@@ -974,7 +1023,7 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     const int T = sp.total();
 
     XTile<XI> xt;
-    srv_load_x(xt, x, B);
+    srv_activation<XL>(xt, x, B);
     __builtin_amdgcn_sched_barrier(0);
     using Grp = RowGroup<NBL, R, true, TAIL>;
     Grp grp;
@@ -999,15 +1048,26 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
         }
         __syncthreads();  // csb is rewritten by the next chunk
     }
-    if (c.K2) srv_store_glu(sp, c, out);
-    else sp.store(c, out);
+    srv_store(sp, c, out);
 }
 
-template <int NBL, bool TAIL>
+template <int NBL, bool TAIL, bool XL = false>
 __device__ __forceinline__ void srv_job(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                         float *out, float *csb) {
-    if (c.mode == kSrvGgmlQ8) srv_rows_q8<NBL, TAIL>(c, B, lds, x, out, csb);
-    else srv_rows<NBL, TAIL>(c, B, lds, x, out);
+    if (c.mode == kSrvGgmlQ8) srv_rows_q8<NBL, TAIL, XL>(c, B, lds, x, out, csb);
+    else srv_rows<NBL, TAIL, XL>(c, B, lds, x, out);
+}
+
+// A stage whose activation (c.K <= kSrvLdsXMax columns) is in LDS.
+constexpr int kSrvLdsXMax = 4096;
+__device__ __forceinline__ void srv_stage_lds(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb) {
+    const int B = c.K / 32;
+    switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
+    case 2: srv_job<1, false, true>(c, B, lds, x, outb, csb); break;
+    case 3: srv_job<1, true, true>(c, B, lds, x, outb, csb); break;
+    case 4: srv_job<2, false, true>(c, B, lds, x, outb, csb); break;
+    default: srv_job<2, true, true>(c, B, lds, x, outb, csb); break;  // B < 128 (the host checks K)
+    }
 }
 
 // One stage of a command: its jobs over the activation x of c.K columns.
@@ -1028,8 +1088,96 @@ __device__ __forceinline__ void srv_stage(const SrvCmd &c, uint4 *lds, const flo
     case 13: srv_job<6, true>(c, B, lds, x, outb, csb); break;
     case 14: srv_job<7, false>(c, B, lds, x, outb, csb); break;
     case 15: srv_job<7, true>(c, B, lds, x, outb, csb); break;
-    default: srv_job<8, false>(c, B, lds, x, outb, csb); break;  // B = 512 (the host checks K)
+    case 16: srv_job<8, false>(c, B, lds, x, outb, csb); break;
+    default: srv_job<8, true>(c, B, lds, x, outb, csb); break;  // 448 < B < 512 (the host checks K <= 16384)
     }
+}
+
+// Grid barrier inside a command (thread 0 of every workgroup; `n` = barriers
+// this launch has passed, this one included).  256 arrivals on one counter
+// serialise (~25 ns each, measured); in two levels, as the completion count,
+// each counter takes at most 32, and the pollers read their group's flag
+// line, not a counter line that takes atomics.  Bounded like every wait:
+// returns 1 (and raises quit) after `limit` ticks or when quit is raised.
+__device__ __forceinline__ uint32_t srv_barrier(SrvDev *dev, int g, int G, uint64_t n, uint64_t limit) {
+    const int gi = g & 7;
+    const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
+    const uint64_t a = __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    if (a == n * members) {
+        const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
+        const uint64_t t = __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        if (t == n * groups)
+            for (int i = 0; i < static_cast<int>(groups); ++i)
+                __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(n), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint64_t t0 = srv_clock();
+    while (static_cast<int32_t>(__hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
+                                static_cast<uint32_t>(n)) < 0) {
+        if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 || srv_clock() - t0 > limit) {
+            __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return 1;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return 0;
+}
+
+// RMSNorm of the block command, every workgroup for itself: r (H floats,
+// written by other workgroups in this command) into rb, then
+// xn[i] = r[i] * s * w[i] into xnb with s = 1 / sqrt(float(ss / H) + eps), the
+// f32 steps and the summation order of the decode host's rmsnorm: ss in
+// double as 16 partial sums p_k = sum over i0 = 0, 16, ... of r[i0 + k]^2
+// (sequential; a square of a float is exact in double), combined as
+// ((p0+p4)+(p8+p12)) + ((p1+p5)+(p9+p13)) + ... lane-wise, then
+// (l0 + l1) + (l2 + l3).  H: a multiple of 256.
+__device__ __forceinline__ void srv_rmsnorm(const float *r, const float *w, float eps, int H, float *rb, float *xnb,
+                                            double *pbuf, float *sbuf) {
+#pragma clang fp contract(off)
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r), 0, static_cast<uint32_t>(4 * H), kBufferWord3);
+    // r into rb, and transposed into xnb (free until the end): partial sum k's
+    // elements r[k], r[16 + k], ... side by side at xnb[k * H / 16 ..], so its
+    // lane reads them 4 at a time (rows L + 4 floats apart: 16-byte aligned,
+    // and the 16 rows start in different banks)
+    const int L = H / 16, LS = L + 4;
+    for (int i = 4 * static_cast<int>(threadIdx.x); i < H; i += 4 * static_cast<int>(blockDim.x)) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * i, 0, kSysCoherent);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = v[e];
+            const float f = __builtin_bit_cast(float, u);
+            rb[i + e] = f;
+            xnb[((i + e) & 15) * LS + ((i + e) >> 4)] = f;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const float4 *q = reinterpret_cast<const float4 *>(xnb + threadIdx.x * LS);  // L: a multiple of 16
+        double p = 0.0;
+#pragma unroll 4
+        for (int j = 0; j < L / 4; ++j) {
+            const float4 f = q[j];
+            const double a = f.x, b = f.y, c = f.z, d = f.w;
+            p = __builtin_fma(a, a, p);
+            p = __builtin_fma(b, b, p);
+            p = __builtin_fma(c, c, p);
+            p = __builtin_fma(d, d, p);
+        }
+        pbuf[threadIdx.x] = p;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double l[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l[k] = (pbuf[k] + pbuf[4 + k]) + (pbuf[8 + k] + pbuf[12 + k]);
+        const double ss = (l[0] + l[1]) + (l[2] + l[3]);
+        *sbuf = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
+    }
+    __syncthreads();
+    const float sc = *sbuf;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) xnb[i] = rb[i] * sc * w[i];
+    __syncthreads();
 }
 
 // Command-record fields as 32-bit words (the record is copied word by word).
@@ -1046,7 +1194,11 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
     __shared__ uint32_t verdict;  // 0 run, 1 leave
     __shared__ int32_t shk;       // K of this command (workgroup 0)
     __shared__ SrvCmd cs;         // this command
-    __shared__ SrvCmd cs2;        // the second stage of a SwiGLU command
+    __shared__ SrvCmd cs2;        // the later stages of SwiGLU and block commands
+    __shared__ __align__(16) float rb[kSrvLdsXMax];   // block command: r
+    __shared__ __align__(16) float xnb[kSrvLdsXMax + 64];  // block command: rmsnorm(r) * norm_w
+    __shared__ double pbuf[16];
+    __shared__ float sbuf;
     __shared__ float outb[kSrvOutMax];
     __shared__ __align__(16) float csb[kSrvCsFloats];  // block contributions (Q8_0 jobs)
     const int G = static_cast<int>(gridDim.x), g = static_cast<int>(blockIdx.x);
@@ -1134,56 +1286,56 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             __syncthreads();
             if (cs.exit) return;
         }
-        srv_stage(cs, lds_dp, dx, outb, csb);
-        if (cs.K2) {
-            // SwiGLU: every workgroup's h stores have completed before its
-            // arrival at the grid barrier (all workgroups are resident: the
-            // launch is cooperative); the wait is bounded like the others
+        // a grid barrier: every workgroup's stores of the stage before have
+        // completed before its arrival (all workgroups are resident: the
+        // launch is cooperative)
+        auto barrier = [&]() {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             ++nbar;
-            if (threadIdx.x == 0) {
-                // 256 arrivals on one counter serialise (~25 ns each, measured);
-                // in two levels, as the completion count below, each counter
-                // takes at most 32, and the pollers read their group's flag
-                // line, not a counter line that takes atomics
-                const int gi = g & 7;
-                const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
-                const uint64_t a =
-                    __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-                if (a == nbar * members) {
-                    const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
-                    const uint64_t t =
-                        __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-                    if (t == nbar * groups)
-                        for (int i = 0; i < static_cast<int>(groups); ++i)
-                            __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(nbar), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                }
-                const uint64_t t0 = srv_clock();
-                uint32_t leave = 0;
-                while (static_cast<int32_t>(
-                           __hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                           static_cast<uint32_t>(nbar)) < 0) {
-                    if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                        srv_clock() - t0 > 2 * idle_ticks) {
-                        leave = 1;
-                        __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                verdict = leave;
-                // the second stage: the down job over h
-                cs2.K = cs.K2;
-                cs2.njobs = 1;
-                cs2.mode = cs.mode;
-                cs2.K2 = 0;
-                cs2.jobs[0] = cs.down;
-            }
+            if (threadIdx.x == 0) verdict = srv_barrier(dev, g, G, nbar, 2 * idle_ticks);
             __syncthreads();
-            if (verdict) return;
-            srv_stage(cs2, lds_dp, cs.h, outb, csb);
+            return verdict != 0;
+        };
+        // cs2 = cs, one word per thread (then thread 0 patches the stage)
+        auto copy_cmd = [&]() {
+            uint32_t *d = reinterpret_cast<uint32_t *>(&cs2);
+            for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x) d[i] = csw[i];
+            __syncthreads();
+        };
+        // stages: plain 1; SwiGLU 2 (gate|up -> h, down); block 3 (pre -> r,
+        // gate|up over rmsnorm(r) -> h, down + r).  One call site per stage
+        // form keeps the kernel's register count at that of one stage.
+        const bool blk = cs.pre.N > 0;
+        const int nst = blk ? 3 : (cs.K2 ? 2 : 1);
+        for (int st = 0; st < nst; ++st) {
+            if (st > 0 && barrier()) return;
+            if (blk && st == 1) srv_rmsnorm(cs.r_dev, cs.norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
+            if (st > 0 || blk) {
+                copy_cmd();
+                if (threadIdx.x == 0) {
+                    if (st == 0) {
+                        // block: r = resid + pre x, resid after x in the payload
+                        cs2.njobs = 1;
+                        cs2.jobs[0] = {cs.pre.W, cs.r_dev, cs.pre.N};
+                        cs2.kind = kSrvStoreAddG;
+                        cs2.add = dx + cs.K;
+                    } else if (st == 1 && blk) {
+                        cs2.K = cs.H;
+                        cs2.kind = kSrvStoreGlu;
+                    } else {
+                        cs2.K = cs.K2;
+                        cs2.njobs = 1;
+                        cs2.jobs[0] = cs.down;
+                        cs2.kind = blk ? kSrvStoreAddL : kSrvStoreY;
+                        cs2.add = rb;
+                    }
+                }
+                __syncthreads();
+            }
+            const SrvCmd &c = st > 0 || blk ? cs2 : cs;
+            if (blk && st == 1) srv_stage_lds(c, lds_dp, xnb, outb, csb);
+            else srv_stage(c, lds_dp, st == 0 ? dx : cs.h, outb, csb);
         }
         // every wave's output stores have completed (they write through) before
         // the barrier, and so before thread 0 counts the arrival; no fence:
@@ -2152,6 +2304,7 @@ struct ServerImpl {
     SrvDev *dev = nullptr;
     float *dx = nullptr;   // device copy of x (written by workgroup 0)
     float *dh = nullptr;   // h of SwiGLU commands (max_k floats)
+    float *dr = nullptr;   // r of block commands (kSrvLdsXMax floats)
     uint32_t seq = 0;      // last command number handed out
     bool running = false;
     std::chrono::steady_clock::time_point last{};
@@ -2234,9 +2387,11 @@ bool server_rows_fit(const ServerImpl &s, const mi355x_server_job *jobs, int njo
     return rows <= kSrvOutMax;
 }
 
-// Hands command c (its jobs and stages filled in) with x of K columns to the
-// resident kernel, launching it first when needed, and waits for completion.
-int server_submit(ServerImpl &s, const float *x, int64_t K, const SrvCmd &c, const char *who) {
+// Hands command c (its jobs and stages filled in) with the payload x (nx
+// floats, then x2's nx2) to the resident kernel, launching it first when
+// needed, and waits for completion.
+int server_submit(ServerImpl &s, const float *x, int64_t nx, const float *x2, int64_t nx2, const SrvCmd &c,
+                  const char *who) {
     std::lock_guard<std::mutex> sl(s.mu);
     DeviceScope dg(s.ctx->device);
     const auto now = std::chrono::steady_clock::now();
@@ -2248,16 +2403,18 @@ int server_submit(ServerImpl &s, const float *x, int64_t K, const SrvCmd &c, con
         int rc = server_launch(&s);
         if (rc) return rc;
     }
-    std::memcpy(s.hx_h, x, static_cast<size_t>(K) * sizeof(float));
-    s.cmd_h->K = static_cast<int32_t>(K);
-    s.cmd_h->njobs = c.njobs;
-    s.cmd_h->mode = c.mode;
-    for (int j = 0; j < kSrvMaxJobs; ++j) s.cmd_h->jobs[j] = c.jobs[j];
-    s.cmd_h->K2 = c.K2;
-    s.cmd_h->h = c.h;
-    s.cmd_h->down = c.down;
+    std::memcpy(s.hx_h, x, static_cast<size_t>(nx) * sizeof(float));
+    if (nx2) std::memcpy(s.hx_h + nx, x2, static_cast<size_t>(nx2) * sizeof(float));
+    {
+        // every field but the command number, which goes last
+        SrvCmd r = c;
+        r.seqk = s.cmd_h->seqk;
+        r.exit = 0;
+        *s.cmd_h = r;
+    }
     const uint32_t v = ++s.seq;
-    __hip_atomic_store(&s.cmd_h->seqk, static_cast<uint64_t>(v) | (static_cast<uint64_t>(K) << 32), __ATOMIC_RELEASE,
+    const uint64_t n = static_cast<uint64_t>(nx + nx2);  // payload floats for the relay
+    __hip_atomic_store(&s.cmd_h->seqk, static_cast<uint64_t>(v) | (n << 32), __ATOMIC_RELEASE,
                        __HIP_MEMORY_SCOPE_SYSTEM);
     const auto t0 = std::chrono::steady_clock::now();
     for (int i = 0;; ++i) {
@@ -2328,6 +2485,8 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
     if (e == hipSuccess) s.dx = static_cast<float *>(p);
     if (e == hipSuccess) e = hipMalloc(&p, static_cast<size_t>(max_k) * sizeof(float));
     if (e == hipSuccess) s.dh = static_cast<float *>(p);
+    if (e == hipSuccess) e = hipMalloc(&p, mi355x::kSrvLdsXMax * sizeof(float));
+    if (e == hipSuccess) s.dr = static_cast<float *>(p);
     int per_cu = 0;
     if (e == hipSuccess)
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -2369,10 +2528,11 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
     if (!mi355x::server_rows_fit(s, jobs, njobs))
         return set_error(MI355X_EUNSUPPORTED, "mi355x_server_gemv: jobs of more rows than the server holds");
     mi355x::SrvCmd c{};
+    c.K = static_cast<int32_t>(K);
     c.njobs = njobs;
     c.mode = mode;
     for (int j = 0; j < njobs; ++j) c.jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
-    return mi355x::server_submit(s, x, K, c, "mi355x_server_gemv");
+    return mi355x::server_submit(s, x, K, nullptr, 0, c, "mi355x_server_gemv");
 }
 
 int mi355x_server_swiglu(mi355x_server *srv, const float *x, int64_t K, const void *W_gate, const void *W_up,
@@ -2395,14 +2555,58 @@ int mi355x_server_swiglu(mi355x_server *srv, const float *x, int64_t K, const vo
     if (!mi355x::server_rows_fit(s, up_stage, 2) || !mi355x::server_rows_fit(s, down_stage, 1))
         return set_error(MI355X_EUNSUPPORTED, "mi355x_server_swiglu: jobs of more rows than the server holds");
     mi355x::SrvCmd c{};
+    c.K = static_cast<int32_t>(K);
+    c.njobs = 2;
+    c.mode = variant == MI355X_VARIANT_GGML_Q8 ? mi355x::kSrvGgmlQ8 : mi355x::kSrvDigits;
+    c.jobs[0] = {static_cast<const uint8_t *>(W_gate), s.dh, F};
+    c.jobs[1] = {static_cast<const uint8_t *>(W_up), s.dh, F};
+    c.kind = mi355x::kSrvStoreGlu;
+    c.K2 = static_cast<int32_t>(F);
+    c.h = s.dh;
+    c.down = {static_cast<const uint8_t *>(W_down), y, N};
+    return mi355x::server_submit(s, x, K, nullptr, 0, c, "mi355x_server_swiglu");
+}
+
+int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const void *W_o, const float *resid,
+                        int64_t H, const float *norm_w, float eps, const void *W_gate, const void *W_up, int64_t F,
+                        const void *W_down, float *y) {
+    clear_error();
+    if (!srv || !x || !W_o || !resid || !norm_w || !W_gate || !W_up || !W_down || !y)
+        return set_error(MI355X_EINVAL, "mi355x_server_block: null pointer");
+    mi355x::ServerImpl &s = srv->impl;
+    if (K <= 0 || K % 256 != 0 || F <= 0 || F % 256 != 0 || F > s.max_k || H <= 0 || H % 256 != 0 ||
+        H > mi355x::kSrvLdsXMax || K + H > s.max_k)
+        return set_error(MI355X_EINVAL,
+                         "mi355x_server_block: K, H and F must be multiples of 256, H <= 4096, F and K + H <= max_k");
+    for (const void *w : {W_o, W_gate, W_up, W_down})
+        if (reinterpret_cast<uintptr_t>(w) % 16 != 0)
+            return set_error(MI355X_EINVAL, "mi355x_server_block: weights must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(norm_w) % 4 != 0)
+        return set_error(MI355X_EINVAL, "mi355x_server_block: norm_w must be 4-byte aligned");
+    const int variant = s.ctx->kernel_variant;
+    if (variant == MI355X_VARIANT_EXACT_F32)
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_block: no exact-f32 form in the server");
+    const mi355x_server_job pre_stage[1] = {{W_o, H, s.dr}};
+    const mi355x_server_job up_stage[2] = {{W_gate, F, s.dh}, {W_up, F, s.dh}};
+    const mi355x_server_job down_stage[1] = {{W_down, H, y}};
+    if (!mi355x::server_rows_fit(s, pre_stage, 1) || !mi355x::server_rows_fit(s, up_stage, 2) ||
+        !mi355x::server_rows_fit(s, down_stage, 1))
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_block: jobs of more rows than the server holds");
+    mi355x::SrvCmd c{};
+    c.K = static_cast<int32_t>(K);
     c.njobs = 2;
     c.mode = variant == MI355X_VARIANT_GGML_Q8 ? mi355x::kSrvGgmlQ8 : mi355x::kSrvDigits;
     c.jobs[0] = {static_cast<const uint8_t *>(W_gate), s.dh, F};
     c.jobs[1] = {static_cast<const uint8_t *>(W_up), s.dh, F};
     c.K2 = static_cast<int32_t>(F);
+    c.H = static_cast<int32_t>(H);
     c.h = s.dh;
-    c.down = {static_cast<const uint8_t *>(W_down), y, N};
-    return mi355x::server_submit(s, x, K, c, "mi355x_server_swiglu");
+    c.down = {static_cast<const uint8_t *>(W_down), y, H};
+    c.pre = {static_cast<const uint8_t *>(W_o), s.dr, H};
+    c.r_dev = s.dr;
+    c.norm_w = norm_w;
+    c.eps = eps;
+    return mi355x::server_submit(s, x, K, resid, H, c, "mi355x_server_block");
 }
 
 int mi355x_server_stop(mi355x_server *srv) {
@@ -2441,6 +2645,7 @@ void mi355x_server_destroy(mi355x_server *srv) {
         if (s.dev) (void)hipFree(s.dev);
         if (s.dx) (void)hipFree(s.dx);
         if (s.dh) (void)hipFree(s.dh);
+        if (s.dr) (void)hipFree(s.dr);
     }
     if (s.cmd_h) (void)hipHostFree(s.cmd_h);
     if (s.hx_h) (void)hipHostFree(s.hx_h);

@@ -52,6 +52,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_last_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_quantize_q4_0.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
     lib.qd_silu_mul.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    lib.qd_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+    lib.qd_set_block.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_fuse.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_variant.restype = C.c_int
     lib.qd_set_variant.argtypes = [C.c_void_p, C.c_int]
@@ -88,6 +90,16 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     assert g.shape == u.shape and g.ndim == 1
     load().qd_silu_mul(g.ctypes.data, u.ctypes.data, g.size)
     return g
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """The decoder's host RMSNorm (the steps mi355x_server_block states)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    assert x.shape == w.shape and x.ndim == 1
+    out = np.empty_like(x)
+    load().qd_rmsnorm(x.ctypes.data, w.ctypes.data, out.ctypes.data, x.size, eps)
+    return out
 
 
 def prompt_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
@@ -143,6 +155,10 @@ class Model:
 
     def set_fuse(self, on: bool) -> None:
         self.lib.qd_set_fuse(self.h, 1 if on else 0)
+
+    def set_block(self, on: bool) -> None:
+        """Server mode: o through down as one command (default on)."""
+        self.lib.qd_set_block(self.h, 1 if on else 0)
 
     def set_variant(self, variant: int) -> None:
         """GEMV kernel variant on the GPU path (mi355x.VARIANT_*)."""

@@ -198,8 +198,10 @@ struct qd_model {
     mi355x_ctx *ctx = nullptr;
     void *weights = nullptr;  // every matrix, resident, back to back in id order
     bool fuse = true;         // one launch for matrices that are adjacent in HBM
+    bool block = true;        // server mode: o through down as one command
     int64_t last_launches = 0;
     float *dx = nullptr, *dy = nullptr;  // activation in, outputs out
+    float *ffn_norm_dev = nullptr;       // the FFN norm weights, n_layers * hidden
     size_t dy_floats = 0;
     float *hx = nullptr, *hy = nullptr;  // pinned staging
     // device addresses of hx / hy (pinned host memory the kernels can read
@@ -221,6 +223,7 @@ struct qd_model {
             if (weights) mi355x_free(ctx, weights);
             if (dx) mi355x_free(ctx, dx);
             if (dy) mi355x_free(ctx, dy);
+            if (ffn_norm_dev) mi355x_free(ctx, ffn_norm_dev);
             mi355x_ctx_destroy(ctx);
         }
         if (hx) mi355x_host_free(hx);
@@ -610,6 +613,12 @@ int qd_attach_gpu(qd_model *m, int device) {
     m->hx_dev = static_cast<const float *>(dp);
     if (hipHostGetDevicePointer(&dp, m->hy, 0) != hipSuccess) return fail("qd_attach_gpu: hipHostGetDevicePointer");
     m->hy_dev = static_cast<float *>(dp);
+    const size_t H = static_cast<size_t>(m->c.hidden);
+    if (mi355x_malloc(m->ctx, m->c.n_layers * H * 4, &p) != MI355X_OK) return fail(mi355x_last_error());
+    m->ffn_norm_dev = static_cast<float *>(p);
+    for (int l = 0; l < m->c.n_layers; ++l)
+        if (mi355x_memcpy_h2d(m->ctx, m->ffn_norm_dev + l * H, m->ffn_norm[l].data(), H * 4) != MI355X_OK)
+            return fail(mi355x_last_error());
     return 0;
 }
 
@@ -717,11 +726,15 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
         max_k = std::max<int64_t>(max_k, mat.K);
         if (mat.K % 256 != 0) use_server = false;
     }
+    // the block command's payload is the attention output and the residual
+    max_k = std::max<int64_t>(max_k, (m->q_dim() + H + 255) / 256 * 256);
     if (use_server && !m->server && mi355x_server_create(m->ctx, max_k, &m->server) != MI355X_OK)
         use_server = false;  // e.g. no cooperative launch: one launch per group
     const int wait = !use_server && m->wait_mode == QD_WAIT_SERVER ? QD_WAIT_FENCE : m->wait_mode;
-    // the feed-forward block as one SwiGLU server command (fused groups only)
+    // the feed-forward block as one SwiGLU server command (fused groups
+    // only); with `block`, also o, both residual adds and the FFN norm
     const bool swiglu = backend == 0 && use_server && m->fuse && c.ffn % 256 == 0;
+    const bool block = swiglu && m->block && H % 256 == 0 && H <= 4096 && QD % 256 == 0;
 
     // per layer: keys [g][t / 8][i][t % 8], values [g][t][i] (see attention())
     const int tcap = (T + 7) / 8 * 8;
@@ -890,6 +903,23 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             }
             attention(q.data(), kl, vl, pos + 1, tcap, c.n_heads, c.n_kv_heads, hd, sc.data(), att.data());
             t_host += now() - th;
+            if (block) {
+                // o, residual, FFN norm, gate|up, SiLU, down, residual: one command
+                const double t0 = now();
+                const Matrix &wo = m->mats[7 * l + QD_O], &wg = m->mats[7 * l + QD_GATE],
+                             &wu = m->mats[7 * l + QD_UP], &wd = m->mats[7 * l + QD_DOWN];
+                if (mi355x_server_block(m->server, att.data(), QD, wo.dev, h.data(), H,
+                                        m->ffn_norm_dev + static_cast<size_t>(l) * H, c.norm_eps, wg.dev, wu.dev,
+                                        c.ffn, wd.dev, m->hy_dev) != MI355X_OK) {
+                    rc = -1;
+                    break;
+                }
+                std::memcpy(h.data(), m->hy, static_cast<size_t>(H) * 4);
+                launches += 3;
+                t_gemv += now() - t0;
+                th = now();
+                continue;
+            }
             if ((rc = gemvs(att.data(), QD, {7 * l + QD_O}, {o.data()}))) break;
             th = now();
             for (int i = 0; i < H; ++i) h[i] += o[i];
@@ -947,5 +977,11 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
 }
 
 void qd_silu_mul(float *g, const float *u, int n) { silu_mul(g, u, n); }
+
+void qd_rmsnorm(const float *x, const float *w, float *out, int n, float eps) { rmsnorm(x, w, out, n, eps); }
+
+void qd_set_block(qd_model *m, int on) {
+    if (m) m->block = on != 0;
+}
 
 }  // extern "C"

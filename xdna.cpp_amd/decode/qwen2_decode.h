@@ -69,6 +69,9 @@ QD_API void qd_quantize_q4_0(const float *x, int64_t N, int64_t K, uint8_t *out)
 /* The host's SwiGLU step, g[i] = silu(g[i]) * u[i], in the f32 steps that
  * mi355x_server_swiglu states (exposed for tests). */
 QD_API void qd_silu_mul(float *g, const float *u, int n);
+/* The host's RMSNorm, out = x * s * w with s from the double sum of squares
+ * in the order mi355x_server_block states (exposed for tests). */
+QD_API void qd_rmsnorm(const float *x, const float *w, float *out, int n, float eps);
 
 /* Moves every matrix into HBM (prepacked) on `device`; later runs with
  * backend 0 use it. */
@@ -78,6 +81,11 @@ QD_API int qd_attach_gpu(qd_model *m, int device);
  * as one launch when `on` (the default); off = one launch per matrix, as a
  * ggml graph with one MUL_MAT node per weight dispatches them. */
 QD_API void qd_set_fuse(qd_model *m, int on);
+/* Server mode with fused groups: the layer's o projection, both residual
+ * adds, the FFN norm, gate|up, SiLU and down as one mi355x_server_block
+ * command when `on` (the default); off = the o command, then the FFN as one
+ * mi355x_server_swiglu command. */
+QD_API void qd_set_block(qd_model *m, int on);
 /* How activations and outputs cross PCIe on the GPU path:
  * QD_IO_STAGED: x is copied into HBM and y back from HBM around the launches
  * (the traffic pattern of a ggml backend whose buffers are device memory);

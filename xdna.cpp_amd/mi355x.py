@@ -49,6 +49,8 @@ _SIGNATURES = {
     "mi355x_server_create": (_c.c_int, [_vp, _c.c_int64, _c.POINTER(_vp)]),
     "mi355x_server_gemv": (_c.c_int, [_vp, _vp, _c.c_int64, _c.c_int, _vp]),
     "mi355x_server_swiglu": (_c.c_int, [_vp, _vp, _c.c_int64, _vp, _vp, _c.c_int64, _vp, _c.c_int64, _vp]),
+    "mi355x_server_block": (_c.c_int, [_vp, _vp, _c.c_int64, _vp, _vp, _c.c_int64, _vp, _c.c_float, _vp, _vp,
+                                       _c.c_int64, _vp, _vp]),
     "mi355x_server_stop": (_c.c_int, [_vp]),
     "mi355x_server_running": (_c.c_int, [_vp]),
     "mi355x_server_destroy": (None, [_vp]),
@@ -231,6 +233,18 @@ class Server:
 
     def swiglu(self, x: np.ndarray, w_gate: int, w_up: int, F: int, w_down: int, N: int, y: int) -> None:
         check(self.swiglu_ptr(x, w_gate, w_up, F, w_down, N, y))
+
+    def block_ptr(self, x: np.ndarray, w_o: int, resid: np.ndarray, norm_w: int, eps: float, w_gate: int,
+                  w_up: int, F: int, w_down: int, y: int) -> int:
+        """y = r + W_down (silu(W_gate xn) * (W_up xn)), xn = rmsnorm(r) * norm_w,
+        r = resid + W_o x, as one command (x, resid: host f32; the rest device)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        resid = np.ascontiguousarray(resid, dtype=np.float32)
+        return self.lib.mi355x_server_block(self.h, x.ctypes.data, x.size, w_o, resid.ctypes.data, resid.size,
+                                            norm_w, eps, w_gate, w_up, F, w_down, y)
+
+    def block(self, *args) -> None:
+        check(self.block_ptr(*args))
 
     def stop(self) -> None:
         check(self.lib.mi355x_server_stop(self.h))
