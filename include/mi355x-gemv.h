@@ -346,11 +346,15 @@ MI355X_API int mi355x_server_swiglu(mi355x_server *s, const float *x, int64_t K,
  * l_k = (p_k + p_{4+k}) + (p_{8+k} + p_{12+k}) for k < 4,
  * ss = (l_0 + l_1) + (l_2 + l_3);  s = 1 / sqrt(float(ss / H) + eps) in f32
  * (correctly rounded);  xn_i = (r_i * s) * norm_w_i.  K, H, F: multiples of
- * 256, H <= 4096, F <= max_k and K + H <= max_k; y device-visible. */
+ * 256, H <= 4096, F <= max_k and K + H <= max_k; y device-visible.
+ * With W_next (else NULL, and the three after it ignored): after another
+ * grid barrier, y_next = W_next (rmsnorm(y) * next_norm_w) -- the next
+ * layer's q|k|v (N_next rows, H columns) -- in the same command. */
 MI355X_API int mi355x_server_block(mi355x_server *s, const float *x, int64_t K, const void *W_o,
                                    const float *resid, int64_t H, const float *norm_w, float eps,
                                    const void *W_gate, const void *W_up, int64_t F, const void *W_down,
-                                   float *y);
+                                   float *y, const float *next_norm_w, const void *W_next, int64_t N_next,
+                                   float *y_next);
 MI355X_API int mi355x_server_stop(mi355x_server *s);
 /* 1 while the server's resident kernel is running, 0 once it has left (after
  * its idle time, a stop, or before the first command); < 0 on error. */

@@ -338,14 +338,21 @@ def block_separate(ctx, server, ws, x, resid, norm_w):
     return r + dn
 
 
-def block_fused(ctx, server, ws, x, resid, nw):
+def block_fused(ctx, server, ws, x, resid, nw, nxt=None):
+    """nxt: (next norm weights on the device, resident W_next) or None;
+    returns y and, with nxt, y_next."""
     H, F = ws[0].N, ws[1].N
     y = ctx.alloc(4 * H)
+    yn = ctx.alloc(4 * nxt[1].N) if nxt else None
     try:
-        server.block(x, ws[0].ptr, resid, nw.ptr, EPS, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, y.ptr)
-        return y.download(np.float32, H)
+        extra = (nxt[0].ptr, nxt[1].ptr, nxt[1].N, yn.ptr) if nxt else ()
+        server.block(x, ws[0].ptr, resid, nw.ptr, EPS, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, y.ptr, *extra)
+        out = y.download(np.float32, H)
+        return (out, yn.download(np.float32, nxt[1].N)) if nxt else out
     finally:
         y.free()
+        if yn:
+            yn.free()
 
 
 @pytest.mark.parametrize("v", [mi355x.VARIANT_AUTO, mi355x.VARIANT_GGML_Q8])
@@ -353,23 +360,33 @@ def block_fused(ctx, server, ws, x, resid, nw):
 def test_server_block_matches_separate_steps(ctx, server, K, H, F, v):
     """mi355x_server_block (o, residual, RMSNorm on the device, gate|up, SiLU,
     down, residual, with grid barriers) equals the separate steps around the
-    host's RMSNorm and SwiGLU step, bit for bit, in both arithmetics."""
+    host's RMSNorm and SwiGLU step, bit for bit, in both arithmetics; with
+    the next stage (RMSNorm of y, then the next layer's q|k|v), y is the same
+    and y_next equals a server GEMV over the host's RMSNorm of y."""
     _, ws = block_weights(ctx, K, H, F, seed=K ^ H ^ F)
     rng = np.random.default_rng(H + F)
     x = synth.activations(K, seed=K + 9)
     resid = (rng.standard_normal(H) * 0.5).astype(np.float32)
     norm_w = rng.uniform(0.5, 1.5, H).astype(np.float32)
     nw = ctx.to_device(norm_w)
+    next_norm = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    nn = ctx.to_device(next_norm)
+    n_next = 2560 if H == 2048 else 3 * H // 2 + 17
+    w_next = ctx.resident(Q4_0, synth.random_q4_0(n_next, H, seed=H + 5), n_next, H)
     try:
         with variant(ctx, v):
             want = block_separate(ctx, server, ws, x, resid, norm_w)
+            (want_next,) = run_server(ctx, server, [w_next], decode.rmsnorm(want, next_norm, EPS))
             got = block_fused(ctx, server, ws, x, resid, nw)
             again = block_fused(ctx, server, ws, x, resid, nw)
+            got2, got_next = block_fused(ctx, server, ws, x, resid, nw, (nn, w_next))
     finally:
-        for b in ws + [nw]:
+        for b in ws + [nw, nn, w_next]:
             b.free()
     assert np.array_equal(got, want), (K, H, F, np.abs(got - want).max())
     assert np.array_equal(again, got)
+    assert np.array_equal(got2, want)
+    assert np.array_equal(got_next, want_next), (K, H, F, np.abs(got_next - want_next).max())
 
 
 def test_server_block_between_other_commands(ctx, server):
@@ -421,6 +438,9 @@ def test_server_block_rejects_bad_arguments(ctx, server):
         assert call(w_down=d + 8) == mi355x.EINVAL
         assert call(norm_w=0) == mi355x.EINVAL
         assert call(y=0) == mi355x.EINVAL
+        assert call(w_next=g, next_norm_w=nw.ptr, N_next=0, y_next=y.ptr) == mi355x.EINVAL
+        assert call(w_next=g, next_norm_w=0, N_next=64, y_next=y.ptr) == mi355x.EINVAL
+        assert call(w_next=g + 4, next_norm_w=nw.ptr, N_next=64, y_next=y.ptr) == mi355x.EINVAL
         with variant(ctx, mi355x.VARIANT_EXACT_F32):
             assert call() == mi355x.EUNSUPPORTED
         assert call() == mi355x.OK  # still serves

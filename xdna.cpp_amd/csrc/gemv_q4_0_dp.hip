@@ -734,6 +734,13 @@ struct SrvCmd {
     const float *norm_w;
     float eps;
     int32_t pad2_;
+    // block command with a next stage (post.N > 0): the down stage also
+    // writes y into r_dev; after a grid barrier, post (H columns) runs over
+    // rmsnorm(y) * post_norm_w (eps) into post.y
+    SrvJob post;
+    const float *post_norm_w;
+    // residual store kinds: also write the result here (device memory)
+    float *mirror;
 };
 // store-pass kinds
 constexpr int32_t kSrvStoreY = 0;     // y[row] = out
@@ -920,7 +927,9 @@ __device__ __forceinline__ void srv_store_add(const SrvSpan<ROWS> &sp, const Srv
         const int r = sp.lo0 + i;
         const float a = c.kind == kSrvStoreAddG ? __hip_atomic_load(&c.add[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
                                                 : c.add[r];
-        __hip_atomic_store(&y[r], out[i] + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const float v = out[i] + a;
+        __hip_atomic_store(&y[r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (c.mirror) __hip_atomic_store(&c.mirror[r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -1304,13 +1313,15 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             __syncthreads();
         };
         // stages: plain 1; SwiGLU 2 (gate|up -> h, down); block 3 (pre -> r,
-        // gate|up over rmsnorm(r) -> h, down + r).  One call site per stage
-        // form keeps the kernel's register count at that of one stage.
+        // gate|up over rmsnorm(r) -> h, down + r), 4 with post (over
+        // rmsnorm(down + r)).  One call site per stage form keeps the
+        // kernel's register count at that of one stage.
         const bool blk = cs.pre.N > 0;
-        const int nst = blk ? 3 : (cs.K2 ? 2 : 1);
+        const int nst = blk ? (cs.post.N > 0 ? 4 : 3) : (cs.K2 ? 2 : 1);
         for (int st = 0; st < nst; ++st) {
             if (st > 0 && barrier()) return;
             if (blk && st == 1) srv_rmsnorm(cs.r_dev, cs.norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
+            if (st == 3) srv_rmsnorm(cs.r_dev, cs.post_norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
             if (st > 0 || blk) {
                 copy_cmd();
                 if (threadIdx.x == 0) {
@@ -1323,18 +1334,25 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                     } else if (st == 1 && blk) {
                         cs2.K = cs.H;
                         cs2.kind = kSrvStoreGlu;
+                    } else if (st == 3) {
+                        cs2.K = cs.H;
+                        cs2.njobs = 1;
+                        cs2.jobs[0] = cs.post;
+                        cs2.kind = kSrvStoreY;
                     } else {
                         cs2.K = cs.K2;
                         cs2.njobs = 1;
                         cs2.jobs[0] = cs.down;
                         cs2.kind = blk ? kSrvStoreAddL : kSrvStoreY;
                         cs2.add = rb;
+                        // r_dev's readers finished before the barrier above
+                        cs2.mirror = blk && cs.post.N > 0 ? cs.r_dev : nullptr;
                     }
                 }
                 __syncthreads();
             }
             const SrvCmd &c = st > 0 || blk ? cs2 : cs;
-            if (blk && st == 1) srv_stage_lds(c, lds_dp, xnb, outb, csb);
+            if (blk && (st & 1)) srv_stage_lds(c, lds_dp, xnb, outb, csb);
             else srv_stage(c, lds_dp, st == 0 ? dx : cs.h, outb, csb);
         }
         // every wave's output stores have completed (they write through) before
@@ -2569,10 +2587,15 @@ int mi355x_server_swiglu(mi355x_server *srv, const float *x, int64_t K, const vo
 
 int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const void *W_o, const float *resid,
                         int64_t H, const float *norm_w, float eps, const void *W_gate, const void *W_up, int64_t F,
-                        const void *W_down, float *y) {
+                        const void *W_down, float *y, const float *next_norm_w, const void *W_next, int64_t N_next,
+                        float *y_next) {
     clear_error();
     if (!srv || !x || !W_o || !resid || !norm_w || !W_gate || !W_up || !W_down || !y)
         return set_error(MI355X_EINVAL, "mi355x_server_block: null pointer");
+    const bool post = W_next != nullptr;
+    if (post && (!next_norm_w || !y_next || N_next <= 0 || reinterpret_cast<uintptr_t>(W_next) % 16 != 0 ||
+                 reinterpret_cast<uintptr_t>(next_norm_w) % 4 != 0))
+        return set_error(MI355X_EINVAL, "mi355x_server_block: bad next stage");
     mi355x::ServerImpl &s = srv->impl;
     if (K <= 0 || K % 256 != 0 || F <= 0 || F % 256 != 0 || F > s.max_k || H <= 0 || H % 256 != 0 ||
         H > mi355x::kSrvLdsXMax || K + H > s.max_k)
@@ -2589,8 +2612,9 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
     const mi355x_server_job pre_stage[1] = {{W_o, H, s.dr}};
     const mi355x_server_job up_stage[2] = {{W_gate, F, s.dh}, {W_up, F, s.dh}};
     const mi355x_server_job down_stage[1] = {{W_down, H, y}};
+    const mi355x_server_job next_stage[1] = {{W_next, N_next, y_next}};
     if (!mi355x::server_rows_fit(s, pre_stage, 1) || !mi355x::server_rows_fit(s, up_stage, 2) ||
-        !mi355x::server_rows_fit(s, down_stage, 1))
+        !mi355x::server_rows_fit(s, down_stage, 1) || (post && !mi355x::server_rows_fit(s, next_stage, 1)))
         return set_error(MI355X_EUNSUPPORTED, "mi355x_server_block: jobs of more rows than the server holds");
     mi355x::SrvCmd c{};
     c.K = static_cast<int32_t>(K);
@@ -2606,6 +2630,10 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
     c.r_dev = s.dr;
     c.norm_w = norm_w;
     c.eps = eps;
+    if (post) {
+        c.post = {static_cast<const uint8_t *>(W_next), y_next, N_next};
+        c.post_norm_w = next_norm_w;
+    }
     return mi355x::server_submit(s, x, K, resid, H, c, "mi355x_server_block");
 }
 

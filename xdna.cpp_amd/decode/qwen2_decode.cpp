@@ -202,6 +202,7 @@ struct qd_model {
     int64_t last_launches = 0;
     float *dx = nullptr, *dy = nullptr;  // activation in, outputs out
     float *ffn_norm_dev = nullptr;       // the FFN norm weights, n_layers * hidden
+    float *attn_norm_dev = nullptr;      // the attention norm weights, n_layers * hidden
     size_t dy_floats = 0;
     float *hx = nullptr, *hy = nullptr;  // pinned staging
     // device addresses of hx / hy (pinned host memory the kernels can read
@@ -224,6 +225,7 @@ struct qd_model {
             if (dx) mi355x_free(ctx, dx);
             if (dy) mi355x_free(ctx, dy);
             if (ffn_norm_dev) mi355x_free(ctx, ffn_norm_dev);
+            if (attn_norm_dev) mi355x_free(ctx, attn_norm_dev);
             mi355x_ctx_destroy(ctx);
         }
         if (hx) mi355x_host_free(hx);
@@ -598,7 +600,9 @@ int qd_attach_gpu(qd_model *m, int device) {
             return fail(std::string("qd_attach_gpu: ") + mi355x_last_error());
     }
     const size_t xf = static_cast<size_t>(std::max(m->c.ffn, std::max(m->c.hidden, m->q_dim())));
-    m->dy_floats = static_cast<size_t>(std::max<int64_t>(2 * m->c.ffn, std::max<int64_t>(m->c.vocab, m->q_dim() + 2 * m->kv_dim())));
+    // outputs of a block command: y, then the next layer's q|k|v
+    m->dy_floats = static_cast<size_t>(std::max<int64_t>(
+        2 * m->c.ffn, std::max<int64_t>(m->c.vocab, m->c.hidden + m->q_dim() + 2 * m->kv_dim())));
     void *p = nullptr;
     if (mi355x_malloc(m->ctx, xf * 4, &p) != MI355X_OK) return fail(mi355x_last_error());
     m->dx = static_cast<float *>(p);
@@ -616,8 +620,11 @@ int qd_attach_gpu(qd_model *m, int device) {
     const size_t H = static_cast<size_t>(m->c.hidden);
     if (mi355x_malloc(m->ctx, m->c.n_layers * H * 4, &p) != MI355X_OK) return fail(mi355x_last_error());
     m->ffn_norm_dev = static_cast<float *>(p);
+    if (mi355x_malloc(m->ctx, m->c.n_layers * H * 4, &p) != MI355X_OK) return fail(mi355x_last_error());
+    m->attn_norm_dev = static_cast<float *>(p);
     for (int l = 0; l < m->c.n_layers; ++l)
-        if (mi355x_memcpy_h2d(m->ctx, m->ffn_norm_dev + l * H, m->ffn_norm[l].data(), H * 4) != MI355X_OK)
+        if (mi355x_memcpy_h2d(m->ctx, m->ffn_norm_dev + l * H, m->ffn_norm[l].data(), H * 4) != MI355X_OK ||
+            mi355x_memcpy_h2d(m->ctx, m->attn_norm_dev + l * H, m->attn_norm[l].data(), H * 4) != MI355X_OK)
             return fail(mi355x_last_error());
     return 0;
 }
@@ -735,6 +742,13 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     // only); with `block`, also o, both residual adds and the FFN norm
     const bool swiglu = backend == 0 && use_server && m->fuse && c.ffn % 256 == 0;
     const bool block = swiglu && m->block && H % 256 == 0 && H <= 4096 && QD % 256 == 0;
+    // q, k and v back to back in HBM: the block command can run them as one job
+    bool qkv_adjacent = true;
+    for (int l = 0; l < L; ++l) {
+        const Matrix &mq = m->mats[7 * l + QD_Q], &mk = m->mats[7 * l + QD_K], &mv = m->mats[7 * l + QD_V];
+        const auto *bq = static_cast<const uint8_t *>(mq.dev), *bk = static_cast<const uint8_t *>(mk.dev);
+        qkv_adjacent = qkv_adjacent && mk.dev == bq + mq.N * (H / 32) * 18 && mv.dev == bk + mk.N * (H / 32) * 18;
+    }
 
     // per layer: keys [g][t / 8][i][t % 8], values [g][t][i] (see attention())
     const int tcap = (T + 7) / 8 * 8;
@@ -882,12 +896,21 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             rope_cs[hd / 2 + i] = std::sin(f);
         }
         dequant_q4_0_row(m->mats[7 * L].q.data() + static_cast<int64_t>(tok) * (H / 32) * 18, H, h.data());
+        bool have_qkv = false;  // the last block command computed this layer's q|k|v
         for (int l = 0; l < L; ++l) {
-            rmsnorm(h.data(), m->attn_norm[l].data(), xn.data(), H, c.norm_eps);
-            t_host += now() - th;
-            if ((rc = gemvs(xn.data(), H, {7 * l + QD_Q, 7 * l + QD_K, 7 * l + QD_V}, {q.data(), k.data(), v.data()})))
-                break;
-            th = now();
+            if (have_qkv) {
+                std::memcpy(q.data(), m->hy + H, static_cast<size_t>(QD) * 4);
+                std::memcpy(k.data(), m->hy + H + QD, static_cast<size_t>(KVD) * 4);
+                std::memcpy(v.data(), m->hy + H + QD + KVD, static_cast<size_t>(KVD) * 4);
+                have_qkv = false;
+            } else {
+                rmsnorm(h.data(), m->attn_norm[l].data(), xn.data(), H, c.norm_eps);
+                t_host += now() - th;
+                if ((rc = gemvs(xn.data(), H, {7 * l + QD_Q, 7 * l + QD_K, 7 * l + QD_V},
+                                {q.data(), k.data(), v.data()})))
+                    break;
+                th = now();
+            }
             for (int i = 0; i < QD; ++i) q[i] += m->bq[l][i];
             for (int i = 0; i < KVD; ++i) {
                 k[i] += m->bk[l][i];
@@ -904,18 +927,24 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             attention(q.data(), kl, vl, pos + 1, tcap, c.n_heads, c.n_kv_heads, hd, sc.data(), att.data());
             t_host += now() - th;
             if (block) {
-                // o, residual, FFN norm, gate|up, SiLU, down, residual: one command
+                // o, residual, FFN norm, gate|up, SiLU, down, residual -- and
+                // the next layer's attention norm and q|k|v -- one command
                 const double t0 = now();
                 const Matrix &wo = m->mats[7 * l + QD_O], &wg = m->mats[7 * l + QD_GATE],
                              &wu = m->mats[7 * l + QD_UP], &wd = m->mats[7 * l + QD_DOWN];
+                const bool next = l + 1 < L && qkv_adjacent;
+                const Matrix &wq = m->mats[7 * (next ? l + 1 : l) + QD_Q];
                 if (mi355x_server_block(m->server, att.data(), QD, wo.dev, h.data(), H,
                                         m->ffn_norm_dev + static_cast<size_t>(l) * H, c.norm_eps, wg.dev, wu.dev,
-                                        c.ffn, wd.dev, m->hy_dev) != MI355X_OK) {
+                                        c.ffn, wd.dev, m->hy_dev,
+                                        next ? m->attn_norm_dev + static_cast<size_t>(l + 1) * H : nullptr,
+                                        next ? wq.dev : nullptr, QD + 2 * KVD, m->hy_dev + H) != MI355X_OK) {
                     rc = -1;
                     break;
                 }
                 std::memcpy(h.data(), m->hy, static_cast<size_t>(H) * 4);
-                launches += 3;
+                launches += next ? 4 : 3;
+                have_qkv = next;
                 t_gemv += now() - t0;
                 th = now();
                 continue;

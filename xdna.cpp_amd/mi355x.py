@@ -50,7 +50,7 @@ _SIGNATURES = {
     "mi355x_server_gemv": (_c.c_int, [_vp, _vp, _c.c_int64, _c.c_int, _vp]),
     "mi355x_server_swiglu": (_c.c_int, [_vp, _vp, _c.c_int64, _vp, _vp, _c.c_int64, _vp, _c.c_int64, _vp]),
     "mi355x_server_block": (_c.c_int, [_vp, _vp, _c.c_int64, _vp, _vp, _c.c_int64, _vp, _c.c_float, _vp, _vp,
-                                       _c.c_int64, _vp, _vp]),
+                                       _c.c_int64, _vp, _vp, _vp, _vp, _c.c_int64, _vp]),
     "mi355x_server_stop": (_c.c_int, [_vp]),
     "mi355x_server_running": (_c.c_int, [_vp]),
     "mi355x_server_destroy": (None, [_vp]),
@@ -235,13 +235,16 @@ class Server:
         check(self.swiglu_ptr(x, w_gate, w_up, F, w_down, N, y))
 
     def block_ptr(self, x: np.ndarray, w_o: int, resid: np.ndarray, norm_w: int, eps: float, w_gate: int,
-                  w_up: int, F: int, w_down: int, y: int) -> int:
+                  w_up: int, F: int, w_down: int, y: int, next_norm_w: int = 0, w_next: int = 0, N_next: int = 0,
+                  y_next: int = 0) -> int:
         """y = r + W_down (silu(W_gate xn) * (W_up xn)), xn = rmsnorm(r) * norm_w,
-        r = resid + W_o x, as one command (x, resid: host f32; the rest device)."""
+        r = resid + W_o x, as one command (x, resid: host f32; the rest device);
+        with w_next also y_next = W_next (rmsnorm(y) * next_norm_w)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         resid = np.ascontiguousarray(resid, dtype=np.float32)
         return self.lib.mi355x_server_block(self.h, x.ctypes.data, x.size, w_o, resid.ctypes.data, resid.size,
-                                            norm_w, eps, w_gate, w_up, F, w_down, y)
+                                            norm_w, eps, w_gate, w_up, F, w_down, y, next_norm_w or None,
+                                            w_next or None, N_next, y_next or None)
 
     def block(self, *args) -> None:
         check(self.block_ptr(*args))
