@@ -745,8 +745,7 @@ struct SrvCmd {
 // store-pass kinds
 constexpr int32_t kSrvStoreY = 0;     // y[row] = out
 constexpr int32_t kSrvStoreGlu = 1;   // h[row] = silu(out of job 0) * out of job 1
-constexpr int32_t kSrvStoreAddG = 2;  // y[row] = out + add[row], add in device memory written this command
-constexpr int32_t kSrvStoreAddL = 3;  // y[row] = out + add[row], add in this workgroup's LDS
+constexpr int32_t kSrvStoreAddL = 2;  // y[row] = out + add[row], add in this workgroup's LDS
 // job arithmetic: the row form's digit planes, or ggml-cpu's Q8_0 numerics
 constexpr int32_t kSrvDigits = 0;
 constexpr int32_t kSrvGgmlQ8 = 1;
@@ -915,9 +914,8 @@ __device__ __forceinline__ void srv_store_glu(const SrvSpan<ROWS> &sp, const Srv
                            __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Residual store pass (one job): y[lo0 + i] = out[i] + add[lo0 + i]; the
-// add vector is read through the system-coherent path when another
-// workgroup wrote it in this command (kSrvStoreAddG), else from LDS.
+// Residual store pass (one job): y[lo0 + i] = out[i] + add[lo0 + i], add
+// in this workgroup's LDS; with c.mirror, the sums also go there.
 template <int ROWS>
 __device__ __forceinline__ void srv_store_add(const SrvSpan<ROWS> &sp, const SrvCmd &c, const float *out) {
 #pragma clang fp contract(off)
@@ -925,9 +923,7 @@ __device__ __forceinline__ void srv_store_add(const SrvSpan<ROWS> &sp, const Srv
     float *y = c.jobs[0].y;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int r = sp.lo0 + i;
-        const float a = c.kind == kSrvStoreAddG ? __hip_atomic_load(&c.add[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
-                                                : c.add[r];
-        const float v = out[i] + a;
+        const float v = out[i] + c.add[r];
         __hip_atomic_store(&y[r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (c.mirror) __hip_atomic_store(&c.mirror[r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
@@ -1133,18 +1129,21 @@ __device__ __forceinline__ uint32_t srv_barrier(SrvDev *dev, int g, int G, uint6
 }
 
 // RMSNorm of the block command, every workgroup for itself: r (H floats,
-// written by other workgroups in this command) into rb, then
+// written by other workgroups in this command; plus r2 when given, one f32
+// add) into rb, then
 // xn[i] = r[i] * s * w[i] into xnb with s = 1 / sqrt(float(ss / H) + eps), the
 // f32 steps and the summation order of the decode host's rmsnorm: ss in
 // double as 16 partial sums p_k = sum over i0 = 0, 16, ... of r[i0 + k]^2
 // (sequential; a square of a float is exact in double), combined as
 // ((p0+p4)+(p8+p12)) + ((p1+p5)+(p9+p13)) + ... lane-wise, then
 // (l0 + l1) + (l2 + l3).  H: a multiple of 256.
-__device__ __forceinline__ void srv_rmsnorm(const float *r, const float *w, float eps, int H, float *rb, float *xnb,
-                                            double *pbuf, float *sbuf) {
+__device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, const float *w, float eps, int H,
+                                            float *rb, float *xnb, double *pbuf, float *sbuf) {
 #pragma clang fp contract(off)
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r), 0, static_cast<uint32_t>(4 * H), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r2 ? r2 : r), 0,
+                                                                        static_cast<uint32_t>(4 * H), kBufferWord3);
     // r into rb, and transposed into xnb (free until the end): partial sum k's
     // elements r[k], r[16 + k], ... side by side at xnb[k * H / 16 ..], so its
     // lane reads them 4 at a time (rows L + 4 floats apart: 16-byte aligned,
@@ -1152,10 +1151,11 @@ __device__ __forceinline__ void srv_rmsnorm(const float *r, const float *w, floa
     const int L = H / 16, LS = L + 4;
     for (int i = 4 * static_cast<int>(threadIdx.x); i < H; i += 4 * static_cast<int>(blockDim.x)) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * i, 0, kSysCoherent);
+        const u32x4 v2 = __builtin_amdgcn_raw_buffer_load_b128(rs2, 4 * i, 0, kSysCoherent);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t u = v[e];
-            const float f = __builtin_bit_cast(float, u);
+            const uint32_t u = v[e], u2 = v2[e];
+            const float f = r2 ? __builtin_bit_cast(float, u) + __builtin_bit_cast(float, u2) : __builtin_bit_cast(float, u);
             rb[i + e] = f;
             xnb[((i + e) & 15) * LS + ((i + e) >> 4)] = f;
         }
@@ -1320,17 +1320,19 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
         const int nst = blk ? (cs.post.N > 0 ? 4 : 3) : (cs.K2 ? 2 : 1);
         for (int st = 0; st < nst; ++st) {
             if (st > 0 && barrier()) return;
-            if (blk && st == 1) srv_rmsnorm(cs.r_dev, cs.norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
-            if (st == 3) srv_rmsnorm(cs.r_dev, cs.post_norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
+            // r = (pre x) + resid (resid after x in the payload); the next
+            // stage's r = down h + r, added in the down stage's store pass
+            if (blk && st == 1) srv_rmsnorm(cs.r_dev, dx + cs.K, cs.norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
+            if (st == 3) srv_rmsnorm(cs.r_dev, nullptr, cs.post_norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
             if (st > 0 || blk) {
                 copy_cmd();
                 if (threadIdx.x == 0) {
                     if (st == 0) {
-                        // block: r = resid + pre x, resid after x in the payload
+                        // block: pre x into r_dev (the residual is added
+                        // when every workgroup reads it back)
                         cs2.njobs = 1;
                         cs2.jobs[0] = {cs.pre.W, cs.r_dev, cs.pre.N};
-                        cs2.kind = kSrvStoreAddG;
-                        cs2.add = dx + cs.K;
+                        cs2.kind = kSrvStoreY;
                     } else if (st == 1 && blk) {
                         cs2.K = cs.H;
                         cs2.kind = kSrvStoreGlu;
