@@ -288,6 +288,11 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
             mode = f"fence (server failed: {e})"
         passes = t["gen_passes"]
         launches = model.last_launches() / passes
+        # the server with one command per GEMV group (SwiGLU still fused)
+        # instead of one block command per layer
+        model.set_block(False)
+        nb_toks, tn, _ = run()
+        model.set_block(True)
         # the same numerics with one launch per group, the host spinning on a
         # completion word or waiting with hipStreamSynchronize
         model.set_wait(model.WAIT_FENCE)
@@ -311,7 +316,8 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         # the digit-plane f32-activation arithmetic (library default)
         model.set_variant(mi355x.VARIANT_AUTO)
         dg_toks, td, dg_tok_s = run()
-        log(f"bench: decode (ggml Q8_0 numerics): launch + fence {passes / tf['gen_s']:.1f} tok/s; "
+        log(f"bench: decode (ggml Q8_0 numerics): server, a command per GEMV group {passes / tn['gen_s']:.1f} "
+            f"tok/s; launch + fence {passes / tf['gen_s']:.1f} tok/s; "
             f"hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s; staged I/O {passes / ts['gen_s']:.1f} "
             f"tok/s; through the ggml plugin's graph_compute {passes / tp['gen_s']:.1f} tok/s")
         log(f"bench: decode: GPU {tok_s:.1f} tok/s in ggml Q8_0 numerics ({t['gen_s'] / passes * 1e3:.3f} "
@@ -334,6 +340,12 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
             "prompt_tok_s": round(n_prompt / t["prompt_s"], 2),
             "gemv_launches_per_token": launches,
             "mode": mode,
+            "per_group_server": {"tok_s": round(passes / tn["gen_s"], 2),
+                                 "gemv_ms_per_token": round(tn["gen_gemv_s"] / passes * 1e3, 4),
+                                 "host_ms_per_token": round(tn["gen_host_s"] / passes * 1e3, 4),
+                                 "tokens_match": bool(np.array_equal(nb_toks, gq_toks)),
+                                 "note": "server commands per GEMV group (q|k|v; o; gate|up + SiLU + down as "
+                                         "one SwiGLU command), norms and residual adds on the host"},
             "fence": {"tok_s": round(passes / tf["gen_s"], 2),
                       "gemv_ms_per_token": round(tf["gen_gemv_s"] / passes * 1e3, 4),
                       "tokens_match": bool(np.array_equal(fence_toks, gq_toks)),
@@ -365,11 +377,14 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                                        "||w|| ||x|| of the reference's f32 GEMV)",
                            "mode": {0: "stream", 1: "fence", 2: "server"}.get(model.last_wait(), "?")},
             "split": "the 253 weight GEMVs per token on the GPU (q|k|v and gate|up, adjacent in HBM, as one "
-                     "job each); norms, RoPE, attention, SwiGLU, argmax on the host; mode 'server': each GEMV "
-                     "group is a command to a resident server kernel (mi355x_server_*) that reads the activation "
-                     "and the command from pinned host memory and writes outputs there; the 'fence', "
-                     "'stream_wait' and 'staged_io' runs launch one kernel per group instead, the 'plugin' run "
-                     "goes through the ggml backend interface",
+                     "job each); mode 'server': a resident server kernel (mi355x_server_*) takes commands through "
+                     "pinned host memory -- per layer one block command (o, residual add, FFN RMSNorm, gate|up, "
+                     "SiLU, down, residual add, then the next layer's attention RMSNorm and q|k|v, with grid "
+                     "barriers between the stages), so the host runs only RoPE, the KV cache, attention, the "
+                     "first layer's norm and q|k|v command, the final norm and argmax; the 'per_group_server' run "
+                     "sends one command per GEMV group (SwiGLU fused) with norms and residuals on the host; the "
+                     "'fence', 'stream_wait' and 'staged_io' runs launch one kernel per group, the 'plugin' run "
+                     "goes through the ggml backend interface; every run computes the same tokens",
         }
         if cpu:
             sys.path.insert(0, os.path.join(ROOT, "oracle"))

@@ -174,7 +174,10 @@ def test_server_stop_and_idle_relaunch(ctx, server):
     try:
         job = [(w.ptr, N, y.ptr)]
         server.gemv(x, job)
+        t0 = time.perf_counter()
         out.append(y.download(np.float32, N))
+        # the copy ran beside the resident kernel (room for it on the CUs)
+        assert time.perf_counter() - t0 < 0.2
         assert server.running()
         server.stop()
         assert not server.running()

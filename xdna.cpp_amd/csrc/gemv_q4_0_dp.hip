@@ -809,6 +809,21 @@ constexpr int kSrvOutMax = 4096;  // rows of a command's jobs per workgroup (pad
 // group's loads are in flight across job boundaries too, and the outputs of
 // all jobs are stored once at the end.  Indices are uniform; the per-job
 // values sit in registers behind constant-index selects.
+// A workgroup's share [lo, hi) of a job's N rows: a run of whole 64-byte
+// lines of y (16 outputs; the first unit ends at y's first line boundary):
+// workgroups that stored parts of one line of pinned host memory would
+// serialise on it (~6 us per job of small shares).
+// (32-bit arithmetic: N < 2^27 and G <= 1024, which the host checks through
+// the rows a workgroup holds, keep U * G below 2^32.)
+__device__ __forceinline__ void srv_share(int64_t N64, const float *y, int g, int G, int &lo, int &hi) {
+    const uint32_t N = static_cast<uint32_t>(N64);
+    const uint32_t b0 = (16u - (static_cast<uint32_t>(reinterpret_cast<uintptr_t>(y)) >> 2)) & 15u;
+    const uint32_t U = 1 + (N > b0 ? N - b0 + 15 : 0) / 16;
+    auto at = [&](uint32_t u) { return u == 0 ? 0u : min(N, b0 + 16 * (u - 1)); };
+    lo = static_cast<int>(at(U * static_cast<uint32_t>(g) / static_cast<uint32_t>(G)));
+    hi = static_cast<int>(at(U * static_cast<uint32_t>(g + 1) / static_cast<uint32_t>(G)));
+}
+
 template <int ROWS>
 struct SrvSpan {
     static_assert(kSrvMaxJobs == 4, "four jobs per command");
@@ -817,19 +832,9 @@ struct SrvSpan {
     int lo0, lo1, lo2, lo3, hi0, hi1, hi2, hi3, st1, st2, st3, tot;
     __device__ __forceinline__ SrvSpan(const SrvCmd &c, int g, int G) {
         const int n = c.njobs;
-        // A workgroup's share of a job is a run of whole 64-byte lines of
-        // y (16 outputs; the first unit ends at y's first line boundary):
-        // workgroups that stored parts of one line of pinned host memory
-        // would serialise on it (~6 us per job of small shares).
         auto share = [&](int j, int &lo, int &hi) {
             lo = hi = 0;
-            if (j >= n) return;
-            const int64_t N = c.jobs[j].N;
-            const int64_t b0 = static_cast<int64_t>((16u - (reinterpret_cast<uintptr_t>(c.jobs[j].y) >> 2)) & 15u);
-            const int64_t U = 1 + (max(N - b0, int64_t(0)) + 15) / 16;
-            auto at = [&](int64_t u) { return u == 0 ? int64_t(0) : min(N, b0 + 16 * (u - 1)); };
-            lo = static_cast<int>(at(U * g / G));
-            hi = static_cast<int>(at(U * (g + 1) / G));
+            if (j < n) srv_share(c.jobs[j].N, c.jobs[j].y, g, G, lo, hi);
         };
         share(0, lo0, hi0);
         share(1, lo1, hi1);
@@ -944,6 +949,14 @@ __device__ __forceinline__ void srv_activation(XTile<XI> &xt, const float *x, in
     else srv_load_x(xt, x, B);
 }
 
+// A wavefront requests its next row group before computing the current one,
+// except for rows of more than 6 block columns (K > 12288): two groups of
+// those would raise the server kernel's register count (one for all its
+// forms) above what leaves room on each CU for other kernels, such as HIP's
+// copy kernels, while the server is resident.
+template <int NBL>
+constexpr bool kSrvNextGroup = NBL <= 6;
+
 template <int NBL, bool TAIL, bool XL>
 __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
                                          float *out) {
@@ -973,7 +986,7 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 
     for (int L = wave * R; L < T; L += ROWS) {
         RowGroup<NBL, R, true, TAIL> nxt;
-        sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
+        if constexpr (kSrvNextGroup<NBL>) sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -983,7 +996,8 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
             const float s = wave_sum(acc[r]);
             if (lane == 0) out[L + r] = s;  // padding rows (zero loads) are never stored
         }
-        grp = nxt;
+        if constexpr (kSrvNextGroup<NBL>) grp = nxt;
+        else sp.load(grp, c, L + ROWS, B, row_bytes, lane);
     }
     __syncthreads();
     srv_store(sp, c, out);
@@ -1040,10 +1054,11 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
         const int c1 = min(T, c0 + chunk);
         for (int L = c0 + wave * R; L < c1; L += ROWS) {
             Grp nxt;
-            sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
+            if constexpr (kSrvNextGroup<NBL>) sp.load(nxt, c, L + ROWS, B, row_bytes, lane);
             q8_blocks<NBL, R, true, TAIL>(grp, csb + (L - c0) * stride, stride, Q, dxs, sxs, B, lane, bc,
                                           tail_mask);
-            grp = nxt;
+            if constexpr (kSrvNextGroup<NBL>) grp = nxt;
+            else sp.load(grp, c, L + ROWS, B, row_bytes, lane);
         }
         __syncthreads();
         const int t = static_cast<int>(threadIdx.x);
