@@ -880,6 +880,138 @@ struct SrvSpan {
     }
 };
 
+// Grid barrier inside a command (thread 0 of every workgroup: arrive, then
+// wait; `n` = barriers this launch has passed, this one included).  256 arrivals on one counter
+// serialise (~25 ns each, measured); in two levels, as the completion count,
+// each counter takes at most 32, and the pollers read their group's flag
+// line, not a counter line that takes atomics.  Bounded like every wait:
+// srv_wait returns 1 (and raises quit) after `limit` ticks or when quit is
+// raised.
+__device__ __forceinline__ void srv_arrive(SrvDev *dev, int g, int G, uint64_t n) {
+    const int gi = g & 7;
+    const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
+    const uint64_t a = __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    if (a == n * members) {
+        const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
+        const uint64_t t = __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        if (t == n * groups)
+            for (int i = 0; i < static_cast<int>(groups); ++i)
+                __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(n), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__device__ __forceinline__ uint32_t srv_wait(SrvDev *dev, int g, uint64_t n, uint64_t limit) {
+    const int gi = g & 7;
+    const uint64_t t0 = srv_clock();
+    while (static_cast<int32_t>(__hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
+                                static_cast<uint32_t>(n)) < 0) {
+        if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 || srv_clock() - t0 > limit) {
+            __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return 1;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return 0;
+}
+
+// RMSNorm of the block command, every workgroup for itself: r (H floats,
+// written by other workgroups in this command; plus r2 when given, one f32
+// add) into rb, then
+// xn[i] = r[i] * s * w[i] into xnb with s = 1 / sqrt(float(ss / H) + eps), the
+// f32 steps and the summation order of the decode host's rmsnorm: ss in
+// double as 16 partial sums p_k = sum over i0 = 0, 16, ... of r[i0 + k]^2
+// (sequential; a square of a float is exact in double), combined as
+// ((p0+p4)+(p8+p12)) + ((p1+p5)+(p9+p13)) + ... lane-wise, then
+// (l0 + l1) + (l2 + l3).  H: a multiple of 256.
+__device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, const float *w, float eps, int H,
+                                            float *rb, float *xnb, double *pbuf, float *sbuf) {
+#pragma clang fp contract(off)
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r), 0, static_cast<uint32_t>(4 * H), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r2 ? r2 : r), 0,
+                                                                        static_cast<uint32_t>(4 * H), kBufferWord3);
+    // r into rb, and transposed into xnb (free until the end): partial sum k's
+    // elements r[k], r[16 + k], ... side by side at xnb[k * H / 16 ..], so its
+    // lane reads them 4 at a time (rows L + 4 floats apart: 16-byte aligned,
+    // and the 16 rows start in different banks)
+    const int L = H / 16, LS = L + 4;
+    for (int i = 4 * static_cast<int>(threadIdx.x); i < H; i += 4 * static_cast<int>(blockDim.x)) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * i, 0, kSysCoherent);
+        const u32x4 v2 = __builtin_amdgcn_raw_buffer_load_b128(rs2, 4 * i, 0, kSysCoherent);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = v[e], u2 = v2[e];
+            const float f = r2 ? __builtin_bit_cast(float, u) + __builtin_bit_cast(float, u2) : __builtin_bit_cast(float, u);
+            rb[i + e] = f;
+            xnb[((i + e) & 15) * LS + ((i + e) >> 4)] = f;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const float4 *q = reinterpret_cast<const float4 *>(xnb + threadIdx.x * LS);  // L: a multiple of 16
+        double p = 0.0;
+#pragma unroll 4
+        for (int j = 0; j < L / 4; ++j) {
+            const float4 f = q[j];
+            const double a = f.x, b = f.y, c = f.z, d = f.w;
+            p = __builtin_fma(a, a, p);
+            p = __builtin_fma(b, b, p);
+            p = __builtin_fma(c, c, p);
+            p = __builtin_fma(d, d, p);
+        }
+        pbuf[threadIdx.x] = p;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double l[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l[k] = (pbuf[k] + pbuf[4 + k]) + (pbuf[8 + k] + pbuf[12 + k]);
+        const double ss = (l[0] + l[1]) + (l[2] + l[3]);
+        *sbuf = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
+    }
+    __syncthreads();
+    const float sc = *sbuf;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) xnb[i] = rb[i] * sc * w[i];
+    __syncthreads();
+}
+
+// What a stage waits for between requesting its first weight rows and
+// reading its activation: the grid barrier after the stage before (whose
+// stores must be complete: they are waited for before the arrival, so the
+// new row loads are issued after it and arrive during the wait), then the
+// block command's RMSNorm.  One type for every stage (runtime fields), so
+// the row functions are instantiated once.
+struct SrvPre {
+    bool barrier = false;
+    SrvDev *dev = nullptr;
+    int g = 0, G = 1;
+    uint64_t n = 0, limit = 0;  // barrier number, wait bound in ticks
+    uint32_t *verdict = nullptr;
+    const float *norm_r = nullptr;  // RMSNorm of norm_r (+ norm_r2) when set
+    const float *norm_r2 = nullptr, *norm_w = nullptr;
+    float eps = 0.0f;
+    int H = 0;
+    float *rb = nullptr, *xnb = nullptr, *sbuf = nullptr;
+    double *pbuf = nullptr;
+    __device__ __forceinline__ void arrive() const {
+        if (!barrier) return;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) srv_arrive(dev, g, G, n);
+    }
+    // true: leave (the barrier timed out or quit was raised)
+    __device__ __forceinline__ bool wait() const {
+        if (barrier) {
+            if (threadIdx.x == 0) *verdict = srv_wait(dev, g, n, limit);
+            __syncthreads();
+            if (*verdict) return true;
+        }
+        if (norm_r) srv_rmsnorm(norm_r, norm_r2, norm_w, eps, H, rb, xnb, pbuf, sbuf);
+        return false;
+    }
+};
+
 // silu(g) * u = g / (1 + e^-g) * u, each step one IEEE f32 operation as
 // written (contraction off, fmas explicit), so a host that performs the same
 // steps gets the same bits.  e^t: t clamped to [-87.3, 88]; n = t / ln2
@@ -958,8 +1090,8 @@ template <int NBL>
 constexpr bool kSrvNextGroup = NBL <= 6;
 
 template <int NBL, bool TAIL, bool XL>
-__device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
-                                         float *out) {
+__device__ __forceinline__ bool srv_rows(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                         float *out, const SrvPre &pre) {
     constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
     constexpr int ROWS = kSrvWaves * R;
     constexpr int XI = (4 * NBL + kSrvWaves - 1) / kSrvWaves;
@@ -975,12 +1107,14 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
     const SrvSpan<ROWS> sp(c, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
     const int T = sp.total();
 
-    // the first group's rows are requested before the staging math
-    XTile<XI> xt;
-    srv_activation<XL>(xt, x, B);
-    __builtin_amdgcn_sched_barrier(0);
+    // the first group's rows are requested before the wait and the
+    // staging math
+    pre.arrive();
     RowGroup<NBL, R, true, TAIL> grp;
     sp.load(grp, c, wave * R, B, row_bytes, lane);
+    if (pre.wait()) return false;
+    XTile<XI> xt;
+    srv_activation<XL>(xt, x, B);
     xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
     __syncthreads();
 
@@ -1001,6 +1135,7 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
     }
     __syncthreads();
     srv_store(sp, c, out);
+    return true;
 }
 
 // ggml-cpu numerics job form (MI355X_VARIANT_GGML_Q8): the arithmetic of
@@ -1017,8 +1152,8 @@ __device__ __forceinline__ void srv_rows(const SrvCmd &c, int B, uint4 *lds, con
 constexpr int kSrvCsFloats = 8192;
 
 template <int NBL, bool TAIL, bool XL>
-__device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
-                                            float *out, float *csb) {
+__device__ __forceinline__ bool srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                            float *out, float *csb, const SrvPre &pre) {
 #pragma clang fp contract(off)
     constexpr int R = NBL <= 1 ? 4 : (NBL == 2 ? 2 : 1);
     constexpr int ROWS = kSrvWaves * R;
@@ -1041,12 +1176,13 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     const SrvSpan<ROWS> sp(c, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
     const int T = sp.total();
 
-    XTile<XI> xt;
-    srv_activation<XL>(xt, x, B);
-    __builtin_amdgcn_sched_barrier(0);
+    pre.arrive();
     using Grp = RowGroup<NBL, R, true, TAIL>;
     Grp grp;
     sp.load(grp, c, wave * R, B, row_bytes, lane);
+    if (pre.wait()) return false;
+    XTile<XI> xt;
+    srv_activation<XL>(xt, x, B);
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dxs, sxs);
     __syncthreads();
 
@@ -1069,139 +1205,51 @@ __device__ __forceinline__ void srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
         __syncthreads();  // csb is rewritten by the next chunk
     }
     srv_store(sp, c, out);
+    return true;
 }
 
 template <int NBL, bool TAIL, bool XL = false>
-__device__ __forceinline__ void srv_job(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
-                                        float *out, float *csb) {
-    if (c.mode == kSrvGgmlQ8) srv_rows_q8<NBL, TAIL, XL>(c, B, lds, x, out, csb);
-    else srv_rows<NBL, TAIL, XL>(c, B, lds, x, out);
+__device__ __forceinline__ bool srv_job(const SrvCmd &c, int B, uint4 *lds, const float *__restrict__ x,
+                                        float *out, float *csb, const SrvPre &pre) {
+    if (c.mode == kSrvGgmlQ8) return srv_rows_q8<NBL, TAIL, XL>(c, B, lds, x, out, csb, pre);
+    return srv_rows<NBL, TAIL, XL>(c, B, lds, x, out, pre);
 }
 
 // A stage whose activation (c.K <= kSrvLdsXMax columns) is in LDS.
 constexpr int kSrvLdsXMax = 4096;
-__device__ __forceinline__ void srv_stage_lds(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb) {
+__device__ __forceinline__ bool srv_stage_lds(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb,
+                                              const SrvPre &pre) {
     const int B = c.K / 32;
     switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
-    case 2: srv_job<1, false, true>(c, B, lds, x, outb, csb); break;
-    case 3: srv_job<1, true, true>(c, B, lds, x, outb, csb); break;
-    case 4: srv_job<2, false, true>(c, B, lds, x, outb, csb); break;
-    default: srv_job<2, true, true>(c, B, lds, x, outb, csb); break;  // B < 128 (the host checks K)
+    case 2: return srv_job<1, false, true>(c, B, lds, x, outb, csb, pre);
+    case 3: return srv_job<1, true, true>(c, B, lds, x, outb, csb, pre);
+    case 4: return srv_job<2, false, true>(c, B, lds, x, outb, csb, pre);
+    default: return srv_job<2, true, true>(c, B, lds, x, outb, csb, pre);  // B < 128 (the host checks K)
     }
 }
 
 // One stage of a command: its jobs over the activation x of c.K columns.
-__device__ __forceinline__ void srv_stage(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb) {
+__device__ __forceinline__ bool srv_stage(const SrvCmd &c, uint4 *lds, const float *x, float *outb, float *csb,
+                                          const SrvPre &pre) {
     const int B = c.K / 32;
     switch ((B + 63) / 64 * 2 + (B % 64 != 0 ? 1 : 0)) {
-    case 2: srv_job<1, false>(c, B, lds, x, outb, csb); break;
-    case 3: srv_job<1, true>(c, B, lds, x, outb, csb); break;
-    case 4: srv_job<2, false>(c, B, lds, x, outb, csb); break;
-    case 5: srv_job<2, true>(c, B, lds, x, outb, csb); break;
-    case 6: srv_job<3, false>(c, B, lds, x, outb, csb); break;
-    case 7: srv_job<3, true>(c, B, lds, x, outb, csb); break;
-    case 8: srv_job<4, false>(c, B, lds, x, outb, csb); break;
-    case 9: srv_job<4, true>(c, B, lds, x, outb, csb); break;
-    case 10: srv_job<5, false>(c, B, lds, x, outb, csb); break;
-    case 11: srv_job<5, true>(c, B, lds, x, outb, csb); break;
-    case 12: srv_job<6, false>(c, B, lds, x, outb, csb); break;
-    case 13: srv_job<6, true>(c, B, lds, x, outb, csb); break;
-    case 14: srv_job<7, false>(c, B, lds, x, outb, csb); break;
-    case 15: srv_job<7, true>(c, B, lds, x, outb, csb); break;
-    case 16: srv_job<8, false>(c, B, lds, x, outb, csb); break;
-    default: srv_job<8, true>(c, B, lds, x, outb, csb); break;  // 448 < B < 512 (the host checks K <= 16384)
+    case 2: return srv_job<1, false>(c, B, lds, x, outb, csb, pre);
+    case 3: return srv_job<1, true>(c, B, lds, x, outb, csb, pre);
+    case 4: return srv_job<2, false>(c, B, lds, x, outb, csb, pre);
+    case 5: return srv_job<2, true>(c, B, lds, x, outb, csb, pre);
+    case 6: return srv_job<3, false>(c, B, lds, x, outb, csb, pre);
+    case 7: return srv_job<3, true>(c, B, lds, x, outb, csb, pre);
+    case 8: return srv_job<4, false>(c, B, lds, x, outb, csb, pre);
+    case 9: return srv_job<4, true>(c, B, lds, x, outb, csb, pre);
+    case 10: return srv_job<5, false>(c, B, lds, x, outb, csb, pre);
+    case 11: return srv_job<5, true>(c, B, lds, x, outb, csb, pre);
+    case 12: return srv_job<6, false>(c, B, lds, x, outb, csb, pre);
+    case 13: return srv_job<6, true>(c, B, lds, x, outb, csb, pre);
+    case 14: return srv_job<7, false>(c, B, lds, x, outb, csb, pre);
+    case 15: return srv_job<7, true>(c, B, lds, x, outb, csb, pre);
+    case 16: return srv_job<8, false>(c, B, lds, x, outb, csb, pre);
+    default: return srv_job<8, true>(c, B, lds, x, outb, csb, pre);  // 448 < B < 512 (the host checks K <= 16384)
     }
-}
-
-// Grid barrier inside a command (thread 0 of every workgroup; `n` = barriers
-// this launch has passed, this one included).  256 arrivals on one counter
-// serialise (~25 ns each, measured); in two levels, as the completion count,
-// each counter takes at most 32, and the pollers read their group's flag
-// line, not a counter line that takes atomics.  Bounded like every wait:
-// returns 1 (and raises quit) after `limit` ticks or when quit is raised.
-__device__ __forceinline__ uint32_t srv_barrier(SrvDev *dev, int g, int G, uint64_t n, uint64_t limit) {
-    const int gi = g & 7;
-    const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
-    const uint64_t a = __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-    if (a == n * members) {
-        const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
-        const uint64_t t = __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-        if (t == n * groups)
-            for (int i = 0; i < static_cast<int>(groups); ++i)
-                __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(n), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const uint64_t t0 = srv_clock();
-    while (static_cast<int32_t>(__hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                                static_cast<uint32_t>(n)) < 0) {
-        if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 || srv_clock() - t0 > limit) {
-            __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return 1;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return 0;
-}
-
-// RMSNorm of the block command, every workgroup for itself: r (H floats,
-// written by other workgroups in this command; plus r2 when given, one f32
-// add) into rb, then
-// xn[i] = r[i] * s * w[i] into xnb with s = 1 / sqrt(float(ss / H) + eps), the
-// f32 steps and the summation order of the decode host's rmsnorm: ss in
-// double as 16 partial sums p_k = sum over i0 = 0, 16, ... of r[i0 + k]^2
-// (sequential; a square of a float is exact in double), combined as
-// ((p0+p4)+(p8+p12)) + ((p1+p5)+(p9+p13)) + ... lane-wise, then
-// (l0 + l1) + (l2 + l3).  H: a multiple of 256.
-__device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, const float *w, float eps, int H,
-                                            float *rb, float *xnb, double *pbuf, float *sbuf) {
-#pragma clang fp contract(off)
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r), 0, static_cast<uint32_t>(4 * H), kBufferWord3);
-    const __amdgpu_buffer_rsrc_t rs2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(r2 ? r2 : r), 0,
-                                                                        static_cast<uint32_t>(4 * H), kBufferWord3);
-    // r into rb, and transposed into xnb (free until the end): partial sum k's
-    // elements r[k], r[16 + k], ... side by side at xnb[k * H / 16 ..], so its
-    // lane reads them 4 at a time (rows L + 4 floats apart: 16-byte aligned,
-    // and the 16 rows start in different banks)
-    const int L = H / 16, LS = L + 4;
-    for (int i = 4 * static_cast<int>(threadIdx.x); i < H; i += 4 * static_cast<int>(blockDim.x)) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * i, 0, kSysCoherent);
-        const u32x4 v2 = __builtin_amdgcn_raw_buffer_load_b128(rs2, 4 * i, 0, kSysCoherent);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t u = v[e], u2 = v2[e];
-            const float f = r2 ? __builtin_bit_cast(float, u) + __builtin_bit_cast(float, u2) : __builtin_bit_cast(float, u);
-            rb[i + e] = f;
-            xnb[((i + e) & 15) * LS + ((i + e) >> 4)] = f;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < 16) {
-        const float4 *q = reinterpret_cast<const float4 *>(xnb + threadIdx.x * LS);  // L: a multiple of 16
-        double p = 0.0;
-#pragma unroll 4
-        for (int j = 0; j < L / 4; ++j) {
-            const float4 f = q[j];
-            const double a = f.x, b = f.y, c = f.z, d = f.w;
-            p = __builtin_fma(a, a, p);
-            p = __builtin_fma(b, b, p);
-            p = __builtin_fma(c, c, p);
-            p = __builtin_fma(d, d, p);
-        }
-        pbuf[threadIdx.x] = p;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double l[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) l[k] = (pbuf[k] + pbuf[4 + k]) + (pbuf[8 + k] + pbuf[12 + k]);
-        const double ss = (l[0] + l[1]) + (l[2] + l[3]);
-        *sbuf = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
-    }
-    __syncthreads();
-    const float sc = *sbuf;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) xnb[i] = rb[i] * sc * w[i];
-    __syncthreads();
 }
 
 // Command-record fields as 32-bit words (the record is copied word by word).
@@ -1310,35 +1358,47 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             __syncthreads();
             if (cs.exit) return;
         }
-        // a grid barrier: every workgroup's stores of the stage before have
-        // completed before its arrival (all workgroups are resident: the
-        // launch is cooperative)
-        auto barrier = [&]() {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            ++nbar;
-            if (threadIdx.x == 0) verdict = srv_barrier(dev, g, G, nbar, 2 * idle_ticks);
-            __syncthreads();
-            return verdict != 0;
-        };
-        // cs2 = cs, one word per thread (then thread 0 patches the stage)
+        // cs2 = cs, one word per thread, once every thread is done with the
+        // stage before (then thread 0 patches the stage)
         auto copy_cmd = [&]() {
+            __syncthreads();
             uint32_t *d = reinterpret_cast<uint32_t *>(&cs2);
             for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x) d[i] = csw[i];
             __syncthreads();
         };
         // stages: plain 1; SwiGLU 2 (gate|up -> h, down); block 3 (pre -> r,
         // gate|up over rmsnorm(r) -> h, down + r), 4 with post (over
-        // rmsnorm(down + r)).  One call site per stage form keeps the
+        // rmsnorm(down + r)).  Every stage after the first starts with a
+        // grid barrier (all workgroups are resident: the launch is
+        // cooperative), inside the row functions, after the stage's first
+        // rows were requested.  One call site per stage form keeps the
         // kernel's register count at that of one stage.
         const bool blk = cs.pre.N > 0;
         const int nst = blk ? (cs.post.N > 0 ? 4 : 3) : (cs.K2 ? 2 : 1);
         for (int st = 0; st < nst; ++st) {
-            if (st > 0 && barrier()) return;
+            SrvPre pre;
+            if (st > 0) {
+                pre.barrier = true;
+                pre.dev = dev;
+                pre.g = g;
+                pre.G = G;
+                pre.n = ++nbar;
+                pre.limit = 2 * idle_ticks;
+                pre.verdict = &verdict;
+            }
             // r = (pre x) + resid (resid after x in the payload); the next
             // stage's r = down h + r, added in the down stage's store pass
-            if (blk && st == 1) srv_rmsnorm(cs.r_dev, dx + cs.K, cs.norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
-            if (st == 3) srv_rmsnorm(cs.r_dev, nullptr, cs.post_norm_w, cs.eps, cs.H, rb, xnb, pbuf, &sbuf);
+            if ((blk && st == 1) || st == 3) {
+                pre.norm_r = cs.r_dev;
+                pre.norm_r2 = st == 1 ? dx + cs.K : nullptr;
+                pre.norm_w = st == 1 ? cs.norm_w : cs.post_norm_w;
+                pre.eps = cs.eps;
+                pre.H = cs.H;
+                pre.rb = rb;
+                pre.xnb = xnb;
+                pre.pbuf = pbuf;
+                pre.sbuf = &sbuf;
+            }
             if (st > 0 || blk) {
                 copy_cmd();
                 if (threadIdx.x == 0) {
@@ -1362,15 +1422,16 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                         cs2.jobs[0] = cs.down;
                         cs2.kind = blk ? kSrvStoreAddL : kSrvStoreY;
                         cs2.add = rb;
-                        // r_dev's readers finished before the barrier above
+                        // r_dev's readers finished before this stage's barrier
                         cs2.mirror = blk && cs.post.N > 0 ? cs.r_dev : nullptr;
                     }
                 }
                 __syncthreads();
             }
             const SrvCmd &c = st > 0 || blk ? cs2 : cs;
-            if (blk && (st & 1)) srv_stage_lds(c, lds_dp, xnb, outb, csb);
-            else srv_stage(c, lds_dp, st == 0 ? dx : cs.h, outb, csb);
+            const bool ok = blk && (st & 1) ? srv_stage_lds(c, lds_dp, xnb, outb, csb, pre)
+                                            : srv_stage(c, lds_dp, st == 0 ? dx : cs.h, outb, csb, pre);
+            if (!ok) return;
         }
         // every wave's output stores have completed (they write through) before
         // the barrier, and so before thread 0 counts the arrival; no fence:
