@@ -347,6 +347,10 @@ MI355X_API int mi355x_server_swiglu(mi355x_server *s, const float *x, int64_t K,
  * ss = (l_0 + l_1) + (l_2 + l_3);  s = 1 / sqrt(float(ss / H) + eps) in f32
  * (correctly rounded);  xn_i = (r_i * s) * norm_w_i.  K, H, F: multiples of
  * 256, H <= 4096, F <= max_k and K + H <= max_k; y device-visible.
+ * The server keeps y in device memory until the next block command: resid
+ * NULL takes the residual from there (the previous block command's y, same
+ * H), and y NULL leaves it there only -- a layer loop passes the host's
+ * residual once and reads y back after its last layer.
  * With W_next (else NULL, and the three after it ignored): after another
  * grid barrier, y_next = W_next (rmsnorm(y) * next_norm_w) -- the next
  * layer's q|k|v (N_next rows, H columns) -- in the same command. */

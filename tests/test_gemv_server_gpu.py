@@ -392,6 +392,40 @@ def test_server_block_matches_separate_steps(ctx, server, K, H, F, v):
     assert np.array_equal(got_next, want_next), (K, H, F, np.abs(got_next - want_next).max())
 
 
+@pytest.mark.parametrize("v", [mi355x.VARIANT_AUTO, mi355x.VARIANT_GGML_Q8])
+def test_server_block_residual_kept_in_the_server(ctx, server, v):
+    """A chain of block commands that pass the residual only to the first and
+    read y back only after the last (the server keeps it in between, with
+    plain and SwiGLU commands in the way): the same bits as the separate
+    steps with the residual on the host."""
+    K, H, F = 2048, 2048, 2816
+    _, ws = block_weights(ctx, K, H, F, seed=90)
+    rng = np.random.default_rng(91)
+    norm_w = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    nw = ctx.to_device(norm_w)
+    xs = [synth.activations(K, seed=900 + it) for it in range(4)]
+    r0 = (rng.standard_normal(H) * 0.5).astype(np.float32)
+    y = ctx.alloc(4 * H)
+    yp = ctx.alloc(4 * F)
+    try:
+        with variant(ctx, v):
+            want = r0
+            for x in xs:
+                want = block_separate(ctx, server, ws, x, want, norm_w)
+            for it, x in enumerate(xs):
+                last = it == len(xs) - 1
+                server.block(x, ws[0].ptr, r0 if it == 0 else H, nw.ptr, EPS, ws[1].ptr, ws[2].ptr, F, ws[3].ptr,
+                             y.ptr if last else 0)
+                if not last:  # other commands between the blocks leave the kept residual alone
+                    server.gemv(x, [(ws[0].ptr, H, yp.ptr)])
+                    server.swiglu(x, ws[1].ptr, ws[2].ptr, F, ws[3].ptr, H, yp.ptr)
+            got = y.download(np.float32, H)
+    finally:
+        for b in [y, yp, nw] + ws:
+            b.free()
+    assert np.array_equal(got, want), np.abs(got - want).max()
+
+
 def test_server_block_between_other_commands(ctx, server):
     """Block, SwiGLU and plain commands in turn on one resident kernel (the
     barrier count carries across commands of both kinds)."""
@@ -440,7 +474,6 @@ def test_server_block_rejects_bad_arguments(ctx, server):
         assert call(w_o=o + 2) == mi355x.EINVAL
         assert call(w_down=d + 8) == mi355x.EINVAL
         assert call(norm_w=0) == mi355x.EINVAL
-        assert call(y=0) == mi355x.EINVAL
         assert call(w_next=g, next_norm_w=nw.ptr, N_next=0, y_next=y.ptr) == mi355x.EINVAL
         assert call(w_next=g, next_norm_w=0, N_next=64, y_next=y.ptr) == mi355x.EINVAL
         assert call(w_next=g + 4, next_norm_w=nw.ptr, N_next=64, y_next=y.ptr) == mi355x.EINVAL

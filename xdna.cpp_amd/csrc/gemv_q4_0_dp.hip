@@ -741,6 +741,14 @@ struct SrvCmd {
     const float *post_norm_w;
     // residual store kinds: also write the result here (device memory)
     float *mirror;
+    // rows per share unit of this stage's jobs: 16 (one 64-byte line of y,
+    // for outputs in pinned host memory) or, with unit8, 8 (device outputs)
+    int32_t unit8;
+    // block command: the residual is resid_dev (device) instead of the H
+    // floats after x in the payload; the down stage writes y + into
+    // resid_dev (and into down.y unless it is null)
+    int32_t resid_on_dev;
+    float *resid_dev;
 };
 // store-pass kinds
 constexpr int32_t kSrvStoreY = 0;     // y[row] = out
@@ -809,17 +817,19 @@ constexpr int kSrvOutMax = 4096;  // rows of a command's jobs per workgroup (pad
 // group's loads are in flight across job boundaries too, and the outputs of
 // all jobs are stored once at the end.  Indices are uniform; the per-job
 // values sit in registers behind constant-index selects.
-// A workgroup's share [lo, hi) of a job's N rows: a run of whole 64-byte
-// lines of y (16 outputs; the first unit ends at y's first line boundary):
-// workgroups that stored parts of one line of pinned host memory would
-// serialise on it (~6 us per job of small shares).
+// A workgroup's share [lo, hi) of a job's N rows: a run of whole units of
+// `unit` outputs, the first ending at y's first unit boundary.  16 outputs
+// are one 64-byte line: workgroups that stored parts of one line of pinned
+// host memory would serialise on it (~6 us per job of small shares); for
+// outputs in device memory 8 spreads short jobs over twice the workgroups.
 // (32-bit arithmetic: N < 2^27 and G <= 1024, which the host checks through
 // the rows a workgroup holds, keep U * G below 2^32.)
-__device__ __forceinline__ void srv_share(int64_t N64, const float *y, int g, int G, int &lo, int &hi) {
+__device__ __forceinline__ void srv_share(int64_t N64, const float *y, int g, int G, int &lo, int &hi,
+                                          uint32_t unit = 16) {
     const uint32_t N = static_cast<uint32_t>(N64);
-    const uint32_t b0 = (16u - (static_cast<uint32_t>(reinterpret_cast<uintptr_t>(y)) >> 2)) & 15u;
-    const uint32_t U = 1 + (N > b0 ? N - b0 + 15 : 0) / 16;
-    auto at = [&](uint32_t u) { return u == 0 ? 0u : min(N, b0 + 16 * (u - 1)); };
+    const uint32_t b0 = (unit - (static_cast<uint32_t>(reinterpret_cast<uintptr_t>(y)) >> 2)) & (unit - 1);
+    const uint32_t U = 1 + (N > b0 ? N - b0 + unit - 1 : 0) / unit;
+    auto at = [&](uint32_t u) { return u == 0 ? 0u : min(N, b0 + unit * (u - 1)); };
     lo = static_cast<int>(at(U * static_cast<uint32_t>(g) / static_cast<uint32_t>(G)));
     hi = static_cast<int>(at(U * static_cast<uint32_t>(g + 1) / static_cast<uint32_t>(G)));
 }
@@ -834,7 +844,7 @@ struct SrvSpan {
         const int n = c.njobs;
         auto share = [&](int j, int &lo, int &hi) {
             lo = hi = 0;
-            if (j < n) srv_share(c.jobs[j].N, c.jobs[j].y, g, G, lo, hi);
+            if (j < n) srv_share(c.jobs[j].N, c.jobs[j].y, g, G, lo, hi, c.unit8 ? 8u : 16u);
         };
         share(0, lo0, hi0);
         share(1, lo1, hi1);
@@ -1386,11 +1396,12 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                 pre.limit = 2 * idle_ticks;
                 pre.verdict = &verdict;
             }
-            // r = (pre x) + resid (resid after x in the payload); the next
-            // stage's r = down h + r, added in the down stage's store pass
+            // r = (pre x) + resid (resid after x in the payload, or in
+            // resid_dev); the next stage's r = down h + r, added in the down
+            // stage's store pass and kept in resid_dev
             if ((blk && st == 1) || st == 3) {
-                pre.norm_r = cs.r_dev;
-                pre.norm_r2 = st == 1 ? dx + cs.K : nullptr;
+                pre.norm_r = st == 1 ? cs.r_dev : cs.resid_dev;
+                pre.norm_r2 = st == 3 ? nullptr : cs.resid_on_dev ? cs.resid_dev : dx + cs.K;
                 pre.norm_w = st == 1 ? cs.norm_w : cs.post_norm_w;
                 pre.eps = cs.eps;
                 pre.H = cs.H;
@@ -1399,18 +1410,21 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                 pre.pbuf = pbuf;
                 pre.sbuf = &sbuf;
             }
-            if (st > 0 || blk) {
+            if (st > 0 || blk || cs.K2) {
                 copy_cmd();
                 if (threadIdx.x == 0) {
-                    if (st == 0) {
+                    if (blk && st == 0) {
                         // block: pre x into r_dev (the residual is added
                         // when every workgroup reads it back)
                         cs2.njobs = 1;
                         cs2.jobs[0] = {cs.pre.W, cs.r_dev, cs.pre.N};
                         cs2.kind = kSrvStoreY;
-                    } else if (st == 1 && blk) {
-                        cs2.K = cs.H;
+                        cs2.unit8 = 1;
+                    } else if (st == (blk ? 1 : 0)) {
+                        // gate|up -> h (device)
+                        if (blk) cs2.K = cs.H;
                         cs2.kind = kSrvStoreGlu;
+                        cs2.unit8 = 1;
                     } else if (st == 3) {
                         cs2.K = cs.H;
                         cs2.njobs = 1;
@@ -1422,13 +1436,20 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                         cs2.jobs[0] = cs.down;
                         cs2.kind = blk ? kSrvStoreAddL : kSrvStoreY;
                         cs2.add = rb;
-                        // r_dev's readers finished before this stage's barrier
-                        cs2.mirror = blk && cs.post.N > 0 ? cs.r_dev : nullptr;
+                        // a block's result goes to resid_dev (the next
+                        // stage's or command's residual; its readers
+                        // finished before this stage's barrier), and to
+                        // down.y when given
+                        if (blk && !cs.down.y) {
+                            cs2.jobs[0].y = cs.resid_dev;
+                            cs2.unit8 = 1;
+                        }
+                        cs2.mirror = blk && cs.down.y ? cs.resid_dev : nullptr;
                     }
                 }
                 __syncthreads();
             }
-            const SrvCmd &c = st > 0 || blk ? cs2 : cs;
+            const SrvCmd &c = st > 0 || blk || cs.K2 ? cs2 : cs;
             const bool ok = blk && (st & 1) ? srv_stage_lds(c, lds_dp, xnb, outb, csb, pre)
                                             : srv_stage(c, lds_dp, st == 0 ? dx : cs.h, outb, csb, pre);
             if (!ok) return;
@@ -2400,7 +2421,8 @@ struct ServerImpl {
     SrvDev *dev = nullptr;
     float *dx = nullptr;   // device copy of x (written by workgroup 0)
     float *dh = nullptr;   // h of SwiGLU commands (max_k floats)
-    float *dr = nullptr;   // r of block commands (kSrvLdsXMax floats)
+    float *dr = nullptr;   // pre x of block commands (kSrvLdsXMax floats)
+    float *dres = nullptr; // the residual a block command leaves (kSrvLdsXMax floats)
     uint32_t seq = 0;      // last command number handed out
     bool running = false;
     std::chrono::steady_clock::time_point last{};
@@ -2583,6 +2605,8 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
     if (e == hipSuccess) s.dh = static_cast<float *>(p);
     if (e == hipSuccess) e = hipMalloc(&p, mi355x::kSrvLdsXMax * sizeof(float));
     if (e == hipSuccess) s.dr = static_cast<float *>(p);
+    if (e == hipSuccess) e = hipMalloc(&p, mi355x::kSrvLdsXMax * sizeof(float));
+    if (e == hipSuccess) s.dres = static_cast<float *>(p);
     int per_cu = 0;
     if (e == hipSuccess)
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -2668,7 +2692,7 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
                         const void *W_down, float *y, const float *next_norm_w, const void *W_next, int64_t N_next,
                         float *y_next) {
     clear_error();
-    if (!srv || !x || !W_o || !resid || !norm_w || !W_gate || !W_up || !W_down || !y)
+    if (!srv || !x || !W_o || !norm_w || !W_gate || !W_up || !W_down)
         return set_error(MI355X_EINVAL, "mi355x_server_block: null pointer");
     const bool post = W_next != nullptr;
     if (post && (!next_norm_w || !y_next || N_next <= 0 || reinterpret_cast<uintptr_t>(W_next) % 16 != 0 ||
@@ -2676,7 +2700,7 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
         return set_error(MI355X_EINVAL, "mi355x_server_block: bad next stage");
     mi355x::ServerImpl &s = srv->impl;
     if (K <= 0 || K % 256 != 0 || F <= 0 || F % 256 != 0 || F > s.max_k || H <= 0 || H % 256 != 0 ||
-        H > mi355x::kSrvLdsXMax || K + H > s.max_k)
+        H > mi355x::kSrvLdsXMax || K + (resid ? H : 0) > s.max_k)
         return set_error(MI355X_EINVAL,
                          "mi355x_server_block: K, H and F must be multiples of 256, H <= 4096, F and K + H <= max_k");
     for (const void *w : {W_o, W_gate, W_up, W_down})
@@ -2689,7 +2713,7 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
         return set_error(MI355X_EUNSUPPORTED, "mi355x_server_block: no exact-f32 form in the server");
     const mi355x_server_job pre_stage[1] = {{W_o, H, s.dr}};
     const mi355x_server_job up_stage[2] = {{W_gate, F, s.dh}, {W_up, F, s.dh}};
-    const mi355x_server_job down_stage[1] = {{W_down, H, y}};
+    const mi355x_server_job down_stage[1] = {{W_down, H, y ? y : s.dres}};
     const mi355x_server_job next_stage[1] = {{W_next, N_next, y_next}};
     if (!mi355x::server_rows_fit(s, pre_stage, 1) || !mi355x::server_rows_fit(s, up_stage, 2) ||
         !mi355x::server_rows_fit(s, down_stage, 1) || (post && !mi355x::server_rows_fit(s, next_stage, 1)))
@@ -2708,11 +2732,13 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
     c.r_dev = s.dr;
     c.norm_w = norm_w;
     c.eps = eps;
+    c.resid_on_dev = resid ? 0 : 1;
+    c.resid_dev = s.dres;
     if (post) {
         c.post = {static_cast<const uint8_t *>(W_next), y_next, N_next};
         c.post_norm_w = next_norm_w;
     }
-    return mi355x::server_submit(s, x, K, resid, H, c, "mi355x_server_block");
+    return mi355x::server_submit(s, x, K, resid, resid ? H : 0, c, "mi355x_server_block");
 }
 
 int mi355x_server_stop(mi355x_server *srv) {
@@ -2752,6 +2778,7 @@ void mi355x_server_destroy(mi355x_server *srv) {
         if (s.dx) (void)hipFree(s.dx);
         if (s.dh) (void)hipFree(s.dh);
         if (s.dr) (void)hipFree(s.dr);
+        if (s.dres) (void)hipFree(s.dres);
     }
     if (s.cmd_h) (void)hipHostFree(s.cmd_h);
     if (s.hx_h) (void)hipHostFree(s.hx_h);

@@ -896,7 +896,8 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
             rope_cs[hd / 2 + i] = std::sin(f);
         }
         dequant_q4_0_row(m->mats[7 * L].q.data() + static_cast<int64_t>(tok) * (H / 32) * 18, H, h.data());
-        bool have_qkv = false;  // the last block command computed this layer's q|k|v
+        bool have_qkv = false;    // the last block command computed this layer's q|k|v
+        bool have_dev_h = false;  // the server holds the residual (a block command ran this pass)
         for (int l = 0; l < L; ++l) {
             if (have_qkv) {
                 std::memcpy(q.data(), m->hy + H, static_cast<size_t>(QD) * 4);
@@ -934,15 +935,19 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
                              &wu = m->mats[7 * l + QD_UP], &wd = m->mats[7 * l + QD_DOWN];
                 const bool next = l + 1 < L && qkv_adjacent;
                 const Matrix &wq = m->mats[7 * (next ? l + 1 : l) + QD_Q];
-                if (mi355x_server_block(m->server, att.data(), QD, wo.dev, h.data(), H,
-                                        m->ffn_norm_dev + static_cast<size_t>(l) * H, c.norm_eps, wg.dev, wu.dev,
-                                        c.ffn, wd.dev, m->hy_dev,
+                // the residual stays in the server between layers: the host
+                // sends it with layer 0 and reads it back when it needs it
+                const bool need_h = !next;
+                if (mi355x_server_block(m->server, att.data(), QD, wo.dev, l == 0 || !have_dev_h ? h.data() : nullptr,
+                                        H, m->ffn_norm_dev + static_cast<size_t>(l) * H, c.norm_eps, wg.dev, wu.dev,
+                                        c.ffn, wd.dev, need_h ? m->hy_dev : nullptr,
                                         next ? m->attn_norm_dev + static_cast<size_t>(l + 1) * H : nullptr,
                                         next ? wq.dev : nullptr, QD + 2 * KVD, m->hy_dev + H) != MI355X_OK) {
                     rc = -1;
                     break;
                 }
-                std::memcpy(h.data(), m->hy, static_cast<size_t>(H) * 4);
+                if (need_h) std::memcpy(h.data(), m->hy, static_cast<size_t>(H) * 4);
+                have_dev_h = true;
                 launches += next ? 4 : 3;
                 have_qkv = next;
                 t_gemv += now() - t0;

@@ -239,12 +239,18 @@ class Server:
                   y_next: int = 0) -> int:
         """y = r + W_down (silu(W_gate xn) * (W_up xn)), xn = rmsnorm(r) * norm_w,
         r = resid + W_o x, as one command (x, resid: host f32; the rest device);
-        with w_next also y_next = W_next (rmsnorm(y) * next_norm_w)."""
+        with w_next also y_next = W_next (rmsnorm(y) * next_norm_w).  resid as
+        an int H: the residual the server kept from the last block command;
+        y 0: y is only kept in the server."""
         x = np.ascontiguousarray(x, dtype=np.float32)
-        resid = np.ascontiguousarray(resid, dtype=np.float32)
-        return self.lib.mi355x_server_block(self.h, x.ctypes.data, x.size, w_o, resid.ctypes.data, resid.size,
-                                            norm_w, eps, w_gate, w_up, F, w_down, y, next_norm_w or None,
-                                            w_next or None, N_next, y_next or None)
+        if isinstance(resid, int):  # H, the residual the server holds
+            rp, H = None, resid
+        else:
+            resid = np.ascontiguousarray(resid, dtype=np.float32)
+            rp, H = resid.ctypes.data, resid.size
+        return self.lib.mi355x_server_block(self.h, x.ctypes.data, x.size, w_o, rp, H, norm_w, eps, w_gate, w_up, F,
+                                            w_down, y or None, next_norm_w or None, w_next or None, N_next,
+                                            y_next or None)
 
     def block(self, *args) -> None:
         check(self.block_ptr(*args))
