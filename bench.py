@@ -520,11 +520,12 @@ def main() -> int:
                 ms2, c2, _ = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle)
                 gbs2 = algorithmic_bytes(t, n2, k2) / (ms2 * 1e-3) / 1e9
                 mso = gemv_rate(ctx, t, raw2, n2, k2, x2, args.steps, args.warmup, ROTATE_BYTES, args.settle,
-                                overlap=min(overlap, 2))[0] if overlap else ms2
+                                overlap=overlap)[0] if overlap else ms2
                 gbo = algorithmic_bytes(t, n2, k2) / (mso * 1e-3) / 1e9
                 sweep[f"{n2}x{k2}"] = {"us": round(ms2 * 1e3, 3), "GB/s": round(gbs2, 1),
                                        "frac": round(gbs2 / HBM_PEAK_GBS, 4), "copies": c2,
-                                       "us_overlap": round(mso * 1e3, 3), "frac_overlap": round(gbo / HBM_PEAK_GBS, 4)}
+                                       "us_overlap": round(mso * 1e3, 3), "frac_overlap": round(gbo / HBM_PEAK_GBS, 4),
+                                       "overlap_streams": overlap}
                 log(f"bench: Q4_0 {n2}x{k2}: {ms2 * 1e3:.2f} us, {gbs2:.1f} GB/s; overlapped {mso * 1e3:.2f} us "
                     f"({gbo / HBM_PEAK_GBS:.1%})")
 

@@ -285,6 +285,19 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
         delete ctx;
         return hip_error(e, "hipStreamCreateWithFlags");
     }
+    // MI355X_OPT_OVERLAP's streams, created right after the context's own:
+    // HIP hands hardware queues to streams in turn (GPU_MAX_HW_QUEUES, 4 by
+    // default), so four streams created together sit on four queues, which
+    // overlapped launches need; created later, other streams made in between
+    // could put two of them on one queue
+    for (int i = 0; i < 3 && e == hipSuccess; ++i) e = hipStreamCreateWithFlags(&ctx->ov_streams[i], hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        for (hipStream_t st : ctx->ov_streams)
+            if (st) (void)hipStreamDestroy(st);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_error(e, "hipStreamCreateWithFlags");
+    }
     void *word = nullptr, *word_dev = nullptr;
     e = hipHostMalloc(&word, 64, hipHostMallocMapped);
     if (e == hipSuccess) {
@@ -293,6 +306,7 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
     }
     if (e != hipSuccess) {
         if (word) (void)hipHostFree(word);
+        for (hipStream_t st : ctx->ov_streams) (void)hipStreamDestroy(st);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return hip_error(e, "completion word allocation");
