@@ -130,7 +130,8 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     arithmetic, any K).
  *   MI355X_OPT_OVERLAP: 0 (default: off) or S = 2, 3, 4.  With S,
  *     consecutive mi355x_gemv calls may run at the same time: the context
- *     gets S - 1 more streams of the same kind, and GEMVs with f32
+ *     uses S - 1 of the 3 more streams of the same kind it creates with its
+ *     own (consecutive streams get distinct hardware queues), and GEMVs with f32
  *     activations on a 16-byte boundary (IQ3_XXS and IQ2_S once the context
  *     holds the current grid, after one such GEMV) take the S streams in
  *     turn, so that up to S launches are in flight and each one's start
