@@ -480,6 +480,8 @@ def test_server_block_rejects_bad_arguments(ctx, server):
         with variant(ctx, mi355x.VARIANT_EXACT_F32):
             assert call() == mi355x.EUNSUPPORTED
         assert call() == mi355x.OK  # still serves
+        assert call(resid=H) == mi355x.OK  # the residual that call left
+        assert call(resid=2 * H) == mi355x.EINVAL  # none of that length kept
     finally:
         for b in [y, nw] + ws:
             b.free()

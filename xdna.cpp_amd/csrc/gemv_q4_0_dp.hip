@@ -2423,6 +2423,7 @@ struct ServerImpl {
     float *dh = nullptr;   // h of SwiGLU commands (max_k floats)
     float *dr = nullptr;   // pre x of block commands (kSrvLdsXMax floats)
     float *dres = nullptr; // the residual a block command leaves (kSrvLdsXMax floats)
+    int64_t dres_h = 0;    // its length, 0 until a block command completed
     uint32_t seq = 0;      // last command number handed out
     bool running = false;
     std::chrono::steady_clock::time_point last{};
@@ -2708,6 +2709,8 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
             return set_error(MI355X_EINVAL, "mi355x_server_block: weights must be 16-byte aligned");
     if (reinterpret_cast<uintptr_t>(norm_w) % 4 != 0)
         return set_error(MI355X_EINVAL, "mi355x_server_block: norm_w must be 4-byte aligned");
+    if (!resid && s.dres_h != H)
+        return set_error(MI355X_EINVAL, "mi355x_server_block: no residual of H values kept from an earlier block command");
     const int variant = s.ctx->kernel_variant;
     if (variant == MI355X_VARIANT_EXACT_F32)
         return set_error(MI355X_EUNSUPPORTED, "mi355x_server_block: no exact-f32 form in the server");
@@ -2738,7 +2741,10 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
         c.post = {static_cast<const uint8_t *>(W_next), y_next, N_next};
         c.post_norm_w = next_norm_w;
     }
-    return mi355x::server_submit(s, x, K, resid, resid ? H : 0, c, "mi355x_server_block");
+    s.dres_h = 0;  // set again once the command completed
+    const int rc = mi355x::server_submit(s, x, K, resid, resid ? H : 0, c, "mi355x_server_block");
+    if (rc == MI355X_OK) s.dres_h = H;
+    return rc;
 }
 
 int mi355x_server_stop(mi355x_server *srv) {
