@@ -714,7 +714,7 @@ struct SrvCmd {
     // how the store pass writes job 0's rows (kSrvStore*) and, for the
     // residual kinds, the vector added to them
     int32_t kind;
-    int32_t pad_;
+    int32_t stage;  // the stage's number within its command (phase stamps)
     const float *add;
     // SwiGLU command (K2 > 0): jobs 0 and 1 are the gate and up matrices,
     // both of K2 rows and both with y = h; the first stage writes
@@ -773,6 +773,31 @@ struct SrvDev {
 };
 
 __device__ __forceinline__ uint64_t srv_clock() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Phase timestamps of server commands, in builds with MI355X_SRV_STAMPS only
+// (the stamps library, xdna.cpp_amd/server_phases.py): thread 0 of each of
+// the first 256 workgroups records s_memrealtime at fixed points of the last
+// 64 commands; mi355x_server_stamps copies the table out.  Slots: 0 command
+// seen, 1 record and x read, 2 + 2s / 3 + 2s stage s staged / rows done,
+// 10 last stores done, 11 arrived, 12 completion stored (the last arrival),
+// 12 + s stage s's barrier passed (s >= 1), 16 / 17 / 18 RMSNorm: r read,
+// sums done, done (the last RMSNorm of the command).
+#ifdef MI355X_SRV_STAMPS
+constexpr int kSrvStampSlots = 20;
+__device__ uint64_t g_srv_stamps[64][256][kSrvStampSlots];
+__shared__ uint32_t s_srv_cmd;
+#define SRV_STAMP(cmd, k)                                                                                         \
+    do {                                                                                                          \
+        if (threadIdx.x == 0 && blockIdx.x < 256)                                                                 \
+            g_srv_stamps[(cmd) & 63][blockIdx.x][k] = __builtin_amdgcn_s_memrealtime();                           \
+    } while (0)
+#define SRV_CMD() s_srv_cmd
+#else
+#define SRV_STAMP(cmd, k) \
+    do {                  \
+    } while (0)
+#define SRV_CMD() 0u
+#endif
 
 // Cache policy sc0 sc1 (system coherent): the load reads host memory itself,
 // never a line a GPU cache kept from an earlier command.
@@ -958,6 +983,7 @@ __device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, con
         }
     }
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 16);
     if (threadIdx.x < 16) {
         const float4 *q = reinterpret_cast<const float4 *>(xnb + threadIdx.x * LS);  // L: a multiple of 16
         double p = 0.0;
@@ -973,6 +999,7 @@ __device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, con
         pbuf[threadIdx.x] = p;
     }
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 17);
     if (threadIdx.x == 0) {
         double l[4];
 #pragma unroll
@@ -984,6 +1011,7 @@ __device__ __forceinline__ void srv_rmsnorm(const float *r, const float *r2, con
     const float sc = *sbuf;
     for (int i = threadIdx.x; i < H; i += blockDim.x) xnb[i] = rb[i] * sc * w[i];
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 18);
 }
 
 // What a stage waits for between requesting its first weight rows and
@@ -998,6 +1026,7 @@ struct SrvPre {
     int g = 0, G = 1;
     uint64_t n = 0, limit = 0;  // barrier number, wait bound in ticks
     uint32_t *verdict = nullptr;
+    int stage = 0;
     const float *norm_r = nullptr;  // RMSNorm of norm_r (+ norm_r2) when set
     const float *norm_r2 = nullptr, *norm_w = nullptr;
     float eps = 0.0f;
@@ -1015,6 +1044,7 @@ struct SrvPre {
         if (barrier) {
             if (threadIdx.x == 0) *verdict = srv_wait(dev, g, n, limit);
             __syncthreads();
+            SRV_STAMP(SRV_CMD(), 12 + stage);
             if (*verdict) return true;
         }
         if (norm_r) srv_rmsnorm(norm_r, norm_r2, norm_w, eps, H, rb, xnb, pbuf, sbuf);
@@ -1127,6 +1157,7 @@ __device__ __forceinline__ bool srv_rows(const SrvCmd &c, int B, uint4 *lds, con
     srv_activation<XL>(xt, x, B);
     xt.store(B, reinterpret_cast<uint32_t *>(planes), ub);
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 2 + 2 * c.stage);
 
     for (int L = wave * R; L < T; L += ROWS) {
         RowGroup<NBL, R, true, TAIL> nxt;
@@ -1144,6 +1175,7 @@ __device__ __forceinline__ bool srv_rows(const SrvCmd &c, int B, uint4 *lds, con
         else sp.load(grp, c, L + ROWS, B, row_bytes, lane);
     }
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 3 + 2 * c.stage);
     srv_store(sp, c, out);
     return true;
 }
@@ -1195,6 +1227,7 @@ __device__ __forceinline__ bool srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
     srv_activation<XL>(xt, x, B);
     q8_stage<XI>(xt, B, reinterpret_cast<uint32_t *>(Q), dxs, sxs);
     __syncthreads();
+    SRV_STAMP(SRV_CMD(), 2 + 2 * c.stage);
 
     for (int c0 = 0; c0 < T; c0 += chunk) {
         const int c1 = min(T, c0 + chunk);
@@ -1214,6 +1247,7 @@ __device__ __forceinline__ bool srv_rows_q8(const SrvCmd &c, int B, uint4 *lds, 
         }
         __syncthreads();  // csb is rewritten by the next chunk
     }
+    SRV_STAMP(SRV_CMD(), 3 + 2 * c.stage);
     srv_store(sp, c, out);
     return true;
 }
@@ -1307,6 +1341,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                     __builtin_amdgcn_s_sleep(2);
                 }
                 verdict = leave;
+                SRV_STAMP(expect, 0);
             }
             __syncthreads();
             if (verdict) {
@@ -1343,6 +1378,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             __builtin_amdgcn_s_waitcnt(0);  // every copy store has completed
             __syncthreads();  // and the record is in LDS
             if (threadIdx.x == 0) __hip_atomic_store(&dev->seq[0], expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            SRV_STAMP(expect, 1);
             if (cs.exit) return;
         } else {
             if (threadIdx.x == 0) {
@@ -1359,6 +1395,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                     __builtin_amdgcn_s_sleep(2);
                 }
                 verdict = leave;
+                SRV_STAMP(expect, 0);
             }
             __syncthreads();
             if (verdict) return;
@@ -1366,6 +1403,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             for (int i = threadIdx.x; i < kSrvCmdWords; i += blockDim.x)
                 csw[i] = __hip_atomic_load(&dcw[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __syncthreads();
+            SRV_STAMP(expect, 1);
             if (cs.exit) return;
         }
         // cs2 = cs, one word per thread, once every thread is done with the
@@ -1383,6 +1421,9 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
         // cooperative), inside the row functions, after the stage's first
         // rows were requested.  One call site per stage form keeps the
         // kernel's register count at that of one stage.
+#ifdef MI355X_SRV_STAMPS
+        if (threadIdx.x == 0) s_srv_cmd = expect;
+#endif
         const bool blk = cs.pre.N > 0;
         const int nst = blk ? (cs.post.N > 0 ? 4 : 3) : (cs.K2 ? 2 : 1);
         for (int st = 0; st < nst; ++st) {
@@ -1395,6 +1436,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                 pre.n = ++nbar;
                 pre.limit = 2 * idle_ticks;
                 pre.verdict = &verdict;
+                pre.stage = st;
             }
             // r = (pre x) + resid (resid after x in the payload, or in
             // resid_dev); the next stage's r = down h + r, added in the down
@@ -1413,6 +1455,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
             if (st > 0 || blk || cs.K2) {
                 copy_cmd();
                 if (threadIdx.x == 0) {
+                    cs2.stage = st;
                     if (blk && st == 0) {
                         // block: pre x into r_dev (the residual is added
                         // when every workgroup reads it back)
@@ -1459,6 +1502,7 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
         // a release fence writes back the whole L2, once per workgroup
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // also: LDS planes are rewritten by the next command
+        SRV_STAMP(expect, 10);
         if (threadIdx.x == 0) {
             const int gi = g & 7;
             const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
@@ -1469,8 +1513,12 @@ __global__ __launch_bounds__(64 * kSrvWaves) void gemv_q4_0_server_kernel(SrvCmd
                 const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
                 const uint64_t t =
                     __hip_atomic_fetch_add(&dev->top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-                if (t == n * groups) __hip_atomic_store(done, expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (t == n * groups) {
+                    __hip_atomic_store(done, expect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    SRV_STAMP(expect, 12);
+                }
             }
+            SRV_STAMP(expect, 11);
         }
     }
 }
@@ -2746,6 +2794,15 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
     if (rc == MI355X_OK) s.dres_h = H;
     return rc;
 }
+
+#ifdef MI355X_SRV_STAMPS
+// The phase-stamp table of the stamps build (64 commands x 256 workgroups x
+// kSrvStampSlots), for xdna.cpp_amd/server_phases.py; stop the server first.
+__attribute__((visibility("default"))) int mi355x_server_stamps(uint64_t *out) {
+    const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(mi355x::g_srv_stamps), sizeof(mi355x::g_srv_stamps));
+    return e == hipSuccess ? MI355X_OK : hip_error(e, "mi355x_server_stamps");
+}
+#endif
 
 int mi355x_server_stop(mi355x_server *srv) {
     clear_error();
