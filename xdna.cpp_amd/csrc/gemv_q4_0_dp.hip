@@ -769,6 +769,10 @@ struct SrvDev {
     uint64_t bar_group[8][16];
     uint64_t bar_top[16];
     uint32_t bar_flag[8][32];
+    // the same barrier as one slot per workgroup (kSrvBarSlots workgroups at
+    // most): each workgroup stores its barrier count, one wavefront reads
+    // them all
+    uint32_t bar_slot[1024];
     SrvCmd cmd;  // copy of the current command record
 };
 
@@ -936,6 +940,42 @@ __device__ __forceinline__ void srv_arrive(SrvDev *dev, int g, int G, uint64_t n
     }
 }
 
+// The slot form of the barrier: a workgroup's arrival is one store of its
+// barrier count into its own word (no atomics to serialise), and wavefront 0
+// waits until every word of the grid has reached the count, reading all of
+// them (4 per lane, system-coherent loads) per poll.  Used when the grid has
+// at most kSrvBarSlots workgroups.
+constexpr int kSrvBarSlots = 1024;
+__device__ __forceinline__ void srv_arrive_slot(SrvDev *dev, int g, uint64_t n) {
+    __hip_atomic_store(&dev->bar_slot[g], static_cast<uint32_t>(n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// wavefront 0 of the workgroup (all its lanes); returns 1 as srv_wait does
+__device__ __forceinline__ uint32_t srv_wait_slot(SrvDev *dev, int G, uint64_t n, uint64_t limit) {
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(dev->bar_slot, 0, static_cast<uint32_t>(4 * G), kBufferWord3);
+    const uint32_t want = static_cast<uint32_t>(n);
+    const uint64_t t0 = srv_clock();
+    for (;;) {
+        bool ok = true;
+        for (int i = 4 * lane; i < G; i += 256) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * i, 0, kSysCoherent);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = v[e];
+                ok = ok && (i + e >= G || static_cast<int32_t>(u - want) >= 0);
+            }
+        }
+        if (__all(ok)) return 0;
+        if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 || srv_clock() - t0 > limit) {
+            if (lane == 0) __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return 1;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 __device__ __forceinline__ uint32_t srv_wait(SrvDev *dev, int g, uint64_t n, uint64_t limit) {
     const int gi = g & 7;
     const uint64_t t0 = srv_clock();
@@ -1037,12 +1077,22 @@ struct SrvPre {
         if (!barrier) return;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (threadIdx.x == 0) srv_arrive(dev, g, G, n);
+        if (threadIdx.x == 0) {
+            if (G <= kSrvBarSlots) srv_arrive_slot(dev, g, n);
+            else srv_arrive(dev, g, G, n);
+        }
     }
     // true: leave (the barrier timed out or quit was raised)
     __device__ __forceinline__ bool wait() const {
         if (barrier) {
-            if (threadIdx.x == 0) *verdict = srv_wait(dev, g, n, limit);
+            if (G <= kSrvBarSlots) {
+                if (threadIdx.x < 64) {
+                    const uint32_t v = srv_wait_slot(dev, G, n, limit);
+                    if (threadIdx.x == 0) *verdict = v;
+                }
+            } else if (threadIdx.x == 0) {
+                *verdict = srv_wait(dev, g, n, limit);
+            }
             __syncthreads();
             SRV_STAMP(SRV_CMD(), 12 + stage);
             if (*verdict) return true;
