@@ -35,6 +35,9 @@
  *                                            reference takes from ggml-cpu when it
  *                                            is loaded (src/xdna-gemv-engine.cpp:
  *                                            1382-1399)
+ *   ggml_backend_mi355x_set_group_mode       no counterpart: how graph_compute runs
+ *                                            a group of single-row MUL_MATs whose
+ *                                            activation and outputs are host-resident
  *
  * The compatibility API takes host pointers in `data` (like the reference's
  * harness); ggml graphs handed to graph_compute hold device pointers of
@@ -111,6 +114,23 @@ GGML_MI355X_API int ggml_backend_mi355x_load_iq_grids_from_ggml(void);
  * GEMVs; also reachable through the registry's get_proc_address.  False for a
  * backend of another type or an unknown variant. */
 GGML_MI355X_API bool ggml_backend_mi355x_set_kernel_variant(struct ggml_backend *backend, int variant);
+/* Small tensors of the plugin's non-weight buffers (an activation row, a
+ * group's outputs) stay in a page-locked host shadow of the buffer once the
+ * host writes them or a single-row MUL_MAT outputs them, so a decode step
+ * moves them with memcpy instead of copy commands.  graph_compute runs a
+ * group of consecutive single-row MUL_MATs that share such an activation,
+ * with every output host-resident, as
+ *   GGML_MI355X_GROUPS_SERVER (default): Q4_0 rows of a multiple of 256
+ *     values (up to 16384) as one command to the backend's persistent GEMV
+ *     server (mi355x_server_gemv: no launch; returns with the outputs in the
+ *     shadow); other groups as GGML_MI355X_GROUPS_LAUNCH;
+ *   GGML_MI355X_GROUPS_LAUNCH: one launch reading and writing the shadow
+ *     through its device address, then a wait on a completion word.
+ * Either way graph_compute returns after every kernel that touches a shadow
+ * has finished.  False for a backend of another type or an unknown mode. */
+#define GGML_MI355X_GROUPS_SERVER 0
+#define GGML_MI355X_GROUPS_LAUNCH 1
+GGML_MI355X_API bool ggml_backend_mi355x_set_group_mode(struct ggml_backend *backend, int mode);
 
 #ifdef __cplusplus
 }

@@ -58,12 +58,39 @@ extern "C" {
 
 typedef struct mi355x_ctx mi355x_ctx; /* one device + one HIP stream */
 
+/* Device id of a host-only context (mi355x_ctx_create): bound to no GPU, it
+ * needs no HIP device.  Options can be set on it; every entry point that
+ * would reach a device fails before doing so, as a lost device would: it
+ * returns MI355X_EHIP with "<entry>: hipErrorNoDevice (...) [host-only
+ * context]".  For running the device-error paths of host code (the ggml
+ * plugin's) on machines without a GPU.  No counterpart in the reference,
+ * whose engine without hardware computes on the CPU instead
+ * (src/xdna-gemv-engine.cpp:1738-1749). */
+#define MI355X_DEVICE_HOST_ONLY (-1)
+
 /* Message of the last failing call on this thread ("" if none). */
 MI355X_API const char *mi355x_last_error(void);
 
+/* Fault injection for tests: no GPU fault and no device needed.  No
+ * counterpart in the reference, whose engine reports device failures by
+ * throwing and whose plugin turns that into GGML_STATUS_FAILED
+ * (src/ggml-xdna.cpp:299-305, 803-807).  After `skip` more calls that reach
+ * it, the next call of the entry point named `entry` ("mi355x_gemv",
+ * "mi355x_gemv_multi", "mi355x_memcpy_h2d", "mi355x_ctx_fence",
+ * "mi355x_server_gemv", ...; "*" for any entry point that would reach a
+ * device) fails before any device work, as if HIP had returned `hip_error`
+ * (a hipError_t value): MI355X_EHIP (MI355X_ENOMEM for hipErrorOutOfMemory)
+ * with mi355x_last_error() = "<entry>: <hipErrorName> (<hipErrorString>)
+ * [injected]".  One fault at a time, process-wide, disarmed once it fired;
+ * entry NULL disarms.  The environment variable
+ * MI355X_INJECT_FAULT="<entry>:<hip_error>[:<skip>]" arms one at first use
+ * of the library. */
+MI355X_API int mi355x_inject_fault(const char *entry, int hip_error, int skip);
+
 /* ---- devices and contexts ------------------------------------------------ */
 MI355X_API int mi355x_device_count(int *count);
-/* Creates a context on `device` with its own non-blocking HIP stream. */
+/* Creates a context on `device` with its own non-blocking HIP stream
+ * (MI355X_DEVICE_HOST_ONLY: a host-only context, see above). */
 MI355X_API int mi355x_ctx_create(int device, mi355x_ctx **out);
 MI355X_API void mi355x_ctx_destroy(mi355x_ctx *ctx);
 /* Waits for all work queued on the context's stream. */
@@ -169,6 +196,9 @@ MI355X_API int mi355x_free(mi355x_ctx *ctx, void *dptr);
 /* Page-locked host memory (hipHostMalloc) for staging transfers. */
 MI355X_API int mi355x_host_malloc(size_t bytes, void **hptr);
 MI355X_API int mi355x_host_free(void *hptr);
+/* The device address of page-locked host memory from mi355x_host_malloc
+ * (kernels read and write it over PCIe), for any byte inside it. */
+MI355X_API int mi355x_host_device_ptr(const void *hptr, void **dptr);
 MI355X_API int mi355x_memcpy_h2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2h(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);
 MI355X_API int mi355x_memcpy_d2d(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes);

@@ -111,7 +111,14 @@ def bind_compat(lib):
     lib.ggml_backend_mi355x_set_op_mul_mat.restype = C.c_bool
     lib.ggml_backend_mi355x_set_op_mul_mat.argtypes = [C.c_int]
     lib.ggml_backend_mi355x_load_iq_grids_from_ggml.restype = C.c_int
+    lib.ggml_backend_mi355x_set_kernel_variant.restype = C.c_bool
+    lib.ggml_backend_mi355x_set_kernel_variant.argtypes = [C.c_void_p, C.c_int]
+    lib.ggml_backend_mi355x_set_group_mode.restype = C.c_bool
+    lib.ggml_backend_mi355x_set_group_mode.argtypes = [C.c_void_p, C.c_int]
     return lib
+
+GROUPS_SERVER, GROUPS_LAUNCH = 0, 1
+USAGE_ANY, USAGE_WEIGHTS, USAGE_COMPUTE = 0, 1, 2
 
 _P = C.c_void_p
 # (slot index, restype, argtypes) of every vtable entry the host calls
@@ -286,6 +293,10 @@ class Buffer:
         dst = (C.c_uint8 * nbytes)()
         self.call("get_tensor", C.addressof(t), C.addressof(dst), offset, nbytes)
         return bytes(dst)
+
+    def set_usage(self, usage):
+        """ggml_backend_buffer_set_usage: the field after size."""
+        C.c_int.from_address(self.addr + BUF_SLOTS * C.sizeof(C.c_void_p) + 24).value = usage
 
     def free(self):
         if self.addr:

@@ -807,6 +807,40 @@ def test_gemv_q4_0_q8_0_against_f32_path_on_dequantized_activation(oracle):
     assert np.all(np.abs(y8 - y32) <= 2e-2 * norms * np.linalg.norm(x))
 
 
+def test_q8_0_ties_round_half_away_from_zero(oracle):
+    # exact halves of odd and even k, both signs, at d_x = 1 and d_x = 0.5:
+    # ggml's quantize_row_q8_0 uses roundf (2.5 -> 3, -2.5 -> -3), so a
+    # round-half-to-even quantizer (rintf) fails here
+    import ggml_q8_cases as gq
+
+    q = oracle.quantize_q8_0(gq.activation()).reshape(-1, 34)
+    codes = q[:, 2:].view(np.int8).astype(np.int32)
+    d16 = q[:, 0:2].copy().view(np.uint16).reshape(-1)
+    for b, want in enumerate(gq.expected_codes()):
+        assert list(codes[b]) == want, (b, list(codes[b]))
+    assert list(d16[:7]) == [0x3C00, 0x3800, 0x3C00, 0x3C00, 0x3C00, 0x3C00, 0x3A00]  # 1, 0.5, 1 x 4, 0.75
+    assert list(codes[6]) == [127] * 31 + [3]
+    rint = np.rint(np.array(gq.B0_X, np.float64)).astype(np.int32)
+    assert not np.array_equal(rint, codes[0])       # the case tells the two rules apart
+
+
+def test_gemv_q4_0_q8_0_product_order_and_block_order(oracle):
+    """ggml_vec_dot_q4_0_q8_0 forms sumi * d_w * d_x = (sumi * d_w) * d_x and
+    adds the blocks to one f32 sum in block order.  Rows 0..63 read single
+    Q8_0 codes, row 64 has block terms 2^24, 1, 1, -2^24 (0 in order; 2
+    reversed, 1 pairwise), row 65 a product whose two associations differ
+    in f32 (tests/ggml_q8_cases.py)."""
+    import ggml_q8_cases as gq
+
+    y = oracle.gemv_q4_0_q8_0(gq.weights(), gq.N, gq.K, gq.activation())
+    want = gq.expected_y()
+    bad = np.nonzero(y.view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, (bad, y[bad], want[bad])
+    # every plausible mistake gives a different row somewhere
+    for name, alt in gq.alternatives().items():
+        assert not np.array_equal(alt.view(np.uint32), want.view(np.uint32)), name
+
+
 def test_gemv_q4_0_q8_0_known_answer(oracle):
     # codes 9 (+1) with d = 1 against x = 1: Q8_0 gives d_x = fp16(1/127),
     # q = 127, so each block adds 32 * 127 * fp16(1/127)

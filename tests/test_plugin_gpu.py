@@ -579,3 +579,35 @@ def test_kq_batched_rows_through_plugin(plugin, oracle, name):
             check_gemv(y[m], oracle.gemv(t, raw, N, K, xs[m]), norms, xs[m], f"{name} row {m}")
     finally:
         buf.free()
+
+
+@pytest.mark.parametrize("group_mode,entry,nodes", [(gh.GROUPS_LAUNCH, "mi355x_gemv", 1),
+                                                    (gh.GROUPS_LAUNCH, "mi355x_gemv_multi", 2),
+                                                    (gh.GROUPS_SERVER, "mi355x_server_gemv", 2)])
+def test_injected_device_error_fails_the_graph_then_recovers(plugin, oracle, group_mode, entry, nodes):
+    """A HIP error on the real device (injected at the C-ABI before any
+    device work, so no GPU fault) makes graph_compute return
+    GGML_STATUS_FAILED (src/ggml-xdna.cpp:299-305, 803-807); the next graph
+    on the same backend computes the right answer."""
+    N, K = 256, 2048
+    raw = synth.random_q4_0(N, K, seed=5)
+    x = synth.activations(K, seed=6)
+    buf = plugin.buft.alloc(N * RB(K) + 4 * (K + 2 * N) + 4 * 256)
+    try:
+        w = weight_tensor(buf, raw, N, K)
+        xt = f32_tensor(buf, x, [K, 1])
+        ds = [gh.mul_mat(w, xt, [N, 1], name=f"d{i}".encode()) for i in range(nodes)]
+        for d in ds:
+            buf.place(d, 4 * N)
+        assert plugin.lib.ggml_backend_mi355x_set_group_mode(plugin.backend.addr, group_mode)
+        mi355x.inject_fault(entry, mi355x.HIP_ERROR_LAUNCH_FAILURE)
+        assert plugin.backend.compute(ds) == gh.STATUS_FAILED
+        assert plugin.backend.compute(ds) == gh.STATUS_SUCCESS
+        plugin.backend.call("synchronize")
+        ref = oracle.gemv(Q4_0, raw, N, K, x)
+        for d in ds:
+            check_gemv(read_f32(buf, d, N), ref, oracle.row_norms(Q4_0, raw, N, K), x, "after the injected error")
+    finally:
+        mi355x.inject_fault(None)
+        plugin.lib.ggml_backend_mi355x_set_group_mode(plugin.backend.addr, gh.GROUPS_SERVER)
+        buf.free()

@@ -764,14 +764,9 @@ struct SrvDev {
     uint32_t quit[32];
     uint64_t group[8][16];
     uint64_t top[16];
-    // grid barrier of SwiGLU commands: arrivals per group, then on the top
-    // counter; the last arrival raises every group's flag
-    uint64_t bar_group[8][16];
-    uint64_t bar_top[16];
-    uint32_t bar_flag[8][32];
-    // the same barrier as one slot per workgroup (kSrvBarSlots workgroups at
-    // most): each workgroup stores its barrier count, one wavefront reads
-    // them all
+    // grid barrier of multi-stage commands, one slot per workgroup (the
+    // host refuses grids of more than kSrvBarSlots workgroups): each
+    // workgroup stores its barrier count, one wavefront reads them all
     uint32_t bar_slot[1024];
     SrvCmd cmd;  // copy of the current command record
 };
@@ -919,38 +914,23 @@ struct SrvSpan {
     }
 };
 
-// Grid barrier inside a command (thread 0 of every workgroup: arrive, then
-// wait; `n` = barriers this launch has passed, this one included).  256 arrivals on one counter
-// serialise (~25 ns each, measured); in two levels, as the completion count,
-// each counter takes at most 32, and the pollers read their group's flag
-// line, not a counter line that takes atomics.  Bounded like every wait:
-// srv_wait returns 1 (and raises quit) after `limit` ticks or when quit is
-// raised.
-__device__ __forceinline__ void srv_arrive(SrvDev *dev, int g, int G, uint64_t n) {
-    const int gi = g & 7;
-    const uint64_t members = static_cast<uint64_t>((G - gi + 7) / 8);
-    const uint64_t a = __hip_atomic_fetch_add(&dev->bar_group[gi][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-    if (a == n * members) {
-        const uint64_t groups = static_cast<uint64_t>(G < 8 ? G : 8);
-        const uint64_t t = __hip_atomic_fetch_add(&dev->bar_top[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-        if (t == n * groups)
-            for (int i = 0; i < static_cast<int>(groups); ++i)
-                __hip_atomic_store(&dev->bar_flag[i][0], static_cast<uint32_t>(n), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-// The slot form of the barrier: a workgroup's arrival is one store of its
-// barrier count into its own word (no atomics to serialise), and wavefront 0
-// waits until every word of the grid has reached the count, reading all of
-// them (4 per lane, system-coherent loads) per poll.  Used when the grid has
-// at most kSrvBarSlots workgroups.
+// Grid barrier inside a command (`n` = barriers this launch has passed, this
+// one included).  A workgroup's arrival is one store of its barrier count
+// into its own word (256 arrivals on one atomic counter serialised at ~25 ns
+// each, measured), and wavefront 0 of every workgroup waits until every
+// word of the grid has reached the count, reading all of them (4 per lane,
+// system-coherent loads) per poll.  The arrival is ordered after the
+// workgroup's stores of the stage by s_waitcnt(0) + __syncthreads() (the
+// stores are write-through at system scope: acknowledged once memory holds
+// them), not by a release fence, which would write back the whole L2.
+// Bounded like every wait: srv_wait_slot returns 1 (and raises quit) after
+// `limit` ticks or when quit is raised.
 constexpr int kSrvBarSlots = 1024;
 __device__ __forceinline__ void srv_arrive_slot(SrvDev *dev, int g, uint64_t n) {
     __hip_atomic_store(&dev->bar_slot[g], static_cast<uint32_t>(n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// wavefront 0 of the workgroup (all its lanes); returns 1 as srv_wait does
+// wavefront 0 of the workgroup (all its lanes); 0 once every slot reached n
 __device__ __forceinline__ uint32_t srv_wait_slot(SrvDev *dev, int G, uint64_t n, uint64_t limit) {
     const int lane = threadIdx.x & 63;
     const __amdgpu_buffer_rsrc_t rs =
@@ -974,20 +954,6 @@ __device__ __forceinline__ uint32_t srv_wait_slot(SrvDev *dev, int G, uint64_t n
         }
         __builtin_amdgcn_s_sleep(1);
     }
-}
-
-__device__ __forceinline__ uint32_t srv_wait(SrvDev *dev, int g, uint64_t n, uint64_t limit) {
-    const int gi = g & 7;
-    const uint64_t t0 = srv_clock();
-    while (static_cast<int32_t>(__hip_atomic_load(&dev->bar_flag[gi][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                                static_cast<uint32_t>(n)) < 0) {
-        if (__hip_atomic_load(&dev->quit[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 || srv_clock() - t0 > limit) {
-            __hip_atomic_store(&dev->quit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return 1;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return 0;
 }
 
 // RMSNorm of the block command, every workgroup for itself: r (H floats,
@@ -1077,21 +1043,14 @@ struct SrvPre {
         if (!barrier) return;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (threadIdx.x == 0) {
-            if (G <= kSrvBarSlots) srv_arrive_slot(dev, g, n);
-            else srv_arrive(dev, g, G, n);
-        }
+        if (threadIdx.x == 0) srv_arrive_slot(dev, g, n);
     }
     // true: leave (the barrier timed out or quit was raised)
     __device__ __forceinline__ bool wait() const {
         if (barrier) {
-            if (G <= kSrvBarSlots) {
-                if (threadIdx.x < 64) {
-                    const uint32_t v = srv_wait_slot(dev, G, n, limit);
-                    if (threadIdx.x == 0) *verdict = v;
-                }
-            } else if (threadIdx.x == 0) {
-                *verdict = srv_wait(dev, g, n, limit);
+            if (threadIdx.x < 64) {
+                const uint32_t v = srv_wait_slot(dev, G, n, limit);
+                if (threadIdx.x == 0) *verdict = v;
             }
             __syncthreads();
             SRV_STAMP(SRV_CMD(), 12 + stage);
@@ -2494,8 +2453,9 @@ namespace {
 struct DeviceScope {
     int prev = -1;
     explicit DeviceScope(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
+        // a host-only context (device < 0) touches no device
+        if (dev < 0 || hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (dev >= 0 && prev != dev) (void)hipSetDevice(dev);
     }
     ~DeviceScope() {
         int cur = -1;
@@ -2663,6 +2623,7 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
     *out = nullptr;
     if (max_k <= 0 || max_k % 256 != 0 || max_k > 64 * 8 * 32)
         return set_error(MI355X_EINVAL, "mi355x_server_create: max_k must be a multiple of 256 up to 16384");
+    if (const int rc = mi355x::device_gate(ctx, "mi355x_server_create")) return rc;
     mi355x::DeviceScope dg(ctx->device);
     int coop = 0;
     MI355X_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device));
@@ -2716,6 +2677,10 @@ int mi355x_server_create(mi355x_ctx *ctx, int64_t max_k, mi355x_server **out) {
                                : set_error(MI355X_EUNSUPPORTED, "mi355x_server_create: kernel does not fit a CU");
     }
     s.grid = ctx->num_cus;
+    if (s.grid > mi355x::kSrvBarSlots) {
+        mi355x_server_destroy(srv);
+        return set_error(MI355X_EUNSUPPORTED, "mi355x_server_create: more CUs than the grid barrier has slots");
+    }
     {
         std::lock_guard<std::mutex> lk(mi355x::g_srv_mu);
         mi355x::g_servers.push_back(srv);
@@ -2751,6 +2716,7 @@ int mi355x_server_gemv(mi355x_server *srv, const float *x, int64_t K, int njobs,
     c.njobs = njobs;
     c.mode = mode;
     for (int j = 0; j < njobs; ++j) c.jobs[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].y, jobs[j].N};
+    if (const int grc = mi355x::device_gate(s.ctx, "mi355x_server_gemv")) return grc;
     return mi355x::server_submit(s, x, K, nullptr, 0, c, "mi355x_server_gemv");
 }
 
@@ -2783,6 +2749,7 @@ int mi355x_server_swiglu(mi355x_server *srv, const float *x, int64_t K, const vo
     c.K2 = static_cast<int32_t>(F);
     c.h = s.dh;
     c.down = {static_cast<const uint8_t *>(W_down), y, N};
+    if (const int grc = mi355x::device_gate(s.ctx, "mi355x_server_swiglu")) return grc;
     return mi355x::server_submit(s, x, K, nullptr, 0, c, "mi355x_server_swiglu");
 }
 
@@ -2839,6 +2806,7 @@ int mi355x_server_block(mi355x_server *srv, const float *x, int64_t K, const voi
         c.post = {static_cast<const uint8_t *>(W_next), y_next, N_next};
         c.post_norm_w = next_norm_w;
     }
+    if (const int grc = mi355x::device_gate(s.ctx, "mi355x_server_block")) return grc;
     s.dres_h = 0;  // set again once the command completed
     const int rc = mi355x::server_submit(s, x, K, resid, resid ? H : 0, c, "mi355x_server_block");
     if (rc == MI355X_OK) s.dres_h = H;

@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <new>
@@ -244,6 +245,39 @@ struct DevCtx {
         if (!xfer && mi355x_ctx_create(device, &xfer) != MI355X_OK) xfer = nullptr;
         return xfer;
     }
+
+    // The device's persistent GEMV server, shared by its backends (one
+    // resident kernel per device: it holds every CU), on a context of its
+    // own whose variant is set per command; made on first use.  While it is
+    // resident a launched GEMV kernel would find no room on the CUs until
+    // the server's idle exit, so the launch paths stop it first.
+    std::mutex srv_mu;
+    mi355x_ctx *srv_ctx = nullptr;
+    mi355x_server *srv = nullptr;
+    bool srv_failed = false;
+    bool srv_active = false;  // a command ran since the last stop
+    int backends = 0;         // live backends on the device (mu)
+    static constexpr int64_t kServerMaxK = 16384;
+
+    mi355x_server *server() {  // srv_mu held
+        if (!srv && !srv_failed) {
+            if (mi355x_ctx_create(device, &srv_ctx) != MI355X_OK ||
+                mi355x_server_create(srv_ctx, kServerMaxK, &srv) != MI355X_OK) {
+                srv = nullptr;
+                srv_failed = true;
+            }
+        }
+        return srv;
+    }
+    // Before a launch on this device: the server leaves the CUs.
+    void yield_cus() {
+        std::lock_guard<std::mutex> lk(srv_mu);
+        if (srv && srv_active) {
+            if (mi355x_server_stop(srv) != MI355X_OK)
+                std::fprintf(stderr, "[mi355x error] server stop: %s\n", mi355x_last_error());
+            srv_active = false;
+        }
+    }
 };
 
 ggml_backend_reg g_reg{};
@@ -260,16 +294,160 @@ DevCtx *buft_dev(ggml_backend_buffer_type_t buft) {
 // ---------------------------------------------------------------------------
 // device buffer (HBM)
 // ---------------------------------------------------------------------------
+// Disjoint byte ranges [start, end) of a buffer, merged where they touch.
+class RangeSet {
+  public:
+    bool empty() const { return r_.empty(); }
+    void clear() { r_.clear(); }
+    // [a, b) lies inside one range
+    bool covers(size_t a, size_t b) const {
+        if (a >= b) return true;
+        auto it = r_.upper_bound(a);
+        if (it == r_.begin()) return false;
+        --it;
+        return it->second >= b;
+    }
+    // some byte of [a, b) lies in a range
+    bool touches(size_t a, size_t b) const {
+        if (a >= b || r_.empty()) return false;
+        auto it = r_.lower_bound(b);
+        if (it == r_.begin()) return false;
+        --it;
+        return it->second > a;
+    }
+    void remove(size_t a, size_t b) {
+        if (a >= b) return;
+        auto it = r_.upper_bound(a);
+        if (it != r_.begin()) {
+            auto p = std::prev(it);
+            if (p->first < a && p->second > a) {
+                const size_t end = p->second;
+                p->second = a;
+                if (end > b) {
+                    r_.emplace(b, end);
+                    return;
+                }
+            }
+        }
+        it = r_.lower_bound(a);
+        while (it != r_.end() && it->first < b) {
+            if (it->second > b) {
+                const size_t end = it->second;
+                r_.erase(it);
+                r_.emplace(b, end);
+                return;
+            }
+            it = r_.erase(it);
+        }
+    }
+    void add(size_t a, size_t b) {
+        if (a >= b) return;
+        remove(a, b);
+        auto it = r_.emplace(a, b).first;
+        if (it != r_.begin()) {
+            auto p = std::prev(it);
+            if (p->second == a) {
+                p->second = b;
+                r_.erase(it);
+                it = p;
+            }
+        }
+        auto n = std::next(it);
+        if (n != r_.end() && n->first == it->second) {
+            it->second = n->second;
+            r_.erase(n);
+        }
+    }
+    // the parts of [a, b) that lie in ranges, in order
+    std::vector<std::pair<size_t, size_t>> parts(size_t a, size_t b) const {
+        std::vector<std::pair<size_t, size_t>> out;
+        if (a >= b) return out;
+        auto it = r_.upper_bound(a);
+        if (it != r_.begin()) --it;
+        for (; it != r_.end() && it->first < b; ++it) {
+            const size_t lo = std::max(a, it->first), hi = std::min(b, it->second);
+            if (lo < hi) out.emplace_back(lo, hi);
+        }
+        return out;
+    }
+
+  private:
+    std::map<size_t, size_t> r_;  // start -> end
+};
+
+// Host-resident ranges of a device buffer.  A decode step hands the device
+// one activation row (a few KB) per group of MUL_MATs and takes the group's
+// outputs back; a copy command each way costs more than the GEMV itself.  A
+// buffer that does not hold weights (ggml's compute and KV buffers) therefore
+// gets a page-locked host shadow of its own size on first use, and the
+// bytes of tensors of at most kMirrorMax bytes that the host writes
+// (set_tensor, memset) or a single-row MUL_MAT outputs live there: their
+// range of the buffer is "host-resident".  GEMV kernels read activations from
+// and write outputs to the shadow through its device address (the persistent
+// server takes the activation from the shadow directly), and get_tensor reads
+// it with a memcpy.  The device bytes of a host-resident range are stale: any
+// access that needs them (a larger or strided MUL_MAT, a device-to-device
+// copy, reads of prepacked tensors) first copies the range to the device and
+// drops it from the set.  Every path that reads or writes a buffer's bytes
+// goes through this file, so the set is the whole truth.
+constexpr size_t kMirrorMax = size_t(1) << 20;
+constexpr size_t kShadowMaxBuffer = size_t(256) << 20;
+
 struct BufCtx {
     DevCtx *dc = nullptr;
     void *base = nullptr;  // device pointer (or pinned host pointer)
     size_t size = 0;
     bool host = false;
     bool own_struct = false;  // ggml_backend_buffer allocated here (no ggml-base)
+    std::mutex smu;           // shadow, shadow_dev, resident
+    uint8_t *shadow = nullptr;      // page-locked host copy, made on first use
+    uint8_t *shadow_dev = nullptr;  // its device address
+    bool shadow_failed = false;
+    RangeSet resident;  // host-resident byte ranges (offsets into the buffer)
+
+    size_t off(const void *p) const {
+        return static_cast<size_t>(static_cast<const uint8_t *>(p) - static_cast<const uint8_t *>(base));
+    }
 };
 
 void log_error(const char *what) {
     std::fprintf(stderr, "[mi355x error] %s: %s\n", what, mi355x_last_error());
+}
+
+// The shadow of a buffer that may hold host-resident ranges, made on first
+// use (smu held): none for host buffers, weight buffers and buffers larger
+// than kShadowMaxBuffer.
+bool shadow_ready(ggml_backend_buffer_t buffer, BufCtx *bc) {
+    if (bc->shadow) return true;
+    if (bc->host || bc->shadow_failed || bc->size > kShadowMaxBuffer ||
+        buffer->usage == GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+        return false;
+    void *h = nullptr, *d = nullptr;
+    if (mi355x_host_malloc(bc->size, &h) != MI355X_OK || mi355x_host_device_ptr(h, &d) != MI355X_OK) {
+        if (h) mi355x_host_free(h);
+        bc->shadow_failed = true;
+        return false;
+    }
+    bc->shadow = static_cast<uint8_t *>(h);
+    bc->shadow_dev = static_cast<uint8_t *>(d);
+    return true;
+}
+
+// Copies the host-resident parts of [a, b) to the device with `x` and drops
+// them from the set (smu held).  False if a copy failed (that part stays
+// host-resident).
+bool materialise(BufCtx *bc, mi355x_ctx *x, size_t a, size_t b) {
+    bool ok = true;
+    for (const auto &p : bc->resident.parts(a, b)) {
+        if (mi355x_memcpy_h2d(x, static_cast<uint8_t *>(bc->base) + p.first, bc->shadow + p.first,
+                              p.second - p.first) != MI355X_OK) {
+            log_error("materialise host-resident range");
+            ok = false;
+            continue;
+        }
+        bc->resident.remove(p.first, p.second);
+    }
+    return ok;
 }
 
 // The base tensor whose rows define the resident layout of `t`'s bytes.
@@ -294,6 +472,7 @@ void buf_free(ggml_backend_buffer_t buffer) {
     } else if (mi355x_ctx *x = bc->dc->transfer_ctx()) {
         mi355x_free(x, bc->base);
     }
+    if (bc->shadow) mi355x_host_free(bc->shadow);
     const bool own = bc->own_struct;
     delete bc;
     buffer->context = nullptr;
@@ -333,6 +512,54 @@ void download(mi355x_ctx *x, const ggml_tensor *tensor, void *data, size_t offse
     if (mi355x_memcpy_d2h(x, data, src, size)) log_error("get_tensor");
 }
 
+// A tensor whose bytes may be host-resident: not prepacked, at most
+// kMirrorMax bytes.
+bool mirrorable(const ggml_tensor *t) { return !prepacked(t) && tensor_nbytes(t) <= kMirrorMax; }
+
+// The byte range a write to `t` may change in the device bytes: exactly
+// [offset, offset + size) of t, or, for prepacked tensors (a row-local
+// permutation), the whole base tensor.
+std::pair<size_t, size_t> device_span(const BufCtx *bc, const ggml_tensor *t, size_t offset, size_t size) {
+    if (prepacked(t)) {
+        const ggml_tensor *b = layout_base(t);
+        const size_t a = bc->off(b->data);
+        return {a, a + tensor_nbytes(b)};
+    }
+    const size_t a = bc->off(t->data) + offset;
+    return {a, a + size};
+}
+
+// Host write of [offset, offset + size) of a mirrorable tensor into the
+// shadow (the range becomes host-resident); false if the buffer has no
+// shadow (the caller writes the device).
+bool write_host_resident(ggml_backend_buffer_t buffer, BufCtx *bc, ggml_tensor *t, const void *data, size_t offset,
+                         size_t size) {
+    if (!mirrorable(t)) return false;
+    std::lock_guard<std::mutex> lk(bc->smu);
+    if (!shadow_ready(buffer, bc)) return false;
+    const size_t a = bc->off(t->data) + offset;
+    std::memcpy(bc->shadow + a, data, size);
+    bc->resident.add(a, a + size);
+    return true;
+}
+
+// After a device write of (part of) `t`: its device bytes are current.
+void device_written(BufCtx *bc, const ggml_tensor *t, size_t offset, size_t size) {
+    std::lock_guard<std::mutex> lk(bc->smu);
+    if (bc->resident.empty()) return;
+    const auto sp = device_span(bc, t, offset, size);
+    bc->resident.remove(sp.first, sp.second);
+}
+
+// Before a device read of (part of) `t`: copies its host-resident bytes to
+// the device with `x`.
+bool device_current(BufCtx *bc, mi355x_ctx *x, const ggml_tensor *t, size_t offset, size_t size) {
+    std::lock_guard<std::mutex> lk(bc->smu);
+    if (bc->resident.empty()) return true;
+    const auto sp = device_span(bc, t, offset, size);
+    return materialise(bc, x, sp.first, sp.second);
+}
+
 void buf_set_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, const void *data, size_t offset,
                     size_t size) {
     if (!buffer || !tensor || !tensor->data || !data || size == 0) return;
@@ -341,9 +568,12 @@ void buf_set_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, const voi
         std::memcpy(static_cast<uint8_t *>(tensor->data) + offset, data, size);
         return;
     }
+    if (write_host_resident(buffer, bc, tensor, data, offset, size)) return;
     mi355x_ctx *x = bc->dc->transfer_ctx();
     if (!x) return log_error("set_tensor: no device context");
+    if (prepacked(tensor)) bc->dc->yield_cus();  // the scatter kernel needs CUs
     upload(x, tensor, data, offset, size);
+    device_written(bc, tensor, offset, size);
 }
 
 void buf_get_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *tensor, void *data, size_t offset,
@@ -355,7 +585,26 @@ void buf_get_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *tensor, voi
         return;
     }
     mi355x_ctx *x = bc->dc->transfer_ctx();
+    if (!prepacked(tensor)) {
+        const size_t a = bc->off(tensor->data) + offset;
+        {
+            std::lock_guard<std::mutex> lk(bc->smu);
+            if (bc->resident.covers(a, a + size)) {
+                std::memcpy(data, bc->shadow + a, size);
+                return;
+            }
+        }
+        if (!x) return log_error("get_tensor: no device context");
+        // device bytes, then the host-resident parts over them
+        download(x, tensor, data, offset, size);
+        std::lock_guard<std::mutex> lk(bc->smu);
+        for (const auto &p : bc->resident.parts(a, a + size))
+            std::memcpy(static_cast<uint8_t *>(data) + (p.first - a), bc->shadow + p.first, p.second - p.first);
+        return;
+    }
     if (!x) return log_error("get_tensor: no device context");
+    device_current(bc, x, tensor, offset, size);
+    bc->dc->yield_cus();  // the gather kernel needs CUs
     download(x, tensor, data, offset, size);
 }
 
@@ -368,6 +617,15 @@ void buf_memset_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, uint8_
         std::memset(dst, value, size);
         return;
     }
+    if (mirrorable(tensor)) {
+        std::lock_guard<std::mutex> lk(bc->smu);
+        if (shadow_ready(buffer, bc)) {
+            const size_t a = bc->off(tensor->data) + offset;
+            std::memset(bc->shadow + a, value, size);
+            bc->resident.add(a, a + size);
+            return;
+        }
+    }
     if (prepacked(tensor)) {
         // fill the ggml bytes with `value` through the prepack permutation
         const size_t chunk = std::min<size_t>(size, size_t(16) << 20);
@@ -377,7 +635,8 @@ void buf_memset_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, uint8_
         return;
     }
     mi355x_ctx *x = bc->dc->transfer_ctx();
-    if (!x || mi355x_fill(x, dst, value, size) || mi355x_ctx_sync(x)) log_error("memset_tensor");
+    if (!x || mi355x_fill(x, dst, value, size) || mi355x_ctx_sync(x)) return log_error("memset_tensor");
+    device_written(bc, tensor, offset, size);
 }
 
 bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *src, ggml_tensor *dst) {
@@ -393,7 +652,10 @@ bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *src, ggml_t
     const size_t n = tensor_nbytes(src);
     if (n != tensor_nbytes(dst)) return false;
     mi355x_ctx *x = bc->dc->transfer_ctx();
-    return x && mi355x_memcpy_d2d(x, dst->data, src->data, n) == MI355X_OK;
+    if (!x || !device_current(sbc, x, src, 0, n)) return false;
+    if (mi355x_memcpy_d2d(x, dst->data, src->data, n) != MI355X_OK) return false;
+    device_written(bc, dst, 0, n);
+    return true;
 }
 
 void buf_clear(ggml_backend_buffer_t buffer, uint8_t value) {
@@ -404,7 +666,9 @@ void buf_clear(ggml_backend_buffer_t buffer, uint8_t value) {
         return;
     }
     mi355x_ctx *x = bc->dc->transfer_ctx();
-    if (!x || mi355x_fill(x, bc->base, value, bc->size) || mi355x_ctx_sync(x)) log_error("clear");
+    if (!x || mi355x_fill(x, bc->base, value, bc->size) || mi355x_ctx_sync(x)) return log_error("clear");
+    std::lock_guard<std::mutex> lk(bc->smu);
+    bc->resident.clear();
 }
 
 const ggml_backend_buffer_i kBufferIface = {
@@ -451,7 +715,13 @@ ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t 
         mi355x_ctx *x = dc->transfer_ctx();
         if (!x || mi355x_malloc(x, size, &p) != MI355X_OK) return log_error("alloc_buffer"), nullptr;
     }
-    auto *bc = new (std::nothrow) BufCtx{dc, p, size, host, false};
+    auto *bc = new (std::nothrow) BufCtx();
+    if (bc) {
+        bc->dc = dc;
+        bc->base = p;
+        bc->size = size;
+        bc->host = host;
+    }
     ggml_backend_buffer_t buf = bc ? make_buffer(buft, bc, size) : nullptr;
     if (!buf) {
         if (host) mi355x_host_free(p);
@@ -513,10 +783,24 @@ struct BackendCtx {
         size_t n;
     };
     std::vector<Pending> pending;
+    // something was enqueued on the stream since the last completed wait
+    bool queued = false;
+    // persistent GEMV server for single-row Q4_0 groups whose activation and
+    // outputs are host-resident (made on first use; none where the device
+    // has no cooperative launch)
+    int variant = MI355X_VARIANT_AUTO;
+    int group_mode = GGML_MI355X_GROUPS_SERVER;
 
     ~BackendCtx() {
         if (ctx) {
-            flush();
+            // queued work ends before the bounce memory goes; downloads never
+            // collected by a synchronize are dropped, not copied: their
+            // destinations may be gone with the caller
+            if (mi355x_ctx_sync(ctx) != MI355X_OK) log_error("backend free: sync");
+            if (!pending.empty())
+                std::fprintf(stderr, "[mi355x error] backend freed with %zu get_tensor_async result(s) not "
+                                     "synchronized; dropped\n", pending.size());
+            pending.clear();
             if (scratch) mi355x_free(ctx, scratch);
             mi355x_ctx_destroy(ctx);
         }
@@ -540,11 +824,13 @@ struct BackendCtx {
     int flush() {
         if (!ctx) return -1;
         const int rc = mi355x_ctx_fence(ctx);
+        if (rc == MI355X_OK) queued = false;
         for (const Pending &p : pending) std::memcpy(p.dst, p.src, p.n);
         pending.clear();
         pin_used = 0;
         return rc == MI355X_OK ? 0 : -1;
     }
+
 
     void *ensure_scratch(size_t bytes) {
         if (scratch_bytes >= bytes) return scratch;
@@ -578,8 +864,16 @@ const char *backend_get_name(ggml_backend_t backend) {
 void backend_free(ggml_backend_t backend) {
     BackendCtx *bc = backend_ctx(backend);
     if (!bc) return;
+    DevCtx *dc = bc->dc;
     delete bc;
     delete backend;
+    // the last backend of the device: its server leaves the CUs
+    bool last;
+    {
+        std::lock_guard<std::mutex> lk(dc->mu);
+        last = --dc->backends == 0;
+    }
+    if (last) dc->yield_cus();
 }
 
 // Copies for tensors in this backend's device memory run on the backend's own
@@ -596,15 +890,24 @@ void backend_set_tensor_async(ggml_backend_t backend, ggml_tensor *tensor, const
     if (!bc || !tensor || !tensor->buffer || !tensor->data || !data || size == 0) return;
     if (!on_backend_device(bc, tensor)) return buf_set_tensor(tensor->buffer, tensor, data, offset, size);
     std::lock_guard<std::mutex> lk(bc->mu);
+    auto *buf = static_cast<BufCtx *>(tensor->buffer->context);
+    // an activation row: into the buffer's shadow, nothing enqueued (no
+    // queued kernel reads the shadow: graph_compute waits for every kernel
+    // that does)
+    if (write_host_resident(tensor->buffer, buf, tensor, data, offset, size)) return;
     if (!prepacked(tensor)) {
         if (uint8_t *b = bc->take(size)) {
             std::memcpy(b, data, size);
             if (mi355x_memcpy_h2d_async(bc->ctx, static_cast<uint8_t *>(tensor->data) + offset, b, size))
                 log_error("set_tensor_async");
+            bc->queued = true;
+            device_written(buf, tensor, offset, size);
             return;
         }
     }
+    if (prepacked(tensor)) bc->dc->yield_cus();  // the scatter kernel needs CUs
     upload(bc->ctx, tensor, data, offset, size);
+    device_written(buf, tensor, offset, size);
 }
 
 void backend_get_tensor_async(ggml_backend_t backend, const ggml_tensor *tensor, void *data, size_t offset,
@@ -616,14 +919,29 @@ void backend_get_tensor_async(ggml_backend_t backend, const ggml_tensor *tensor,
         return buf_get_tensor(tensor->buffer, tensor, data, offset, size);
     }
     std::lock_guard<std::mutex> lk(bc->mu);
+    auto *buf = static_cast<BufCtx *>(tensor->buffer->context);
     if (!prepacked(tensor)) {
+        {
+            // host-resident: final already (graph_compute returns after every
+            // kernel that writes the shadow)
+            std::lock_guard<std::mutex> sl(buf->smu);
+            const size_t a = buf->off(tensor->data) + offset;
+            if (buf->resident.covers(a, a + size)) {
+                std::memcpy(data, buf->shadow + a, size);
+                return;
+            }
+        }
+        if (!device_current(buf, bc->ctx, tensor, offset, size)) return;
         if (uint8_t *b = bc->take(size)) {
             if (mi355x_memcpy_d2h_async(bc->ctx, b, static_cast<const uint8_t *>(tensor->data) + offset, size))
                 return log_error("get_tensor_async");
+            bc->queued = true;
             bc->pending.push_back({data, b, size});
             return;
         }
     }
+    if (!device_current(buf, bc->ctx, tensor, offset, size)) return;
+    if (prepacked(tensor)) bc->dc->yield_cus();  // the gather kernel needs CUs
     download(bc->ctx, tensor, data, offset, size);
 }
 
@@ -631,6 +949,7 @@ void backend_synchronize(ggml_backend_t backend) {
     BackendCtx *bc = backend_ctx(backend);
     if (!bc) return;
     std::lock_guard<std::mutex> lk(bc->mu);
+    if (!bc->queued && bc->pending.empty()) return;  // nothing in flight
     if (bc->flush()) log_error("synchronize");
 }
 
@@ -803,6 +1122,136 @@ int gemv_group(ggml_cgraph *g, int i, int mm) {
     return n;
 }
 
+// Where the bytes of a tensor in a device buffer of this plugin are for a
+// kernel: host-resident (the shadow: `host` for the server, `dev` its device
+// address) or on the device (`dev` = data).  Host-resident parts of a range
+// that is not host-resident as a whole are copied to the device first.
+struct Loc {
+    const uint8_t *host = nullptr;
+    uint8_t *dev = nullptr;
+    bool ok = true;
+};
+
+Loc locate_input(BackendCtx *bc, const ggml_tensor *t, size_t bytes) {
+    Loc l;
+    l.dev = static_cast<uint8_t *>(t->data);
+    if (!in_our_device_buffer(t)) return l;
+    auto *buf = static_cast<BufCtx *>(t->buffer->context);
+    std::lock_guard<std::mutex> lk(buf->smu);
+    if (buf->resident.empty()) return l;
+    const size_t a = buf->off(t->data);
+    if (buf->resident.covers(a, a + bytes)) {
+        l.host = buf->shadow + a;
+        l.dev = buf->shadow_dev + a;
+    } else {
+        l.ok = materialise(buf, bc->ctx, a, a + bytes);
+    }
+    return l;
+}
+
+// The output of a single-row GEMV node: into the shadow of its buffer when
+// the tensor may be host-resident there (`host` set), else the device.
+Loc locate_output(const ggml_tensor *t) {
+    Loc l;
+    l.dev = static_cast<uint8_t *>(t->data);
+    if (!in_our_device_buffer(t) || !mirrorable(t)) return l;
+    auto *buf = static_cast<BufCtx *>(t->buffer->context);
+    std::lock_guard<std::mutex> lk(buf->smu);
+    if (!shadow_ready(t->buffer, buf)) return l;
+    const size_t a = buf->off(t->data);
+    l.host = buf->shadow + a;
+    l.dev = buf->shadow_dev + a;
+    return l;
+}
+
+// Marks an output's range host-resident (written into the shadow) or
+// device-current.
+void output_written(const ggml_tensor *t, bool host, size_t bytes) {
+    if (!in_our_device_buffer(t)) return;
+    auto *buf = static_cast<BufCtx *>(t->buffer->context);
+    std::lock_guard<std::mutex> lk(buf->smu);
+    const size_t a = buf->off(t->data);
+    if (host) buf->resident.add(a, a + bytes);
+    else buf->resident.remove(a, a + bytes);
+}
+
+// n >= 1 consecutive single-row GEMV nodes that share their activation row
+// (gemv_group).  With the activation and every output host-resident, Q4_0
+// rows of a multiple of 256 values go to the backend's persistent server:
+// one command, no launch, no copy, returning when the outputs are in the
+// shadow.  Otherwise one launch (mi355x_gemv_multi, or mi355x_gemv) on the
+// backend's stream; *host_io is set when that launch reads or writes a shadow
+// (graph_compute then waits for it before returning).
+bool run_gemv_group(BackendCtx *bc, ggml_tensor *const *nodes, int n, bool *host_io) {
+    const ggml_tensor *a = nodes[0];
+    const ggml_tensor *w0 = a->src[0];
+    const int type = w0->type;
+    const int64_t K = w0->ne[0];
+    const Loc x = locate_input(bc, a->src[1], static_cast<size_t>(K) * sizeof(float));
+    if (!x.ok) {
+        std::fprintf(stderr, "[mi355x error] node '%s' activation not on the device: %s\n", a->name,
+                     mi355x_last_error());
+        return false;
+    }
+    mi355x_gemv_job jobs[MI355X_MULTI_MAX_JOBS] = {};
+    bool out_host[MI355X_MULTI_MAX_JOBS] = {};
+    bool all_host = true, aligned = true;
+    for (int j = 0; j < n; ++j) {
+        const ggml_tensor *t = nodes[j];
+        const Loc y = locate_output(t);
+        out_host[j] = y.host != nullptr;
+        all_host = all_host && out_host[j];
+        aligned = aligned && (reinterpret_cast<uintptr_t>(t->src[0]->data) & 15) == 0;
+        jobs[j] = {t->src[0]->data, t->src[0]->ne[1], reinterpret_cast<float *>(y.dev)};
+    }
+    if (bc->group_mode == GGML_MI355X_GROUPS_SERVER && x.host && all_host && type == GGML_TYPE_Q4_0 &&
+        K % 256 == 0 && K <= DevCtx::kServerMaxK && n <= 4 && aligned &&
+        bc->variant != MI355X_VARIANT_EXACT_F32) {
+        DevCtx *dc = bc->dc;
+        std::lock_guard<std::mutex> sl(dc->srv_mu);
+        if (mi355x_server *srv = dc->server()) {
+            // the server reads the shadow with the host's loads: whatever the
+            // stream still runs must have written it first
+            if (bc->queued && mi355x_ctx_fence(bc->ctx) == MI355X_OK) bc->queued = false;
+            mi355x_server_job sj[4];
+            for (int j = 0; j < n; ++j) sj[j] = {jobs[j].W, jobs[j].N, jobs[j].y};
+            int rc = mi355x_ctx_set_option(dc->srv_ctx, MI355X_OPT_VARIANT, bc->variant);
+            if (rc == MI355X_OK) rc = mi355x_server_gemv(srv, reinterpret_cast<const float *>(x.host), K, n, sj);
+            if (rc == MI355X_OK) {
+                dc->srv_active = true;
+                for (int j = 0; j < n; ++j) output_written(nodes[j], true, static_cast<size_t>(jobs[j].N) * 4);
+                return true;
+            }
+            // EUNSUPPORTED (a row count the server does not hold): the
+            // launch below computes the group
+            if (rc != MI355X_EUNSUPPORTED) {
+                std::fprintf(stderr, "[mi355x error] node '%s' server GEMV: %s\n", a->name, mi355x_last_error());
+                return false;
+            }
+        }
+    }
+    bc->dc->yield_cus();
+    const float *xp = reinterpret_cast<const float *>(x.dev);
+    const int rc = n > 1 ? mi355x_gemv_multi(bc->ctx, type, K, xp, n, jobs)
+                         : mi355x_gemv(bc->ctx, type, jobs[0].W, jobs[0].N, K, xp, jobs[0].y);
+    if (rc != MI355X_OK) {
+        if (n > 1)
+            std::fprintf(stderr, "[mi355x error] nodes '%s'.. (%d sharing one activation) GEMV dispatch: %s\n",
+                         a->name, n, mi355x_last_error());
+        else
+            std::fprintf(stderr, "[mi355x error] node '%s' GEMV dispatch: %s\n", a->name, mi355x_last_error());
+        return false;
+    }
+    bc->queued = true;
+    bool any_host = x.host != nullptr;
+    for (int j = 0; j < n; ++j) {
+        output_written(nodes[j], out_host[j], static_cast<size_t>(jobs[j].N) * 4);
+        any_host = any_host || out_host[j];
+    }
+    if (any_host) *host_io = true;
+    return true;
+}
+
 enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
     if (!backend || !cgraph) return GGML_STATUS_FAILED;
     if (cgraph->n_nodes > 0 && !cgraph->nodes) return GGML_STATUS_FAILED;
@@ -813,31 +1262,44 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
     const bool trace = trace_nodes();
     double total_ms = 0.0;
     int count = 0;
+    bool host_io = false;
+    enum ggml_status status = GGML_STATUS_SUCCESS;
     for (int i = 0; i < cgraph->n_nodes; ++i) {
         ggml_tensor *node = cgraph->nodes[i];
         if (!node || mm < 0 || node->op != mm) continue;  // other nodes carry no work here
-        // consecutive MUL_MATs that share their activation row: one launch
-        // (the per-node trace keeps one call per node)
-        const int n = trace ? 1 : gemv_group(cgraph, i, mm);
-        if (n > 1) {
-            mi355x_gemv_job jobs[MI355X_MULTI_MAX_JOBS];
-            for (int j = 0; j < n; ++j) {
-                const ggml_tensor *t = cgraph->nodes[i + j];
-                jobs[j] = {t->src[0]->data, t->src[0]->ne[1], static_cast<float *>(t->data)};
-            }
-            if (mi355x_gemv_multi(bc->ctx, node->src[0]->type, node->src[0]->ne[0],
-                                  static_cast<const float *>(node->src[1]->data), n, jobs) != MI355X_OK) {
-                std::fprintf(stderr, "[mi355x error] nodes '%s'.. (%d sharing one activation) GEMV dispatch: %s\n",
-                             node->name, n, mi355x_last_error());
-                return GGML_STATUS_FAILED;
+        auto t0 = std::chrono::steady_clock::now();
+        if (single_row_gemv(node)) {
+            // consecutive MUL_MATs that share their activation row: one
+            // command or launch (the per-node trace keeps one per node)
+            const int n = trace ? 1 : gemv_group(cgraph, i, mm);
+            if (!run_gemv_group(bc, cgraph->nodes + i, n, &host_io)) {
+                status = GGML_STATUS_FAILED;
+                break;
             }
             i += n - 1;
-            continue;
+        } else {
+            // M > 1, batches, strided rows: device memory only
+            const size_t in_bytes = tensor_nbytes(node->src[1]);
+            if (in_our_device_buffer(node->src[1])) {
+                auto *buf = static_cast<BufCtx *>(node->src[1]->buffer->context);
+                if (!device_current(buf, bc->ctx, node->src[1], 0, in_bytes)) {
+                    status = GGML_STATUS_FAILED;
+                    break;
+                }
+            }
+            bc->dc->yield_cus();
+            if (!process_mul_mat(bc, node, false)) {
+                status = GGML_STATUS_FAILED;
+                break;
+            }
+            bc->queued = true;
+            output_written(node, false, tensor_nbytes(node));
         }
-        auto t0 = std::chrono::steady_clock::now();
-        if (!process_mul_mat(bc, node, false)) return GGML_STATUS_FAILED;
         if (trace) {
-            if (mi355x_ctx_sync(bc->ctx)) return GGML_STATUS_FAILED;
+            if (mi355x_ctx_sync(bc->ctx)) {
+                status = GGML_STATUS_FAILED;
+                break;
+            }
             const double ms =
                 std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
             total_ms += ms;
@@ -847,8 +1309,18 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
                          (long)node->src[0]->ne[0], ms);
         }
     }
+    // kernels that read or write a shadow finish before the host may touch
+    // it again (a failed graph waits too: its launches may still run)
+    if (host_io) {
+        if (mi355x_ctx_fence(bc->ctx) != MI355X_OK) {
+            log_error("graph_compute: wait");
+            status = GGML_STATUS_FAILED;
+        } else if (bc->pending.empty()) {
+            bc->queued = false;
+        }
+    }
     if (trace && count > 0) std::fprintf(stderr, "[mi355x trace] TOTAL: %d nodes, %6.3f ms\n", count, total_ms);
-    return GGML_STATUS_SUCCESS;
+    return status;
 }
 
 const ggml_backend_i kBackendIface = {
@@ -882,7 +1354,12 @@ ggml_backend_t make_backend(size_t dev_num) {
         return nullptr;
     }
     auto *backend = new (std::nothrow) ggml_backend{backend_guid(), kBackendIface, &bc->dc->dev, bc};
-    if (!backend) delete bc;
+    if (!backend) {
+        delete bc;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(bc->dc->mu);
+    ++bc->dc->backends;
     return backend;
 }
 
@@ -992,6 +1469,8 @@ void *reg_get_proc_address(ggml_backend_reg_t, const char *name) {
         return reinterpret_cast<void *>(ggml_backend_mi355x_load_iq_grids_from_ggml);
     if (!std::strcmp(name, "ggml_backend_mi355x_set_kernel_variant"))
         return reinterpret_cast<void *>(ggml_backend_mi355x_set_kernel_variant);
+    if (!std::strcmp(name, "ggml_backend_mi355x_set_group_mode"))
+        return reinterpret_cast<void *>(ggml_backend_mi355x_set_group_mode);
     return nullptr;
 }
 
@@ -1020,6 +1499,23 @@ void init_registry() {
             } else {
                 dc->description = "AMD Instinct MI355X";
             }
+            dc->dev = ggml_backend_device{kDeviceIface, &g_reg, dc};
+            dc->buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
+            dc->host_buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
+            g_devs.push_back(dc);
+        }
+        // MI355X_HOST_ONLY_DEVICE=1 lists one more device, bound to no GPU
+        // (a host-only context of the C-ABI): its backend and buffers fail
+        // every device call the way a lost device would, so the plugin's
+        // error surface (GGML_STATUS_FAILED, [mi355x error] messages) can
+        // be exercised on a machine without a GPU
+        const char *ho = std::getenv("MI355X_HOST_ONLY_DEVICE");
+        if (ho && *ho && std::strcmp(ho, "0") != 0) {
+            auto *dc = new DevCtx();
+            dc->device = MI355X_DEVICE_HOST_ONLY;
+            dc->name = "MI355X_HOST_ONLY";
+            dc->description = "host-only device (no GPU; every device call fails)";
+            dc->pci = "none";
             dc->dev = ggml_backend_device{kDeviceIface, &g_reg, dc};
             dc->buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
             dc->host_buft = ggml_backend_buffer_type{kBufferTypeIface, &dc->dev, dc};
@@ -1086,6 +1582,7 @@ bool ggml_backend_mi355x_compute_graph(ggml_backend *backend, ggml_tensor_mi355x
     for (size_t i = 0; i < n_nodes; ++i) {
         ggml_tensor_mi355x *node = nodes[i];
         if (!node || node->op != GGML_MI355X_OP_MUL_MAT) continue;
+        bc->dc->yield_cus();
         if (!process_mul_mat(bc, node, true)) return false;
     }
     return true;
@@ -1099,11 +1596,21 @@ bool ggml_backend_mi355x_set_op_mul_mat(int op) {
 
 int ggml_backend_mi355x_load_iq_grids_from_ggml(void) { return mi355x_iq_grids_from_ggml_impl(); }
 
+bool ggml_backend_mi355x_set_group_mode(ggml_backend *backend, int mode) {
+    BackendCtx *bc = backend_ctx(backend);
+    if (!bc || (mode != GGML_MI355X_GROUPS_SERVER && mode != GGML_MI355X_GROUPS_LAUNCH)) return false;
+    std::lock_guard<std::mutex> lk(bc->mu);
+    bc->group_mode = mode;
+    return true;
+}
+
 bool ggml_backend_mi355x_set_kernel_variant(ggml_backend *backend, int variant) {
     BackendCtx *bc = backend_ctx(backend);
     if (!bc) return false;
     std::lock_guard<std::mutex> lk(bc->mu);
-    return mi355x_ctx_set_option(bc->ctx, MI355X_OPT_VARIANT, variant) == MI355X_OK;
+    if (mi355x_ctx_set_option(bc->ctx, MI355X_OPT_VARIANT, variant) != MI355X_OK) return false;
+    bc->variant = variant;
+    return true;
 }
 
 }  // extern "C"

@@ -72,6 +72,13 @@ int set_error(int code, const std::string &msg);
 int hip_error(hipError_t e, const char *what);
 void clear_error();
 
+// Gate of every entry point that would reach the device: MI355X_OK, or the
+// error of an armed injected fault for `entry` (mi355x_inject_fault), or, on
+// a host-only context (device MI355X_DEVICE_HOST_ONLY), hipErrorNoDevice.
+// Nothing here touches the device.
+int device_gate(const mi355x_ctx *ctx, const char *entry);
+inline bool host_only(const mi355x_ctx *ctx) { return ctx && ctx->device < 0; }
+
 #define MI355X_HIP(call)                                \
     do {                                                \
         hipError_t e_ = (call);                         \

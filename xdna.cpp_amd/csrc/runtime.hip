@@ -105,8 +105,9 @@ int ensure_staging(mi355x_ctx *ctx, size_t want) {
 struct DeviceGuard {
     int prev = -1;
     explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
+        // a host-only context (device < 0) touches no device
+        if (dev < 0 || hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (dev >= 0 && prev != dev) (void)hipSetDevice(dev);
     }
     ~DeviceGuard() {
         int cur = -1;
@@ -114,8 +115,10 @@ struct DeviceGuard {
     }
 };
 
+// gate: false for the calls an entry point makes for itself after passing
+// the device gate once
 int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *x, bool xbf16,
-                float *y, const char *who, bool overlap_ok = false) {
+                float *y, const char *who, bool overlap_ok = false, bool gate = true) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
     uint64_t total = 0;
@@ -123,6 +126,7 @@ int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
     if (rc) return rc;
     if (N == 0) return MI355X_OK;
     if (!W || !x || !y) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer argument provided");
+    if (gate && (rc = device_gate(ctx, who))) return rc;
     if (type != MI355X_TYPE_Q4_0 && (reinterpret_cast<uintptr_t>(W) & 1) != 0)
         return set_error(MI355X_EINVAL, std::string(who) + ": W must be a row of a resident tensor (2-byte aligned)");
     if (!mi355x_type_ready(type))
@@ -167,6 +171,67 @@ int gemv_common(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K, 
 int set_error(int code, const std::string &msg) {
     g_last_error = msg;
     return code;
+}
+
+namespace {
+
+// One armed fault at a time, process-wide (mi355x_inject_fault, or the
+// environment variable MI355X_INJECT_FAULT="<entry>:<hipError_t>[:<skip>]"
+// read on first use).
+struct Fault {
+    std::mutex mu;
+    std::atomic<bool> armed{false};
+    std::string entry;
+    int error = 0;
+    int skip = 0;
+};
+Fault g_fault;
+std::once_flag g_fault_env_once;
+
+void arm_fault(const char *entry, int error, int skip) {
+    std::lock_guard<std::mutex> lk(g_fault.mu);
+    g_fault.entry = entry ? entry : "";
+    g_fault.error = error;
+    g_fault.skip = skip > 0 ? skip : 0;
+    g_fault.armed.store(entry != nullptr && *entry != 0 && error != 0);
+}
+
+void read_fault_env() {
+    const char *v = std::getenv("MI355X_INJECT_FAULT");
+    if (!v || !*v) return;
+    const std::string spec(v);
+    const size_t c1 = spec.find(':');
+    if (c1 == std::string::npos) return;
+    const size_t c2 = spec.find(':', c1 + 1);
+    const int error = std::atoi(spec.substr(c1 + 1, c2 == std::string::npos ? std::string::npos : c2 - c1 - 1).c_str());
+    const int skip = c2 == std::string::npos ? 0 : std::atoi(spec.substr(c2 + 1).c_str());
+    arm_fault(spec.substr(0, c1).c_str(), error, skip);
+}
+
+}  // namespace
+
+int device_gate(const mi355x_ctx *ctx, const char *entry) {
+    std::call_once(g_fault_env_once, read_fault_env);
+    if (g_fault.armed.load(std::memory_order_relaxed)) {
+        std::lock_guard<std::mutex> lk(g_fault.mu);
+        if (g_fault.armed.load() && (g_fault.entry == "*" || g_fault.entry == entry)) {
+            if (g_fault.skip > 0) {
+                --g_fault.skip;
+            } else {
+                g_fault.armed.store(false);
+                const hipError_t e = static_cast<hipError_t>(g_fault.error);
+                const int rc = hip_error(e, entry);
+                g_last_error += " [injected]";
+                return rc;
+            }
+        }
+    }
+    if (host_only(ctx)) {
+        const int rc = hip_error(hipErrorNoDevice, entry);
+        g_last_error += " [host-only context]";
+        return rc;
+    }
+    return MI355X_OK;
 }
 
 int hip_error(hipError_t e, const char *what) {
@@ -247,6 +312,15 @@ extern "C" {
 
 const char *mi355x_last_error(void) { return g_last_error.c_str(); }
 
+int mi355x_inject_fault(const char *entry, int hip_error, int skip) {
+    clear_error();
+    if (entry && *entry && (hip_error == 0 || skip < 0))
+        return set_error(MI355X_EINVAL, "mi355x_inject_fault: a fault needs a nonzero hipError_t and skip >= 0");
+    std::call_once(g_fault_env_once, read_fault_env);
+    arm_fault(entry, hip_error, skip);
+    return MI355X_OK;
+}
+
 int mi355x_device_count(int *count) {
     clear_error();
     if (!count) return set_error(MI355X_EINVAL, "mi355x_device_count: null pointer");
@@ -262,8 +336,18 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
     clear_error();
     if (!out) return set_error(MI355X_EINVAL, "mi355x_ctx_create: null output pointer");
     *out = nullptr;
+    if (device == MI355X_DEVICE_HOST_ONLY) {
+        // no device, no stream: every device entry point fails at its gate
+        auto *ctx = new (std::nothrow) mi355x_ctx();
+        if (!ctx) return set_error(MI355X_ENOMEM, "mi355x_ctx_create: out of host memory");
+        ctx->device = MI355X_DEVICE_HOST_ONLY;
+        *out = ctx;
+        return MI355X_OK;
+    }
+    int rc = device_gate(nullptr, "mi355x_ctx_create");
+    if (rc) return rc;
     int n = 0;
-    int rc = mi355x_device_count(&n);
+    rc = mi355x_device_count(&n);
     if (rc) return rc;
     if (device < 0 || device >= n)
         return set_error(MI355X_EINVAL, "mi355x_ctx_create: device " + std::to_string(device) + " of " +
@@ -327,6 +411,10 @@ int mi355x_ctx_create(int device, mi355x_ctx **out) {
 
 void mi355x_ctx_destroy(mi355x_ctx *ctx) {
     if (!ctx) return;
+    if (host_only(ctx)) {
+        delete ctx;
+        return;
+    }
     DeviceGuard dg(ctx->device);
     (void)ov_join(ctx);
     for (void *p : {ctx->staging, ctx->xconv, ctx->mbtiles, ctx->iq3xxs_grid, ctx->iq2s_grid})
@@ -349,7 +437,9 @@ void mi355x_ctx_destroy(mi355x_ctx *ctx) {
 int mi355x_ctx_sync(mi355x_ctx *ctx) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_sync: null context");
-    const int rc = ov_join(ctx);
+    int rc = device_gate(ctx, "mi355x_ctx_sync");
+    if (rc) return rc;
+    rc = ov_join(ctx);
     if (rc) return rc;
     MI355X_HIP(hipStreamSynchronize(ctx->stream));
     return MI355X_OK;
@@ -372,6 +462,8 @@ constexpr double kFenceSpinSeconds = 2e-3;
 int mi355x_ctx_fence(mi355x_ctx *ctx) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_fence: null context");
+    const int grc = device_gate(ctx, "mi355x_ctx_fence");
+    if (grc) return grc;
     DeviceGuard dg(ctx->device);
     const int jrc = ov_join(ctx);
     if (jrc) return jrc;
@@ -396,7 +488,7 @@ int mi355x_ctx_fence(mi355x_ctx *ctx) {
 int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: null context");
-    {
+    if (!host_only(ctx)) {
         DeviceGuard dg(ctx->device);
         const int rc = ov_join(ctx);
         if (rc) return rc;
@@ -406,6 +498,10 @@ int mi355x_ctx_set_option(mi355x_ctx *ctx, int option, int64_t value) {
         if (value < 0 || value > 4)
             return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap must be 0 (off) or 2 to 4 streams");
         if (value == 1) return set_error(MI355X_EINVAL, "mi355x_ctx_set_option: overlap needs 2 to 4 streams");
+        if (value >= 2) {
+            const int rc = device_gate(ctx, "mi355x_ctx_set_option");
+            if (rc) return rc;
+        }
         DeviceGuard dg(ctx->device);
         if (value >= 2 && !ctx->ov_fork) MI355X_HIP(hipEventCreateWithFlags(&ctx->ov_fork, hipEventDisableTiming));
         for (int i = 0; i + 1 < value; ++i) {
@@ -465,6 +561,8 @@ int mi355x_ctx_device(mi355x_ctx *ctx) { return ctx ? ctx->device : -1; }
 int mi355x_mem_info(mi355x_ctx *ctx, size_t *free_bytes, size_t *total_bytes) {
     clear_error();
     if (!ctx || !free_bytes || !total_bytes) return set_error(MI355X_EINVAL, "mi355x_mem_info: null pointer");
+    const int rc = device_gate(ctx, "mi355x_mem_info");
+    if (rc) return rc;
     DeviceGuard dg(ctx->device);
     MI355X_HIP(hipMemGetInfo(free_bytes, total_bytes));
     return MI355X_OK;
@@ -486,8 +584,10 @@ int mi355x_device_describe(int device, char *name, size_t name_len, char *pci, s
 int mi355x_malloc(mi355x_ctx *ctx, size_t bytes, void **dptr) {
     clear_error();
     if (!ctx || !dptr) return set_error(MI355X_EINVAL, "mi355x_malloc: null pointer");
-    DeviceGuard dg(ctx->device);
     *dptr = nullptr;
+    const int rc = device_gate(ctx, "mi355x_malloc");
+    if (rc) return rc;
+    DeviceGuard dg(ctx->device);
     hipError_t e = hipMalloc(dptr, bytes == 0 ? 256 : bytes);
     if (e != hipSuccess) {
         *dptr = nullptr;
@@ -500,6 +600,8 @@ int mi355x_free(mi355x_ctx *ctx, void *dptr) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_free: null context");
     if (!dptr) return MI355X_OK;
+    const int rc = device_gate(ctx, "mi355x_free");
+    if (rc) return rc;
     DeviceGuard dg(ctx->device);
     return free_device(ctx, dptr);
 }
@@ -523,12 +625,22 @@ int mi355x_host_free(void *hptr) {
     return MI355X_OK;
 }
 
+int mi355x_host_device_ptr(const void *hptr, void **dptr) {
+    clear_error();
+    if (!hptr || !dptr) return set_error(MI355X_EINVAL, "mi355x_host_device_ptr: null pointer");
+    *dptr = nullptr;
+    MI355X_HIP(hipHostGetDevicePointer(dptr, const_cast<void *>(hptr), 0));
+    return MI355X_OK;
+}
+
 static int copy_sync(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind,
                      const char *who) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
     if (bytes == 0) return MI355X_OK;
     if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
+    const int grc = device_gate(ctx, who);
+    if (grc) return grc;
     DeviceGuard dg(ctx->device);
     const int jrc = ov_join(ctx);
     if (jrc) return jrc;
@@ -553,6 +665,8 @@ static int copy_async(mi355x_ctx *ctx, void *dst, const void *src, size_t bytes,
     if (!ctx) return set_error(MI355X_EINVAL, std::string(who) + ": null context");
     if (bytes == 0) return MI355X_OK;
     if (!dst || !src) return set_error(MI355X_EINVAL, std::string(who) + ": null pointer");
+    const int grc = device_gate(ctx, who);
+    if (grc) return grc;
     DeviceGuard dg(ctx->device);
     const int jrc = ov_join(ctx);
     if (jrc) return jrc;
@@ -570,8 +684,10 @@ int mi355x_fill(mi355x_ctx *ctx, void *dst, uint8_t value, size_t bytes) {
     clear_error();
     if (!ctx) return set_error(MI355X_EINVAL, "mi355x_fill: null context");
     if (bytes && !dst) return set_error(MI355X_EINVAL, "mi355x_fill: null pointer");
+    int rc = device_gate(ctx, "mi355x_fill");
+    if (rc) return rc;
     DeviceGuard dg(ctx->device);
-    const int rc = ov_join(ctx);
+    rc = ov_join(ctx);
     if (rc) return rc;
     return launch_fill(ctx, dst, value, bytes);
 }
@@ -650,6 +766,8 @@ int mi355x_prepack_from_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, vo
     if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_prepack_from_host: null pointer");
     rc = check_resident_base(type, packed_dev, "mi355x_prepack_from_host");
     if (rc) return rc;
+    rc = device_gate(ctx, "mi355x_prepack_from_host");
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
     rc = ov_join(ctx);
@@ -678,6 +796,8 @@ int mi355x_prepack_from_device(mi355x_ctx *ctx, int type, int64_t N, int64_t K, 
     if (!packed_dev || !raw_dev) return set_error(MI355X_EINVAL, "mi355x_prepack_from_device: null pointer");
     rc = check_resident_base(type, packed_dev, "mi355x_prepack_from_device");
     if (rc) return rc;
+    rc = device_gate(ctx, "mi355x_prepack_from_device");
+    if (rc) return rc;
     DeviceGuard dg(ctx->device);
     rc = ov_join(ctx);
     if (rc) return rc;
@@ -696,6 +816,8 @@ int mi355x_unpack_to_host(mi355x_ctx *ctx, int type, int64_t N, int64_t K, const
     if (rc || size == 0) return rc;
     if (!packed_dev || !raw_host) return set_error(MI355X_EINVAL, "mi355x_unpack_to_host: null pointer");
     rc = check_resident_base(type, packed_dev, "mi355x_unpack_to_host");
+    if (rc) return rc;
+    rc = device_gate(ctx, "mi355x_unpack_to_host");
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     DeviceGuard dg(ctx->device);
@@ -737,6 +859,10 @@ int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int 
         mj[j] = {static_cast<const uint8_t *>(jobs[j].W), jobs[j].N, jobs[j].y};
     }
     {
+        const int rc = device_gate(ctx, who);
+        if (rc) return rc;
+    }
+    {
         DeviceGuard dg(ctx->device);
         const int rc = ov_join(ctx);
         if (rc) return rc;
@@ -753,7 +879,7 @@ int mi355x_gemv_multi(mi355x_ctx *ctx, int type, int64_t K, const float *x, int 
     }
     // one launch per matrix where the shared form does not apply
     for (int j = 0; j < njobs; ++j) {
-        const int rc = gemv_common(ctx, type, jobs[j].W, jobs[j].N, K, x, false, jobs[j].y, who);
+        const int rc = gemv_common(ctx, type, jobs[j].W, jobs[j].N, K, x, false, jobs[j].y, who, false, false);
         if (rc) return rc;
     }
     return MI355X_OK;
@@ -772,6 +898,10 @@ int gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                  float *y, int64_t y_stride, int64_t M, bool noalloc, const char *who) {
     clear_error();
     if (M < 0) return set_error(MI355X_EINVAL, std::string(who) + ": negative M");
+    if (ctx && M > 0) {
+        const int rc = device_gate(ctx, who);
+        if (rc) return rc;
+    }
     if (ctx) {
         DeviceGuard dg(ctx->device);
         const int rc = ov_join(ctx);
@@ -817,7 +947,7 @@ int gemv_batched(mi355x_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
         }
     }
     for (int64_t m = 0; m < M; ++m) {
-        int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, who);
+        int rc = gemv_common(ctx, type, W, N, K, x + m * x_stride, false, y + m * y_stride, who, false, false);
         if (rc) return rc;
     }
     return MI355X_OK;
@@ -840,6 +970,10 @@ int mi355x_time_gemv(mi355x_ctx *ctx, int type, const void *const *weights, int 
     clear_error();
     if (!ctx || !weights || n_weights < 1 || iters < 1 || warmup < 0 || !ms_total)
         return set_error(MI355X_EINVAL, "mi355x_time_gemv: bad arguments");
+    {
+        const int grc = device_gate(ctx, "mi355x_time_gemv");
+        if (grc) return grc;
+    }
     DeviceGuard dg(ctx->device);
     // with MI355X_OPT_OVERLAP (S streams) consecutive launches may run at
     // once: launch i writes y + (i % S) * N

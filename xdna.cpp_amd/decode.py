@@ -54,6 +54,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.qd_silu_mul.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     lib.qd_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float]
     lib.qd_set_block.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_set_swiglu.argtypes = [C.c_void_p, C.c_int]
+    lib.qd_set_plugin_groups.restype = C.c_int
+    lib.qd_set_plugin_groups.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_fuse.argtypes = [C.c_void_p, C.c_int]
     lib.qd_set_variant.restype = C.c_int
     lib.qd_set_variant.argtypes = [C.c_void_p, C.c_int]
@@ -160,6 +163,12 @@ class Model:
         """Server mode: o through down as one command (default on)."""
         self.lib.qd_set_block(self.h, 1 if on else 0)
 
+    def set_swiglu(self, on: bool) -> None:
+        """Server mode: gate|up, SiLU and down as one command (default on);
+        off: two GEMV commands with SiLU on the host, so only the MUL_MATs
+        run on the GPU (block commands need it on)."""
+        self.lib.qd_set_swiglu(self.h, 1 if on else 0)
+
     def set_variant(self, variant: int) -> None:
         """GEMV kernel variant on the GPU path (mi355x.VARIANT_*)."""
         if self.lib.qd_set_variant(self.h, variant) != 0:
@@ -183,6 +192,14 @@ class Model:
         ggml plugin (weights as tensors in its buffer, activation in, one
         graph_compute per group, outputs out, synchronize)."""
         if self.lib.qd_set_wait(self.h, mode) != 0:
+            raise RuntimeError(self.lib.qd_last_error().decode())
+
+    PLUGIN_GROUPS_SERVER, PLUGIN_GROUPS_LAUNCH = 0, 1
+
+    def set_plugin_groups(self, mode: int) -> None:
+        """WAIT_PLUGIN: graph_compute runs a group as a server command
+        (PLUGIN_GROUPS_SERVER, default) or one launch (PLUGIN_GROUPS_LAUNCH)."""
+        if self.lib.qd_set_plugin_groups(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 
     def last_wait(self) -> int:

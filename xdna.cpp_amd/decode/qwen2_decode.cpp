@@ -175,11 +175,14 @@ constexpr int kPluginOpMulMat = 29;
 
 struct PluginDecode {
     ggml_backend *be = nullptr;
-    ggml_backend_buffer *buf = nullptr;
+    // as llama.cpp allocates them: the weights in one buffer (usage WEIGHTS),
+    // the graph's activations and outputs in a compute buffer
+    ggml_backend_buffer *buf = nullptr, *cbuf = nullptr;
     std::vector<ggml_tensor> w, out;  // per matrix id: weight, MUL_MAT node
     ggml_tensor x{};                  // the activation row (ne[0] set per group)
 
     ~PluginDecode() {
+        if (cbuf && cbuf->iface.free_buffer) cbuf->iface.free_buffer(cbuf);
         if (buf && buf->iface.free_buffer) buf->iface.free_buffer(buf);
         if (be) ggml_backend_mi355x_free(be);
     }
@@ -199,6 +202,8 @@ struct qd_model {
     void *weights = nullptr;  // every matrix, resident, back to back in id order
     bool fuse = true;         // one launch for matrices that are adjacent in HBM
     bool block = true;        // server mode: o through down as one command
+    bool swiglu = true;       // server mode: gate|up, SiLU, down as one command
+    int plugin_groups = GGML_MI355X_GROUPS_SERVER;  // plugin mode: how graph_compute runs a group
     int64_t last_launches = 0;
     float *dx = nullptr, *dy = nullptr;  // activation in, outputs out
     float *ffn_norm_dev = nullptr;       // the FFN norm weights, n_layers * hidden
@@ -648,7 +653,7 @@ int attach_plugin(qd_model *m) {
     auto up = [al](size_t v) { return (v + al - 1) / al * al; };
     const size_t n = m->mats.size();
     std::vector<size_t> woff(n), ooff(n);
-    size_t total = 0;
+    size_t total = 0, ctotal = 0;
     int64_t max_k = 0;
     for (size_t i = 0; i < n; ++i) {
         woff[i] = total;
@@ -656,20 +661,24 @@ int attach_plugin(qd_model *m) {
         max_k = std::max(max_k, m->mats[i].K);
     }
     for (size_t i = 0; i < n; ++i) {
-        ooff[i] = total;
-        total = up(total + static_cast<size_t>(m->mats[i].N) * 4);
+        ooff[i] = ctotal;
+        ctotal = up(ctotal + static_cast<size_t>(m->mats[i].N) * 4);
     }
-    const size_t xoff = total;
-    total = up(total + static_cast<size_t>(max_k) * 4);
+    const size_t xoff = ctotal;
+    ctotal = up(ctotal + static_cast<size_t>(max_k) * 4);
     P->buf = buft->iface.alloc_buffer(buft, total);
     if (!P->buf) return fail("plugin decode: buffer allocation failed");
     P->buf->usage = GGML_BACKEND_BUFFER_USAGE_WEIGHTS;
+    P->cbuf = buft->iface.alloc_buffer(buft, ctotal);
+    if (!P->cbuf) return fail("plugin decode: compute buffer allocation failed");
+    P->cbuf->usage = GGML_BACKEND_BUFFER_USAGE_COMPUTE;
     auto *base = static_cast<uint8_t *>(P->buf->iface.get_base(P->buf));
+    auto *cbase = static_cast<uint8_t *>(P->cbuf->iface.get_base(P->cbuf));
     P->w.resize(n);
     P->out.resize(n);
     P->x.type = GGML_TYPE_F32;
-    P->x.buffer = P->buf;
-    P->x.data = base + xoff;
+    P->x.buffer = P->cbuf;
+    P->x.data = cbase + xoff;
     std::snprintf(P->x.name, sizeof(P->x.name), "x");
     for (size_t i = 0; i < n; ++i) {
         const Matrix &mat = m->mats[i];
@@ -697,8 +706,8 @@ int attach_plugin(qd_model *m) {
         o.op = kPluginOpMulMat;
         o.src[0] = &P->w[i];
         o.src[1] = &P->x;
-        o.buffer = P->buf;
-        o.data = base + ooff[i];
+        o.buffer = P->cbuf;
+        o.data = cbase + ooff[i];
         std::snprintf(o.name, sizeof(o.name), "mm%zu", i);
     }
     P->be->iface.synchronize(P->be);
@@ -726,6 +735,8 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
         if (attach_plugin(m)) return -1;
         if (!ggml_backend_mi355x_set_kernel_variant(m->plugin->be, m->variant))
             return fail("qd_generate: plugin kernel variant");
+        if (!ggml_backend_mi355x_set_group_mode(m->plugin->be, m->plugin_groups))
+            return fail("qd_generate: plugin group mode");
     }
     bool use_server = backend == 0 && m->wait_mode == QD_WAIT_SERVER && m->variant != MI355X_VARIANT_EXACT_F32;
     int64_t max_k = 0;
@@ -740,7 +751,7 @@ int qd_generate(qd_model *m, int backend, qd_gemv_fn cpu_gemv, void *user, const
     const int wait = !use_server && m->wait_mode == QD_WAIT_SERVER ? QD_WAIT_FENCE : m->wait_mode;
     // the feed-forward block as one SwiGLU server command (fused groups
     // only); with `block`, also o, both residual adds and the FFN norm
-    const bool swiglu = backend == 0 && use_server && m->fuse && c.ffn % 256 == 0;
+    const bool swiglu = backend == 0 && use_server && m->fuse && m->swiglu && c.ffn % 256 == 0;
     const bool block = swiglu && m->block && H % 256 == 0 && H <= 4096 && QD % 256 == 0;
     // q, k and v back to back in HBM: the block command can run them as one job
     bool qkv_adjacent = true;
@@ -1016,6 +1027,17 @@ void qd_rmsnorm(const float *x, const float *w, float *out, int n, float eps) { 
 
 void qd_set_block(qd_model *m, int on) {
     if (m) m->block = on != 0;
+}
+
+void qd_set_swiglu(qd_model *m, int on) {
+    if (m) m->swiglu = on != 0;
+}
+
+int qd_set_plugin_groups(qd_model *m, int mode) {
+    if (!m || (mode != GGML_MI355X_GROUPS_SERVER && mode != GGML_MI355X_GROUPS_LAUNCH))
+        return fail("qd_set_plugin_groups: unknown mode");
+    m->plugin_groups = mode;
+    return 0;
 }
 
 }  // extern "C"

@@ -86,6 +86,12 @@ QD_API void qd_set_fuse(qd_model *m, int on);
  * command when `on` (the default); off = the o command, then the FFN as one
  * mi355x_server_swiglu command. */
 QD_API void qd_set_block(qd_model *m, int on);
+/* Server mode with fused groups: gate|up, SiLU and down as one
+ * mi355x_server_swiglu command when `on` (the default); off = gate|up and
+ * down as two GEMV commands with SiLU on the host, so that only the
+ * matrix-vector products run on the GPU (the split of a ggml backend that
+ * claims MUL_MAT alone).  Block commands need it on. */
+QD_API void qd_set_swiglu(qd_model *m, int on);
 /* How activations and outputs cross PCIe on the GPU path:
  * QD_IO_STAGED: x is copied into HBM and y back from HBM around the launches
  * (the traffic pattern of a ggml backend whose buffers are device memory);
@@ -116,6 +122,10 @@ QD_API int qd_set_io(qd_model *m, int mode);
  * backend's split of a graph.  qd_last_launches counts MUL_MAT nodes. */
 #define QD_WAIT_PLUGIN 3
 QD_API int qd_set_wait(qd_model *m, int mode);
+/* QD_WAIT_PLUGIN: how the plugin's graph_compute runs a group
+ * (GGML_MI355X_GROUPS_SERVER, the default, or GGML_MI355X_GROUPS_LAUNCH of
+ * ggml-mi355x.h). */
+QD_API int qd_set_plugin_groups(qd_model *m, int mode);
 QD_API int qd_last_wait(const qd_model *m);
 /* Kernel variant of the GPU GEMVs (MI355X_OPT_VARIANT of mi355x-gemv.h):
  * MI355X_VARIANT_GGML_Q8 gives ggml-cpu's Q8_0-activation arithmetic. */

@@ -41,6 +41,7 @@ _c = ctypes
 _vp = _c.c_void_p
 _SIGNATURES = {
     "mi355x_last_error": (_c.c_char_p, []),
+    "mi355x_inject_fault": (_c.c_int, [_c.c_char_p, _c.c_int, _c.c_int]),
     "mi355x_device_count": (_c.c_int, [_c.POINTER(_c.c_int)]),
     "mi355x_ctx_create": (_c.c_int, [_c.c_int, _c.POINTER(_vp)]),
     "mi355x_ctx_destroy": (None, [_vp]),
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "mi355x_free": (_c.c_int, [_vp, _vp]),
     "mi355x_host_malloc": (_c.c_int, [_c.c_size_t, _c.POINTER(_vp)]),
     "mi355x_host_free": (_c.c_int, [_vp]),
+    "mi355x_host_device_ptr": (_c.c_int, [_vp, _c.POINTER(_vp)]),
     "mi355x_memcpy_h2d": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
     "mi355x_memcpy_d2h": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
     "mi355x_memcpy_d2d": (_c.c_int, [_vp, _vp, _vp, _c.c_size_t]),
@@ -93,6 +95,16 @@ class GemvJob(_c.Structure):
 
 
 MULTI_MAX_JOBS = 8
+# device id of a host-only context (no GPU; every device call fails)
+DEVICE_HOST_ONLY = -1
+# hipError_t values used with mi355x_inject_fault
+HIP_ERROR_OUT_OF_MEMORY, HIP_ERROR_NO_DEVICE, HIP_ERROR_ILLEGAL_ADDRESS, HIP_ERROR_LAUNCH_FAILURE = 2, 100, 700, 719
+
+
+def inject_fault(entry: str | None, hip_error: int = 0, skip: int = 0) -> None:
+    """Arms a one-shot injected HIP error on the C-ABI entry point `entry`
+    ("*": any device entry point) after `skip` more calls; None disarms."""
+    check(load().mi355x_inject_fault(entry.encode() if entry else None, hip_error, skip))
 
 _lib = None
 
