@@ -330,9 +330,9 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         model.generate(prompt[:8], 4)  # places the weights in the plugin's buffer
         plugin_toks, tp, _ = run()
         plugin_nodes = model.last_launches() / passes
-        model.set_plugin_groups(model.PLUGIN_GROUPS_LAUNCH)
-        pl_toks, tpl, _ = run()
         model.set_plugin_groups(model.PLUGIN_GROUPS_SERVER)
+        pl_toks, tpl, _ = run()
+        model.set_plugin_groups(model.PLUGIN_GROUPS_LAUNCH)
         model.set_wait(model.WAIT_SERVER)
         # beyond config 5's split: the FFN (gate|up, SiLU, down) as one
         # server command, and whole-layer block commands
@@ -346,8 +346,8 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
         dg_toks, td, dg_tok_s = run()
         log(f"bench: decode (ggml Q8_0 numerics): launch + fence {passes / tf['gen_s']:.1f} tok/s; "
             f"hipStreamSynchronize waits {passes / tw['gen_s']:.1f} tok/s; staged I/O {passes / ts['gen_s']:.1f} "
-            f"tok/s; through the ggml plugin's graph_compute {passes / tp['gen_s']:.1f} tok/s (server), "
-            f"{passes / tpl['gen_s']:.1f} tok/s (launches); beyond the "
+            f"tok/s; through the ggml plugin's graph_compute {passes / tp['gen_s']:.1f} tok/s (launches), "
+            f"{passes / tpl['gen_s']:.1f} tok/s (server); beyond the "
             f"MUL_MAT split: SwiGLU commands {passes / tsw['gen_s']:.1f}, block commands "
             f"{passes / tb['gen_s']:.1f} tok/s")
         log(f"bench: decode: GPU {tok_s:.1f} tok/s in ggml Q8_0 numerics, MUL_MATs only on the GPU "
@@ -385,14 +385,12 @@ def decode_leg(n_prompt: int, n_gen: int, cpu: bool):
                                "weights are ggml tensors in the plugin's weight buffer (set_tensor prepacks them), "
                                "activation and outputs tensors of its compute buffer; per group the activation goes "
                                "in (set_tensor_async: into the buffer's page-locked shadow), one graph_compute runs "
-                               "the group's MUL_MAT nodes as one command to the device's persistent GEMV server "
-                               "(outputs into the shadow), the outputs come out (get_tensor_async: memcpy), then "
-                               "synchronize"),
+                               "the group's MUL_MAT nodes as one launch that reads and writes the shadow and waits "
+                               "for it, the outputs come out (get_tensor_async: memcpy), then synchronize"),
                        "mul_mat_nodes_per_token": plugin_nodes,
-                       "launch_groups": brief(tpl, pl_toks, gq_toks,
-                                              "the same, graph_compute running each group as one launch that reads "
-                                              "and writes the shadow, then a wait on a completion word "
-                                              "(GGML_MI355X_GROUPS_LAUNCH)")},
+                       "server_groups": brief(tpl, pl_toks, gq_toks,
+                                              "the same, graph_compute sending each group as one command to the "
+                                              "device's persistent GEMV server (GGML_MI355X_GROUPS_SERVER)")},
             "beyond_split": {
                 "note": "not config 5's split (non-MUL_MAT ops on the GPU); labelled extras",
                 "swiglu_commands": brief(tsw, sw_toks, gq_toks, "server commands per GEMV group with gate|up, "
@@ -600,20 +598,28 @@ def main() -> int:
                    "N": N, "K": K, "weight_type": "Q4_0", "rotate_copies": copies,
                    "launches_per_step": LAUNCHES_PER_STEP, "launches_timed": launches,
                    "launch_overlap": overlap, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "note": "achieved = algorithmic bytes / mean time per launch of the timed back-to-back "
-                             "launches (HIP events on the library's stream" +
-                             (", after it has joined the other streams): consecutive launches overlap "
-                              "(MI355X_OPT_OVERLAP), so a kernel trace shows each kernel running longer than the "
-                              "launch interval" if overlap else
-                              "): each launch starts after the previous one ends, so the figure includes the "
-                              "gap between kernels")},
+        # the roofline of the kernel: its own duration, which in-order
+        # launches expose (each starts after the previous one ends, so the
+        # HIP-event interval is the kernel plus the dispatch gap) and which a
+        # rocprofv3 kernel trace of the same command reports; overlapped
+        # launches sustain `value`, but a trace serialises them
+        "roofline": {"bound": "hbm", "achieved": round(alg / (ms_seq * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / (ms_seq * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "note": f"achieved = {alg} algorithmic bytes per launch / {ms_seq * 1e3:.3f} us, the mean "
+                             f"interval of {launches} in-order launches on the library's stream (HIP events): the "
+                             "kernel's duration plus the dispatch gap, the figure a rocprofv3 kernel trace of the "
+                             "same command gives per dispatch; with up to "
+                             f"{overlap or 1} launches in flight the same kernel sustains `value`"},
         "in_order": {"us_per_launch": round(ms_seq * 1e3, 3), "GB/s": round(alg / (ms_seq * 1e-3) / 1e9, 2),
                      "frac": round(alg / (ms_seq * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "note": "the same launches on one stream, each starting after the previous one ends "
                              "(includes the gap between kernels); this is the rate a caller whose GEMVs depend "
                              "on each other sees -- the decode and the plugin's graph_compute"},
+        "overlapped": {"us_per_launch": round(ms * 1e3, 3), "GB/s": round(gbs, 2),
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "streams": overlap,
+                       "note": "`value`: consecutive independent launches, up to `streams` in flight "
+                               "(MI355X_OPT_OVERLAP), HIP events on the library's stream after it has joined the "
+                               "others; each launch's start overlaps the previous ones' drain"},
         "cache_hot": {"us_per_launch": round(ms_hot * 1e3, 3),
                       "GB/s": round(alg / (ms_hot * 1e-3) / 1e9, 2),
                       "note": "single resident copy, served partly from MALL/L2; not the HBM figure"},

@@ -120,12 +120,12 @@ GGML_MI355X_API bool ggml_backend_mi355x_set_kernel_variant(struct ggml_backend 
  * moves them with memcpy instead of copy commands.  graph_compute runs a
  * group of consecutive single-row MUL_MATs that share such an activation,
  * with every output host-resident, as
- *   GGML_MI355X_GROUPS_SERVER (default): Q4_0 rows of a multiple of 256
- *     values (up to 16384) as one command to the backend's persistent GEMV
- *     server (mi355x_server_gemv: no launch; returns with the outputs in the
- *     shadow); other groups as GGML_MI355X_GROUPS_LAUNCH;
- *   GGML_MI355X_GROUPS_LAUNCH: one launch reading and writing the shadow
- *     through its device address, then a wait on a completion word.
+ *   GGML_MI355X_GROUPS_LAUNCH (default): one launch reading and writing the
+ *     shadow through its device address, then a wait on a completion word;
+ *   GGML_MI355X_GROUPS_SERVER: Q4_0 rows of a multiple of 256 values (up to
+ *     16384) as one command to the device's persistent GEMV server
+ *     (mi355x_server_gemv: no launch; returns with the outputs in the
+ *     shadow); other groups as GGML_MI355X_GROUPS_LAUNCH.
  * Either way graph_compute returns after every kernel that touches a shadow
  * has finished.  False for a backend of another type or an unknown mode. */
 #define GGML_MI355X_GROUPS_SERVER 0

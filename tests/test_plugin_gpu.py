@@ -609,5 +609,5 @@ def test_injected_device_error_fails_the_graph_then_recovers(plugin, oracle, gro
             check_gemv(read_f32(buf, d, N), ref, oracle.row_norms(Q4_0, raw, N, K), x, "after the injected error")
     finally:
         mi355x.inject_fault(None)
-        plugin.lib.ggml_backend_mi355x_set_group_mode(plugin.backend.addr, gh.GROUPS_SERVER)
+        plugin.lib.ggml_backend_mi355x_set_group_mode(plugin.backend.addr, gh.GROUPS_LAUNCH)
         buf.free()

@@ -174,7 +174,7 @@ def test_decode_layer_groups(plugin, oracle, group_mode, variant):
             check_gemv(ych, oracle.gemv(Q4_0, raws[7], 1024, H, yq), oracle.row_norms(Q4_0, raws[7], 1024, H), yq,
                        "chain")
     finally:
-        mode(plugin, gh.GROUPS_SERVER)
+        mode(plugin, gh.GROUPS_LAUNCH)
         cbuf.free()
         wbuf.free()
 
@@ -199,7 +199,7 @@ def test_modes_are_bit_identical_in_ggml_numerics(plugin):
             outs.append(read_f32(cbuf, d, N))
         assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
     finally:
-        mode(plugin, gh.GROUPS_SERVER)
+        mode(plugin, gh.GROUPS_LAUNCH)
         cbuf.free()
         wbuf.free()
 
@@ -237,6 +237,7 @@ def test_large_outputs_and_batched_nodes_use_device_memory(plugin, ctx, oracle):
         for m in range(2):
             check_gemv(y2[m], oracle.gemv(Q4_0, raw2, 64, 512, xs[m]), norms, xs[m], f"M=2 row {m}")
     finally:
+        mode(plugin, gh.GROUPS_LAUNCH)
         cbuf.free()
         wbuf.free()
 
@@ -278,5 +279,62 @@ def test_server_and_launched_kernels_alternate(plugin, oracle):
         check_gemv(yk, oracle.gemv(12, rawk, 512, H, x), oracle.row_norms(12, rawk, 512, H), x, "q4_k")
         check_gemv(y2, oracle.gemv(Q4_0, raw, H, H, y1), n0, y1, "q4_0 chained")
     finally:
+        mode(plugin, gh.GROUPS_LAUNCH)
         cbuf.free()
         wbuf.free()
+
+
+def test_views_partial_overlaps_and_large_fills(plugin, ctx):
+    """Writes through views (parts of a tensor become host-resident), a
+    device-side copy into another part, and fills larger than the
+    host-resident size: every read returns the last write, byte for byte."""
+    cbuf = plugin.buft.alloc(8 << 20)
+    try:
+        cbuf.set_usage(gh.USAGE_COMPUTE)
+        cbuf.call("clear", 0)
+        n = 4096
+        base = f32_tensor(cbuf, None, [n], b"base")
+        want = np.zeros(n, np.float32)
+        # views of 256 floats at a few offsets, written through set_tensor
+        for i, off in enumerate((0, 1000, 3840)):
+            v = gh.tensor(gh.TYPE_F32, [256], gh.contiguous_nb(4, 1, [256, 1, 1, 1]), b"view")
+            v.buffer, v.data, v.view_src = base.buffer, base.data + 4 * off, C.addressof(base)
+            vals = np.arange(256, dtype=np.float32) + 1000 * (i + 1)
+            cbuf.call("set_tensor", C.addressof(v), vals.ctypes.data, 0, vals.nbytes)
+            want[off:off + 256] = vals
+        assert np.array_equal(read_f32(cbuf, base, n), want)
+        # a device-to-device copy into [2000, 2256) from a host-resident tensor
+        src = f32_tensor(cbuf, -np.ones(256, np.float32), [256], b"src")
+        dv = gh.tensor(gh.TYPE_F32, [256], gh.contiguous_nb(4, 1, [256, 1, 1, 1]), b"dview")
+        dv.buffer, dv.data, dv.view_src = base.buffer, base.data + 4 * 2000, C.addressof(base)
+        assert cbuf.call("cpy_tensor", C.addressof(src), C.addressof(dv))
+        want[2000:2256] = -1.0
+        assert np.array_equal(read_f32(cbuf, base, n), want)
+        # odd-sized byte ranges straddling host-resident and device parts
+        raw = np.frombuffer(cbuf.get(base, 4 * n), np.uint8)
+        for off, size in ((3, 5), (990 * 4 + 1, 40 * 4), (3839 * 4, 8), (0, 4 * n)):
+            assert cbuf.get(base, size, off) == raw[off:off + size].tobytes(), (off, size)
+        # a fill of a tensor above 1 MiB goes to the device and covers the
+        # host-resident ranges inside it
+        big = f32_tensor(cbuf, None, [300000], b"big")
+        small = gh.tensor(gh.TYPE_F32, [100], gh.contiguous_nb(4, 1, [100, 1, 1, 1]), b"in_big")
+        small.buffer, small.data, small.view_src = big.buffer, big.data + 4 * 5000, C.addressof(big)
+        cbuf.call("set_tensor", C.addressof(small), np.full(100, 7.0, np.float32).ctypes.data, 0, 400)
+        cbuf.call("memset_tensor", C.addressof(big), 0, 0, 4 * 300000)
+        assert not read_f32(cbuf, small, 100).any()
+        assert not device_bytes(ctx, big, 4 * 300000).any()
+    finally:
+        cbuf.free()
+
+
+def test_usage_set_after_allocation(plugin, ctx):
+    """ggml allocates a buffer, then marks it WEIGHTS: a buffer marked before
+    its first write never gets a shadow (its small tensors are device bytes
+    from the first write on)."""
+    buf = plugin.buft.alloc(1 << 16)
+    try:
+        buf.set_usage(gh.USAGE_WEIGHTS)
+        t = f32_tensor(buf, np.full(64, 3.0, np.float32), [64], b"bias")
+        assert np.array_equal(device_bytes(ctx, t, 256).view(np.float32), np.full(64, 3.0, np.float32))
+    finally:
+        buf.free()

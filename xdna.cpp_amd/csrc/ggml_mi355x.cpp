@@ -789,7 +789,9 @@ struct BackendCtx {
     // outputs are host-resident (made on first use; none where the device
     // has no cooperative launch)
     int variant = MI355X_VARIANT_AUTO;
-    int group_mode = GGML_MI355X_GROUPS_SERVER;
+    // launches measured ahead of server commands for the 3B decode (285-290
+    // against 279-287 tok/s on the same boxes)
+    int group_mode = GGML_MI355X_GROUPS_LAUNCH;
 
     ~BackendCtx() {
         if (ctx) {

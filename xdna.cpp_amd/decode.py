@@ -197,8 +197,8 @@ class Model:
     PLUGIN_GROUPS_SERVER, PLUGIN_GROUPS_LAUNCH = 0, 1
 
     def set_plugin_groups(self, mode: int) -> None:
-        """WAIT_PLUGIN: graph_compute runs a group as a server command
-        (PLUGIN_GROUPS_SERVER, default) or one launch (PLUGIN_GROUPS_LAUNCH)."""
+        """WAIT_PLUGIN: graph_compute runs a group as one launch
+        (PLUGIN_GROUPS_LAUNCH, default) or a server command (PLUGIN_GROUPS_SERVER)."""
         if self.lib.qd_set_plugin_groups(self.h, mode) != 0:
             raise RuntimeError(self.lib.qd_last_error().decode())
 

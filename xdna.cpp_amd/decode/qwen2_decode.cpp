@@ -203,7 +203,7 @@ struct qd_model {
     bool fuse = true;         // one launch for matrices that are adjacent in HBM
     bool block = true;        // server mode: o through down as one command
     bool swiglu = true;       // server mode: gate|up, SiLU, down as one command
-    int plugin_groups = GGML_MI355X_GROUPS_SERVER;  // plugin mode: how graph_compute runs a group
+    int plugin_groups = GGML_MI355X_GROUPS_LAUNCH;  // plugin mode: how graph_compute runs a group
     int64_t last_launches = 0;
     float *dx = nullptr, *dy = nullptr;  // activation in, outputs out
     float *ffn_norm_dev = nullptr;       // the FFN norm weights, n_layers * hidden

@@ -123,7 +123,7 @@ QD_API int qd_set_io(qd_model *m, int mode);
 #define QD_WAIT_PLUGIN 3
 QD_API int qd_set_wait(qd_model *m, int mode);
 /* QD_WAIT_PLUGIN: how the plugin's graph_compute runs a group
- * (GGML_MI355X_GROUPS_SERVER, the default, or GGML_MI355X_GROUPS_LAUNCH of
+ * (GGML_MI355X_GROUPS_LAUNCH, the default, or GGML_MI355X_GROUPS_SERVER of
  * ggml-mi355x.h). */
 QD_API int qd_set_plugin_groups(qd_model *m, int mode);
 QD_API int qd_last_wait(const qd_model *m);
