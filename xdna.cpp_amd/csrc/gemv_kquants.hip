@@ -131,11 +131,15 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, const t
 template <int TYPE, int R, int NIT, bool DG, bool PF>
 __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     using K = Kq<TYPE>;
+    // the codebook in static LDS (its address is known when the lookups are
+    // compiled, so no base is added per lookup), the lane-major records (f32
+    // or digit) in the dynamic LDS
     extern __shared__ float4 lds_kq[];
-    // lane-major records (f32 or digit), then the codebook
+    constexpr int kTableWords = DG ? dg_table_words(TYPE) : Kq<TYPE>::kGrid;
+    __shared__ uint32_t table_kq[kTableWords > 0 ? kTableWords : 1];
     constexpr int SH = slice_shape(TYPE);
+    uint32_t *grid = table_kq;
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_kq);
-    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + (DG ? dg_lds_bytes(a.nb) : x_lds_bytes(a.nb)));
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1179,39 +1183,35 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
     const int64_t n_chunks = (B + kChunkBlocks - 1) / kChunkBlocks;
     const int64_t per_chunk = (B + n_chunks - 1) / n_chunks;
     // Default forms (variant and form AUTO), from sweeps of the BASELINE
-    // shapes on MI355X (us, 14336x4096 / 4096x14336; 8192x8192 for IQ):
-    //  * Q4_K: digit rows (9.8 vs pipelined 10.0, f32 rows 10.4 at two
-    //    steps; 10.5 vs 11.6 f32 at seven);
-    //  * Q5_K: digit rows, with prefetch up to two steps (10.3 vs 10.9
-    //    without, pipelined 11.1; 11.8 vs f32 12.9 at seven steps, where
-    //    prefetch costs 0.9);
-    //  * Q6_K: digit rows up to two steps (11.8-12.0 vs pipelined 12.6, f32
-    //    11.9 with prefetch), f32 rows beyond (13.7 vs 13.9 digits);
-    //  * IQ3_S, IQ3_XXS, IQ2_S up to four steps (N >= 4096): digit rows, two
-    //    rows per wavefront step (12.4 / 11.1 / 11.2 vs one row 12.5 / 10.9
-    //    / 11.4, f32 14.0 / 12.7 / 12.2): table-driven sign application and
-    //    dot4 products cost fewer VALU instructions than the f32 decode;
-    //  * IQ4_XS up to four steps: digit rows (11.4 vs f32 11.6-11.8);
-    //  * Q3_K and the rest: f32 rows, one row per step, with prefetch up to
-    //    two steps (Q3_K 10.5 vs 10.8 without, 12.0-12.3 digits; 12.0 vs
-    //    13.1 with prefetch at seven steps).
+    // shapes on MI355X (us, 14336x4096 / 4096x14336; 8192x8192 for IQ;
+    // boxes differ by up to ~0.4 us):
+    //  * Q4_K, Q5_K, Q6_K: digit rows, one row per step (Q4_K 8.1 / 9.9,
+    //    Q5_K 9.7 / 11.4, Q6_K 11.1 / 13.3; prefetch 0.2-2 us slower, f32
+    //    rows 13.7 for Q6_K at seven steps);
+    //  * Q3_K: digit rows, with prefetch up to two steps (10.3 vs 10.4
+    //    without and 10.5 for f32 rows with prefetch; 12.0 vs f32 12.4 at
+    //    seven steps);
+    //  * IQ4_XS up to four steps: digit rows (10.9 vs f32 11.6-11.8);
+    //  * IQ3_S, IQ2_S up to four steps (N >= 4096): digit rows, two rows per
+    //    wavefront step (11.7 / 10.8 vs one row 11.8 / 11.2); IQ3_XXS one row
+    //    (10.3 vs 10.7): table-driven sign application and dot4 products cost
+    //    fewer VALU instructions than the f32 decode (f32 14.0 / 12.2 / 12.7).
     // Prefetch (the next row group requested before the current one's
-    // decode) pays where a wavefront has several short groups; with long
-    // rows it lets every wavefront's second group compete with the first
-    // groups' loads and costs more than it hides.
+    // decode) pays only for Q3_K's short rows; elsewhere, it lets every
+    // wavefront's second group compete with the first groups' loads and the
+    // second register set lowers the occupancy.
     const bool auto_form = ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO;
     auto dg_rows_auto = [&](int nit) {
         switch (a.type) {
+        case MI355X_TYPE_Q3_K:
         case MI355X_TYPE_Q4_K:
-        case MI355X_TYPE_Q5_K: return true;
-        case MI355X_TYPE_Q6_K: return nit <= 2;
+        case MI355X_TYPE_Q5_K:
+        case MI355X_TYPE_Q6_K: return true;
         case MI355X_TYPE_IQ4_XS: return nit <= 4;
         default: return grid_type && nit <= max_nit_r2(a.type) && a.N >= 4096;
         }
     };
-    auto pf_auto = [&](int nit) {
-        return auto_form && nit <= 2 && (a.type == MI355X_TYPE_Q5_K || a.type == MI355X_TYPE_Q3_K);
-    };
+    auto pf_auto = [&](int nit) { return auto_form && nit <= 2 && a.type == MI355X_TYPE_Q3_K; };
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
         const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
@@ -1263,14 +1263,15 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         }
         const bool dg_auto = ctx->kernel_variant == MI355X_VARIANT_AUTO && dg_rows_auto(nit);
         const bool dg = dg_forced || dg_auto;
-        int R = dg_auto && grid_type ? 2 : 1;
+        int R = dg_auto && (a.type == MI355X_TYPE_IQ3_S || a.type == MI355X_TYPE_IQ2_S) ? 2 : 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const bool pf = R == 1 && (ctx->prefetch_override == 1 || (ctx->prefetch_override == 0 && pf_auto(nit)));
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf);
         const int64_t n_groups = (a.N + R - 1) / R;
-        const size_t lds = (dg ? dg_lds_bytes(nb) : x_lds_bytes(nb)) +
-                           (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u;
-        if (lds > ctx->max_lds_per_block) return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
+        // dynamic LDS: the records (the codebook is the kernel's static LDS)
+        const size_t lds = dg ? dg_lds_bytes(nb) : x_lds_bytes(nb);
+        if (lds + (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u > ctx->max_lds_per_block)
+            return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
         const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
         int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
         if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);

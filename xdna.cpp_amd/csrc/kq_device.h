@@ -728,29 +728,47 @@ struct KqDg<MI355X_TYPE_Q6_K> {
 
 template <>
 struct KqDg<MI355X_TYPE_Q3_K> {
+    // Run j's 3-bit codes (2 code bits + the hmask bit) are formed in place,
+    // scaled by 1, 4, 16, 16 for j = 0..3 -- code bits kept where they sit in
+    // the byte (moved down two for j = 3, whose top bits would read as a
+    // negative byte), the hmask bit ORed in above them -- so each costs a
+    // mask and an OR.  Every scaled code is a multiple of its scale and below
+    // 128, so the plane sums are exact multiples of it and combine_shr
+    // divides it out exactly: the sums equal those of the unscaled codes.
+    template <int SHR>
+    __device__ static int combine_shr(const int (&s)[3]) {
+        return (s[0] >> SHR) + s[1] * (1 << (8 - SHR)) + s[2] * (1 << (16 - SHR));
+    }
     __device__ static float compute(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
         int sg[4][3] = {};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t code =
-                    ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
-                dot3(code, x, 2 * j + w, sg[j], w == 0);
-            }
+            const uint32_t q = g.q[w];
+            const uint32_t hs = g.hm[w] >> (4 * hh);  // bit j of each byte: run j's high bit
+            dot3((q & 0x03030303u) | ((hs << 2) & 0x04040404u), x, 0 + w, sg[0], w == 0);
+            dot3((q & 0x0C0C0C0Cu) | ((hs << 3) & 0x10101010u), x, 2 + w, sg[1], w == 0);
+            dot3((q & 0x30303030u) | ((hs << 4) & 0x40404040u), x, 4 + w, sg[2], w == 0);
+            dot3(((q >> 2) & 0x30303030u) | ((hs << 3) & 0x40404040u), x, 6 + w, sg[3], w == 0);
         }
+        // The four 6-bit scales sidx = 8hh + kk + 2j (kk = k / 2) in one word,
+        // bytes in run order 0, 2, 1, 3: low nibbles from bytes kk, kk + 2
+        // (word 0) and kk + 4, kk + 6 (word 1) of scales[0..7], nibble hh; high
+        // bit pairs from bytes kk (runs 0, 2) and kk + 2 (runs 1, 3) of
+        // scales[8..11], pairs 2hh and 2hh + 1 (include/xdna/kquants.h:350-389).
         const int kk = k >> 1;
+        const uint32_t L = ((g.sw01[0] >> (8 * kk)) & 0x00FF00FFu) | (((g.sw01[1] >> (8 * kk)) & 0x00FF00FFu) << 8);
+        const uint32_t H = g.sw2 >> (8 * kk + 4 * hh);
+        const uint32_t SC = ((L >> (4 * hh)) & 0x0F0F0F0Fu) | ((H & 0x00030003u) << 4) | ((H & 0x000C000Cu) << 10);
+        const float sc0 = static_cast<float>(SC & 0xFFu) - 32.0f;
+        const float sc2 = static_cast<float>((SC >> 8) & 0xFFu) - 32.0f;
+        const float sc1 = static_cast<float>((SC >> 16) & 0xFFu) - 32.0f;
+        const float sc3 = static_cast<float>(SC >> 24) - 32.0f;
         float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int lo_byte = 2 * j + kk;
-            const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
-            const uint32_t lo = (byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u;
-            const uint32_t hi = (byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
-            const float sc = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
-            acc = fmaf(sc, ldexpf(combine_i(sg[j]) - 4.0f * x.zs[j], x.e[j]), acc);
-        }
+        acc = fmaf(sc0, ldexpf(static_cast<float>(combine_shr<0>(sg[0])) - 4.0f * x.zs[0], x.e[0]), acc);
+        acc = fmaf(sc1, ldexpf(static_cast<float>(combine_shr<2>(sg[1])) - 4.0f * x.zs[1], x.e[1]), acc);
+        acc = fmaf(sc2, ldexpf(static_cast<float>(combine_shr<4>(sg[2])) - 4.0f * x.zs[2], x.e[2]), acc);
+        acc = fmaf(sc3, ldexpf(static_cast<float>(combine_shr<4>(sg[3])) - 4.0f * x.zs[3], x.e[3]), acc);
         return half_f(g.d) * acc;
     }
 };
