@@ -235,26 +235,6 @@ constexpr int kPlqDepth = 3;
 constexpr int kPlqStageBlocks = 2;  // records staged per thread
 static_assert(kChunkBlocks <= kBlocksPerStep * kPlqWaves * kPlqStageBlocks, "staging covers a chunk");
 
-// Buffer view of one row; rows at or past `lim` get an empty range.
-template <int TYPE>
-__device__ __forceinline__ Row make_row_pl(const KqArgs &a, int64_t row, int64_t lim) {
-    constexpr KqLayout L = kq_layout(TYPE);
-    const uint8_t *base = a.W + row * a.row_bytes;
-    Row r;
-    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
-                                               row < lim ? static_cast<uint32_t>(a.row_bytes) : 0u, kBufferWord3);
-    const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
-    if constexpr (L.grouped) {
-        r.P[0] = static_cast<uint32_t>(a.B);
-        r.P[1] = flipped ? 1u : 0u;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 5; ++i)
-            r.P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
-    }
-    return r;
-}
-
 template <int TYPE, int NIT, bool XREG>
 __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int rows) {
     using K = Kq<TYPE>;

@@ -82,6 +82,26 @@ __device__ __forceinline__ u32x3 ld96(const Row &r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b96(r.rsrc, static_cast<int>(off), 0, kNonTemporal);
 }
 
+// Buffer view of one row; rows at or past `lim` get an empty range.
+template <int TYPE>
+__device__ __forceinline__ Row make_row_pl(const KqArgs &a, int64_t row, int64_t lim) {
+    constexpr KqLayout L = kq_layout(TYPE);
+    const uint8_t *base = a.W + row * a.row_bytes;
+    Row r;
+    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
+                                               row < lim ? static_cast<uint32_t>(a.row_bytes) : 0u, kBufferWord3);
+    const bool flipped = kq_row_flipped(reinterpret_cast<uintptr_t>(base));
+    if constexpr (L.grouped) {
+        r.P[0] = static_cast<uint32_t>(a.B);
+        r.P[1] = flipped ? 1u : 0u;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 5; ++i)
+            r.P[i] = i < L.nfields ? static_cast<uint32_t>(kq_plane_start(L, i, a.B, flipped)) : 0u;
+    }
+    return r;
+}
+
 // Group-layout position of superblock b for slice s (kq_layout.h): the
 // group's start, its size g, the lane record index s * g + bl and the fp16
 // d's offset.  Row.P[0] holds B and P[1] the row's flip for these types.
