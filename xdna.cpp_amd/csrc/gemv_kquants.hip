@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kPlqThreads) void gemv_kq_pl_kernel(KqArgs a, int r
     for (int j = 0; j < kPlqStageBlocks; ++j) {
         const int rt = wave + kPlqWaves * j;
         if (kBlocksPerStep * rt < a.nb)
-            put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lane, xv[j], kBlocksPerStep * rt + bl < a.nb);
+            put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lm_chunk(lane), xv[j], kBlocksPerStep * rt + bl < a.nb);
     }
     gr.put_dg(grid, threadIdx.x, kPlqThreads);
     __builtin_amdgcn_sched_barrier(0);
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(kXsThreads) void gemv_kq_xs_kernel(KqArgs a, int G,
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. digit records into LDS (waits for the activation loads only); codebook
-    if (wave < S) put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lane, xv, rbc < a.nb);
+    if (wave < S) put_record_dg<SH>(lds + kDgGroupBytes * rt + 16 * lm_chunk(lane), xv, rbc < a.nb);
     gr.put_dg(grid, threadIdx.x, nthr);
     __syncthreads();
 

@@ -132,10 +132,11 @@ struct XSlice {
 
 // ---- lane-major activation staging ---------------------------------------------
 // At step t of a row, lane l = 8 s + bl works on slice s of superblock
-// 8 t + bl.  Staging stores each (superblock, slice) record at index l of
-// its superblock's 8-superblock group, in 16-byte slots laid out
-// [slot][lane]: every slot read of the row loops is one contiguous 1 KB per
-// wavefront, which the LDS serves at its full rate whatever the slice shape.
+// 8 t + bl.  Staging stores each (superblock, slice) record at position
+// lm_chunk(l) of its superblock's 8-superblock group, in 16-byte slots laid
+// out [slot][position]: every slot read of the row loops is one contiguous
+// 1 KB per wavefront, which the LDS serves at its full rate whatever the
+// slice shape.
 // (A superblock-major layout, even padded, leaves the Q4_K and Q6_K slice
 // shapes and the digit slices with 2- and 3-way bank conflicts, measured
 // with SQ_LDS_BANK_CONFLICT on MI355X.)
@@ -164,9 +165,16 @@ __device__ __forceinline__ int run_of(int s, int p) {
 constexpr int kLmSlot = 16 * 64;                // bytes of one slot row (64 records)
 constexpr int kXGroupBytes = 9 * kLmSlot;       // f32: 8 value slots, the run sums
 constexpr int kDgGroupBytes = 8 * kLmSlot;      // digits: 3 planes x 2, exponents, Z sums
+// 16-byte position of record l = 8s + bl in its slot rows: l with bits 1-2
+// XORed by bits 4-5.  Readers take one record per lane (a permutation of
+// the 64 positions either way); the row kernels' staging stores (one 8-value
+// run per lane, so a wavefront writes the records of two superblocks, all
+// eight slices each) then fall on 16 distinct positions, i.e. every LDS
+// bank, instead of 4.
+__device__ __forceinline__ int lm_chunk(int l) { return l ^ (((l >> 4) & 3) << 1); }
 // byte offset of the record of slice s of chunk superblock bc
 __device__ __forceinline__ int lm_record(int group_bytes, int bc, int s) {
-    return group_bytes * (bc >> 3) + 16 * (8 * s + (bc & 7));
+    return group_bytes * (bc >> 3) + 16 * lm_chunk(8 * s + (bc & 7));
 }
 constexpr size_t x_lds_bytes(int nb) { return static_cast<size_t>((nb + 7) / 8) * kXGroupBytes; }
 constexpr size_t dg_lds_bytes(int nb) { return static_cast<size_t>((nb + 7) / 8) * kDgGroupBytes; }
