@@ -379,6 +379,8 @@ constexpr scores_fn kScores[8] = {scores_block<1>, scores_block<2>, scores_block
 constexpr pv_fn kPv[8] = {pv_slice<1>, pv_slice<2>, pv_slice<3>, pv_slice<4>,
                           pv_slice<5>, pv_slice<6>, pv_slice<7>, pv_slice<8>};
 
+constexpr int kAttThreads = 8;
+
 void attention(const float *q, const float *K, const float *V, int n_t, int tcap, int n_heads, int n_kv, int hd,
                float *sc, float *att) {
     const int group = n_heads / n_kv;
@@ -386,8 +388,9 @@ void attention(const float *q, const float *K, const float *V, int n_t, int tcap
     const int hb_count = (group + 7) / 8;  // blocks of up to 8 heads per KV head
     const int n_chunks = (n_t + 31) / 32;  // score blocks: enough tasks for a 16-thread team
     const int n_slices = hd / 8;
-    // a thread team pays off only for long contexts
-#pragma omp parallel if (n_t >= 64)
+    // a thread team pays off only for long contexts, and a team of more
+    // than kAttThreads costs more in synchronisation than it saves
+#pragma omp parallel if (n_t >= 64) num_threads(std::min(omp_get_max_threads(), kAttThreads))
     {
 #pragma omp for collapse(3) schedule(static)
         for (int g = 0; g < n_kv; ++g)
