@@ -2031,10 +2031,10 @@ q8j_kernel_t pick_q8j_at(bool a16, bool tail) {
     return tail ? gemv_q4_0_q8j_kernel<NBL, R, false, true> : gemv_q4_0_q8j_kernel<NBL, R, false, false>;
 }
 
-q8j_kernel_t pick_q8j(int nbl, bool a16, bool tail) {
+q8j_kernel_t pick_q8j(int nbl, int R, bool a16, bool tail) {
     switch (nbl) {
-    case 1: return pick_q8j_at<1, 4>(a16, tail);
-    case 2: return pick_q8j_at<2, 2>(a16, tail);
+    case 1: return R == 4 ? pick_q8j_at<1, 4>(a16, tail) : R == 2 ? pick_q8j_at<1, 2>(a16, tail) : pick_q8j_at<1, 1>(a16, tail);
+    case 2: return R == 2 ? pick_q8j_at<2, 2>(a16, tail) : pick_q8j_at<2, 1>(a16, tail);
     case 3: return pick_q8j_at<3, 1>(a16, tail);
     case 4: return pick_q8j_at<4, 1>(a16, tail);
     case 5: return pick_q8j_at<5, 1>(a16, tail);
@@ -2044,12 +2044,13 @@ q8j_kernel_t pick_q8j(int nbl, bool a16, bool tail) {
     }
 }
 
-// rows per wavefront as the digit kernel's defaults: 4 for one block
-// column, 2 for two, 1 beyond
-q8_kernel_t pick_q8(int nbl, bool a16, bool tail) {
+// rows per wavefront: R = 4 for one block column, 2 for two, 1 beyond (the
+// digit kernel's defaults), or fewer where R would leave CUs without a group
+// (q8_rows)
+q8_kernel_t pick_q8(int nbl, int R, bool a16, bool tail) {
     switch (nbl) {
-    case 1: return pick_q8_at<1, 4>(a16, tail);
-    case 2: return pick_q8_at<2, 2>(a16, tail);
+    case 1: return R == 4 ? pick_q8_at<1, 4>(a16, tail) : R == 2 ? pick_q8_at<1, 2>(a16, tail) : pick_q8_at<1, 1>(a16, tail);
+    case 2: return R == 2 ? pick_q8_at<2, 2>(a16, tail) : pick_q8_at<2, 1>(a16, tail);
     case 3: return pick_q8_at<3, 1>(a16, tail);
     case 4: return pick_q8_at<4, 1>(a16, tail);
     case 5: return pick_q8_at<5, 1>(a16, tail);
@@ -2152,6 +2153,16 @@ int launch_gemv_q4_0_dp(mi355x_ctx *ctx, const GemvArgs &a) {
 size_t q8_lds_bytes(int64_t B, int cg);
 int q8_chunk_groups(int64_t B, int64_t n_groups, int64_t grid);
 
+// Rows per wavefront of the Q8_0 kernels for `rows` rows: the default for
+// the row length (4 for one block column, 2 for two, 1 beyond), halved while
+// the launch would have fewer row groups (8 R rows each) than CUs -- at the
+// decode's 2048-2560-row matrices R = 4 left 176 of 256 CUs idle.
+int q8_rows(int nbl, int64_t rows, int num_cus) {
+    int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
+    while (R > 1 && (rows + 8 * R - 1) / (8 * R) < num_cus) R /= 2;
+    return R;
+}
+
 // ggml-cpu numerics: the Q8_0 kernel's row groups of every matrix in one
 // launch (row sums in block order by one lane, so bit-identical to one
 // launch per matrix)
@@ -2159,9 +2170,11 @@ static int launch_q8_multi(mi355x_ctx *ctx, int64_t K, const float *x, const Mul
     const int64_t B = K / 32;
     const int64_t row_bytes = 18 * B;
     const int nbl = static_cast<int>((B + 63) / 64);
-    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
     if (n < 1 || n > kPlMaxJobs || B <= 0 || B > kDpMaxBlocks || q8_lds_bytes(B, 1) > ctx->max_lds_per_block)
         return MI355X_OK;
+    int64_t total_rows = 0;
+    for (int j = 0; j < n; ++j) total_rows += std::max<int64_t>(jobs[j].N, 0);
+    const int R = q8_rows(nbl, total_rows, ctx->num_cus);
     bool a16 = row_bytes % 16 == 0;
     PlJobs pj{};
     pj.n = n;
@@ -2177,7 +2190,7 @@ static int launch_q8_multi(mi355x_ctx *ctx, int64_t K, const float *x, const Mul
     }
     if (groups > INT32_MAX) return MI355X_OK;
     pj.first[n] = static_cast<int>(groups);
-    const q8j_kernel_t k = pick_q8j(nbl, a16, B % 64 != 0);
+    const q8j_kernel_t k = pick_q8j(nbl, R, a16, B % 64 != 0);
     // occupancy with the largest chunk, then the chunk this grid needs
     const int occ = occupancy(reinterpret_cast<const void *>(k), 512, q8_lds_bytes(B, q8_chunk_groups(B, groups, 1)));
     int64_t grid = std::min<int64_t>(groups, static_cast<int64_t>(ctx->num_cus) * (nbl >= 3 ? std::min(occ, 2) : occ));
@@ -2276,8 +2289,8 @@ int launch_gemv_q4_0_q8(mi355x_ctx *ctx, const GemvArgs &a) {
     const bool a16 = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(a.W) % 16 == 0);
     const bool x_al16 = reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
     const int nbl = static_cast<int>((B + 63) / 64);
-    const int R = nbl <= 1 ? 4 : (nbl == 2 ? 2 : 1);
-    const q8_kernel_t k = pick_q8(nbl, a16, B % 64 != 0);
+    const int R = q8_rows(nbl, a.N, ctx->num_cus);
+    const q8_kernel_t k = pick_q8(nbl, R, a16, B % 64 != 0);
     const int64_t n_groups = (a.N + 8 * R - 1) / (8 * R);
     // occupancy with the largest chunk, then the chunk this grid needs
     const int occ = occupancy(reinterpret_cast<const void *>(k), 512, q8_lds_bytes(B, q8_chunk_groups(B, n_groups, 1)));
