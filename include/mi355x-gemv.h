@@ -118,10 +118,9 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply;
  *       for the K/IQ types 22-bit activation digits (row form) for Q3_K,
  *       Q4_K, Q5_K and Q6_K, IQ4_XS rows of at most 8192 values, and
- *       IQ3_S/IQ3_XXS/IQ2_S rows of at most 8192 values with N >= 4096 (two
- *       rows per wavefront for IQ3_S and IQ2_S), f32 activations for the
- *       rest: longer IQ rows and smaller IQ matrices; Q3_K rows of at most
- *       4096 values with prefetch),
+ *       IQ3_S/IQ3_XXS/IQ2_S rows of at most 8192 values with N >= 4096, one
+ *       row per wavefront step; f32 activations for the rest: longer IQ rows
+ *       and smaller IQ matrices),
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
  *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit

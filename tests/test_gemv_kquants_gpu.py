@@ -42,14 +42,17 @@ def install_grids():
     yield
 
 
-@pytest.fixture(params=["digits", "exact_f32", "pipelined", "digits_prefetch", "f32_prefetch", "auto"], autouse=True)
+@pytest.fixture(params=["digits", "exact_f32", "pipelined", "digits_prefetch", "f32_prefetch", "digits_two_rows",
+                        "auto"], autouse=True)
 def variant(request, ctx):
     """Every test runs on each kernel family: activations as 22-bit digit
-    planes with integer dot products (several workgroups per CU), f32
-    activations as given, the pipelined form (digit arithmetic, one
-    workgroup per CU, each lane's digit slices kept in registers), the row
-    form with prefetch (each wavefront's next row group requested before
-    the current one's decode) in both arithmetics, and the defaults."""
+    planes with integer dot products (several workgroups per CU; each
+    step's registers refilled with the next row group's step after its
+    decode), f32 activations as given, the pipelined form (digit arithmetic,
+    one workgroup per CU, each lane's digit slices kept in registers), the
+    row form with prefetch (each wavefront's next row group requested before
+    the current one's decode) in both arithmetics, the digit row form with
+    two rows per wavefront step, and the defaults."""
     p = request.param
     if p != "auto":
         v = mi355x.VARIANT_EXACT_F32 if p.startswith(("exact", "f32")) else mi355x.VARIANT_DIGITS
@@ -59,6 +62,8 @@ def variant(request, ctx):
     if p.endswith("prefetch"):
         ctx.set_option(mi355x.OPT_PREFETCH, 1)
         ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 1)
+    if p.endswith("two_rows"):
+        ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 2)
     yield p
     ctx.set_option(mi355x.OPT_VARIANT, mi355x.VARIANT_AUTO)
     ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
@@ -248,3 +253,27 @@ def test_ksplit_tile_rows_option(ctx, variant, name):
         ctx.set_option(mi355x.OPT_ROWS_PER_WAVE, 0)
         ctx.set_option(mi355x.OPT_FORM, mi355x.FORM_AUTO)
     assert np.array_equal(y4.view(np.uint32), yr.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(ALL))
+@pytest.mark.parametrize("N,K", [(1023, 4096), (515, 8192), (257, 14336)])
+def test_many_row_groups_per_wavefront(ctx, name, variant, N, K):
+    """With the grid capped at 1 or 3 workgroups each wavefront walks dozens
+    of row groups: every refill (or prefetch) of the next group's registers
+    lands, the last group's reads nothing, and the rows come out bit for bit
+    as with the full grid (the arithmetic of a row does not depend on which
+    wavefront computes it)."""
+    if variant not in ("digits", "digits_two_rows", "digits_prefetch"):
+        pytest.skip("row-form options only")
+    t = ALL[name]
+    raw = blocks(t, N, K, 5 * N + K)
+    x = np.random.default_rng(N).uniform(-0.5, 0.5, K).astype(np.float32)
+    y_full = run(ctx, t, raw, N, K, x)
+    for cap in (1, 3):
+        ctx.set_option(mi355x.OPT_GRID, cap)
+        try:
+            y_cap = run(ctx, t, raw, N, K, x)
+        finally:
+            ctx.set_option(mi355x.OPT_GRID, 0)
+        bad = np.nonzero(y_cap.view(np.uint32) != y_full.view(np.uint32))[0]
+        assert bad.size == 0, f"{name} {N}x{K} grid {cap}: {bad.size} rows differ, first {bad[:5]}"

@@ -82,12 +82,18 @@ __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, in
 constexpr int kRunsPerThread = (32 * kChunkBlocks + kThreads - 1) / kThreads;
 
 // One row group: its NIT steps against the staged activations, then the
-// wavefront sums and the stores of its R outputs.
-template <int TYPE, int R, int NIT, bool DG>
-__device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, const typename Kq<TYPE>::Regs (&regs)[R][NIT],
-                                             const uint8_t *lds, const uint32_t *grid, int s, int bl, int lane) {
+// wavefront sums and the stores of its R outputs.  With RF the registers of
+// step t are refilled, right after its decode, with step t of row group gn
+// (an empty range when `next` is false: such loads read nothing), so the
+// next group's loads are in flight while the rest of this group decodes.
+template <int TYPE, int R, int NIT, bool DG, bool RF>
+__device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typename Kq<TYPE>::Regs (&regs)[R][NIT],
+                                             const uint8_t *lds, const uint32_t *grid, int s, int bl, int lane,
+                                             int64_t gn = 0, bool next = false) {
     using K = Kq<TYPE>;
     constexpr int SH = slice_shape(TYPE);
+    Row nrows[RF ? R : 1];
+    if constexpr (RF) make_rows<TYPE, R>(a, gn, nrows, next);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -112,6 +118,13 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, const t
                 const float p = K::compute(regs[r][t], s, x, grid);
                 acc[r] += valid ? p : 0.f;
             }
+        }
+        if constexpr (RF) {
+            // after the decode, so the loads reuse its registers
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t babs = static_cast<uint32_t>(a.b0 + bc);
+#pragma unroll
+            for (int r = 0; r < R; ++r) regs[r][t] = K::load(nrows[r], babs, s);
         }
         // one step's activations live at a time (no hoisting of the
         // next step's LDS reads into this one)
@@ -193,20 +206,29 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             for (;;) {
                 const int64_t g1 = g + stride;
                 load_group<TYPE, R, NIT>(a, g1 < n_groups ? g1 : n_groups - 1, s, bl, nxt, g1 < n_groups);
-                kq_row_group<TYPE, R, NIT, DG>(a, g, regs, lds, grid, s, bl, lane);
+                kq_row_group<TYPE, R, NIT, DG, false>(a, g, regs, lds, grid, s, bl, lane);
                 if (g1 >= n_groups) break;
                 const int64_t g2 = g1 + stride;
                 load_group<TYPE, R, NIT>(a, g2 < n_groups ? g2 : n_groups - 1, s, bl, regs, g2 < n_groups);
-                kq_row_group<TYPE, R, NIT, DG>(a, g1, nxt, lds, grid, s, bl, lane);
+                kq_row_group<TYPE, R, NIT, DG, false>(a, g1, nxt, lds, grid, s, bl, lane);
                 if (g2 >= n_groups) break;
                 g = g2;
             }
         }
     } else {
+        // refill per step, except where two rows of four steps are at the
+        // register limit already, and for Q5_K's short rows (0.2-0.3 us
+        // slower with the refill at 14336x4096)
+        constexpr bool RF = (R == 1 || NIT < 4) && !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2);
         for (; g < n_groups; g += stride) {
-            kq_row_group<TYPE, R, NIT, DG>(a, g, regs, lds, grid, s, bl, lane);
             const int64_t gn = g + stride;
-            if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
+            if constexpr (RF) {
+                kq_row_group<TYPE, R, NIT, DG, true>(a, g, regs, lds, grid, s, bl, lane,
+                                                     gn < n_groups ? gn : n_groups - 1, gn < n_groups);
+            } else {
+                kq_row_group<TYPE, R, NIT, DG, false>(a, g, regs, lds, grid, s, bl, lane);
+                if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
+            }
         }
     }
 }
@@ -804,6 +826,7 @@ __device__ __forceinline__ void k6_partial(const Kq<MI355X_TYPE_Q6_K>::Regs &g, 
 __device__ __forceinline__ void k3_partial(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const int8_t *q8,
                                            int (&part)[8]) {
     const int hh = s >> 2, k = s & 3, kk = k >> 1;
+    const u32x2 hm = Kq<MI355X_TYPE_Q3_K>::hmask(g);
 #pragma unroll
     for (int t = 0; t < 8; ++t) part[t] = 0;
 #pragma unroll
@@ -817,7 +840,7 @@ __device__ __forceinline__ void k3_partial(const Kq<MI355X_TYPE_Q3_K>::Regs &g, 
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const uint32_t code =
-                ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
+                ((g.q[w] >> (2 * j)) & 0x03030303u) | (((hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
             const uint32_t Q = qv[w];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -1165,22 +1188,21 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
     // Default forms (variant and form AUTO), from sweeps of the BASELINE
     // shapes on MI355X (us, 14336x4096 / 4096x14336; 8192x8192 for IQ;
     // boxes differ by up to ~0.4 us):
-    //  * Q4_K, Q5_K, Q6_K: digit rows, one row per step (Q4_K 8.1 / 9.9,
-    //    Q5_K 9.7 / 11.4, Q6_K 11.1 / 13.3; prefetch 0.2-2 us slower, f32
-    //    rows 13.7 for Q6_K at seven steps);
-    //  * Q3_K: digit rows, with prefetch up to two steps (10.3 vs 10.4
-    //    without and 10.5 for f32 rows with prefetch; 12.0 vs f32 12.4 at
-    //    seven steps);
-    //  * IQ4_XS up to four steps: digit rows (10.9 vs f32 11.6-11.8);
-    //  * IQ3_S, IQ2_S up to four steps (N >= 4096): digit rows, two rows per
-    //    wavefront step (11.7 / 10.8 vs one row 11.8 / 11.2); IQ3_XXS one row
-    //    (10.3 vs 10.7): table-driven sign application and dot4 products cost
-    //    fewer VALU instructions than the f32 decode (f32 14.0 / 12.2 / 12.7).
-    // Prefetch (the next row group requested before the current one's
-    // decode) pays only for Q3_K's short rows; elsewhere, it lets every
-    // wavefront's second group compete with the first groups' loads and the
-    // second register set lowers the occupancy.
-    const bool auto_form = ctx->form_override == MI355X_FORM_AUTO && ctx->kernel_variant == MI355X_VARIANT_AUTO;
+    //  * every type: digit rows, one row per wavefront step, each step's
+    //    registers refilled with the next row group's step right after its
+    //    decode (Q3_K 9.1 / 10.9, Q4_K 7.9 / 9.3, Q5_K 9.8 / 11.1, Q6_K
+    //    11.1 / 13.2, IQ4_XS 10.7, IQ3_S 11.4, IQ2_S 10.6, IQ3_XXS 9.8; the
+    //    next group loaded after the whole decode: 10.2 / 11.5, 8.3 / 9.9,
+    //    9.8 / 11.4, 11.2 / 13.3, 11.0, 11.6 (two rows per step), 10.8 (two
+    //    rows), 10.0);
+    //  * IQ4_XS only up to four steps and the codebook types only up to
+    //    four steps and N >= 4096 (f32 rows otherwise): table-driven sign
+    //    application and dot4 products cost fewer VALU instructions than the
+    //    f32 decode (f32 14.0 / 12.2 / 12.7 for IQ3_S / IQ3_XXS / IQ2_S).
+    // Prefetch (a second register set for the next row group, requested
+    // before the current one's decode) is off by default: the refill gives
+    // the loads the same head start without the second set (Q3_K 9.2 / 10.9
+    // with prefetch).
     auto dg_rows_auto = [&](int nit) {
         switch (a.type) {
         case MI355X_TYPE_Q3_K:
@@ -1191,7 +1213,6 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         default: return grid_type && nit <= max_nit_r2(a.type) && a.N >= 4096;
         }
     };
-    auto pf_auto = [&](int nit) { return auto_form && nit <= 2 && a.type == MI355X_TYPE_Q3_K; };
     for (int64_t b0 = 0; b0 < B; b0 += per_chunk) {
         const int nb = static_cast<int>(std::min<int64_t>(per_chunk, B - b0));
         const int nit = (nb + kBlocksPerStep - 1) / kBlocksPerStep;
@@ -1243,9 +1264,9 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         }
         const bool dg_auto = ctx->kernel_variant == MI355X_VARIANT_AUTO && dg_rows_auto(nit);
         const bool dg = dg_forced || dg_auto;
-        int R = dg_auto && (a.type == MI355X_TYPE_IQ3_S || a.type == MI355X_TYPE_IQ2_S) ? 2 : 1;
+        int R = 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
-        const bool pf = R == 1 && (ctx->prefetch_override == 1 || (ctx->prefetch_override == 0 && pf_auto(nit)));
+        const bool pf = R == 1 && ctx->prefetch_override == 1;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf);
         const int64_t n_groups = (a.N + R - 1) / R;
         // dynamic LDS: the records (the codebook is the kernel's static LDS)

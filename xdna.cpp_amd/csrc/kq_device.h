@@ -360,31 +360,39 @@ template <>
 struct Kq<MI355X_TYPE_Q3_K> {
     static constexpr int kGrid = 0;
     struct Regs {
-        u32x2 q, hm, sw01;
+        u32x2 q;
+        uint32_t h;
+        u32x2 sw01;
         uint32_t sw2, d;
     };
-    // lane record (8 code bytes, this slice's half of the 8 hmask bytes it
-    // shares with slice s ^ 4, whose lane is lane ^ 32: one permlane32 swap
-    // brings the other half), the 12 scale bytes, d.  The swap of the
-    // record's word 2 returns, in every lane, the lower lane's (slice hh = 0)
-    // half first and the upper lane's second: the 8 bytes in order.
+    // lane record (8 code bytes, this slice's half h of the 8 hmask bytes it
+    // shares with slice s ^ 4, whose lane is lane ^ 32), the 12 scale bytes,
+    // d.  The loads return raw words; the exchange of h happens at decode
+    // (hmask), so no load has to complete before the next one is issued.
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 110, b, s);
         const u32x3 rec = ld96(r, q.base + 12 * q.m);
         const u32x3 sc = ld96(r, q.base + 96 * q.g + 12 * q.bl);
-        const auto sw = __builtin_amdgcn_permlane32_swap(rec[2], rec[2], false, false);
-        return {u32x2{rec[0], rec[1]}, u32x2{static_cast<uint32_t>(sw[0]), static_cast<uint32_t>(sw[1])},
-                u32x2{sc[0], sc[1]}, sc[2], ld16(r, q.d)};
+        return {u32x2{rec[0], rec[1]}, rec[2], u32x2{sc[0], sc[1]}, sc[2], ld16(r, q.d)};
+    }
+    // The slice's 8 hmask bytes: one permlane32 swap of h returns, in every
+    // lane, the lower lane's (slice hh = 0) half first and the upper lane's
+    // second, i.e. the 8 bytes in order.  Every lane of the wavefront takes
+    // part.
+    __device__ static u32x2 hmask(const Regs &g) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(g.h, g.h, false, false);
+        return u32x2{static_cast<uint32_t>(sw[0]), static_cast<uint32_t>(sw[1])};
     }
     __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
+        const u32x2 hm = hmask(g);
         float sg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t code =
-                    ((g.q[w] >> (2 * j)) & 0x03030303u) | (((g.hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
+                    ((g.q[w] >> (2 * j)) & 0x03030303u) | (((hm[w] >> (4 * hh + j)) & 0x01010101u) << 2);
                 sg[j] = dot4(code, &x.v[8 * j + 4 * w], sg[j]);
             }
         }
@@ -769,11 +777,12 @@ struct KqDg<MI355X_TYPE_Q3_K> {
     }
     __device__ static float compute(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
+        const u32x2 hm = Kq<MI355X_TYPE_Q3_K>::hmask(g);
         int sg[4][3] = {};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const uint32_t q = g.q[w];
-            const uint32_t hs = g.hm[w] >> (4 * hh);  // bit j of each byte: run j's high bit
+            const uint32_t hs = hm[w] >> (4 * hh);  // bit j of each byte: run j's high bit
             dot3((q & 0x03030303u) | ((hs << 2) & 0x04040404u), x, 0 + w, sg[0], w == 0);
             dot3((q & 0x0C0C0C0Cu) | ((hs << 3) & 0x10101010u), x, 2 + w, sg[1], w == 0);
             dot3((q & 0x30303030u) | ((hs << 4) & 0x40404040u), x, 4 + w, sg[2], w == 0);
