@@ -591,9 +591,12 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// s0 + 2^8 s1 + 2^16 s2 in f32
+// s0 + 2^8 s1 + 2^16 s2 in f32.  s0 + 2^8 s1 is formed in int32 (exact:
+// each |s_p| <= 32 * 127 * 128 for the 32-value slices that call this) and
+// rounded once, as fmaf(s1, 256, s0) would round it; the s2 term is added
+// with one more rounding.
 __device__ __forceinline__ float combine(const int (&s)[3]) {
-    return fmaf(static_cast<float>(s[2]), 65536.0f, fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0])));
+    return fmaf(static_cast<float>(s[2]), 65536.0f, static_cast<float>(s[0] + s[1] * 256));
 }
 
 // The same sum formed in int32 before one conversion.  It equals
@@ -866,7 +869,8 @@ struct KqDg<MI355X_TYPE_IQ3_XXS> {
             dot3(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, 2 * l, sm, l == 0);
             dot3(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, 2 * l + 1, sm);
         }
-        const float db = half_f(g.d) * (0.5f + static_cast<float>(g.aux >> 28)) * 0.5f;
+        // (0.5 + s) * 0.5 = s / 2 + 1/4, exact either way (s < 16)
+        const float db = half_f(g.d) * fmaf(static_cast<float>(g.aux >> 28), 0.5f, 0.25f);
         return db * ldexpf(combine(sm), x.e[0]);
     }
 };
@@ -890,10 +894,15 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
                 dot3(g1, x, 2 * l + 1, s1);
             }
         }
-        const float d = half_f(g.d);
-        const float db0 = d * (0.5f + static_cast<float>(g.scb & 15u)) * 0.25f;
-        const float db1 = d * (0.5f + static_cast<float>(g.scb >> 4)) * 0.25f;
-        return ldexpf(db0 * combine(s0) + db1 * combine(s1), x.e[0]);
+        // db_h = d * (0.5 + ls_h) / 4 = d * (2 ls_h + 1) / 8: the odd factors
+        // a_h = 2 ls_h + 1 <= 31 mix the halves' plane sums exactly in 24-bit
+        // products (|s_p| <= 16 * 127 * 128), then one combine and d 2^(e-3)
+        const int a0 = static_cast<int>(((g.scb << 1) & 0x1Eu) | 1u);
+        const int a1 = static_cast<int>((g.scb >> 3) | 1u);  // scb < 256
+        int t[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) t[p] = __mul24(a0, s0[p]) + __mul24(a1, s1[p]);
+        return ldexpf(half_f(g.d), x.e[0] - 3) * combine(t);
     }
 };
 
