@@ -61,6 +61,21 @@ __device__ __forceinline__ void make_rows(const KqArgs &a, int64_t g, Row (&rows
     }
 }
 
+// Every launch of the row kernels has NIT = ceil(nb / 8) (at most 8), so the
+// superblocks of steps before the last lie inside the chunk for every lane:
+// only the last step needs the lane's bounds check.
+template <int NIT>
+__device__ __forceinline__ bool step_in_chunk(int t, int bloc, int nb) {
+    return t < NIT - 1 || bloc < nb;
+}
+
+// a + b, never fused with the multiply that formed b: the forms that share a
+// decode (row, pipelined, K-split) round every step's product alike.
+__device__ __forceinline__ float add_unfused(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+
 // Loads of row group g: regs[r][t] for step t (superblock it = 8t + lane/8,
 // clamped into the chunk; lanes past the chunk's end are masked at use).
 template <int TYPE, int R, int NIT>
@@ -71,7 +86,7 @@ __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, in
 #pragma unroll
     for (int t = 0; t < NIT; ++t) {
         const int bloc = kBlocksPerStep * t + bl;
-        const int bc = bloc < a.nb ? bloc : a.nb - 1;
+        const int bc = step_in_chunk<NIT>(t, bloc, a.nb) ? bloc : a.nb - 1;
         const uint32_t babs = static_cast<uint32_t>(a.b0 + bc);
 #pragma unroll
         for (int r = 0; r < R; ++r) regs[r][t] = Kq<TYPE>::load(rows[r], babs, s);
@@ -100,7 +115,7 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typenam
 #pragma unroll
     for (int t = 0; t < NIT; ++t) {
         const int bloc = kBlocksPerStep * t + bl;
-        const bool valid = bloc < a.nb;
+        const bool valid = step_in_chunk<NIT>(t, bloc, a.nb);
         const int bc = valid ? bloc : a.nb - 1;
         if constexpr (DG) {
             XDig x;
@@ -108,7 +123,7 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typenam
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float p = KqDg<TYPE>::compute(regs[r][t], s, x, grid);
-                acc[r] += valid ? p : 0.f;
+                acc[r] = add_unfused(acc[r], valid ? p : 0.f);
             }
         } else {
             XSlice x;
@@ -116,7 +131,7 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typenam
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float p = K::compute(regs[r][t], s, x, grid);
-                acc[r] += valid ? p : 0.f;
+                acc[r] = add_unfused(acc[r], valid ? p : 0.f);
             }
         }
         if constexpr (RF) {
