@@ -277,3 +277,28 @@ def test_many_row_groups_per_wavefront(ctx, name, variant, N, K):
             ctx.set_option(mi355x.OPT_GRID, 0)
         bad = np.nonzero(y_cap.view(np.uint32) != y_full.view(np.uint32))[0]
         assert bad.size == 0, f"{name} {N}x{K} grid {cap}: {bad.size} rows differ, first {bad[:5]}"
+
+
+def test_iq2s_extreme_grid_and_scales(ctx, oracle, variant):
+    """IQ2_S at the edge of the digit arithmetic: every grid magnitude 127
+    (the largest a grid may hold), every sign positive, every 4-bit scale
+    15, and a constant activation whose middle digits are all -128 in the
+    22-bit form: the scaled plane sums of a slice then reach 2^24 and their
+    first combine stage exceeds int32, which the decode must not wrap."""
+    t = ALL["IQ2_S"]
+    N, K = 64, 2048
+    grid = np.full(1024, 0x7F7F7F7F7F7F7F7F, dtype=np.uint64)
+    raw = blocks(t, N, K, 3).reshape(N, K // 256, 82)
+    raw[..., 0:2] = np.frombuffer(np.float16(1.0).tobytes(), dtype=np.uint8)
+    raw[..., 34:66] = 0  # signs
+    raw[..., 74:82] = 0xFF  # scales
+    raw = raw.reshape(N, -1)
+    x = np.full(K, 1.015625, dtype=np.float32)
+    mi355x.set_iq_grid(t, grid)
+    try:
+        y = run(ctx, t, raw, N, K, x)
+    finally:
+        mi355x.set_iq_grid(t, GRIDS[t])
+    ref = oracle.gemv(t, raw, N, K, x, grid=grid)
+    norms = oracle.row_norms(t, raw, N, K, grid=grid)
+    check_gemv(y, ref, norms, x, "IQ2_S extreme grid")

@@ -598,6 +598,11 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 __device__ __forceinline__ float combine(const int (&s)[3]) {
     return fmaf(static_cast<float>(s[2]), 65536.0f, static_cast<float>(s[0] + s[1] * 256));
 }
+// The same in f32 throughout, for sums up to 2^24 in magnitude whose
+// s0 + 2^8 s1 may exceed int32.
+__device__ __forceinline__ float combine_f(const int (&s)[3]) {
+    return fmaf(static_cast<float>(s[2]), 65536.0f, fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0])));
+}
 
 // The same sum formed in int32 before one conversion.  It equals
 // sum_i code_i * Z_i with |Z_i| <= 2^22, so it stays below 2^31 for 16
@@ -896,13 +901,14 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
         }
         // db_h = d * (0.5 + ls_h) / 4 = d * (2 ls_h + 1) / 8: the odd factors
         // a_h = 2 ls_h + 1 <= 31 mix the halves' plane sums exactly in 24-bit
-        // products (|s_p| <= 16 * 127 * 128), then one combine and d 2^(e-3)
+        // products (|s_p| <= 16 * 127 * 128, so |t_p| < 2^24), then one f32
+        // combine and d 2^(e-3)
         const int a0 = static_cast<int>(((g.scb << 1) & 0x1Eu) | 1u);
         const int a1 = static_cast<int>((g.scb >> 3) | 1u);  // scb < 256
         int t[3];
 #pragma unroll
         for (int p = 0; p < 3; ++p) t[p] = __mul24(a0, s0[p]) + __mul24(a1, s1[p]);
-        return ldexpf(half_f(g.d), x.e[0] - 3) * combine(t);
+        return ldexpf(half_f(g.d), x.e[0] - 3) * combine_f(t);
     }
 };
 
