@@ -116,14 +116,14 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
 /* Per-context options.
  *   MI355X_OPT_VARIANT: which kernel family computes GEMVs --
  *     MI355X_VARIANT_AUTO (default: for Q4_0 digit planes where they apply;
- *       for the K/IQ types 22-bit activation digits (row form) for Q3_K,
+ *       for the K/IQ types 16-bit activation digits (row form) for Q3_K,
  *       Q4_K, Q5_K and Q6_K, IQ4_XS rows of at most 8192 values, and
  *       IQ3_S/IQ3_XXS/IQ2_S rows of at most 8192 values with N >= 4096, one
  *       row per wavefront step; f32 activations for the rest: longer IQ rows
  *       and smaller IQ matrices),
  *     MI355X_VARIANT_EXACT_F32 (codes -> f32, fp32 FMA; activations used
  *       exactly as given), MI355X_VARIANT_DIGITS (activations as fixed point
- *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 22-bit
+ *       per 32-value block -- 20-bit for Q4_0 with int4 dot8 products, 16-bit
  *       for the K/IQ types with int8 dot4 products),
  *     MI355X_VARIANT_GGML_Q8 (the arithmetic of ggml's CPU backend, so that
  *       results follow ggml-cpu rather than the f32 references: Q4_0 -- the
@@ -152,7 +152,7 @@ MI355X_API int mi355x_device_describe(int device, char *name, size_t name_len, c
  *     four for the K/IQ types -- each wavefront owning a run of consecutive
  *     rows whose loads are issued two (Q4_0) or three (K/IQ) rows ahead of
  *     their dot products; Q4_0: K a multiple of 2048 up to 16384, 16-byte
- *     aligned weights and activation row; K/IQ types: 22-bit digit
+ *     aligned weights and activation row; K/IQ types: 16-bit digit
  *     arithmetic, any K).
  *   MI355X_OPT_OVERLAP: 0 (default: off) or S = 2, 3, 4.  With S,
  *     consecutive mi355x_gemv calls may run at the same time: the context

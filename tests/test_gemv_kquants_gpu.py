@@ -45,7 +45,7 @@ def install_grids():
 @pytest.fixture(params=["digits", "exact_f32", "pipelined", "digits_prefetch", "f32_prefetch", "digits_two_rows",
                         "auto"], autouse=True)
 def variant(request, ctx):
-    """Every test runs on each kernel family: activations as 22-bit digit
+    """Every test runs on each kernel family: activations as 16-bit digit
     planes with integer dot products (several workgroups per CU; each
     step's registers refilled with the next row group's step after its
     decode), f32 activations as given, the pipelined form (digit arithmetic,
@@ -282,9 +282,10 @@ def test_many_row_groups_per_wavefront(ctx, name, variant, N, K):
 def test_iq2s_extreme_grid_and_scales(ctx, oracle, variant):
     """IQ2_S at the edge of the digit arithmetic: every grid magnitude 127
     (the largest a grid may hold), every sign positive, every 4-bit scale
-    15, and a constant activation whose middle digits are all -128 in the
-    22-bit form: the scaled plane sums of a slice then reach 2^24 and their
-    first combine stage exceeds int32, which the decode must not wrap."""
+    15, and a constant activation whose digits all sit at the top of their
+    range (Z = 32638, high digit 127): the scale-mixed plane sums of a slice
+    then come near 2^24 and their combine exceeds int32, which the decode
+    must not wrap."""
     t = ALL["IQ2_S"]
     N, K = 64, 2048
     grid = np.full(1024, 0x7F7F7F7F7F7F7F7F, dtype=np.uint64)

@@ -256,10 +256,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
 // it.  This form applies what the Q4_0 pipelined form does:
 //  * one workgroup of four wavefronts per CU (grid <= CU count); wavefront v
 //    owns the consecutive rows [v*rows, v*rows + rows) of the launch;
-//  * activations as 22-bit digits (the digit path's arithmetic, v_dot4 on
-//    three signed-byte planes), staged once per CU; with XREG each lane then
+//  * activations as 16-bit digits (the digit path's arithmetic, v_dot4 on
+//    two signed-byte planes), staged once per CU; with XREG each lane then
 //    copies the digit slices of its NIT steps into registers once, so the
-//    row loop reads no LDS (32 VGPRs per step; NIT <= 4);
+//    row loop reads no LDS (24 VGPRs per step; NIT <= 4);
 //  * a row's loads are issued kPlqDepth rows ahead of its decode, the first
 //    two rows' before the staging math;
 //  * loads of rows past the wavefront's range use an empty buffer range and
@@ -1288,8 +1288,16 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         const size_t lds = dg ? dg_lds_bytes(nb) : x_lds_bytes(nb);
         if (lds + (dg ? dg_table_words(a.type) : grid_words(a.type)) * 4u > ctx->max_lds_per_block)
             return set_error(MI355X_EUNSUPPORTED, "activation chunk exceeds LDS");
+        // Workgroups per CU: every workgroup stages the whole chunk, so long
+        // chunks take one per CU (each wavefront then walks more row groups,
+        // its refills overlapping them) and 16-31 superblocks at most two
+        // (measured, us: 8192x8192 IQ2_S / IQ3_XXS / IQ4_XS 9.1 / 8.8 / 9.5
+        // with one against 9.5 / 9.3 / 9.8 with two; 4096x14336 Q4_K 8.7 vs
+        // 10.2; 14336x4096 Q3_K / Q4_K / Q6_K 8.4 / 7.5 / 11.0 with two
+        // against 8.8 / 8.1 / 11.7 with three).
         const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
-        int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * occ);
+        const int per_cu = nb >= 32 ? 1 : nb >= 16 ? std::min(occ, 2) : occ;
+        int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * per_cu);
         if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);
         KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, x, a.y, b0 > 0 ? 1 : 0,
                     grid};

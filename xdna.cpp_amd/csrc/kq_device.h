@@ -164,7 +164,7 @@ __device__ __forceinline__ int run_of(int s, int p) {
 }
 constexpr int kLmSlot = 16 * 64;                // bytes of one slot row (64 records)
 constexpr int kXGroupBytes = 9 * kLmSlot;       // f32: 8 value slots, the run sums
-constexpr int kDgGroupBytes = 8 * kLmSlot;      // digits: 3 planes x 2, exponents, Z sums
+constexpr int kDgGroupBytes = 6 * kLmSlot;      // digits: 2 planes x 2, units, Z sums
 // 16-byte position of record l = 8s + bl in its slot rows: l with bits 1-2
 // XORed by bits 4-5.  Readers take one record per lane (a permutation of
 // the 64 positions either way); the row kernels' staging stores (one 8-value
@@ -568,50 +568,52 @@ struct Kq<MI355X_TYPE_IQ2_S> {
 };
 
 // ---- digit path ---------------------------------------------------------------
-// Activations as fixed point: each 32-value block b of x has a power-of-two
-// scale with x = Z * 2^e(b), |Z| < 2^22 (the block's largest |x| maps into
-// [2^21, 2^22)), and Z = z0 + 2^8 z1 + 2^16 z2 in balanced signed bytes.  A
+// Activations as 16-bit fixed point: each 32-value block b of x has a scale
+// c(b) = 32638 / m(b), m(b) its largest |x|, and x = Z * u(b) with
+// Z = round(x * c(b)), |Z| <= 32638, u(b) = 1 / c(b); Z = z0 + 2^8 z1 in
+// balanced signed bytes (z1 stays in [-128, 127] because |Z| <= 32639).  A
 // staged slice record (lane-major, as the f32 records above) holds, per
 // digit plane, the 4 runs' 8 bytes in position order (slots 2p, 2p + 1),
-// then e(b) of the block each run lies in (slot 6) and each run's sum of Z
-// (slot 7); K4 records, whose computes take an exponent and a Z sum per
-// 16-value half, hold those four words in slot 6 (one full-width read).
-// Weight codes (small unsigned integers, or signed bytes for the signed
-// codebooks) meet the digits in v_dot4_i32_i8: sum_i code_i * Z_i over a run
-// is s0 + 2^8 s1 + 2^16 s2 with s_p = sum_i code_i * z_p,i, exact in int32.
-// Rounding x to Z changes each product by at most 2^-22 of its block's
-// largest |x|, well inside the GEMV tolerance of 1e-4 * |w_r| * |x|.
+// then u of the block each run lies in (slot 4) and each run's sum of Z
+// (slot 5); K4 records, whose computes take a unit and a Z sum per 16-value
+// half, hold those four words in slot 4 (one full-width read).  Weight codes
+// (small unsigned integers, or signed bytes for the signed codebooks) meet
+// the digits in v_dot4_i32_i8: sum_i code_i * Z_i over a run is s0 + 2^8 s1
+// with s_p = sum_i code_i * z_p,i, exact in int32.
+// Error: rounding x to Z u moves each value by at most u / 2 = m / 65276
+// (1.54e-5 m, with the reciprocals' rounding), so a row's result moves by at
+// most 1.54e-5 * sum_b m(b) * sum_{i in b} |w_i| <= 1.54e-5 * sqrt(32) *
+// |w_r| * |x| = 8.7e-5 |w_r| |x| (Cauchy-Schwarz twice: within a block, then
+// over blocks with m(b) <= |x_b|), inside the GEMV tolerance of
+// 1e-4 * |w_r| * |x|; for random data the error is orders of magnitude
+// smaller.
 struct XDig {
-    uint32_t z[3][8];  // digit planes: 8 dwords (32 values) per plane
-    int e[4];          // exponents of the 32-blocks the slice's runs lie in
+    uint32_t z[2][8];  // digit planes: 8 dwords (32 values) per plane
+    float u[4];        // units of the 32-blocks the slice's runs lie in
     float zs[4];       // sum of Z over each run
 };
+
+// Scale c and unit u of a block whose largest |x| is m: m * c <= 32638
+// (1 + 2^-22) < 32638.5, so |Z| <= 32638.  An all-zero (or denormal-small)
+// block takes c = 2^126: its Z are 0 (or tiny) and u is a normal number.
+__device__ __forceinline__ void dg_scale(float m, float &c, float &u) {
+    c = fminf(32638.0f * __builtin_amdgcn_rcpf(m), 0x1p126f);
+    u = __builtin_amdgcn_rcpf(c);
+}
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// s0 + 2^8 s1 + 2^16 s2 in f32.  s0 + 2^8 s1 is formed in int32 (exact:
-// each |s_p| <= 32 * 127 * 128 for the 32-value slices that call this) and
-// rounded once, as fmaf(s1, 256, s0) would round it; the s2 term is added
-// with one more rounding.
-__device__ __forceinline__ float combine(const int (&s)[3]) {
-    return fmaf(static_cast<float>(s[2]), 65536.0f, static_cast<float>(s[0] + s[1] * 256));
-}
-// The same in f32 throughout, for sums up to 2^24 in magnitude whose
-// s0 + 2^8 s1 may exceed int32.
-__device__ __forceinline__ float combine_f(const int (&s)[3]) {
-    return fmaf(static_cast<float>(s[2]), 65536.0f, fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0])));
+// s0 + 2^8 s1 in f32: formed in int32 (exact: it is sum_i code_i * Z_i over
+// at most 32 values, |code_i| <= 127, |Z_i| <= 32638) and rounded once.
+__device__ __forceinline__ float combine(const int (&s)[2]) { return static_cast<float>(s[0] + s[1] * 256); }
+// The same in f32, for sums up to 2^24 in magnitude whose s0 + 2^8 s1 may
+// exceed int32 (one rounding: both converts are exact).
+__device__ __forceinline__ float combine_f(const int (&s)[2]) {
+    return fmaf(static_cast<float>(s[1]), 256.0f, static_cast<float>(s[0]));
 }
 
-// The same sum formed in int32 before one conversion.  It equals
-// sum_i code_i * Z_i with |Z_i| <= 2^22, so it stays below 2^31 for 16
-// values of codes below 32 (Q4_K, Q5_K) and 8 values of codes below 64
-// (Q6_K, Q3_K), as do the partial terms (|s2| <= 8 * 63 * 64 or 16 * 31 * 64:
-// |s2| * 2^16 + |s1| * 2^8 + |s0| < 2.14e9).
-__device__ __forceinline__ float combine_i(const int (&s)[3]) {
-    return static_cast<float>(s[0] + s[1] * 256 + s[2] * 65536);
-}
 
 // (scale, min) of sub-blocks 2c and 2c+1 of a Q4_K/Q5_K block at once: their
 // bytes are adjacent in each of the three scale words (w0 = bytes 0-3,
@@ -638,17 +640,15 @@ __device__ __forceinline__ int sdot4_0(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, true);
 }
 
-// Accumulates code dword `c` (4 values) against dword `i` of the 3 planes;
+// Accumulates code dword `c` (4 values) against dword `i` of the 2 planes;
 // with `first` (a compile-time constant at every call) the sums start here.
-__device__ __forceinline__ void dot3(uint32_t c, const XDig &x, int i, int (&s)[3], bool first = false) {
+__device__ __forceinline__ void dot2(uint32_t c, const XDig &x, int i, int (&s)[2], bool first = false) {
     if (first) {
         s[0] = sdot4_0(c, x.z[0][i]);
         s[1] = sdot4_0(c, x.z[1][i]);
-        s[2] = sdot4_0(c, x.z[2][i]);
     } else {
         s[0] = sdot4(c, x.z[0][i], s[0]);
         s[1] = sdot4(c, x.z[1][i], s[1]);
-        s[2] = sdot4(c, x.z[2][i], s[2]);
     }
 }
 
@@ -669,12 +669,12 @@ __device__ __forceinline__ void signed8(uint32_t g_lo, uint32_t g_hi, uint32_t b
     hi = signed4(g_hi, (b >> 4) & 15u);
 }
 
-// The slice of a digit record (K4: e and Z sums per 16-value half; K6: per
-// run; S32: the block's exponent).
+// The slice of a digit record (K4: units and Z sums per 16-value half; K6:
+// per run; S32: the block's unit).
 template <int SH>
 __device__ __forceinline__ void dg_slice_lm(const uint8_t *rec, XDig &x) {
 #pragma unroll
-    for (int p = 0; p < 3; ++p) {
+    for (int p = 0; p < 2; ++p) {
         const uint4 a = *reinterpret_cast<const uint4 *>(rec + kLmSlot * (2 * p));
         const uint4 b = *reinterpret_cast<const uint4 *>(rec + kLmSlot * (2 * p + 1));
         x.z[p][0] = a.x;
@@ -686,21 +686,22 @@ __device__ __forceinline__ void dg_slice_lm(const uint8_t *rec, XDig &x) {
         x.z[p][6] = b.z;
         x.z[p][7] = b.w;
     }
-    const int4 E = *reinterpret_cast<const int4 *>(rec + kLmSlot * 6);
     if constexpr (SH == kS32) {
-        x.e[0] = E.x;
+        x.u[0] = *reinterpret_cast<const float *>(rec + kLmSlot * 4);
     } else if constexpr (SH == kK4) {
-        // slot 6 holds both halves' exponents and Z sums (put_record_dg)
-        x.e[0] = E.x;
-        x.e[1] = E.y;
-        x.zs[0] = __builtin_bit_cast(float, E.z);
-        x.zs[1] = __builtin_bit_cast(float, E.w);
+        // slot 4 holds both halves' units and Z sums (put_record_dg)
+        const float4 E = *reinterpret_cast<const float4 *>(rec + kLmSlot * 4);
+        x.u[0] = E.x;
+        x.u[1] = E.y;
+        x.zs[0] = E.z;
+        x.zs[1] = E.w;
     } else {
-        const float4 Z = *reinterpret_cast<const float4 *>(rec + kLmSlot * 7);
-        x.e[0] = E.x;
-        x.e[1] = E.y;
-        x.e[2] = E.z;
-        x.e[3] = E.w;
+        const float4 E = *reinterpret_cast<const float4 *>(rec + kLmSlot * 4);
+        const float4 Z = *reinterpret_cast<const float4 *>(rec + kLmSlot * 5);
+        x.u[0] = E.x;
+        x.u[1] = E.y;
+        x.u[2] = E.z;
+        x.u[3] = E.w;
         x.zs[0] = Z.x;
         x.zs[1] = Z.y;
         x.zs[2] = Z.z;
@@ -714,18 +715,18 @@ struct KqDg;
 template <>
 struct KqDg<MI355X_TYPE_Q4_K> {
     __device__ static float compute(const Kq<MI355X_TYPE_Q4_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
-        int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
+        int sa[2] = {0, 0}, sb[2] = {0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            dot3(g.q[i] & 0x0F0F0F0Fu, x, i, sa, i == 0);
-            dot3((g.q[i] >> 4) & 0x0F0F0F0Fu, x, 4 + i, sb, i == 0);
+            dot2(g.q[i] & 0x0F0F0F0Fu, x, i, sa, i == 0);
+            dot2((g.q[i] >> 4) & 0x0F0F0F0Fu, x, 4 + i, sb, i == 0);
         }
         const int c = s >> 1;
         float sc0, m0, sc1, m1;
         scale_min_pair_k4(c, g.hd[1], g.hd[2], g.hd[3], sc0, m0, sc1, m1);
         const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
-        return ldexpf((d * sc0) * combine_i(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
-               ldexpf((d * sc1) * combine_i(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+        return ((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0]) * x.u[0] +
+               ((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1]) * x.u[1];
     }
 };
 
@@ -733,38 +734,38 @@ template <>
 struct KqDg<MI355X_TYPE_Q5_K> {
     __device__ static float compute(const Kq<MI355X_TYPE_Q5_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int c = s >> 1;
-        int sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
+        int sa[2] = {0, 0}, sb[2] = {0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            dot3((g.q[i] & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c)) & 0x01010101u) << 4), x, i, sa, i == 0);
-            dot3(((g.q[i] >> 4) & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c + 1)) & 0x01010101u) << 4), x, 4 + i, sb,
+            dot2((g.q[i] & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c)) & 0x01010101u) << 4), x, i, sa, i == 0);
+            dot2(((g.q[i] >> 4) & 0x0F0F0F0Fu) | (((g.qh[i] >> (2 * c + 1)) & 0x01010101u) << 4), x, 4 + i, sb,
                  i == 0);
         }
         float sc0, m0, sc1, m1;
         scale_min_pair_k4(c, g.hd[1], g.hd[2], g.hd[3], sc0, m0, sc1, m1);
         const float d = half_f(g.hd[0] & 0xFFFF), dmin = half_f(g.hd[0] >> 16);
-        return ldexpf((d * sc0) * combine_i(sa) - (dmin * m0) * x.zs[0], x.e[0]) +
-               ldexpf((d * sc1) * combine_i(sb) - (dmin * m1) * x.zs[1], x.e[1]);
+        return ((d * sc0) * combine(sa) - (dmin * m0) * x.zs[0]) * x.u[0] +
+               ((d * sc1) * combine(sb) - (dmin * m1) * x.zs[1]) * x.u[1];
     }
 };
 
 template <>
 struct KqDg<MI355X_TYPE_Q6_K> {
     __device__ static float compute(const Kq<MI355X_TYPE_Q6_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
-        int sg[4][3] = {};
+        int sg[4][2] = {};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const uint32_t A = g.qa[w], Bq = g.qb[w], H = g.qh[w];
-            dot3((A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u), x, 0 + w, sg[0], w == 0);
-            dot3((Bq & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u), x, 2 + w, sg[1], w == 0);
-            dot3(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), x, 4 + w, sg[2], w == 0);
-            dot3(((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u), x, 6 + w, sg[3], w == 0);
+            dot2((A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u), x, 0 + w, sg[0], w == 0);
+            dot2((Bq & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u), x, 2 + w, sg[1], w == 0);
+            dot2(((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u), x, 4 + w, sg[2], w == 0);
+            dot2(((Bq >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u), x, 6 + w, sg[3], w == 0);
         }
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float sc = static_cast<float>(static_cast<int32_t>(g.sw4 << (24 - 8 * j)) >> 24);
-            acc = fmaf(sc, ldexpf(combine_i(sg[j]) - 32.0f * x.zs[j], x.e[j]), acc);
+            acc = fmaf(sc, (combine(sg[j]) - 32.0f * x.zs[j]) * x.u[j], acc);
         }
         return half_f(g.d) * acc;
     }
@@ -780,21 +781,21 @@ struct KqDg<MI355X_TYPE_Q3_K> {
     // 128, so the plane sums are exact multiples of it and combine_shr
     // divides it out exactly: the sums equal those of the unscaled codes.
     template <int SHR>
-    __device__ static int combine_shr(const int (&s)[3]) {
-        return (s[0] >> SHR) + s[1] * (1 << (8 - SHR)) + s[2] * (1 << (16 - SHR));
+    __device__ static int combine_shr(const int (&s)[2]) {
+        return (s[0] >> SHR) + s[1] * (1 << (8 - SHR));
     }
     __device__ static float compute(const Kq<MI355X_TYPE_Q3_K>::Regs &g, int s, const XDig &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
         const u32x2 hm = Kq<MI355X_TYPE_Q3_K>::hmask(g);
-        int sg[4][3] = {};
+        int sg[4][2] = {};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const uint32_t q = g.q[w];
             const uint32_t hs = hm[w] >> (4 * hh);  // bit j of each byte: run j's high bit
-            dot3((q & 0x03030303u) | ((hs << 2) & 0x04040404u), x, 0 + w, sg[0], w == 0);
-            dot3((q & 0x0C0C0C0Cu) | ((hs << 3) & 0x10101010u), x, 2 + w, sg[1], w == 0);
-            dot3((q & 0x30303030u) | ((hs << 4) & 0x40404040u), x, 4 + w, sg[2], w == 0);
-            dot3(((q >> 2) & 0x30303030u) | ((hs << 3) & 0x40404040u), x, 6 + w, sg[3], w == 0);
+            dot2((q & 0x03030303u) | ((hs << 2) & 0x04040404u), x, 0 + w, sg[0], w == 0);
+            dot2((q & 0x0C0C0C0Cu) | ((hs << 3) & 0x10101010u), x, 2 + w, sg[1], w == 0);
+            dot2((q & 0x30303030u) | ((hs << 4) & 0x40404040u), x, 4 + w, sg[2], w == 0);
+            dot2(((q >> 2) & 0x30303030u) | ((hs << 3) & 0x40404040u), x, 6 + w, sg[3], w == 0);
         }
         // The four 6-bit scales sidx = 8hh + kk + 2j (kk = k / 2) in one word,
         // bytes in run order 0, 2, 1, 3: low nibbles from bytes kk, kk + 2
@@ -810,10 +811,10 @@ struct KqDg<MI355X_TYPE_Q3_K> {
         const float sc1 = static_cast<float>((SC >> 16) & 0xFFu) - 32.0f;
         const float sc3 = static_cast<float>(SC >> 24) - 32.0f;
         float acc = 0.f;
-        acc = fmaf(sc0, ldexpf(static_cast<float>(combine_shr<0>(sg[0])) - 4.0f * x.zs[0], x.e[0]), acc);
-        acc = fmaf(sc1, ldexpf(static_cast<float>(combine_shr<2>(sg[1])) - 4.0f * x.zs[1], x.e[1]), acc);
-        acc = fmaf(sc2, ldexpf(static_cast<float>(combine_shr<4>(sg[2])) - 4.0f * x.zs[2], x.e[2]), acc);
-        acc = fmaf(sc3, ldexpf(static_cast<float>(combine_shr<4>(sg[3])) - 4.0f * x.zs[3], x.e[3]), acc);
+        acc = fmaf(sc0, (static_cast<float>(combine_shr<0>(sg[0])) - 4.0f * x.zs[0]) * x.u[0], acc);
+        acc = fmaf(sc1, (static_cast<float>(combine_shr<2>(sg[1])) - 4.0f * x.zs[1]) * x.u[1], acc);
+        acc = fmaf(sc2, (static_cast<float>(combine_shr<4>(sg[2])) - 4.0f * x.zs[2]) * x.u[2], acc);
+        acc = fmaf(sc3, (static_cast<float>(combine_shr<4>(sg[3])) - 4.0f * x.zs[3]) * x.u[3], acc);
         return half_f(g.d) * acc;
     }
 };
@@ -827,16 +828,16 @@ struct KqDg<MI355X_TYPE_IQ4_XS> {
         return iq4_lookup(n, kT0, kT1, kT2, kT3);
     }
     __device__ static float compute(const Kq<MI355X_TYPE_IQ4_XS>::Regs &g, int s, const XDig &x, const uint32_t *) {
-        int sm[3] = {0, 0, 0};
+        int sm[2] = {0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            dot3(lookup(g.q[i] & 0x0F0F0F0Fu), x, i, sm, i == 0);
-            dot3(lookup((g.q[i] >> 4) & 0x0F0F0F0Fu), x, 4 + i, sm);
+            dot2(lookup(g.q[i] & 0x0F0F0F0Fu), x, i, sm, i == 0);
+            dot2(lookup((g.q[i] >> 4) & 0x0F0F0F0Fu), x, 4 + i, sm);
         }
         const float d = half_f(g.hd[0] & 0xFFFF);
         const uint32_t sh = g.hd[0] >> 16;
         const uint32_t ls = ((g.hd[1] >> (4 * s)) & 15u) | (((sh >> (2 * s)) & 3u) << 4);
-        return (d * static_cast<float>(static_cast<int>(ls) - 32)) * ldexpf(combine(sm), x.e[0]);
+        return (d * static_cast<float>(static_cast<int>(ls) - 32)) * (combine(sm) * x.u[0]);
     }
 };
 
@@ -846,17 +847,17 @@ struct KqDg<MI355X_TYPE_IQ3_S> {
                                     const uint32_t *grid) {
         const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
         const uint2 *st = gt + kIq3sGridSize;
-        int sm[3] = {0, 0, 0};
+        int sm[2] = {0, 0};
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
             const uint32_t i0 = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
             const uint32_t i1 = byte_u(g.qs[k >> 2], (k & 3) + 1) | (((g.qh >> (k + 1)) & 1u) << 8);
             const uint2 e0 = gt[i0], e1 = gt[i1], sl = st[byte_u(g.sg, k >> 1)];
-            dot3(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, k, sm, k == 0);
-            dot3(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, k + 1, sm);
+            dot2(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, k, sm, k == 0);
+            dot2(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, k + 1, sm);
         }
         const float db = half_f(g.d) * (1.0f + 2.0f * static_cast<float>((g.scb >> (4 * (s & 1))) & 15u));
-        return db * ldexpf(combine(sm), x.e[0]);
+        return db * (combine(sm) * x.u[0]);
     }
 };
 
@@ -866,17 +867,17 @@ struct KqDg<MI355X_TYPE_IQ3_XXS> {
                                     const uint32_t *grid) {
         const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
         const uint2 *st = gt + 256;
-        int sm[3] = {0, 0, 0};
+        int sm[2] = {0, 0};
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint2 e0 = gt[byte_u(g.qs[l >> 1], 2 * (l & 1))], e1 = gt[byte_u(g.qs[l >> 1], 2 * (l & 1) + 1)];
             const uint2 sl = st[(g.aux >> (7 * l)) & 127u];
-            dot3(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, 2 * l, sm, l == 0);
-            dot3(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, 2 * l + 1, sm);
+            dot2(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, 2 * l, sm, l == 0);
+            dot2(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, 2 * l + 1, sm);
         }
         // (0.5 + s) * 0.5 = s / 2 + 1/4, exact either way (s < 16)
         const float db = half_f(g.d) * fmaf(static_cast<float>(g.aux >> 28), 0.5f, 0.25f);
-        return db * ldexpf(combine(sm), x.e[0]);
+        return db * (combine(sm) * x.u[0]);
     }
 };
 
@@ -884,7 +885,7 @@ template <>
 struct KqDg<MI355X_TYPE_IQ2_S> {
     __device__ static float compute(const Kq<MI355X_TYPE_IQ2_S>::Regs &g, int, const XDig &x,
                                     const uint32_t *grid) {
-        int s0[3] = {0, 0, 0}, s1[3] = {0, 0, 0};
+        int s0[2] = {0, 0}, s1[2] = {0, 0};
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t idx = byte_u(g.qs, l) | (((g.qh >> (2 * l)) & 3u) << 8);
@@ -892,23 +893,23 @@ struct KqDg<MI355X_TYPE_IQ2_S> {
             const uint2 sl = reinterpret_cast<const uint2 *>(grid + 4096)[byte_u(g.sg, l)];
             const uint32_t g0 = __builtin_amdgcn_perm(e.y, e.x, sl.x), g1 = __builtin_amdgcn_perm(e.w, e.z, sl.y);
             if (l < 2) {
-                dot3(g0, x, 2 * l, s0, l == 0);
-                dot3(g1, x, 2 * l + 1, s0);
+                dot2(g0, x, 2 * l, s0, l == 0);
+                dot2(g1, x, 2 * l + 1, s0);
             } else {
-                dot3(g0, x, 2 * l, s1, l == 2);
-                dot3(g1, x, 2 * l + 1, s1);
+                dot2(g0, x, 2 * l, s1, l == 2);
+                dot2(g1, x, 2 * l + 1, s1);
             }
         }
         // db_h = d * (0.5 + ls_h) / 4 = d * (2 ls_h + 1) / 8: the odd factors
         // a_h = 2 ls_h + 1 <= 31 mix the halves' plane sums exactly in 24-bit
         // products (|s_p| <= 16 * 127 * 128, so |t_p| < 2^24), then one f32
-        // combine and d 2^(e-3)
+        // combine, d / 8 and the unit
         const int a0 = static_cast<int>(((g.scb << 1) & 0x1Eu) | 1u);
         const int a1 = static_cast<int>((g.scb >> 3) | 1u);  // scb < 256
-        int t[3];
+        int t[2];
 #pragma unroll
-        for (int p = 0; p < 3; ++p) t[p] = __mul24(a0, s0[p]) + __mul24(a1, s1[p]);
-        return ldexpf(half_f(g.d), x.e[0] - 3) * combine_f(t);
+        for (int p = 0; p < 2; ++p) t[p] = __mul24(a0, s0[p]) + __mul24(a1, s1[p]);
+        return (half_f(g.d) * 0.125f) * (combine_f(t) * x.u[0]);
     }
 };
 
@@ -930,15 +931,15 @@ __device__ __forceinline__ float swz16_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
 
-// Digit record of the values v (load_record).  Each run takes the exponent
-// of its 32-value block, whose largest |x| is the maximum over the runs of
-// that block: all in this record (S32); two here and two in the record of
-// slice s ^ 1, lane ^ 8 (K4); one here and one in each record of slices
-// 4hh + k', lanes ^ 8, ^ 16, ^ 24 (K6).  Every lane of the wavefront must
-// take part (the exchanges read other lanes); `store` masks the stores.
-// The digits, exponent fields and Z sums equal those of staging each
-// 32-value block at once: the maximum is exact in any order and each Z and
-// dword sum is formed from the same values.
+// Digit record of the values v (load_record).  Each run takes the scale of
+// its 32-value block, whose largest |x| is the maximum over the runs of that
+// block: all in this record (S32); two here and two in the record of slice
+// s ^ 1, lane ^ 8 (K4); one here and one in each record of slices 4hh + k',
+// lanes ^ 8, ^ 16, ^ 24 (K6).  Every lane of the wavefront must take part
+// (the exchanges read other lanes); `store` masks the stores.  The digits,
+// units and Z sums equal those of staging each 32-value block at once: the
+// maximum is exact in any order and each Z and dword sum is formed from the
+// same values.
 template <int SH>
 __device__ __forceinline__ void put_record_dg(uint8_t *rec, const float4 (&v)[8], bool store) {
     float m[4];
@@ -964,60 +965,53 @@ __device__ __forceinline__ void put_record_dg(uint8_t *rec, const float4 (&v)[8]
             m[p] = fmaxf(m[p], swz16_f(m[p]));
         }
     }
-    uint32_t pl[3][8];
-    int ef[4];
+    uint32_t pl[2][8];
+    float uf[4];
     float zs[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m[p]) >> 23) & 0xFFu);
-        const int se = min(275 - E, 254);  // biased exponent of s = 2^-e: m * s in [2^21, 2^22)
-        const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
-        ef[p] = 127 - se;
-        // F = bits of 1.5 * 2^23 + v * s: |v * s| < 2^22, so the sum lies in
+        float c;
+        dg_scale(m[p], c, uf[p]);
+        // F = bits of 1.5 * 2^23 + v * c: |v * c| < 2^22, so the sum lies in
         // [2^23, 2^24) where f32 spacing is 1 and F = 0x4B400000 + Z, Z the
-        // rounded integer.  The signed digits z0 + 2^8 z1 + 2^16 z2 = Z
-        // (z0, z1 in [-128, 127]) have z0 = sext(byte 0 of Z), z1 = sext(byte
-        // 1 of Z + 128) and z2 = (Z + 32896) >> 16, whose byte is byte 2 of
-        // Z + 32896; 0x4B400000 adds nothing below bit 16 and 0x40 to byte
-        // 2, so the three digit bytes are bytes 0, 1, 2 of F, F + 128 and
-        // F + 32896 - 0x400000.
-        uint32_t F[8], G1[8], G2[8];
+        // rounded integer.  The signed digits z0 + 2^8 z1 = Z (z0 in
+        // [-128, 127]) have z0 = sext(byte 0 of Z) and z1 = (Z + 128) >> 8,
+        // whose byte is byte 1 of Z + 128; 0x4B400000 adds nothing below bit
+        // 16, so the two digit bytes are bytes 0 and 1 of F and F + 128.
+        uint32_t F[8], G1[8];
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             const float4 f = v[2 * p + w];
             const float q[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                F[4 * w + t] = __builtin_bit_cast(uint32_t, fmaf(q[t], sc, 12582912.0f));
+                F[4 * w + t] = __builtin_bit_cast(uint32_t, fmaf(q[t], c, 12582912.0f));
                 G1[4 * w + t] = F[4 * w + t] + 128u;
-                G2[4 * w + t] = F[4 * w + t] + (32896u - 0x400000u);
             }
         }
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             pl[0][2 * p + w] = gather_byte<0>(F[4 * w], F[4 * w + 1], F[4 * w + 2], F[4 * w + 3]);
             pl[1][2 * p + w] = gather_byte<1>(G1[4 * w], G1[4 * w + 1], G1[4 * w + 2], G1[4 * w + 3]);
-            pl[2][2 * p + w] = gather_byte<2>(G2[4 * w], G2[4 * w + 1], G2[4 * w + 2], G2[4 * w + 3]);
         }
         // sum of the eight Z: the F sum less 8 * 0x4B400000 (mod 2^32; the
-        // true sum is below 2^25 in magnitude)
+        // true sum is below 2^18 in magnitude)
         const uint32_t fs = (F[0] + F[1] + F[2]) + (F[3] + F[4] + F[5]) + (F[6] + F[7]);
         zs[p] = static_cast<float>(static_cast<int>(fs - 8u * 0x4B400000u));
     }
     if (store) {
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
+        for (int p = 0; p < 2; ++p) {
             *reinterpret_cast<uint4 *>(rec + kLmSlot * (2 * p)) = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
             *reinterpret_cast<uint4 *>(rec + kLmSlot * (2 * p + 1)) =
                 make_uint4(pl[p][4], pl[p][5], pl[p][6], pl[p][7]);
         }
         if constexpr (SH == kK4) {
-            // the reader needs each 16-value half's exponent and Z sum: one slot
-            *reinterpret_cast<int4 *>(rec + kLmSlot * 6) =
-                make_int4(ef[0], ef[2], __builtin_bit_cast(int, zs[0] + zs[1]), __builtin_bit_cast(int, zs[2] + zs[3]));
+            // the reader needs each 16-value half's unit and Z sum: one slot
+            *reinterpret_cast<float4 *>(rec + kLmSlot * 4) = make_float4(uf[0], uf[2], zs[0] + zs[1], zs[2] + zs[3]);
         } else {
-            *reinterpret_cast<int4 *>(rec + kLmSlot * 6) = make_int4(ef[0], ef[1], ef[2], ef[3]);
-            *reinterpret_cast<float4 *>(rec + kLmSlot * 7) = make_float4(zs[0], zs[1], zs[2], zs[3]);
+            *reinterpret_cast<float4 *>(rec + kLmSlot * 4) = make_float4(uf[0], uf[1], uf[2], uf[3]);
+            *reinterpret_cast<float4 *>(rec + kLmSlot * 5) = make_float4(zs[0], zs[1], zs[2], zs[3]);
         }
     }
 }
@@ -1066,16 +1060,13 @@ __device__ __forceinline__ void stage_run_dg(uint8_t *lds, const float4 &va, con
     m = fmaxf(m, quad_x1_f(m));
     m = fmaxf(m, quad_x2_f(m));
     // scale, F words, digit bytes and Z sum exactly as put_record_dg
-    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
-    const int se = min(275 - E, 254);
-    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
-    const int ef = 127 - se;
-    uint32_t F[8], G1[8], G2[8];
+    float c, uf;
+    dg_scale(m, c, uf);
+    uint32_t F[8], G1[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-        F[t] = __builtin_bit_cast(uint32_t, fmaf(q[t], sc, 12582912.0f));
+        F[t] = __builtin_bit_cast(uint32_t, fmaf(q[t], c, 12582912.0f));
         G1[t] = F[t] + 128u;
-        G2[t] = F[t] + (32896u - 0x400000u);
     }
     const uint32_t fs = (F[0] + F[1] + F[2]) + (F[3] + F[4] + F[5]) + (F[6] + F[7]);
     const float zs = static_cast<float>(static_cast<int>(fs - 8u * 0x4B400000u));
@@ -1088,17 +1079,17 @@ __device__ __forceinline__ void stage_run_dg(uint8_t *lds, const float4 &va, con
         make_uint2(gather_byte<0>(F[0], F[1], F[2], F[3]), gather_byte<0>(F[4], F[5], F[6], F[7]));
     *reinterpret_cast<uint2 *>(rec + kLmSlot * (2 + (p >> 1)) + off) =
         make_uint2(gather_byte<1>(G1[0], G1[1], G1[2], G1[3]), gather_byte<1>(G1[4], G1[5], G1[6], G1[7]));
-    *reinterpret_cast<uint2 *>(rec + kLmSlot * (4 + (p >> 1)) + off) =
-        make_uint2(gather_byte<2>(G2[0], G2[1], G2[2], G2[3]), gather_byte<2>(G2[4], G2[5], G2[6], G2[7]));
     if constexpr (SH == kK4) {
         const float zo = quad_x1_f(zs);  // the half's other run (p ^ 1)
         if ((p & 1) == 0) {
-            *reinterpret_cast<int *>(rec + kLmSlot * 6 + 4 * (p >> 1)) = ef;
-            *reinterpret_cast<float *>(rec + kLmSlot * 6 + 8 + 4 * (p >> 1)) = zs + zo;
+            *reinterpret_cast<float *>(rec + kLmSlot * 4 + 4 * (p >> 1)) = uf;
+            *reinterpret_cast<float *>(rec + kLmSlot * 4 + 8 + 4 * (p >> 1)) = zs + zo;
         }
+    } else if constexpr (SH == kS32) {
+        if (p == 0) *reinterpret_cast<float *>(rec + kLmSlot * 4) = uf;
     } else {
-        *reinterpret_cast<int *>(rec + kLmSlot * 6 + 4 * p) = ef;
-        *reinterpret_cast<float *>(rec + kLmSlot * 7 + 4 * p) = zs;
+        *reinterpret_cast<float *>(rec + kLmSlot * 4 + 4 * p) = uf;
+        *reinterpret_cast<float *>(rec + kLmSlot * 5 + 4 * p) = zs;
     }
 }
 
