@@ -231,10 +231,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             }
         }
     } else {
-        // refill per step, except where two rows of four steps are at the
-        // register limit already, and for Q5_K's short rows (0.2-0.3 us
+        // refill per step, except where IQ3_S's two rows of four steps are at
+        // the register limit already, and for Q5_K's short rows (0.2-0.3 us
         // slower with the refill at 14336x4096)
-        constexpr bool RF = (R == 1 || NIT < 4) && !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2);
+        constexpr bool RF = !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2) && !(TYPE == MI355X_TYPE_IQ3_S && R == 2 && NIT >= 4);
         for (; g < n_groups; g += stride) {
             const int64_t gn = g + stride;
             if constexpr (RF) {
