@@ -101,10 +101,12 @@ constexpr int kRunsPerThread = (32 * kChunkBlocks + kThreads - 1) / kThreads;
 // step t are refilled, right after its decode, with step t of row group gn
 // (an empty range when `next` is false: such loads read nothing), so the
 // next group's loads are in flight while the rest of this group decodes.
-template <int TYPE, int R, int NIT, bool DG, bool RF>
+// With XR (digit rows) the lane's activation slices come from xr, read from
+// LDS once per kernel, instead of from LDS at every step.
+template <int TYPE, int R, int NIT, bool DG, bool RF, bool XR = false>
 __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typename Kq<TYPE>::Regs (&regs)[R][NIT],
                                              const uint8_t *lds, const uint32_t *grid, int s, int bl, int lane,
-                                             int64_t gn = 0, bool next = false) {
+                                             int64_t gn = 0, bool next = false, const XDig *xr = nullptr) {
     using K = Kq<TYPE>;
     constexpr int SH = slice_shape(TYPE);
     Row nrows[RF ? R : 1];
@@ -117,7 +119,13 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typenam
         const int bloc = kBlocksPerStep * t + bl;
         const bool valid = step_in_chunk<NIT>(t, bloc, a.nb);
         const int bc = valid ? bloc : a.nb - 1;
-        if constexpr (DG) {
+        if constexpr (DG && XR) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float p = KqDg<TYPE>::compute(regs[r][t], s, xr[t], grid);
+                acc[r] = add_unfused(acc[r], valid ? p : 0.f);
+            }
+        } else if constexpr (DG) {
             XDig x;
             dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), x);
 #pragma unroll
@@ -235,11 +243,23 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
         // the register limit already, and for Q5_K's short rows (0.2-0.3 us
         // slower with the refill at 14336x4096)
         constexpr bool RF = !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2) && !(TYPE == MI355X_TYPE_IQ3_S && R == 2 && NIT >= 4);
+        // one row of at most four digit steps: the lane's activation slices
+        // stay in registers for all its row groups
+        constexpr bool XR = DG && RF && R == 1 && NIT <= 4;
+        XDig xr[XR ? NIT : 1];
+        if constexpr (XR) {
+#pragma unroll
+            for (int t = 0; t < NIT; ++t) {
+                const int bloc = kBlocksPerStep * t + bl;
+                const int bc = step_in_chunk<NIT>(t, bloc, a.nb) ? bloc : a.nb - 1;
+                dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), xr[t]);
+            }
+        }
         for (; g < n_groups; g += stride) {
             const int64_t gn = g + stride;
             if constexpr (RF) {
-                kq_row_group<TYPE, R, NIT, DG, true>(a, g, regs, lds, grid, s, bl, lane,
-                                                     gn < n_groups ? gn : n_groups - 1, gn < n_groups);
+                kq_row_group<TYPE, R, NIT, DG, true, XR>(a, g, regs, lds, grid, s, bl, lane,
+                                                         gn < n_groups ? gn : n_groups - 1, gn < n_groups, xr);
             } else {
                 kq_row_group<TYPE, R, NIT, DG, false>(a, g, regs, lds, grid, s, bl, lane);
                 if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
