@@ -239,13 +239,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
             }
         }
     } else {
-        // refill per step, except where IQ3_S's two rows of four steps are at
-        // the register limit already, and for Q5_K's short rows (0.2-0.3 us
-        // slower with the refill at 14336x4096)
-        constexpr bool RF = !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2) && !(TYPE == MI355X_TYPE_IQ3_S && R == 2 && NIT >= 4);
-        // one row of at most four digit steps: the lane's activation slices
-        // stay in registers for all its row groups
-        constexpr bool XR = DG && RF && R == 1 && NIT <= 4;
+        // refill per step, except where two rows of four steps are at the
+        // register limit already (IQ3_S's digit rows, the f32 rows), and for
+        // Q5_K's short rows (0.2-0.3 us slower with the refill at 14336x4096)
+        constexpr bool RF = !(TYPE == MI355X_TYPE_Q5_K && NIT <= 2) &&
+                            !(R == 2 && NIT >= 4 && (TYPE == MI355X_TYPE_IQ3_S || !DG));
+        // one digit row per step: the lane's activation slices stay in
+        // registers for all its row groups, up to the step counts whose
+        // registers fit without spilling (six steps of the K6 slices' 24
+        // words, seven of the others')
+        constexpr bool XR = DG && RF && R == 1 && (NIT <= 6 || (NIT == 7 && SH != kK6));
         XDig xr[XR ? NIT : 1];
         if constexpr (XR) {
 #pragma unroll
