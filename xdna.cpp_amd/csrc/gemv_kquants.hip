@@ -11,22 +11,27 @@
 // Work split.  A 512-thread workgroup stages the activations of one K chunk
 // in LDS once, with their sums over every 8 values, and (IQ types) the
 // codebook; each thread converts one 8-value run per pass, so the staging
-// work is spread evenly over the workgroup whatever the chunk length.  Each wavefront owns R rows at a time; its 64 lanes cover 8
-// superblocks per step, 8 lanes per superblock, one 32-value slice per lane,
-// NIT steps per row (NIT = ceil(superblocks / 8), a template parameter).
-// A lane reads its slices' codes and scales from the field planes with
-// buffer loads (out-of-range reads return 0) and forms
+// work is spread evenly over the workgroup whatever the chunk length.  Each
+// wavefront owns R rows at a time; its 64 lanes cover 8 superblocks per
+// step, 8 lanes per superblock, one 32-value slice per lane, NIT steps per
+// row (NIT = ceil(superblocks / 8), a template parameter).  A lane reads its
+// slices' codes and scales from the field planes with buffer loads
+// (out-of-range reads return 0) and forms
 //     sum_i scale_g * (code_i - offset_g) * x_i
 //       = sum_g scale_g * (sum_i code_i * x_i - offset_g * sum_i x_i)
-// so the per-value work is one byte convert and one FMA; the offsets (Q6_K
-// 32, Q3_K 4, IQ4_XS codebook bias 128, Q4_K/Q5_K mins) use the staged sums.
+// so the per-value work is one byte convert and one FMA (f32 rows) or a
+// share of two v_dot4 on 16-bit activation digits (digit rows); the offsets
+// (Q6_K 32, Q3_K 4, IQ4_XS codebook bias 128, Q4_K/Q5_K mins) use the staged
+// sums.
 //
-// Latency.  Every load a row group needs (R rows x NIT steps) is issued at
-// once, before any of it is used, so each wavefront keeps R * row_bytes in
-// flight.  In the prologue the activation loads are issued first, then the
-// first group's weight loads, and only then are the activations written to
-// LDS: loads retire in order, so the LDS writes wait for the activations
-// alone while the weight stream is already under way.
+// Latency.  Every load a row group needs (R rows x NIT steps) is in flight
+// before the group's decode starts: the prologue issues the first group's,
+// and each step's registers are reloaded with the next group's step right
+// after that step is decoded, so the next group's loads travel while the
+// rest of the current one decodes.  In the prologue the activation loads are
+// issued first, then the first group's weight loads, and only then are the
+// activations written to LDS: loads retire in order, so the LDS writes wait
+// for the activations alone while the weight stream is already under way.
 #include "internal.h"
 #include "kq_device.h"
 
