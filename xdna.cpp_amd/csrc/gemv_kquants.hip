@@ -98,8 +98,8 @@ __device__ __forceinline__ void load_group(const KqArgs &a, int64_t g, int s, in
     }
 }
 
-// runs of a chunk each thread of the row kernel stages, at most
-constexpr int kRunsPerThread = (32 * kChunkBlocks + kThreads - 1) / kThreads;
+// runs of a chunk each thread of an NT-thread row kernel stages, at most
+constexpr int runs_per_thread(int nt) { return (32 * kChunkBlocks + nt - 1) / nt; }
 
 // One row group: its NIT steps against the staged activations, then the
 // wavefront sums and the stores of its R outputs.  With RF the registers of
@@ -169,8 +169,13 @@ __device__ __forceinline__ void kq_row_group(const KqArgs &a, int64_t g, typenam
 // PF: a wavefront's next row group is requested before the current one's
 // decode (two register sets, alternating), so its loads travel while the
 // current group computes; requests past the last group read nothing.
-template <int TYPE, int R, int NIT, bool DG, bool PF>
-__global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
+// NT = kThreads: wavefront w of workgroup b takes row groups b * 8 + w,
+// stepping by the grid's wavefront count.  NT = kWideThreads (twelve
+// wavefronts, one workgroup per CU): workgroup b takes a contiguous block of
+// ceil(groups / grid) row groups, its wavefronts interleaved in it, so every
+// SIMD gets the same number of rows within one.
+template <int TYPE, int R, int NIT, bool DG, bool PF, int NT>
+__global__ __launch_bounds__(NT) void gemv_kq_kernel(KqArgs a) {
     using K = Kq<TYPE>;
     // the codebook in static LDS (its address is known when the lookups are
     // compiled, so no base is added per lookup), the lane-major records (f32
@@ -182,64 +187,76 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
     uint32_t *grid = table_kq;
     uint8_t *lds = reinterpret_cast<uint8_t *>(lds_kq);
 
+    constexpr int kNW = NT / 64;
+    constexpr int kRuns = runs_per_thread(NT);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int s = lane / kBlocksPerStep;
     const int bl = lane % kBlocksPerStep;
     const int64_t n_groups = (a.N + R - 1) / R;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
-    int64_t g = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+    int64_t g, g_end, stride;
+    if constexpr (NT == kThreads) {
+        stride = static_cast<int64_t>(gridDim.x) * kNW;
+        g = static_cast<int64_t>(blockIdx.x) * kNW + wave;
+        g_end = n_groups;
+    } else {
+        const int64_t per_wg = (n_groups + gridDim.x - 1) / gridDim.x;
+        const int64_t b0 = static_cast<int64_t>(blockIdx.x) * per_wg;
+        stride = kNW;
+        g = b0 + wave;
+        g_end = b0 + per_wg < n_groups ? b0 + per_wg : n_groups;
+    }
 
-    // 1. activation loads for staging: runs r = threadIdx.x + kThreads k of
+    // 1. activation loads for staging: runs r = threadIdx.x + NT k of
     // the chunk (8 values each)
     const int nruns = 32 * a.nb;
     const float *xc = a.x + static_cast<int64_t>(a.b0) * 256;
-    float4 xv[kRunsPerThread][2];
+    float4 xv[kRuns][2];
 #pragma unroll
-    for (int k = 0; k < kRunsPerThread; ++k) {
-        if (k == 0 || kThreads * k < nruns) {
-            const int r = static_cast<int>(threadIdx.x) + kThreads * k;
+    for (int k = 0; k < kRuns; ++k) {
+        if (k == 0 || NT * k < nruns) {
+            const int r = static_cast<int>(threadIdx.x) + NT * k;
             const float4 *src = reinterpret_cast<const float4 *>(xc + 8 * (r < nruns ? r : nruns - 1));
             xv[k][0] = src[0];
             xv[k][1] = src[1];
         }
     }
-    GridRegs<TYPE, kThreads> gr;
-    gr.fetch(a, threadIdx.x, kThreads);
+    GridRegs<TYPE, NT> gr;
+    gr.fetch(a, threadIdx.x, NT);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads of the first row group (waves without one read nothing)
     typename K::Regs regs[R][NIT];
-    load_group<TYPE, R, NIT>(a, g < n_groups ? g : n_groups - 1, s, bl, regs, g < n_groups);
+    load_group<TYPE, R, NIT>(a, g < g_end ? g : n_groups - 1, s, bl, regs, g < g_end);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. the runs' record fields into LDS (nruns is a multiple of 32, so the
     // quads of stage_run_dg are all in or all out); codebook
 #pragma unroll
-    for (int k = 0; k < kRunsPerThread; ++k) {
-        const int r = static_cast<int>(threadIdx.x) + kThreads * k;
-        if (kThreads * k < nruns && r < nruns) {
+    for (int k = 0; k < kRuns; ++k) {
+        const int r = static_cast<int>(threadIdx.x) + NT * k;
+        if (NT * k < nruns && r < nruns) {
             if constexpr (DG) stage_run_dg<SH>(lds, xv[k][0], xv[k][1], r >> 5, r & 31);
             else stage_run_f32<SH>(lds, xv[k][0], xv[k][1], r >> 5, r & 31);
         }
     }
-    if constexpr (DG) gr.put_dg(grid, threadIdx.x, kThreads);
-    else gr.put(grid, threadIdx.x, kThreads);
+    if constexpr (DG) gr.put_dg(grid, threadIdx.x, NT);
+    else gr.put(grid, threadIdx.x, NT);
     __syncthreads();
 
     // 4. row groups
     if constexpr (PF) {
         typename K::Regs nxt[R][NIT];
-        if (g < n_groups) {
+        if (g < g_end) {
             for (;;) {
                 const int64_t g1 = g + stride;
-                load_group<TYPE, R, NIT>(a, g1 < n_groups ? g1 : n_groups - 1, s, bl, nxt, g1 < n_groups);
+                load_group<TYPE, R, NIT>(a, g1 < g_end ? g1 : n_groups - 1, s, bl, nxt, g1 < g_end);
                 kq_row_group<TYPE, R, NIT, DG, false>(a, g, regs, lds, grid, s, bl, lane);
-                if (g1 >= n_groups) break;
+                if (g1 >= g_end) break;
                 const int64_t g2 = g1 + stride;
-                load_group<TYPE, R, NIT>(a, g2 < n_groups ? g2 : n_groups - 1, s, bl, regs, g2 < n_groups);
+                load_group<TYPE, R, NIT>(a, g2 < g_end ? g2 : n_groups - 1, s, bl, regs, g2 < g_end);
                 kq_row_group<TYPE, R, NIT, DG, false>(a, g1, nxt, lds, grid, s, bl, lane);
-                if (g2 >= n_groups) break;
+                if (g2 >= g_end) break;
                 g = g2;
             }
         }
@@ -263,14 +280,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kq_kernel(KqArgs a) {
                 dg_slice_lm<SH>(lds + lm_record(kDgGroupBytes, bc, s), xr[t]);
             }
         }
-        for (; g < n_groups; g += stride) {
+        for (; g < g_end; g += stride) {
             const int64_t gn = g + stride;
             if constexpr (RF) {
                 kq_row_group<TYPE, R, NIT, DG, true, XR>(a, g, regs, lds, grid, s, bl, lane,
-                                                         gn < n_groups ? gn : n_groups - 1, gn < n_groups, xr);
+                                                         gn < g_end ? gn : n_groups - 1, gn < g_end, xr);
             } else {
                 kq_row_group<TYPE, R, NIT, DG, false>(a, g, regs, lds, grid, s, bl, lane);
-                if (gn < n_groups) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
+                if (gn < g_end) load_group<TYPE, R, NIT>(a, gn, s, bl, regs);
             }
         }
     }
@@ -582,6 +599,9 @@ int xs_default_rows(int type) {
 
 typedef void (*kq_kernel_fn)(KqArgs);
 
+constexpr int kWideThreads = 768;
+constexpr int kWideMaxNit = 4;
+
 // R = 2 rows per wavefront only for short rows (NIT <= 2), where both rows'
 // loads and decode stay within ~128 VGPRs.
 constexpr int kMaxNitR2 = 2;
@@ -594,46 +614,62 @@ constexpr bool small_regs(int type) {
 constexpr int max_nit_r2(int type) { return small_regs(type) ? 4 : kMaxNitR2; }
 
 // R = 2 only without prefetch (two rows' loads and decode already fill the
-// registers); prefetch doubles the weight registers of R = 1.
+// registers); prefetch doubles the weight registers of R = 1.  `wide`: one
+// digit row per step in twelve-wavefront workgroups (rows of at most four
+// steps, whose registers allow three wavefronts per SIMD); IQ3_S only, the
+// one type it measured faster for (8192x8192, us: IQ3_S 9.3 against 9.7
+// with eight wavefronts; IQ2_S 8.2 either way; IQ3_XXS 8.1 against 7.8,
+// IQ4_XS 9.7 against 8.8).
 template <int TYPE, bool DG, bool PF>
-kq_kernel_fn pick_dg(int R, int nit) {
+kq_kernel_fn pick_dg(int R, int nit, bool wide) {
     if constexpr (!PF) {
         if (R == 2 && nit <= max_nit_r2(TYPE)) {
             if constexpr (small_regs(TYPE)) {
-                if (nit == 3) return gemv_kq_kernel<TYPE, 2, 3, DG, false>;
-                if (nit == 4) return gemv_kq_kernel<TYPE, 2, 4, DG, false>;
+                if (nit == 3) return gemv_kq_kernel<TYPE, 2, 3, DG, false, kThreads>;
+                if (nit == 4) return gemv_kq_kernel<TYPE, 2, 4, DG, false, kThreads>;
             }
-            return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG, false> : gemv_kq_kernel<TYPE, 2, 2, DG, false>;
+            return nit == 1 ? gemv_kq_kernel<TYPE, 2, 1, DG, false, kThreads>
+                            : gemv_kq_kernel<TYPE, 2, 2, DG, false, kThreads>;
+        }
+    }
+    if constexpr (DG && !PF && TYPE == MI355X_TYPE_IQ3_S) {
+        if (wide && nit <= kWideMaxNit) {
+            switch (nit) {
+            case 1: return gemv_kq_kernel<TYPE, 1, 1, DG, PF, kWideThreads>;
+            case 2: return gemv_kq_kernel<TYPE, 1, 2, DG, PF, kWideThreads>;
+            case 3: return gemv_kq_kernel<TYPE, 1, 3, DG, PF, kWideThreads>;
+            default: return gemv_kq_kernel<TYPE, 1, 4, DG, PF, kWideThreads>;
+            }
         }
     }
     switch (nit) {
-    case 1: return gemv_kq_kernel<TYPE, 1, 1, DG, PF>;
-    case 2: return gemv_kq_kernel<TYPE, 1, 2, DG, PF>;
-    case 3: return gemv_kq_kernel<TYPE, 1, 3, DG, PF>;
-    case 4: return gemv_kq_kernel<TYPE, 1, 4, DG, PF>;
-    case 5: return gemv_kq_kernel<TYPE, 1, 5, DG, PF>;
-    case 6: return gemv_kq_kernel<TYPE, 1, 6, DG, PF>;
-    case 7: return gemv_kq_kernel<TYPE, 1, 7, DG, PF>;
-    default: return gemv_kq_kernel<TYPE, 1, 8, DG, PF>;
+    case 1: return gemv_kq_kernel<TYPE, 1, 1, DG, PF, kThreads>;
+    case 2: return gemv_kq_kernel<TYPE, 1, 2, DG, PF, kThreads>;
+    case 3: return gemv_kq_kernel<TYPE, 1, 3, DG, PF, kThreads>;
+    case 4: return gemv_kq_kernel<TYPE, 1, 4, DG, PF, kThreads>;
+    case 5: return gemv_kq_kernel<TYPE, 1, 5, DG, PF, kThreads>;
+    case 6: return gemv_kq_kernel<TYPE, 1, 6, DG, PF, kThreads>;
+    case 7: return gemv_kq_kernel<TYPE, 1, 7, DG, PF, kThreads>;
+    default: return gemv_kq_kernel<TYPE, 1, 8, DG, PF, kThreads>;
     }
 }
 
 template <int TYPE>
-kq_kernel_fn pick(int R, int nit, bool dg, bool pf) {
-    if (pf) return dg ? pick_dg<TYPE, true, true>(R, nit) : pick_dg<TYPE, false, true>(R, nit);
-    return dg ? pick_dg<TYPE, true, false>(R, nit) : pick_dg<TYPE, false, false>(R, nit);
+kq_kernel_fn pick(int R, int nit, bool dg, bool pf, bool wide) {
+    if (pf) return dg ? pick_dg<TYPE, true, true>(R, nit, wide) : pick_dg<TYPE, false, true>(R, nit, wide);
+    return dg ? pick_dg<TYPE, true, false>(R, nit, wide) : pick_dg<TYPE, false, false>(R, nit, wide);
 }
 
-kq_kernel_fn pick_kernel(int type, int R, int nit, bool dg, bool pf) {
+kq_kernel_fn pick_kernel(int type, int R, int nit, bool dg, bool pf, bool wide) {
     switch (type) {
-    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, nit, dg, pf);
-    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, nit, dg, pf);
-    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, nit, dg, pf);
-    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, nit, dg, pf);
-    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, nit, dg, pf);
-    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, nit, dg, pf);
-    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, nit, dg, pf);
-    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, nit, dg, pf);
+    case MI355X_TYPE_Q4_K: return pick<MI355X_TYPE_Q4_K>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_Q5_K: return pick<MI355X_TYPE_Q5_K>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_Q3_K: return pick<MI355X_TYPE_Q3_K>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_Q6_K: return pick<MI355X_TYPE_Q6_K>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_IQ4_XS: return pick<MI355X_TYPE_IQ4_XS>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_IQ3_S: return pick<MI355X_TYPE_IQ3_S>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_IQ3_XXS: return pick<MI355X_TYPE_IQ3_XXS>(R, nit, dg, pf, wide);
+    case MI355X_TYPE_IQ2_S: return pick<MI355X_TYPE_IQ2_S>(R, nit, dg, pf, wide);
     default: return nullptr;
     }
 }
@@ -1310,7 +1346,9 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         int R = 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const bool pf = R == 1 && ctx->prefetch_override == 1;
-        const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf);
+        const bool wide = a.type == MI355X_TYPE_IQ3_S && dg && !pf && R == 1 && nit <= kWideMaxNit && nb >= 32;
+        const int nt = wide ? kWideThreads : kThreads;
+        const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf, wide);
         const int64_t n_groups = (a.N + R - 1) / R;
         // dynamic LDS: the records (the codebook is the kernel's static LDS)
         const size_t lds = dg ? dg_lds_bytes(nb) : x_lds_bytes(nb);
@@ -1323,13 +1361,14 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         // with one against 9.5 / 9.3 / 9.8 with two; 4096x14336 Q4_K 8.7 vs
         // 10.2; 14336x4096 Q3_K / Q4_K / Q6_K 8.4 / 7.5 / 11.0 with two
         // against 8.8 / 8.1 / 11.7 with three).
-        const int occ = occupancy(reinterpret_cast<const void *>(k), kThreads, lds);
+        const int occ = occupancy(reinterpret_cast<const void *>(k), nt, lds);
         const int per_cu = nb >= 32 ? 1 : nb >= 16 ? std::min(occ, 2) : occ;
-        int64_t wgs = std::min<int64_t>((n_groups + kWaves - 1) / kWaves, static_cast<int64_t>(ctx->num_cus) * per_cu);
+        const int nw = nt / 64;
+        int64_t wgs = std::min<int64_t>((n_groups + nw - 1) / nw, static_cast<int64_t>(ctx->num_cus) * per_cu);
         if (ctx->grid_override > 0) wgs = std::min<int64_t>(wgs, ctx->grid_override);
         KqArgs args{a.W, a.N, row_bytes, static_cast<int>(B), static_cast<int>(b0), nb, x, a.y, b0 > 0 ? 1 : 0,
                     grid};
-        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(wgs, 1))), dim3(kThreads), lds,
+        hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(std::max<int64_t>(wgs, 1))), dim3(nt), lds,
                            ctx->stream, args);
         MI355X_HIP(hipGetLastError());
     }
