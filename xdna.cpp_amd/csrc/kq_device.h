@@ -1,5 +1,5 @@
 // Device-side pieces of the K-quant and IQ GEMV kernels: resident-row loads,
-// per-type decode (f32 and 22-bit digit arithmetic), activation staging in
+// per-type decode (f32 and 16-bit digit arithmetic), activation staging in
 // lane-major LDS records and codebook staging.  Included by the kernel
 // sources; everything sits in an anonymous namespace, one copy per source.
 #pragma once
