@@ -13,7 +13,7 @@ import synth
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q4_K, IQ4_XS, IQ2_S = mi355x.Q4_0, mi355x.Q4_K, mi355x.IQ4_XS, mi355x.IQ2_S
+Q4_0, Q4_K, IQ4_XS, IQ2_S, IQ3_S = mi355x.Q4_0, mi355x.Q4_K, mi355x.IQ4_XS, mi355x.IQ2_S, mi355x.IQ3_S
 
 
 def synthetic_grid(t, seed):
@@ -43,8 +43,10 @@ def weights(ctx, t, N, K, seed):
 @pytest.fixture(scope="module")
 def mats(ctx):
     mi355x.set_iq_grid(IQ2_S, synthetic_grid(IQ2_S, IQ2_S))
+    # IQ3_S at K = 8192: twelve-wavefront workgroups in order, eight when
+    # overlapped (the same rows either way)
     spec = [(Q4_0, 4096, 4096), (Q4_0, 8192, 8192), (Q4_K, 1000, 4096), (IQ4_XS, 777, 8192), (Q4_0, 300, 2048),
-            (IQ2_S, 4096, 8192)]
+            (IQ2_S, 4096, 8192), (IQ3_S, 1531, 8192)]
     ws = [(t, N, K, weights(ctx, t, N, K, seed=i + 1)) for i, (t, N, K) in enumerate(spec)]
     xs = {K: ctx.to_device(synth.activations(K, seed=K)) for K in {K for _, _, K in spec}}
     yield ws, xs
