@@ -847,11 +847,23 @@ struct KqDg<MI355X_TYPE_IQ3_S> {
                                     const uint32_t *grid) {
         const uint2 *gt = reinterpret_cast<const uint2 *>(grid);
         const uint2 *st = gt + kIq3sGridSize;
+        // The 9-bit grid indices two at a time, as the halfwords of one
+        // word: bit k of qh spread to bit 0 of byte k % 4 of hb[k / 4]
+        // (n * 0x204081 puts copies of the 4-bit n at bits 0, 7, 14, 21: no
+        // two overlap, and bit j of copy j lands at bit 8j), then one v_perm
+        // interleaves those bytes with the low index bytes.
+        uint32_t hb[2] = {((g.qh & 15u) * 0x204081u) & 0x01010101u,
+                          ((g.qh >> 4) * 0x204081u) & 0x01010101u};  // qh < 256
+        // (opaque to the compiler, which otherwise narrows the low halfword's
+        // mask to 0x1FF and loses the one-instruction halfword shift)
+        asm("" : "+v"(hb[0]));
+        asm("" : "+v"(hb[1]));
         int sm[2] = {0, 0};
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
-            const uint32_t i0 = byte_u(g.qs[k >> 2], k & 3) | (((g.qh >> k) & 1u) << 8);
-            const uint32_t i1 = byte_u(g.qs[k >> 2], (k & 3) + 1) | (((g.qh >> (k + 1)) & 1u) << 8);
+            constexpr uint32_t kSel[2] = {0x05010400u, 0x07030602u};
+            const uint32_t pair = __builtin_amdgcn_perm(hb[k >> 2], g.qs[k >> 2], kSel[(k >> 1) & 1]);
+            const uint32_t i0 = pair & 0xFFFFu, i1 = pair >> 16;
             const uint2 e0 = gt[i0], e1 = gt[i1], sl = st[byte_u(g.sg, k >> 1)];
             dot2(__builtin_amdgcn_perm(e0.y, e0.x, sl.x), x, k, sm, k == 0);
             dot2(__builtin_amdgcn_perm(e1.y, e1.x, sl.y), x, k + 1, sm);
