@@ -575,7 +575,7 @@ int orc_row_norms(int type, const uint8_t *W, int64_t N, int64_t K, double *norm
 }
 
 /* ------------------------------------------------------------------------ */
-/* ggml-cpu's Q4_0 x Q8_0 numerics (EXTERNAL, parity unpinned)               */
+/* ggml-cpu's Q4_0 x Q8_0 numerics (EXTERNAL; pinned by known answers)       */
 /* ------------------------------------------------------------------------ */
 /* ggml's CPU backend does not multiply Q4_0 weights by f32 activations: it
  * first quantizes the activation row to Q8_0 (quantize_row_q8_0) and then
@@ -667,7 +667,7 @@ int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, f
 }
 
 /* ------------------------------------------------------------------------ */
-/* ggml-cpu's K-quant / IQ x Q8_K numerics (EXTERNAL, parity unpinned)       */
+/* ggml-cpu's K-quant / IQ x Q8_K numerics (EXTERNAL; pinned by known answers) */
 /* ------------------------------------------------------------------------ */
 /* The reference's live path for the eight 256-value types, whenever
  * ggml-cpu is loaded (src/xdna-gemv-engine.cpp:1382-1399, 1430-1453):

@@ -22,10 +22,16 @@
  *   IQ3_S     include/xdna/kquants.h:443-490, 565-577
  *   IQ3_XXS   ggml dequantize_row_iq3_xxs (external, llama.cpp 0ec4027a2;
  *             called by the reference only through ggml_vec_dot_iq3_xxs_q8_K,
- *             src/xdna-gemv-engine.cpp:1395)         -- parity unpinned
+ *             src/xdna-gemv-engine.cpp:1395)
  *   IQ2_S     ggml dequantize_row_iq2_s (external, same pin; reference call
- *             site src/xdna-gemv-engine.cpp:1396)      -- parity unpinned
- * IQ3_XXS / IQ2_S grids are not in the reference; callers pass them in.
+ *             site src/xdna-gemv-engine.cpp:1396)
+ * IQ3_XXS / IQ2_S grids are not in the reference; callers pass them in.  The
+ * reference holds no vectors for these two decoders, so they are pinned by
+ * encoders written from ggml's quantizer packing (the inverse direction, round
+ * trip through the decoder), known answers for every sign index and its parity
+ * bit, every IQ2_S sign bit, the scale nibbles, the index high bits and the
+ * scale factors, and probe blocks that read a grid back
+ * (tests/test_oracle_cpu.py, test_iq3_xxs_* and test_iq2_s_*).
  */
 #ifndef XDNA_ORACLE_H
 #define XDNA_ORACLE_H
@@ -97,15 +103,19 @@ int orc_row_norms(int type, const uint8_t *W, int64_t N, int64_t K, double *norm
  * ksigns_iq2xs, external).  Returns the byte for index i in [0,128). */
 uint8_t orc_ksigns_iq2xs(int i);
 
-/* ggml-cpu's Q4_0 x Q8_0 path (external restatement, parity unpinned; see
- * oracle.c): f32 -> fp16 round to even, Q8_0 quantization of an activation
- * row (K/32 blocks of [fp16 d][int8 q[32]]), and the Q4_0 x Q8_0 GEMV. */
+/* ggml-cpu's Q4_0 x Q8_0 path (external restatement, see oracle.c; pinned by
+ * the Q8_0 quantizer's invariants and hand-written known answers for its
+ * tie rounding, product association and block order, tests/ggml_q8_cases.py):
+ * f32 -> fp16 round to even, Q8_0 quantization of an activation row (K/32
+ * blocks of [fp16 d][int8 q[32]]), and the Q4_0 x Q8_0 GEMV. */
 uint16_t orc_f32_to_fp16(float f);
 int orc_quantize_row_q8_0(const float *x, int64_t K, uint8_t *out);
 int orc_gemv_q4_0_q8_0(const uint8_t *W, int64_t N, int64_t K, const float *x, float *y);
 
-/* ggml-cpu's K-quant / IQ x Q8_K path (external restatement, parity
- * unpinned; see oracle.c): Q8_K quantization of an activation row (K/256
+/* ggml-cpu's K-quant / IQ x Q8_K path (external restatement, see oracle.c;
+ * pinned by the Q8_K quantizer's invariants, known answers and the float64 dot
+ * of the dequantized operands, tests/test_oracle_cpu.py test_q8_K_* and
+ * test_gemv_q8_K_*): Q8_K quantization of an activation row (K/256
  * blocks of [f32 d][int8 q[256]][int16 bsums[16]]) and the GEMV of any of
  * the eight 256-value types against it. */
 #define ORC_Q8K_BYTES 292

@@ -284,7 +284,8 @@ def decode_gemv(kind: str = "reference"):
     (src/cpu-q4-gemv-engine.cpp), from oracle/_ref;
     kind "oracle": the scalar C restatement (liboracle.so);
     kind "ggml_q8": ggml-cpu's Q8_0-activation numerics, restated in
-    liboracle.so (external, parity unpinned; OpenMP over rows)."""
+    liboracle.so (external restatement, pinned by known answers; OpenMP over
+    rows)."""
     if kind == "reference":
         ref = RefLib()
         eng = RefCpuEngine(ref)

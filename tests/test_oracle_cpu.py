@@ -745,7 +745,9 @@ def test_kq_quantizer_zero_and_constant_blocks(oracle):
 
 # ---- ggml-cpu Q4_0 x Q8_0 numerics (external restatement) -------------------
 # ggml is not vendored in the reference, so this path cannot be compared with
-# ggml itself here ("parity unpinned"); what the mathematics fixes is pinned.
+# ggml itself here; it is pinned by what the mathematics fixes and by
+# hand-written known answers for ggml's rounding, product association and
+# block order (ggml_q8_cases.py).
 
 def test_f32_to_fp16_matches_numpy_round_to_even(oracle):
     # every fp16 value round-trips, and every midpoint between neighbours
@@ -861,8 +863,9 @@ def test_gemv_q4_0_q8_0_known_answer(oracle):
 # ---- ggml-cpu K-quant / IQ x Q8_K numerics (external restatement) -----------
 # The reference's live path for the 256-value types (src/xdna-gemv-engine.cpp:
 # 1382-1399, 1430-1453).  ggml itself is not in this build, so the f32 order
-# of ggml's generic code is restated, not compared ("parity unpinned" against
-# ggml); the quantizer, the integers and the sums are pinned here.
+# of ggml's generic code is restated, not compared with ggml; the quantizer,
+# the integers and the sums are pinned here by invariants, known answers and
+# the float64 dot of the dequantized operands.
 
 KQ_ALL = (Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS, IQ3_S, IQ3_XXS, IQ2_S)
 
