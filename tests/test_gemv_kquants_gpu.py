@@ -279,6 +279,32 @@ def test_many_row_groups_per_wavefront(ctx, name, variant, N, K):
         assert bad.size == 0, f"{name} {N}x{K} grid {cap}: {bad.size} rows differ, first {bad[:5]}"
 
 
+def test_iq3s_every_grid_index_in_every_position(ctx, oracle, variant):
+    """IQ3_S blocks whose 9-bit grid indices (low 8 bits from qs, the high
+    bit from qh: bit j % 8 of qh[j / 8] for index j of a superblock) take
+    all 512 values in each of the 64 index positions across the matrix's
+    512 superblocks, with random signs, scales and d: every index pair the
+    digit decode assembles in one word, and every lookup of the f32 decode,
+    reads the entry the oracle reads.  Rows of 32 superblocks: in order, the
+    default takes the twelve-wavefront kernel."""
+    t = ALL["IQ3_S"]
+    N, K = 16, 8192
+    nb = K // 256
+    raw = blocks(t, N, K, 5).reshape(N * nb, 110)
+    b = np.arange(N * nb)[:, None]
+    j = np.arange(64)[None, :]
+    idx = (b + 7 * j) % 512
+    raw[:, 2:66] = (idx & 255).astype(np.uint8)
+    hi = (idx >> 8).astype(np.uint8).reshape(N * nb, 8, 8)
+    raw[:, 66:74] = (hi << np.arange(8, dtype=np.uint8)).sum(axis=2).astype(np.uint8)
+    raw = raw.reshape(N, -1)
+    x = synth.activations(K, seed=19)
+    y = run(ctx, t, raw, N, K, x)
+    ref = oracle.gemv(t, raw, N, K, x)
+    norms = oracle.row_norms(t, raw, N, K)
+    check_gemv(y, ref, norms, x, "IQ3_S every grid index")
+
+
 def test_iq2s_extreme_grid_and_scales(ctx, oracle, variant):
     """IQ2_S at the edge of the digit arithmetic: every grid magnitude 127
     (the largest a grid may hold), every sign positive, every 4-bit scale
