@@ -52,7 +52,10 @@ def load_units(t, s):
     if t == 23:  # IQ4_XS
         return [(r(8 + 16 * s, 16), 4), (r(0, 8), 4)]
     if t == 11:  # Q3_K: codes + half of the shared hmask bytes, scales, d
-        return [(r(32 + 8 * s, 8) + r(8 * k + 4 * hh, 4), 4), (r(96, 12), 4), (r(108, 2), 2)]
+        # scales: the low-nibble bytes as words kk = 0, 1 ([kk], [kk + 4],
+        # [kk + 2], [kk + 6]), then scales[8..11]
+        lo = [96 + kk + 2 * j for kk in (0, 1) for j in (0, 2, 1, 3)]
+        return [(r(32 + 8 * s, 8) + r(8 * k + 4 * hh, 4), 4), (lo + r(104, 4), 4), (r(108, 2), 2)]
     if t == 14:  # Q6_K: ql, ql, qh runs; one scale word; d
         kk = k >> 1
         return [(r(64 * hh + 8 * k, 8) + r(64 * hh + 32 + 8 * k, 8) + r(128 + 32 * hh + 8 * k, 8), 4),

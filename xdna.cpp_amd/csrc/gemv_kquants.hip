@@ -914,8 +914,7 @@ __device__ __forceinline__ void k3_partial(const Kq<MI355X_TYPE_Q3_K>::Regs &g, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int lo_byte = 2 * j + kk;
-        const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
-        const int lo = static_cast<int>((byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u);
+        const int lo = static_cast<int>((Kq<MI355X_TYPE_Q3_K>::lo_scale_byte(g, kk, j) >> (4 * hh)) & 15u);
         const int hi = static_cast<int>((byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u);
         const int sc = (lo | (hi << 4)) - 32;
         const uint32_t *qv = reinterpret_cast<const uint32_t *>(q8 + 128 * hh + 32 * j + 8 * k);

@@ -366,8 +366,9 @@ struct Kq<MI355X_TYPE_Q3_K> {
         uint32_t sw2, d;
     };
     // lane record (8 code bytes, this slice's half h of the 8 hmask bytes it
-    // shares with slice s ^ 4, whose lane is lane ^ 32), the 12 scale bytes,
-    // d.  The loads return raw words; the exchange of h happens at decode
+    // shares with slice s ^ 4, whose lane is lane ^ 32), the 12 scale bytes
+    // (sw01[kk]: the low-nibble bytes of scales kk, kk + 4, kk + 2, kk + 6;
+    // sw2: scales[8..11]), d.  The loads return raw words; the exchange of h happens at decode
     // (hmask), so no load has to complete before the next one is issued.
     __device__ static Regs load(const Row &r, uint32_t b, int s) {
         const GPos q = gpos(r, 110, b, s);
@@ -382,6 +383,10 @@ struct Kq<MI355X_TYPE_Q3_K> {
     __device__ static u32x2 hmask(const Regs &g) {
         const auto sw = __builtin_amdgcn_permlane32_swap(g.h, g.h, false, false);
         return u32x2{static_cast<uint32_t>(sw[0]), static_cast<uint32_t>(sw[1])};
+    }
+    // The byte whose nibble hh is the low 4 bits of scale 8hh + kk + 2j.
+    __device__ static uint32_t lo_scale_byte(const Regs &g, int kk, int j) {
+        return byte_u(kk ? g.sw01[1] : g.sw01[0], ((j & 1) << 1) | (j >> 1));
     }
     __device__ static float compute(const Regs &g, int s, const XSlice &x, const uint32_t *) {
         const int hh = s >> 2, k = s & 3;
@@ -404,8 +409,7 @@ struct Kq<MI355X_TYPE_Q3_K> {
             // (nibble sidx / 8 = hh), high 2 bits from byte 8 + sidx % 4
             // (bit pair sidx / 4 = 2hh + j/2)
             const int lo_byte = 2 * j + kk;
-            const uint32_t lo_w = lo_byte < 4 ? g.sw01[0] : g.sw01[1];
-            const uint32_t lo = (byte_u(lo_w, lo_byte & 3) >> (4 * hh)) & 15u;
+            const uint32_t lo = (lo_scale_byte(g, kk, j) >> (4 * hh)) & 15u;
             const uint32_t hi = (byte_u(g.sw2, lo_byte & 3) >> (2 * (2 * hh + (j >> 1)))) & 3u;
             const float sc = static_cast<float>(static_cast<int>(lo | (hi << 4)) - 32);
             acc = fmaf(sc, sg[j] - 4.0f * x.s[j], acc);
@@ -798,18 +802,22 @@ struct KqDg<MI355X_TYPE_Q3_K> {
             dot2(((q >> 2) & 0x30303030u) | ((hs << 3) & 0x40404040u), x, 6 + w, sg[3], w == 0);
         }
         // The four 6-bit scales sidx = 8hh + kk + 2j (kk = k / 2) in one word,
-        // bytes in run order 0, 2, 1, 3: low nibbles from bytes kk, kk + 2
-        // (word 0) and kk + 4, kk + 6 (word 1) of scales[0..7], nibble hh; high
-        // bit pairs from bytes kk (runs 0, 2) and kk + 2 (runs 1, 3) of
-        // scales[8..11], pairs 2hh and 2hh + 1 (include/xdna/kquants.h:350-389).
+        // bytes in run order 0, 2, 1, 3: low nibbles (nibble hh) from the
+        // resident word sw01[kk], which holds scales[kk], [kk + 4], [kk + 2],
+        // [kk + 6] in that order; high bit pairs from bytes kk (runs 0, 2)
+        // and kk + 2 (runs 1, 3) of scales[8..11], pairs 2hh and 2hh + 1
+        // (include/xdna/kquants.h:350-389).
         const int kk = k >> 1;
-        const uint32_t L = ((g.sw01[0] >> (8 * kk)) & 0x00FF00FFu) | (((g.sw01[1] >> (8 * kk)) & 0x00FF00FFu) << 8);
+        const uint32_t L = kk ? g.sw01[1] : g.sw01[0];
         const uint32_t H = g.sw2 >> (8 * kk + 4 * hh);
         const uint32_t SC = ((L >> (4 * hh)) & 0x0F0F0F0Fu) | ((H & 0x00030003u) << 4) | ((H & 0x000C000Cu) << 10);
-        const float sc0 = static_cast<float>(SC & 0xFFu) - 32.0f;
-        const float sc2 = static_cast<float>((SC >> 8) & 0xFFu) - 32.0f;
-        const float sc1 = static_cast<float>((SC >> 16) & 0xFFu) - 32.0f;
-        const float sc3 = static_cast<float>(SC >> 24) - 32.0f;
+        // scale - 32 = the 6-bit scale with its top bit flipped, read as a
+        // signed 6-bit field (one signed bitfield extract per scale)
+        const int SX = static_cast<int>(SC ^ 0x20202020u);
+        const float sc0 = static_cast<float>((SX << 26) >> 26);
+        const float sc2 = static_cast<float>((SX << 18) >> 26);
+        const float sc1 = static_cast<float>((SX << 10) >> 26);
+        const float sc3 = static_cast<float>((SX << 2) >> 26);
         float acc = 0.f;
         acc = fmaf(sc0, (static_cast<float>(combine_shr<0>(sg[0])) - 4.0f * x.zs[0]) * x.u[0], acc);
         acc = fmaf(sc1, (static_cast<float>(combine_shr<2>(sg[1])) - 4.0f * x.zs[1]) * x.u[1], acc);

@@ -82,7 +82,11 @@ MI355X_HD constexpr KqLayout kq_layout(int type) {
 //   Q3_K    lane records of 12 B: qs[8s..8s+7] (the 8 codes bytes slice s =
 //             4hh + k reads), hmask[8k + 4hh .. +3] (half of the 8 high-bit
 //             bytes the slice pair (k, hh = 0/1) shares); 96g
-//           scales[12] per superblock at 96g + 12 bl; d at 108g + 2 bl
+//           scales[12] per superblock at 96g + 12 bl, the low-nibble bytes
+//             as two words, word kk = scales[kk], [kk + 4], [kk + 2],
+//             [kk + 6] (the four scales of slices 2kk, 2kk + 1, 4 + 2kk,
+//             5 + 2kk, in the order their high bits sit in scales[8..11]),
+//             then scales[8..11]; d at 108g + 2 bl
 //   Q6_K    lane records of 24 B: ql[64hh + 8k ..+7], ql[64hh + 32 + 8k ..+7],
 //             qh[32hh + 8k ..+7]; 192g
 //           scale words per superblock at 192g + 16 bl: word 2hh + kk holds
@@ -130,6 +134,10 @@ MI355X_HD constexpr uint64_t kq_group_offset(int type, uint64_t blk, int e, uint
             return q.base + 12 * lane(4 * hh + k) + 8 + j;
         }
         if (e < 96) return q.base + 12 * lane((e - 32) >> 3) + ((e - 32) & 7);
+        if (e < 104) {  // low-nibble byte kk + 2j: word kk, byte 0, 2, 1, 3 for j = 0..3
+            const int i = e - 96, kk = i & 1, j = i >> 1;
+            return q.base + 96 * g + 12 * bl + 4 * kk + ((j & 1) << 1) + (j >> 1);
+        }
         if (e < 108) return q.base + 96 * g + 12 * bl + (e - 96);
         return q.d + (e - 108);
     case 14:  // Q6_K
