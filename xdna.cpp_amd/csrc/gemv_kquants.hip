@@ -616,10 +616,11 @@ constexpr int max_nit_r2(int type) { return small_regs(type) ? 4 : kMaxNitR2; }
 // R = 2 only without prefetch (two rows' loads and decode already fill the
 // registers); prefetch doubles the weight registers of R = 1.  `wide`: one
 // digit row per step in twelve-wavefront workgroups (rows of at most four
-// steps, whose registers allow three wavefronts per SIMD); IQ3_S only, the
-// one type it measured faster for (8192x8192, us: IQ3_S 9.3 against 9.7
-// with eight wavefronts; IQ2_S 8.2 either way; IQ3_XXS 8.1 against 7.8,
-// IQ4_XS 9.7 against 8.8), and only for launches in order: with two
+// steps, whose registers allow three wavefronts per SIMD); IQ3_S and IQ2_S,
+// the types it measured faster for (8192x8192, us: IQ3_S 9.3 against 9.7
+// with eight wavefronts; IQ2_S with its 8-byte codebook 8.05-8.24, mean
+// 8.13 over eight runs, against 8.22-8.26, mean 8.24; IQ3_XXS 7.99-8.07 against 7.77-7.93, IQ4_XS 9.7 against 8.8),
+// and only for launches in order: with two
 // overlapped launches in flight IQ3_S took 7.9-8.0 us per launch with it
 // against 7.5 with eight wavefronts (one workgroup per CU leaves the next
 // launch's workgroups no room until it drains).
@@ -635,7 +636,7 @@ kq_kernel_fn pick_dg(int R, int nit, bool wide) {
                             : gemv_kq_kernel<TYPE, 2, 2, DG, false, kThreads>;
         }
     }
-    if constexpr (DG && !PF && TYPE == MI355X_TYPE_IQ3_S) {
+    if constexpr (DG && !PF && (TYPE == MI355X_TYPE_IQ3_S || TYPE == MI355X_TYPE_IQ2_S)) {
         if (wide && nit <= kWideMaxNit) {
             switch (nit) {
             case 1: return gemv_kq_kernel<TYPE, 1, 1, DG, PF, kWideThreads>;
@@ -1348,7 +1349,8 @@ int launch_gemv_kquant(mi355x_ctx *ctx, const GemvArgs &a) {
         int R = 1;
         if (ctx->rows_override == 1 || (ctx->rows_override == 2 && nit <= max_nit_r2(a.type))) R = ctx->rows_override;
         const bool pf = R == 1 && ctx->prefetch_override == 1;
-        const bool wide = a.type == MI355X_TYPE_IQ3_S && dg && !pf && R == 1 && nit <= kWideMaxNit && nb >= 32 &&
+        const bool wide = (a.type == MI355X_TYPE_IQ3_S || a.type == MI355X_TYPE_IQ2_S) && dg && !pf && R == 1 &&
+                          nit <= kWideMaxNit && nb >= 32 &&
                           !ctx->ov_open;
         const int nt = wide ? kWideThreads : kThreads;
         const kq_kernel_fn k = pick_kernel(a.type, R, nit, dg, pf, wide);
